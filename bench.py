@@ -1,0 +1,275 @@
+"""Benchmark: NF4 GEMV HBM GB/s (% of peak) + decode step ms/token, one MI355X.
+
+Step (the `value`): the seven batch-1 linears of one Qwen3-4B-shaped decoder
+layer in NF4 with double-quant absmax (uint8, bs2 256, fp32 scale + offset),
+bf16 activations - q 2560->4096, k/v 2560->1024, o 4096->2560, gate/up
+2560->9728, down 9728->2560 - 52,186,204 algorithmic bytes per step.
+Weights rotate over enough distinct copies (> 512 MB) that every step streams
+from HBM, not from the 256 MB Infinity Cache; launches are replayed from a
+HIP graph so the GPU runs them back to back. value = bytes / time (GB/s).
+
+Also reported: the dominant kernel (gate 9728x2560) timed alone with HIP
+events on its stream -> `roofline`; the single fp16 GEMV of the reference's
+CPU-runnable case (plain fp32 absmax) -> `gemv_fp16_plain`; the synthetic
+Dual-AR decode step -> `decode`; and the CPU baseline (the reference's CPU
+NF4 GEMV algorithm restated in C++, on this host's cores) -> `cpu_baseline`.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+HBM_PEAK_GBS = 8000.0
+MALL_BYTES = 256 * 2**20
+
+# (name, out_features, in_features) of one decoder layer's linears
+LAYER = [("q", 4096, 2560), ("k", 1024, 2560), ("v", 1024, 2560), ("o", 2560, 4096),
+         ("gate", 9728, 2560), ("up", 9728, 2560), ("down", 2560, 9728)]
+
+
+def nf4_bytes(M: int, K: int, nested: bool, dsize: int = 2, bs: int = 64, bs2: int = 256) -> int:
+    """Algorithmic bytes of one GEMV: packed weight + scales + x + y."""
+    nblk = M * K // bs
+    if nested:
+        scales = nblk + 4 * math.ceil(nblk / bs2) + 256 * 4 + 4  # a8, absmax2, code2, offset
+    else:
+        scales = 4 * nblk
+    return M * K // 2 + scales + dsize * K + dsize * M
+
+
+class Linear:
+    """Device buffers of one NF4 linear, random codes and scales."""
+
+    def __init__(self, M, K, nested, seed, device):
+        import torch
+
+        from ttspipe_amd.quant import create_dynamic_map
+
+        g = torch.Generator(device=device).manual_seed(seed)
+        self.M, self.K, self.nested = M, K, nested
+        nblk = M * K // 64
+        self.w = torch.randint(0, 256, (M * K // 2,), dtype=torch.uint8, device=device, generator=g)
+        if nested:
+            self.a8 = torch.randint(0, 256, (nblk,), dtype=torch.uint8, device=device, generator=g)
+            self.amax = torch.rand(-(-nblk // 256), device=device, generator=g) * 0.01 + 0.01
+            self.code2 = create_dynamic_map().to(device)
+            self.offset = 0.04
+        else:
+            self.a8, self.code2, self.offset = None, None, 0.0
+            self.amax = torch.rand(nblk, device=device, generator=g) * 0.04 + 0.02
+
+
+def launch(lib, lut, lin, x, y, dt, stream):
+    from ttspipe_amd import _lib
+
+    rc = lib.ttsp_nf4_gemm(x.data_ptr(), dt, lin.w.data_ptr(), _lib.ptr(lin.a8), lin.amax.data_ptr(),
+                           _lib.ptr(lin.code2), lin.offset, lut.data_ptr(), y.data_ptr(), 0, 0, lin.M, lin.K, 1,
+                           64, 256, stream)
+    if rc:
+        raise RuntimeError(f"ttsp_nf4_gemm failed: {rc}")
+
+
+def time_graph(graph, replays: int, stream) -> float:
+    """Seconds per replay, HIP events on the graph's launch stream."""
+    import torch
+
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record(stream)
+    for _ in range(replays):
+        graph.replay()
+    end.record(stream)
+    end.synchronize()
+    return start.elapsed_time(end) / 1e3 / replays
+
+
+def capture(fn):
+    import torch
+
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        fn()
+    return graph
+
+
+def bench_layer(steps: int, warmup: int):
+    """C2: the seven linears of one layer, nested absmax, bf16 x."""
+    import torch
+
+    from ttspipe_amd import _lib
+    from ttspipe_amd.quant import NF4_CODE
+
+    lib = _lib.load()
+    dev = torch.device("cuda", 0)
+    lut = torch.tensor(NF4_CODE, dtype=torch.float32, device=dev)
+    step_bytes = sum(nf4_bytes(M, K, True) for _, M, K in LAYER)
+    weight_bytes = sum(M * K // 2 for _, M, K in LAYER)
+    ncopy = max(2, math.ceil(2 * MALL_BYTES / weight_bytes))  # > 512 MB of weights in rotation
+    copies = [[Linear(M, K, True, seed=1000 * c + i, device=dev) for i, (_, M, K) in enumerate(LAYER)]
+              for c in range(ncopy)]
+    xs = {K: torch.randn(K, device=dev).to(torch.bfloat16) for K in {K for _, _, K in LAYER}}
+    ys = {name: torch.empty(M, dtype=torch.bfloat16, device=dev) for name, M, _ in LAYER}
+
+    def body():
+        st = torch.cuda.current_stream().cuda_stream
+        for layer in copies:
+            for (name, M, K), lin in zip(LAYER, layer):
+                launch(lib, lut, lin, xs[K], ys[name], _lib.DT_BF16, st)
+
+    body()
+    torch.cuda.synchronize()
+    graph = capture(body)
+    stream = torch.cuda.current_stream()
+    reps_w = max(1, warmup // ncopy)
+    time_graph(graph, reps_w, stream)
+    reps = max(1, steps // ncopy)
+    sec = time_graph(graph, reps, stream) / ncopy
+    return {"step_bytes": step_bytes, "sec_per_step": sec, "steps": reps * ncopy, "copies": ncopy,
+            "warmup": reps_w * ncopy}
+
+
+def bench_kernel(M, K, nested, dtype_name, launches_per_copy=1, min_bytes=2 * MALL_BYTES):
+    """One GEMV shape alone: average seconds per launch over > 512 MB of distinct weights."""
+    import torch
+
+    from ttspipe_amd import _lib
+    from ttspipe_amd.quant import NF4_CODE
+
+    lib = _lib.load()
+    dev = torch.device("cuda", 0)
+    dt = _lib.DT_BF16 if dtype_name == "bf16" else _lib.DT_F16
+    tdt = torch.bfloat16 if dt == _lib.DT_BF16 else torch.float16
+    lut = torch.tensor(NF4_CODE, dtype=torch.float32, device=dev)
+    ncopy = max(2, math.ceil(min_bytes / (M * K // 2)))
+    lins = [Linear(M, K, nested, seed=77 + c, device=dev) for c in range(ncopy)]
+    x = torch.randn(K, device=dev).to(tdt)
+    y = torch.empty(M, dtype=tdt, device=dev)
+
+    def body():
+        st = torch.cuda.current_stream().cuda_stream
+        for lin in lins:
+            launch(lib, lut, lin, x, y, dt, st)
+
+    body()
+    torch.cuda.synchronize()
+    graph = capture(body)
+    stream = torch.cuda.current_stream()
+    time_graph(graph, 3, stream)
+    reps = max(3, 2000 // ncopy)
+    sec = time_graph(graph, reps, stream) / ncopy
+    nbytes = nf4_bytes(M, K, nested, 2)
+    del lins
+    return {"M": M, "K": K, "nested": nested, "dtype": dtype_name, "sec": sec, "bytes": nbytes,
+            "gbs": nbytes / sec / 1e9, "launches": reps * ncopy, "copies": ncopy}
+
+
+def cpu_baseline(seconds: float = 10.0):
+    """The reference's CPU NF4 GEMV algorithm (restated in C++) on this host."""
+    try:
+        from oracle import cpu_baseline as cb
+    except Exception as exc:  # noqa: BLE001
+        return {"value": None, "unit": "GB/s", "cores": None, "kind": "port", "sample": f"unavailable: {exc}"}
+    return cb.run(LAYER, seconds=seconds)
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=4000)
+    ap.add_argument("--warmup", type=int, default=200)
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--skip-cpu", action="store_true")
+    ap.add_argument("--skip-decode", action="store_true")
+    ap.add_argument("--only", choices=["layer", "kernel", "c1"], default=None,
+                    help="run one GPU measurement only (for profiling runs)")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU: this path has no multi-GPU mode (see DESIGN.md on sharding)",
+              file=sys.stderr)
+        return 2
+
+    import torch
+
+    torch.cuda.set_device(0)
+    out = {}
+    if args.only in (None, "layer"):
+        layer = bench_layer(args.steps, args.warmup)
+        out["layer"] = layer
+    if args.only in (None, "kernel"):
+        out["kernel"] = bench_kernel(9728, 2560, True, "bf16")
+    if args.only in (None, "c1"):
+        out["c1"] = bench_kernel(9728, 2560, False, "fp16")
+    if args.only is not None:
+        print(json.dumps(out))
+        return 0
+
+    decode = None
+    if not args.skip_decode:
+        try:
+            from ttspipe_amd import dualar
+
+            decode = dualar.benchmark()
+        except Exception as exc:  # noqa: BLE001
+            decode = {"error": str(exc)}
+    cpu = None if args.skip_cpu else cpu_baseline(args.cpu_seconds)
+
+    layer, kern, c1 = out["layer"], out["kernel"], out["c1"]
+    value = layer["step_bytes"] / layer["sec_per_step"] / 1e9
+    line = {
+        "metric": "NF4 GEMV HBM GB/s (% of peak) + decode step ms/token, 4B-dim model, 1 GPU",
+        "value": round(value, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": layer["steps"],
+        "warmup": layer["warmup"],
+        "ms_per_step": round(layer["sec_per_step"] * 1e3, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {
+            "workload": "one Qwen3-4B-shaped decoder layer, batch 1: q 2560->4096, k/v 2560->1024, "
+                        "o 4096->2560, gate/up 2560->9728, down 9728->2560; NF4 bs64, double-quant absmax "
+                        "(uint8, bs2 256, fp32 scale+offset); x bf16",
+            "bytes_per_step": layer["step_bytes"],
+            "weight_copies_rotated": layer["copies"],
+            "pct_of_hbm_peak": round(100 * value / HBM_PEAK_GBS, 1),
+        },
+        "roofline": {
+            "bound": "hbm",
+            "kernel": "nf4_gemv_kernel (gate 9728x2560, nested, bf16)",
+            "achieved": round(kern["gbs"], 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(kern["gbs"] / HBM_PEAK_GBS, 4),
+            "traffic": None,
+            "avg_launch_us": round(kern["sec"] * 1e6, 3),
+            "bytes_per_launch": kern["bytes"],
+        },
+        "gemv_fp16_plain": {
+            "shape": "9728x2560 fp16 x, fp32 absmax bs64",
+            "gbs": round(c1["gbs"], 1),
+            "pct_of_peak": round(100 * c1["gbs"] / HBM_PEAK_GBS, 1),
+            "avg_launch_us": round(c1["sec"] * 1e6, 3),
+            "bytes_per_launch": c1["bytes"],
+        },
+        "decode": decode,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line))
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

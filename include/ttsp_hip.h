@@ -1,0 +1,128 @@
+/*
+ * C-ABI of libttsp_hip.so - the MI355X (gfx950) NF4 decode hot path.
+ *
+ * Every entry point takes raw device pointers, sizes and a hipStream_t
+ * (passed as void*), launches on that stream, returns a hipError_t (0 on
+ * success, hipErrorInvalidValue = 1 for arguments it rejects) and allocates
+ * nothing. Scratch memory is always caller-provided.
+ *
+ * Element types: TTSP_F16 = 0, TTSP_BF16 = 1, TTSP_F32 = 2 (16-bit types are
+ * passed as raw bit patterns).
+ *
+ * NF4 layout (bitsandbytes): W is the row-major flattened [M, K] weight, two
+ * codes per byte with the even flattened index in the high nibble; scale
+ * block b covers flattened codes [b*bs, (b+1)*bs). Plain scales: fp32
+ * AMAX[b]. Nested (double-quant) scales: A8 uint8 [M*K/bs], AMAX = fp32
+ * absmax2 [ceil(M*K/bs / bs2)], CODE2 = fp32 [256], plus `offset`:
+ * s_b = CODE2[A8[b]] * AMAX[b / bs2] + offset. LUT = the 16 fp32 NF4 codes.
+ *
+ * Citations are into the reference tree (bitNtech/ttspipe); the reference
+ * reaches its CUDA kernels through NVRTC + cuLaunchKernel via ctypes
+ * (app/engine/nvrtc.py:118-198), and these functions are what its ctypes
+ * argument blocks would bind instead.
+ */
+#ifndef TTSP_HIP_H
+#define TTSP_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum { TTSP_F16 = 0, TTSP_BF16 = 1, TTSP_F32 = 2 };
+enum { TTSP_EPI_NONE = 0, TTSP_EPI_RESIDUAL = 1, TTSP_EPI_SILU_GATE = 2 };
+
+/* Y[N][M] = epi(X[N][K] . dequant(W)^T). N == 1 runs the HBM-bound GEMV, N > 1
+ * the LDS-staged MFMA GEMM. epi 1: Y = round(R + round(XW)); epi 2:
+ * Y = round(round(silu(R)) * round(XW)); R has Y's shape. Requires K % 128 == 0,
+ * K % blocksize == 0, blocksize a power of two >= 64, blocksize2 a power of two
+ * (nested only), 16-byte aligned X and W. A8 == NULL selects plain scales.
+ * Replaces: the nf4_mma kernel and its launch, app/engine/nf4gemv.py:108-229,
+ * 459-477 (argument block built at nf4gemv.py:385-405). */
+int ttsp_nf4_gemm(const void* X, int x_dtype, const uint8_t* W, const uint8_t* A8,
+                  const float* AMAX, const float* CODE2, float offset, const float* LUT, void* Y,
+                  const void* R, int epi, int M, int K, int N, int blocksize, int blocksize2,
+                  void* stream);
+
+/* out[k] = round(LUT[q_k] * s_{k / blocksize}) for the n flattened codes, one
+ * rounding, out_dtype TTSP_F16/BF16/F32. Replaces: the dequantisation inside
+ * nf4_mma (app/engine/nf4gemv.py:154-188) and bitsandbytes' dequantize_4bit
+ * that the reference's fallback calls (tests/test_nf4gemv.py:77-80). */
+int ttsp_nf4_dequant(const uint8_t* W, const uint8_t* A8, const float* AMAX, const float* CODE2,
+                     float offset, const float* LUT, void* out, int out_dtype, long long n,
+                     int blocksize, int blocksize2, void* stream);
+
+/* Launch shape the N == 1 GEMV uses for [M, K]: J 64-dword chunks per lane,
+ * K split over KS waves, RPW rows per wave. The arithmetic order depends on KS
+ * only. Host-only query; no GPU needed. Replaces: _config (app/engine/
+ * nf4gemv.py:234-246). */
+int ttsp_gemv_shape(int M, int K, int* J, int* KS, int* RPW);
+
+/* Fork RMSNorm over the last axis: Y = round(round(X * r) * Wt),
+ * r = 1 / sqrt(sum(X^2) / D + eps); rows x D, D % 8 == 0, dtype F16/BF16.
+ * Replaces: rms_norm kernel + launch, app/engine/fusedops.py:61-94, 169-196. */
+int ttsp_rms_norm(const void* X, const void* Wt, void* Y, int rows, int D, float eps, int dtype,
+                  void* stream);
+
+/* Interleaved-pair rotary of X [B, S, heads, 2*half_dim] against
+ * F [S, half_dim, 2] (cos, sin) of type ftype: y0 = x0*c - x1*s, y1 = x1*c + x0*s,
+ * no fma, one rounding. pairs = X elements / 2.
+ * Replaces: rope kernel + launch, app/engine/fusedops.py:103-133, 199-236. */
+int ttsp_rope(const void* X, const void* F, int ftype, void* Y, long long pairs, int half_dim,
+              int heads, int seq, int dtype, void* stream);
+
+/* Per head of QKV [(nh + 2*nkv) * 128]: optional head norm (QW / KW may be
+ * NULL), rotary with F [64, 2], write Q [nh*128] or KC[kv][POS[0]][:], copy V to
+ * VC[kv][POS[0]][:]. Caches are [nkv][max_len][128]; POS is one int64 on the
+ * device; nothing is written if POS[0] is outside [0, max_len).
+ * Replaces: qk_rope_kv, app/engine/fusedlayer.py:56-92, 233-242. */
+int ttsp_qk_rope_kv(const void* QKV, const void* QW, const void* KW, float eps, const void* F,
+                    int ftype, const long long* POS, void* Q, void* KC, void* VC, int nh, int nkv,
+                    int max_len, int dtype, void* stream);
+
+/* Grouped-query decode attention of Q [nh*128] over cache positions
+ * [0, min(POS[0] + 1, max_len)), split into nchunk chunks of
+ * ttsp_attn_chunk() positions, then merged: Y [nh*128]. Scratch (caller's):
+ * PM, PL [nh * nchunk] and PACC [nh * nchunk * 128], fp32. nh % nkv == 0,
+ * nh / nkv <= 16. Replaces: attn_partial + attn_combine,
+ * app/engine/fusedlayer.py:95-159, 244-261. */
+int ttsp_attn_decode(const void* Q, const void* KC, const void* VC, const long long* POS, float* PM,
+                     float* PL, float* PACC, void* Y, int nh, int nkv, int max_len, int nchunk,
+                     float scale, int dtype, void* stream);
+
+/* Cache positions per attention chunk (64). Replaces: CHUNK,
+ * app/engine/fusedlayer.py:40. */
+int ttsp_attn_chunk(void);
+
+/* out[d] = round(sum_{c < ntok} E[(c*vocab + tok[c]) * D + d]) (tok int32 on the
+ * device, clamped into [0, vocab)). Replaces: the codebook-embedding lookup of
+ * a decode step (app/engine/graphs.py:124-131 via the fork's _fast_embed /
+ * embed). */
+int ttsp_embed_sum(const void* E, const int* tok, int ntok, int vocab, int D, void* out, int dtype,
+                   void* stream);
+
+/* out[0] = argmax(X[0..n)), lowest index on ties: greedy decoding in place of
+ * the sampler (app/engine/graphs.py:57-73, fusedsample.py). */
+int ttsp_argmax(const void* X, int n, int dtype, int* out, void* stream);
+
+/* Deterministic synthetic data: element i of a tensor seeded `seed` is a
+ * function of splitmix64(splitmix64(seed) ^ i). kind 0: uint8 (top byte);
+ * 1/2/3: u*scale + offset as bf16/f16/f32 with u uniform in [-1, 1).
+ * No counterpart in the reference: it materialises the random-init weights
+ * of the synthetic benchmark model on the device. */
+int ttsp_synth_fill(void* out, long long n, unsigned long long seed, int kind, float scale,
+                    float offset, void* stream);
+
+/* Numerics self-tests (no counterpart in the reference; for the test suite):
+ * op 0 exp, 1 correctly rounded sqrt, 2 1/sqrt, 3 silu, each as the kernels
+ * compute them; dot2: round(a.lo*b.lo + a.hi*b.hi) on packed F16/BF16 pairs. */
+int ttsp_selftest_math(const float* in, int n, int op, float* out, void* stream);
+int ttsp_selftest_dot2(const uint32_t* a, const uint32_t* b, int n, int dtype, float* out,
+                       void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* TTSP_HIP_H */

@@ -1,0 +1,249 @@
+"""The NF4 GEMV / GEMM / dequantisation kernels against the oracle (GPU).
+
+Bar (written per test): dequantised weights and the one-row GEMV bit for bit
+against the oracle's emulation of the kernel's fixed order; the GEMV and the
+MFMA GEMM within 2e-3 (relative to max |y|, beyond the output type's own
+half-ulp rounding) of the fp64 product on the dequantised weights; epilogues
+bit for bit. Shapes are the reference's (tests/test_nf4gemv.py:119-186) plus
+the Dual-AR fast transformer's.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle as o
+from tests.conftest import beyond_rounding_error, relative_error
+from tests.gpuutil import bits, dt_code, first_mismatch, from_bits, gemv_shape, randn_bits
+from tests.nf4data import dequant_numpy, oracle_args, random_layer, to_linear
+
+pytestmark = pytest.mark.gpu
+
+DTYPES = [torch.float16, torch.bfloat16]
+
+
+@pytest.fixture(scope="module")
+def nf4():
+    from ttspipe_amd import nf4gemv
+
+    assert nf4gemv.install(), "nf4 kernels unavailable on a GPU machine"
+    return nf4gemv
+
+
+# ------------------------------------------------------------ numerics primitives
+
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_dot2_is_one_rounding_of_two_exact_products(hip, dtype):
+    """The kernels' zero-addend dot2 is round(a0*b0 + a1*b1): checked bit for bit
+    against IEEE fp32 on random, tiny, huge and cancelling pairs."""
+    rng = np.random.default_rng(0)
+    n = 1 << 16
+    vals = np.concatenate([rng.standard_normal(n) * 10.0 ** rng.integers(-6, 4, n),
+                           rng.standard_normal(n)]).astype(np.float32)
+    a = o.from_f32(vals[:n].copy(), dt_code(dtype)).view(np.uint32)
+    b = o.from_f32(vals[n:].copy(), dt_code(dtype)).view(np.uint32).copy()
+    # exact cancellations: (x0, x1) . (x1, -x0) = 0
+    b[:1000] = ((a[:1000] >> 16) | ((a[:1000] & 0xFFFF) << 16)) ^ 0x80000000
+    at = torch.from_numpy(a.view(np.int32).copy()).cuda()
+    bt = torch.from_numpy(b.view(np.int32).copy()).cuda()
+    out = torch.empty(a.size, dtype=torch.float32, device="cuda")
+    from ttspipe_amd import _lib
+
+    rc = hip.ttsp_selftest_dot2(at.data_ptr(), bt.data_ptr(), a.size, dt_code(dtype), out.data_ptr(), _lib.stream())
+    assert rc == 0
+    af = o.to_f32(a.view(np.uint16), dt_code(dtype)).reshape(-1, 2)
+    bf = o.to_f32(b.view(np.uint16), dt_code(dtype)).reshape(-1, 2)
+    expect = (af[:, 0] * bf[:, 0]).astype(np.float32) + (af[:, 1] * bf[:, 1]).astype(np.float32)
+    got = out.cpu().numpy()
+    assert np.array_equal(got.view(np.uint32), expect.astype(np.float32).view(np.uint32)), first_mismatch(got, expect)
+
+
+@pytest.mark.parametrize("op", [0, 1, 2, 3])
+def test_device_math_matches_the_oracle_bit_for_bit(hip, orc, op):
+    from ttspipe_amd import _lib
+
+    rng = np.random.default_rng(op)
+    if op == 0:
+        x = np.concatenate([np.linspace(-90, 90, 40001), rng.uniform(-87, 0, 20000)]).astype(np.float32)
+    elif op in (1, 2):
+        x = np.concatenate([10.0 ** rng.uniform(-6, 6, 40000), rng.uniform(1e-6, 4, 20000)]).astype(np.float32)
+    else:
+        x = rng.uniform(-30, 30, 40000).astype(np.float32)
+    xt = torch.from_numpy(x).cuda()
+    out = torch.empty_like(xt)
+    assert hip.ttsp_selftest_math(xt.data_ptr(), x.size, op, out.data_ptr(), _lib.stream()) == 0
+    got = out.cpu().numpy()
+    if op == 0:
+        expect = orc.exp_cw(x)
+    elif op == 1:
+        expect = np.sqrt(x)  # numpy's float32 sqrt is correctly rounded
+    elif op == 2:
+        expect = (np.float32(1.0) / np.sqrt(x)).astype(np.float32)
+    else:
+        e = orc.exp_cw(-x)
+        expect = (x / (np.float32(1.0) + e)).astype(np.float32)
+    assert np.array_equal(got.view(np.uint32), expect.view(np.uint32)), first_mismatch(got, expect)
+
+
+# ------------------------------------------------------------------ dequant
+
+@pytest.mark.parametrize("nested", [True, False])
+@pytest.mark.parametrize("out_dtype", [torch.float16, torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("shape", [(9728, 2560), (13, 64 * 3), (1, 64)])
+def test_dequant_is_bit_exact(nested, out_dtype, shape):
+    from ttspipe_amd.quant import dequantize_4bit
+
+    layer = random_layer(*shape, nested, seed=shape[0])
+    lin = to_linear(layer, torch.bfloat16)
+    got = dequantize_4bit(lin.weight.data, lin.weight.quant_state, out_dtype=out_dtype)
+    expect = dequant_numpy(layer, dt_code(out_dtype))
+    assert np.array_equal(bits(got), expect), first_mismatch(bits(got), expect)
+
+
+# ------------------------------------------------------------------ GEMV
+
+GEMV_SHAPES = [
+    (6144, 2560),  # wqkv
+    (2560, 4096),  # wo
+    (9728, 2560),  # w1 / w3
+    (2560, 9728),  # w2
+    (1544, 2560),  # rows that do not divide into tiles
+    (4096, 2560),  # q
+    (1024, 2560),  # k / v
+    (1536, 1024),  # fast wqkv
+    (3072, 1024),  # fast w1 / w3
+    (1024, 3072),  # fast w2
+    (4096, 1024),  # fast head
+    (1024, 2560),  # fast_project_in
+    (64, 128),     # smallest
+]
+
+
+@pytest.mark.parametrize("shape", GEMV_SHAPES)
+@pytest.mark.parametrize("nested", [True, False])
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_gemv_bit_exact_and_within_bar(nf4, orc, shape, nested, dtype):
+    M, K = shape
+    layer = random_layer(M, K, nested, seed=M * 7 + K)
+    lin = to_linear(layer, dtype)
+    xb = randn_bits(K, dtype, seed=K)
+    x = from_bits(xb, dtype).view(1, 1, K)
+    before = nf4.stats()["fast"]
+    y = lin(x)
+    assert nf4.stats()["fast"] == before + 1
+    assert y.shape == (1, 1, M) and y.dtype == dtype
+    J, KS, _ = gemv_shape(M, K)
+    dt = dt_code(dtype)
+    expect = orc.gemv_emul(xb, dt, **oracle_args(layer), M=M, K=K, bs=64, KS=KS, J=J, bs2=layer["bs2"] or 256)
+    got = bits(y)
+    assert np.array_equal(got, expect), f"M={M} K={K} KS={KS} J={J}: {first_mismatch(got, expect)}"
+    ref = orc.nf4_gemm_ref(xb, dt, **oracle_args(layer), M=M, K=K, N=1, bs=64, bs2=layer["bs2"] or 256)
+    assert beyond_rounding_error(o.to_f32(got, dt), ref.reshape(-1), dt) < 2e-3
+
+
+@pytest.mark.parametrize("epi", [1, 2])
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_gemv_epilogues_bit_exact(nf4, orc, epi, dtype):
+    M, K = 2560, 9728
+    layer = random_layer(M, K, True, seed=11)
+    lin = to_linear(layer, dtype)
+    xb = randn_bits(K, dtype, seed=12, scale=0.5)
+    rb = randn_bits(M, dtype, seed=13)
+    assert nf4.prepare(lin)
+    y = nf4.matmul(lin, from_bits(xb, dtype).view(1, 1, K), epi=epi, operand=from_bits(rb, dtype).view(1, 1, M))
+    J, KS, _ = gemv_shape(M, K)
+    expect = orc.gemv_emul(xb, dt_code(dtype), **oracle_args(layer), M=M, K=K, bs=64, KS=KS, J=J, R=rb, epi=epi)
+    assert np.array_equal(bits(y), expect), first_mismatch(bits(y), expect)
+
+
+@pytest.mark.parametrize("shape", [(1, 1, 2560), (1, 2560), (2560,)])
+def test_every_single_vector_shape_is_served(nf4, shape):
+    layer = random_layer(512, 2560, True, seed=3)
+    lin = to_linear(layer, torch.float16)
+    x = torch.randn(*shape, device="cuda", dtype=torch.float16)
+    before = nf4.stats()["fast"]
+    y = lin(x)
+    assert nf4.stats()["fast"] == before + 1
+    assert y.shape == (*shape[:-1], 512)
+
+
+def test_gemv_is_deterministic(nf4):
+    layer = random_layer(9728, 2560, True, seed=21)
+    lin = to_linear(layer, torch.bfloat16)
+    x = torch.randn(1, 1, 2560, device="cuda", dtype=torch.bfloat16)
+    first = lin(x).clone()
+    for _ in range(5):
+        assert torch.equal(lin(x), first)
+
+
+def test_unsupported_layer_is_declined_not_broken(nf4):
+    """A blocksize that is not a power of two goes to the layer's own forward."""
+    layer = random_layer(256, 2560, True, seed=4)
+    lin = to_linear(layer, torch.float16)
+    lin.weight.quant_state.blocksize = 96
+    x = torch.randn(1, 1, 2560, device="cuda", dtype=torch.float16)
+    assert not nf4.prepare(lin)
+    before = nf4.stats()["fallback"]
+    with pytest.raises(Exception):
+        lin(x)  # the layer's own dequantisation refuses blocksize 96 too
+    assert nf4.stats()["fallback"] == before + 1
+
+
+def test_fp32_activations_are_declined(nf4):
+    layer = random_layer(256, 2560, True, seed=5)
+    lin = to_linear(layer, torch.float16)
+    assert nf4.prepare(lin)
+    assert nf4.matmul(lin, torch.randn(1, 2560, device="cuda")) is None
+
+
+# ------------------------------------------------------------------ GEMM (N > 1)
+
+@pytest.mark.parametrize("rows", [2, 5, 8, 9, 16, 19, 32, 33, 70])
+@pytest.mark.parametrize("shape", [(6144, 2560), (2560, 9728), (1544, 2560)])
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_several_positions_within_bar(nf4, orc, shape, rows, dtype):
+    M, K = shape
+    layer = random_layer(M, K, True, seed=M + rows)
+    lin = to_linear(layer, dtype)
+    xb = randn_bits(rows * K, dtype, seed=rows, scale=0.5)
+    before = nf4.stats()["fast"]
+    y = lin(from_bits(xb, dtype).view(1, rows, K))
+    assert nf4.stats()["fast"] == before + 1
+    dt = dt_code(dtype)
+    ref = orc.nf4_gemm_ref(xb, dt, **oracle_args(layer), M=M, K=K, N=rows, bs=64, bs2=256)
+    assert beyond_rounding_error(o.to_f32(bits(y), dt), ref.reshape(-1), dt) < 2e-3
+
+
+@pytest.mark.parametrize("name,shape", [("q", (4096, 2560)), ("k", (1024, 2560)), ("o", (2560, 4096)),
+                                        ("gate", (9728, 2560)), ("down", (2560, 9728))])
+def test_prefill_gemm_512_rows(nf4, orc, name, shape):
+    """The prefill workload: 512 bf16 rows through each projection shape."""
+    M, K = shape
+    rows, dtype = 512, torch.bfloat16
+    layer = random_layer(M, K, True, seed=len(name))
+    lin = to_linear(layer, dtype)
+    xb = randn_bits(rows * K, dtype, seed=99)
+    y = lin(from_bits(xb, dtype).view(rows, K))
+    dt = dt_code(dtype)
+    sample = np.arange(0, rows, 37)  # a sample of rows keeps the fp64 reference quick
+    ref = orc.nf4_gemm_ref(xb.reshape(rows, K)[sample], dt, **oracle_args(layer), M=M, K=K, N=sample.size, bs=64)
+    got = o.to_f32(bits(y), dt).reshape(rows, M)[sample]
+    assert beyond_rounding_error(got, ref, dt) < 2e-3
+
+
+@pytest.mark.parametrize("epi", [1, 2])
+def test_gemm_epilogues(nf4, orc, epi):
+    M, K, rows, dtype = 2560, 9728, 24, torch.float16
+    layer = random_layer(M, K, True, seed=31)
+    lin = to_linear(layer, dtype)
+    xb = randn_bits(rows * K, dtype, seed=32, scale=0.5)
+    rb = randn_bits(rows * M, dtype, seed=33)
+    assert nf4.prepare(lin)
+    y = nf4.matmul(lin, from_bits(xb, dtype).view(rows, K), epi=epi, operand=from_bits(rb, dtype).view(rows, M))
+    plain = nf4.matmul(lin, from_bits(xb, dtype).view(rows, K))
+    r = o.to_f32(rb, 0).astype(np.float64)
+    p = o.to_f32(bits(plain), 0).astype(np.float64)
+    expect = r + p if epi == 1 else (r / (1 + np.exp(-r))) * p
+    assert relative_error(o.to_f32(bits(y), 0), expect) < 5e-3

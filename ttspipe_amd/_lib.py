@@ -1,0 +1,105 @@
+"""ctypes binding of `libttsp_hip.so`, the C-ABI the Python modules call.
+
+This replaces the reference's NVRTC/driver FFI (app/engine/nvrtc.py:76-198):
+the kernels are compiled ahead of time by hipcc for gfx950 (see `build.py`),
+and every entry point takes raw device pointers, sizes and a `hipStream_t`
+and returns a `hipError_t` (0 = success). Nothing in the library allocates.
+
+Loading is lazy. `gpu_present()` answers whether a GPU is visible without
+raising; `lib()` raises if the library is missing, because on a machine with a
+GPU the kernels are the product and there is no silent substitute for them.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import threading
+from pathlib import Path
+
+LIB_PATH = Path(__file__).resolve().parent / "libttsp_hip.so"
+
+#: Element-type codes of the C-ABI (`include/ttsp_hip.h`).
+DT_F16, DT_BF16, DT_F32 = 0, 1, 2
+
+_lock = threading.Lock()
+_lib: ctypes.CDLL | None = None
+
+_vp = ctypes.c_void_p
+_i = ctypes.c_int
+_f = ctypes.c_float
+_ll = ctypes.c_longlong
+
+#: name -> argtypes (restype is int for all of them)
+SIGNATURES: dict[str, list] = {
+    "ttsp_nf4_gemm": [_vp, _i, _vp, _vp, _vp, _vp, _f, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _vp],
+    "ttsp_nf4_dequant": [_vp, _vp, _vp, _vp, _f, _vp, _vp, _i, _ll, _i, _i, _vp],
+    "ttsp_gemv_shape": [_i, _i, ctypes.POINTER(_i), ctypes.POINTER(_i), ctypes.POINTER(_i)],
+    "ttsp_rms_norm": [_vp, _vp, _vp, _i, _i, _f, _i, _vp],
+    "ttsp_rope": [_vp, _vp, _i, _vp, _ll, _i, _i, _i, _i, _vp],
+    "ttsp_qk_rope_kv": [_vp, _vp, _vp, _f, _vp, _i, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp],
+    "ttsp_attn_decode": [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _f, _i, _vp],
+    "ttsp_attn_chunk": [],
+    "ttsp_embed_sum": [_vp, _vp, _i, _i, _i, _vp, _i, _vp],
+    "ttsp_argmax": [_vp, _i, _i, _vp, _vp],
+    "ttsp_synth_fill": [_vp, _ll, ctypes.c_ulonglong, _i, _f, _f, _vp],
+    "ttsp_selftest_math": [_vp, _i, _i, _vp, _vp],
+    "ttsp_selftest_dot2": [_vp, _vp, _i, _i, _vp, _vp],
+}
+
+
+def load() -> ctypes.CDLL:
+    """Load the library and bind every signature. Raises if it is missing."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is not None:
+            return _lib
+        if not LIB_PATH.exists():
+            raise RuntimeError(
+                f"{LIB_PATH} is not built; run `python -m ttspipe_amd.build` "
+                "(the HIP kernels have no substitute)"
+            )
+        handle = ctypes.CDLL(str(LIB_PATH))
+        for name, argtypes in SIGNATURES.items():
+            fn = getattr(handle, name)
+            fn.argtypes = argtypes
+            fn.restype = ctypes.c_int
+        _lib = handle
+        return _lib
+
+
+def lib() -> ctypes.CDLL:
+    return load()
+
+
+def gpu_present() -> bool:
+    """Whether a ROCm device is visible (never raises)."""
+    try:
+        import torch
+
+        return bool(torch.cuda.is_available())
+    except Exception:  # noqa: BLE001
+        return False
+
+
+def dtype_code(dtype) -> int | None:
+    import torch
+
+    return {torch.float16: DT_F16, torch.bfloat16: DT_BF16, torch.float32: DT_F32}.get(dtype)
+
+
+def stream() -> int:
+    """torch's current stream on the current device, as a raw hipStream_t."""
+    import torch
+
+    return torch.cuda.current_stream().cuda_stream
+
+
+def check(rc: int, what: str) -> None:
+    if rc:
+        raise RuntimeError(f"{what} failed: hipError_t {rc}")
+
+
+def ptr(t) -> int:
+    return 0 if t is None else t.data_ptr()

@@ -1,0 +1,123 @@
+// Small kernels a greedy Dual-AR decode step needs between the transformer
+// blocks (the synthetic frame of app/engine/graphs.py:76-132 with argmax in
+// place of sampling): summed codebook-embedding gather, greedy argmax, and a
+// counter-based fill that materialises seeded synthetic weights on the device.
+#include "ttsp_common.h"
+
+namespace ttsp {
+
+// out[d] = round(sum_{c < ntok} E[(c * vocab + tok[c]) * D + d]), fp32 sum in
+// codebook order. ntok == 1 is a plain row gather.
+template <int DT>
+__global__ __launch_bounds__(256) void embed_sum_kernel(const uint16_t* __restrict__ E,
+                                                       const int* __restrict__ tok, int ntok,
+                                                       int vocab, int D, uint16_t* __restrict__ out) {
+  const int d = blockIdx.x * blockDim.x + threadIdx.x;
+  if (d >= D) return;
+  float acc = 0.0f;
+  for (int c = 0; c < ntok; ++c) {
+    int t = tok[c];
+    t = t < 0 ? 0 : (t >= vocab ? vocab - 1 : t);
+    acc = __fadd_rn(acc, Elem<DT>::load(E[((size_t)c * vocab + t) * D + d]));
+  }
+  out[d] = Elem<DT>::store(acc);
+}
+
+// Index of the largest logit, the lowest index on ties (NaN never wins).
+template <int DT>
+__global__ __launch_bounds__(1024) void argmax_kernel(const uint16_t* __restrict__ X, int n,
+                                                     int* __restrict__ out) {
+  __shared__ float bv[16];
+  __shared__ int bi[16];
+  const int tid = threadIdx.x;
+  float best = -__builtin_inff();
+  int idx = 0x7fffffff;
+  for (int i = tid; i < n; i += blockDim.x) {
+    const float v = Elem<DT>::load(X[i]);
+    if (v > best) { best = v; idx = i; }
+  }
+  for (int off = 32; off >= 1; off >>= 1) {
+    const float ov = __shfl_xor(best, off, 64);
+    const int oi = __shfl_xor(idx, off, 64);
+    if (ov > best || (ov == best && oi < idx)) { best = ov; idx = oi; }
+  }
+  if ((tid & 63) == 0) { bv[tid >> 6] = best; bi[tid >> 6] = idx; }
+  __syncthreads();
+  if (tid == 0) {
+    const int nw = (blockDim.x + 63) >> 6;
+    for (int w = 1; w < nw; ++w)
+      if (bv[w] > best || (bv[w] == best && bi[w] < idx)) { best = bv[w]; idx = bi[w]; }
+    out[0] = idx == 0x7fffffff ? 0 : idx;
+  }
+}
+
+// splitmix64 (Steele, Lea, Flood 2014) of seed-mixed counters.
+__device__ __forceinline__ uint64_t mix64(uint64_t z) {
+  z += 0x9e3779b97f4a7c15ull;
+  z = (z ^ (z >> 30)) * 0xbf58476d1ce4e5b9ull;
+  z = (z ^ (z >> 27)) * 0x94d049bb133111ebull;
+  return z ^ (z >> 31);
+}
+
+__device__ __forceinline__ uint64_t hash_at(uint64_t seed, uint64_t i) {
+  return mix64(mix64(seed) ^ i);
+}
+
+// kind 0: bytes (top 8 bits); kind 1/2/3: value = u * scale + offset with
+// u = (h >> 40) / 2^23 - 1 in [-1, 1) (exact in fp32), one rounding per op,
+// stored as bf16 / fp16 / fp32.
+__global__ __launch_bounds__(256) void synth_fill_kernel(void* __restrict__ out, long long n,
+                                                         unsigned long long seed, int kind,
+                                                         float scale, float offset) {
+  const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  const uint64_t h = hash_at(seed, (uint64_t)i);
+  if (kind == 0) {
+    ((uint8_t*)out)[i] = (uint8_t)(h >> 56);
+    return;
+  }
+  const float u = __fsub_rn(__fmul_rn((float)(uint32_t)(h >> 40), 1.1920928955078125e-07f), 1.0f);
+  const float v = __fadd_rn(__fmul_rn(u, scale), offset);
+  if (kind == 1) ((uint16_t*)out)[i] = f32_to_bf16(v);
+  else if (kind == 2) ((uint16_t*)out)[i] = f32_to_f16(v);
+  else ((float*)out)[i] = v;
+}
+
+}  // namespace ttsp
+
+using namespace ttsp;
+
+extern "C" int ttsp_embed_sum(const void* E, const int* tok, int ntok, int vocab, int D, void* out,
+                              int dtype, hipStream_t stream) {
+  if (ntok <= 0 || vocab <= 0 || D <= 0) return (int)hipErrorInvalidValue;
+  const dim3 grid((D + 255) / 256);
+  if (dtype == DT_F16)
+    hipLaunchKernelGGL(embed_sum_kernel<DT_F16>, grid, dim3(256), 0, stream, (const uint16_t*)E, tok,
+                       ntok, vocab, D, (uint16_t*)out);
+  else if (dtype == DT_BF16)
+    hipLaunchKernelGGL(embed_sum_kernel<DT_BF16>, grid, dim3(256), 0, stream, (const uint16_t*)E, tok,
+                       ntok, vocab, D, (uint16_t*)out);
+  else
+    return (int)hipErrorInvalidValue;
+  TTSP_RETURN_LAUNCH();
+}
+
+extern "C" int ttsp_argmax(const void* X, int n, int dtype, int* out, hipStream_t stream) {
+  if (n <= 0) return (int)hipErrorInvalidValue;
+  if (dtype == DT_F16)
+    hipLaunchKernelGGL(argmax_kernel<DT_F16>, dim3(1), dim3(1024), 0, stream, (const uint16_t*)X, n, out);
+  else if (dtype == DT_BF16)
+    hipLaunchKernelGGL(argmax_kernel<DT_BF16>, dim3(1), dim3(1024), 0, stream, (const uint16_t*)X, n, out);
+  else
+    return (int)hipErrorInvalidValue;
+  TTSP_RETURN_LAUNCH();
+}
+
+extern "C" int ttsp_synth_fill(void* out, long long n, unsigned long long seed, int kind, float scale,
+                               float offset, hipStream_t stream) {
+  if (n < 0 || kind < 0 || kind > 3) return (int)hipErrorInvalidValue;
+  if (n == 0) return 0;
+  hipLaunchKernelGGL(synth_fill_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream, out,
+                     n, seed, kind, scale, offset);
+  TTSP_RETURN_LAUNCH();
+}

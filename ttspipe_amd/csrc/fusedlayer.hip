@@ -1,0 +1,205 @@
+// The three non-matmul kernels of a decode step through a transformer block
+// (app/engine/fusedlayer.py:56-159): per-head norm + rotary + KV-cache write,
+// then grouped-query attention as split-K over fixed chunks of the cache.
+//
+// Layouts (batch 1): QKV is [nh + 2*nkv][128] (q heads, k heads, v heads),
+// the caches are [nkv][max_len][128], Q and Y are [nh][128]. Query head i
+// reads KV head i / (nh / nkv).
+//
+// attn_partial: one workgroup per (kv head, chunk of 64 positions), one wave
+// per query head of the group. The chunk's K and V rows are staged in LDS with
+// coalesced loads; lane j scores position j (fp32 fma over d = 0..127 against
+// q * 1/sqrt(128)), the wave takes the chunk max and sum of exp(s - max), and
+// lane l accumulates dims 2l, 2l+1 over the chunk's positions in order.
+// attn_combine merges chunks with the log-sum-exp rule, chunks in order.
+// Both are deterministic: no atomics, fixed orders.
+#include "ttsp_common.h"
+
+namespace ttsp {
+
+constexpr int HD = 128;        // head dim
+constexpr int ACHUNK = 64;     // positions per attention chunk
+constexpr int KPAD = HD + 2;   // LDS row stride (elements): 65 dwords, conflict-free columns
+
+template <int DT>
+__global__ __launch_bounds__(HD) void qk_rope_kv_kernel(
+    const uint16_t* __restrict__ QKV, const uint16_t* __restrict__ QW,
+    const uint16_t* __restrict__ KW, float eps, const void* __restrict__ F, int ftype,
+    const long long* __restrict__ POS, uint16_t* __restrict__ Q, uint16_t* __restrict__ KC,
+    uint16_t* __restrict__ VC, int nh, int nkv, int max_len) {
+  __shared__ float sx[HD];
+  __shared__ float part[HD / 64];
+  const int head = blockIdx.x, d = threadIdx.x;
+  const long long pos = POS[0];
+  if (pos < 0 || pos >= max_len) return;  // no cache slot to write: leave everything untouched
+  if (head >= nh + nkv) {
+    const int vh = head - nh - nkv;
+    VC[((long long)vh * max_len + pos) * HD + d] = QKV[(size_t)(nh + nkv + vh) * HD + d];
+    return;
+  }
+  const bool is_q = head < nh;
+  float x = Elem<DT>::load(QKV[(size_t)head * HD + d]);
+  const uint16_t* w = is_q ? QW : KW;
+  if (w != nullptr) {
+    const float v = wave_sum(__fmul_rn(x, x));
+    if ((d & 63) == 0) part[d >> 6] = v;
+    __syncthreads();
+    const float ss = __fadd_rn(part[0], part[1]);
+    const float r = rsqrt_rn(__fadd_rn(__fdiv_rn(ss, (float)HD), eps));
+    x = Elem<DT>::load(Elem<DT>::store(__fmul_rn(__fmul_rn(x, r), Elem<DT>::load(w[d]))));
+  }
+  sx[d] = x;
+  __syncthreads();
+  const float x0 = sx[d & ~1], x1 = sx[d | 1];
+  const float fr = load_elem(F, d & ~1, ftype), fi = load_elem(F, d | 1, ftype);
+  const float y = (d & 1) ? __fadd_rn(__fmul_rn(x1, fr), __fmul_rn(x0, fi))
+                          : __fsub_rn(__fmul_rn(x0, fr), __fmul_rn(x1, fi));
+  if (is_q) Q[(size_t)head * HD + d] = Elem<DT>::store(y);
+  else KC[((long long)(head - nh) * max_len + pos) * HD + d] = Elem<DT>::store(y);
+}
+
+template <int DT>
+__global__ __launch_bounds__(1024) void attn_partial_kernel(
+    const uint16_t* __restrict__ Q, const uint16_t* __restrict__ KC,
+    const uint16_t* __restrict__ VC, const long long* __restrict__ POS, float* __restrict__ PM,
+    float* __restrict__ PL, float* __restrict__ PACC, int groups, int max_len, int nchunk,
+    float scale) {
+  extern __shared__ float smem[];
+  float* q_s = smem;                                         // [groups][HD]
+  float* p_s = q_s + groups * HD;                            // [groups][ACHUNK]
+  uint16_t* k_s = reinterpret_cast<uint16_t*>(p_s + groups * ACHUNK);  // [ACHUNK][KPAD]
+  uint16_t* v_s = k_s + ACHUNK * KPAD;                       // [ACHUNK][HD]
+
+  const int kh = blockIdx.x, c = blockIdx.y;
+  const int tid = threadIdx.x, nthr = blockDim.x;
+  const int g = tid >> 6, lane = tid & 63;
+  const int qh = kh * groups + g;
+  // Positions [0, L) are live; the cache holds max_len of them.
+  const long long L = min(POS[0] + 1, (long long)max_len);
+  const long long j0 = (long long)c * ACHUNK;
+  const size_t slot = (size_t)qh * nchunk + c;
+  if (j0 >= L) {
+    if (lane == 0) {
+      PM[slot] = -1e30f;
+      PL[slot] = 0.0f;
+    }
+    return;
+  }
+  const int nvalid = (int)min((long long)ACHUNK, L - j0);
+
+  for (int t = tid; t < groups * HD; t += nthr)
+    q_s[t] = __fmul_rn(Elem<DT>::load(Q[(size_t)(kh * groups) * HD + t]), scale);
+  // K and V rows of the chunk: 16 bytes per thread per step, coalesced.
+  const uint16_t* kb = KC + ((size_t)kh * max_len + j0) * HD;
+  const uint16_t* vb = VC + ((size_t)kh * max_len + j0) * HD;
+  for (int t = tid; t < ACHUNK * (HD / 8); t += nthr) {
+    const int j = t / (HD / 8), e = (t % (HD / 8)) * 8;
+    uint4 kv = make_uint4(0, 0, 0, 0), vv = make_uint4(0, 0, 0, 0);
+    if (j < nvalid) {
+      kv = *reinterpret_cast<const uint4*>(kb + (size_t)j * HD + e);
+      vv = *reinterpret_cast<const uint4*>(vb + (size_t)j * HD + e);
+    }
+    uint32_t* kd = reinterpret_cast<uint32_t*>(k_s + j * KPAD + e);  // KPAD rows are 4-byte aligned
+    kd[0] = kv.x; kd[1] = kv.y; kd[2] = kv.z; kd[3] = kv.w;
+    *reinterpret_cast<uint4*>(v_s + j * HD + e) = vv;
+  }
+  __syncthreads();
+
+  // score of position `lane` for query head g
+  float s = 0.0f;
+  const uint32_t* kr = reinterpret_cast<const uint32_t*>(k_s + lane * KPAD);
+  const float* qg = q_s + g * HD;
+#pragma unroll 8
+  for (int i = 0; i < HD / 2; ++i) {
+    const uint32_t kk = kr[i];
+    s = __builtin_fmaf(qg[2 * i], Elem<DT>::load(kk), s);
+    s = __builtin_fmaf(qg[2 * i + 1], Elem<DT>::load(kk >> 16), s);
+  }
+  const bool valid = lane < nvalid;
+  const float m = wave_max(valid ? s : -3.0e38f);
+  const float p = valid ? exp_cw(__fsub_rn(s, m)) : 0.0f;
+  const float l = wave_sum(p);
+  p_s[g * ACHUNK + lane] = p;
+  __syncthreads();
+
+  float a0 = 0.0f, a1 = 0.0f;
+  const float* pg = p_s + g * ACHUNK;
+  for (int j = 0; j < nvalid; ++j) {
+    const float pj = pg[j];
+    const uint32_t vv = reinterpret_cast<const uint32_t*>(v_s + j * HD)[lane];
+    a0 = __builtin_fmaf(pj, Elem<DT>::load(vv), a0);
+    a1 = __builtin_fmaf(pj, Elem<DT>::load(vv >> 16), a1);
+  }
+  if (lane == 0) {
+    PM[slot] = m;
+    PL[slot] = l;
+  }
+  reinterpret_cast<float2*>(PACC + slot * HD)[lane] = make_float2(a0, a1);
+}
+
+template <int DT>
+__global__ __launch_bounds__(HD) void attn_combine_kernel(const float* __restrict__ PM,
+                                                          const float* __restrict__ PL,
+                                                          const float* __restrict__ PACC,
+                                                          uint16_t* __restrict__ Y, int nchunk) {
+  const int qh = blockIdx.x, d = threadIdx.x;
+  const float* pm = PM + (size_t)qh * nchunk;
+  const float* pl = PL + (size_t)qh * nchunk;
+  float M = -3.0e38f;
+  for (int c = 0; c < nchunk; ++c) M = fmaxf(M, pm[c]);
+  float num = 0.0f, den = 0.0f;
+  for (int c = 0; c < nchunk; ++c) {
+    const float l = pl[c];
+    if (l == 0.0f) continue;
+    const float w = exp_cw(__fsub_rn(pm[c], M));
+    den = __fadd_rn(den, __fmul_rn(l, w));
+    num = __fadd_rn(num, __fmul_rn(PACC[((size_t)qh * nchunk + c) * HD + d], w));
+  }
+  Y[(size_t)qh * HD + d] = Elem<DT>::store(__fdiv_rn(num, den));
+}
+
+}  // namespace ttsp
+
+using namespace ttsp;
+
+extern "C" int ttsp_attn_chunk(void) { return ACHUNK; }
+
+extern "C" int ttsp_qk_rope_kv(const void* QKV, const void* QW, const void* KW, float eps,
+                               const void* F, int ftype, const long long* POS, void* Q, void* KC,
+                               void* VC, int nh, int nkv, int max_len, int dtype,
+                               hipStream_t stream) {
+  if (nh <= 0 || nkv <= 0 || max_len <= 0 || ftype < 0 || ftype > 2) return (int)hipErrorInvalidValue;
+#define TTSP_QK(DTV)                                                                            \
+  hipLaunchKernelGGL(qk_rope_kv_kernel<DTV>, dim3(nh + 2 * nkv), dim3(HD), 0, stream,           \
+                     (const uint16_t*)QKV, (const uint16_t*)QW, (const uint16_t*)KW, eps, F, ftype, \
+                     POS, (uint16_t*)Q, (uint16_t*)KC, (uint16_t*)VC, nh, nkv, max_len)
+  if (dtype == DT_F16) TTSP_QK(DT_F16);
+  else if (dtype == DT_BF16) TTSP_QK(DT_BF16);
+  else return (int)hipErrorInvalidValue;
+#undef TTSP_QK
+  TTSP_RETURN_LAUNCH();
+}
+
+extern "C" int ttsp_attn_decode(const void* Q, const void* KC, const void* VC,
+                                const long long* POS, float* PM, float* PL, float* PACC, void* Y,
+                                int nh, int nkv, int max_len, int nchunk, float scale, int dtype,
+                                hipStream_t stream) {
+  if (nh <= 0 || nkv <= 0 || nh % nkv || nchunk <= 0 || max_len <= 0) return (int)hipErrorInvalidValue;
+  const int groups = nh / nkv;
+  if (groups > 16 || (long long)nchunk * ACHUNK < 1) return (int)hipErrorInvalidValue;
+  const size_t shmem = sizeof(float) * (size_t)groups * (HD + ACHUNK) +
+                       sizeof(uint16_t) * (size_t)ACHUNK * (KPAD + HD);
+#define TTSP_AT(DTV)                                                                            \
+  do {                                                                                          \
+    hipLaunchKernelGGL(attn_partial_kernel<DTV>, dim3(nkv, nchunk), dim3(64 * groups), shmem,    \
+                       stream, (const uint16_t*)Q, (const uint16_t*)KC, (const uint16_t*)VC, POS, \
+                       PM, PL, PACC, groups, max_len, nchunk, scale);                           \
+    hipLaunchKernelGGL(attn_combine_kernel<DTV>, dim3(nh), dim3(HD), 0, stream, PM, PL, PACC,    \
+                       (uint16_t*)Y, nchunk);                                                   \
+  } while (0)
+  if (dtype == DT_F16) TTSP_AT(DT_F16);
+  else if (dtype == DT_BF16) TTSP_AT(DT_BF16);
+  else return (int)hipErrorInvalidValue;
+#undef TTSP_AT
+  TTSP_RETURN_LAUNCH();
+}

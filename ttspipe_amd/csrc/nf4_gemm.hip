@@ -1,0 +1,259 @@
+// NF4 GEMM for several activation rows (prompt prefill): Y[N][M] = X[N][K] . W^T
+// with W the bitsandbytes NF4 weight (nf4_gemv.hip gives the layout).
+//
+// Each workgroup owns a BM x BN tile of the output (BM weight rows, BN input
+// rows). Per K-step of 64 codes, the 256 threads
+//   * dequantise BM x 64 weights, 16 packed bytes (32 codes) each, as
+//     round(code * scale) in the activation type - the exact value
+//     bitsandbytes' dequantize_4bit produces, so the product is the dense
+//     fork's matmul on identical weights - straight into an LDS A tile;
+//   * copy BN x 64 activations into an LDS B tile;
+// and the 4 waves run v_mfma_f32_32x32x16 over their sub-tiles, fp32
+// accumulate. LDS is double-buffered; the next step's packed weights and
+// activations are already in registers while the current step multiplies.
+// Rows are padded to 72 elements (144 B) so the 16-byte operand reads of 16
+// consecutive rows hit disjoint banks.
+//
+// MFMA 32x32x16 operand layout: lane l supplies row (l % 32) of A and column
+// (l % 32) of B, each as 8 consecutive k at 8 * (l / 32); accumulator r of
+// lane l is D[8*(r/4) + 4*(l/32) + r%4][l % 32]. A and B only need to agree on
+// which k a lane carries, so any k permutation inside a step is harmless.
+#include "ttsp_common.h"
+
+namespace ttsp {
+
+typedef __bf16 bf16x8_v __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8_v __attribute__((ext_vector_type(8)));
+typedef float f32x16_v __attribute__((ext_vector_type(16)));
+
+constexpr int GEMM_THREADS = 256;
+constexpr int KT = 64;        // codes per K-step (one bs=64 scale block)
+constexpr int LROW = KT + 8;  // LDS row stride in elements
+
+template <int DT>
+__device__ __forceinline__ f32x16_v mfma32(uint4 a, uint4 b, f32x16_v c) {
+  if constexpr (DT == DT_BF16)
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_v, a),
+                                                   __builtin_bit_cast(bf16x8_v, b), c, 0, 0, 0);
+  else
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8_v, a),
+                                                  __builtin_bit_cast(f16x8_v, b), c, 0, 0, 0);
+}
+
+// WM x WN waves; each wave covers (BM/WM) x (BN/WN) with 32x32 MFMA blocks.
+template <int DT, int BM, int BN, int WM, int WN, bool NESTED>
+__global__ __launch_bounds__(GEMM_THREADS) void nf4_gemm_kernel(
+    const uint16_t* __restrict__ X, const uint8_t* __restrict__ W, const uint8_t* __restrict__ A8,
+    const float* __restrict__ AMAX, const float* __restrict__ CODE2, float offset,
+    const float* __restrict__ LUT, uint16_t* __restrict__ Y, const uint16_t* __restrict__ R,
+    int epi, int M, int K, int N, int bs_shift, int bs2_shift) {
+  static_assert(WM * WN == GEMM_THREADS / 64, "4 waves");
+  constexpr int TM = BM / WM / 32, TN = BN / WN / 32;  // MFMA blocks per wave
+  constexpr int A_PER_T = BM * (KT / 32) / GEMM_THREADS;  // 16-byte packed chunks per thread
+  constexpr int B_PER_T = BN * (KT / 8) / GEMM_THREADS;   // 16-byte activation chunks per thread
+  static_assert(A_PER_T >= 1 && B_PER_T >= 1, "tile too small for the workgroup");
+
+  __shared__ uint16_t As[2][BM * LROW];
+  __shared__ uint16_t Bs[2][BN * LROW];
+  __shared__ float lut_s[16];
+  __shared__ float code2_s[NESTED ? 256 : 1];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave / WN, wn = wave % WN;
+  const int m0 = blockIdx.x * BM, n0 = blockIdx.y * BN;
+  const int nsteps = K / KT;
+  const size_t rowbytes = (size_t)K / 2;
+
+  if (tid < 16) lut_s[tid] = LUT[tid];
+  if constexpr (NESTED) code2_s[tid] = CODE2[tid];
+
+  uint4 wraw[A_PER_T];
+  float wsc[A_PER_T];
+  uint4 xraw[B_PER_T];
+
+  auto load_step = [&](int step) {
+    const int k0 = step * KT;
+#pragma unroll
+    for (int i = 0; i < A_PER_T; ++i) {
+      const int c = tid + i * GEMM_THREADS;  // chunk: row c/2, half c%2
+      const int row = min(m0 + c / 2, M - 1);
+      const int kc = k0 + (c & 1) * 32;
+      typedef uint32_t u32x4_v __attribute__((ext_vector_type(4)));
+      const u32x4_v v = __builtin_nontemporal_load(
+          reinterpret_cast<const u32x4_v*>(W + (size_t)row * rowbytes + kc / 2));
+      wraw[i] = make_uint4(v.x, v.y, v.z, v.w);
+      const long long b = ((long long)row * K + kc) >> bs_shift;
+      if constexpr (NESTED) {
+        wsc[i] = AMAX[b >> bs2_shift];  // absmax2; the code2 index comes from load_a8
+      } else {
+        wsc[i] = AMAX[b];
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < B_PER_T; ++i) {
+      const int c = tid + i * GEMM_THREADS;  // chunk: row c/8, 8 elements at (c%8)*8
+      const int n = n0 + c / (KT / 8);
+      xraw[i] = n < N ? *reinterpret_cast<const uint4*>(X + (size_t)n * K + k0 + (c % (KT / 8)) * 8)
+                      : make_uint4(0, 0, 0, 0);
+    }
+  };
+  uint32_t a8raw[NESTED ? A_PER_T : 1];
+  auto load_a8 = [&](int step) {
+    if constexpr (NESTED) {
+      const int k0 = step * KT;
+#pragma unroll
+      for (int i = 0; i < A_PER_T; ++i) {
+        const int c = tid + i * GEMM_THREADS;
+        const int row = min(m0 + c / 2, M - 1);
+        const long long b = ((long long)row * K + k0 + (c & 1) * 32) >> bs_shift;
+        a8raw[i] = A8[b];
+      }
+    }
+  };
+  auto store_step = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < A_PER_T; ++i) {
+      const int c = tid + i * GEMM_THREADS;
+      float s = wsc[i];
+      if constexpr (NESTED) s = __fadd_rn(__fmul_rn(code2_s[a8raw[i]], s), offset);
+      const uint32_t wv[4] = {wraw[i].x, wraw[i].y, wraw[i].z, wraw[i].w};
+      uint32_t o[16];
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+#pragma unroll
+        for (int bb = 0; bb < 4; ++bb) {
+          const uint32_t byte = (wv[q] >> (8 * bb)) & 0xffu;
+          const uint32_t lo = Elem<DT>::store(__fmul_rn(lut_s[byte >> 4], s));
+          const uint32_t hi = Elem<DT>::store(__fmul_rn(lut_s[byte & 15u], s));
+          o[q * 4 + bb] = lo | (hi << 16);
+        }
+      uint4* dst = reinterpret_cast<uint4*>(&As[buf][(c / 2) * LROW + (c & 1) * 32]);
+#pragma unroll
+      for (int q = 0; q < 4; ++q) dst[q] = make_uint4(o[4 * q], o[4 * q + 1], o[4 * q + 2], o[4 * q + 3]);
+    }
+#pragma unroll
+    for (int i = 0; i < B_PER_T; ++i) {
+      const int c = tid + i * GEMM_THREADS;
+      *reinterpret_cast<uint4*>(&Bs[buf][(c / (KT / 8)) * LROW + (c % (KT / 8)) * 8]) = xraw[i];
+    }
+  };
+
+  f32x16_v acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+
+  load_a8(0);
+  load_step(0);
+  __syncthreads();  // lut_s / code2_s
+  for (int step = 0; step < nsteps; ++step) {
+    const int buf = step & 1;
+    store_step(buf);
+    __syncthreads();
+    if (step + 1 < nsteps) {
+      load_a8(step + 1);
+      load_step(step + 1);
+    }
+    const uint16_t* as = As[buf];
+    const uint16_t* bs = Bs[buf];
+#pragma unroll
+    for (int kk = 0; kk < KT / 16; ++kk) {
+      const int ko = kk * 16 + (lane >> 5) * 8;
+      uint4 af[TM], bf[TN];
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+        af[i] = *reinterpret_cast<const uint4*>(as + (wm * (BM / WM) + i * 32 + (lane & 31)) * LROW + ko);
+#pragma unroll
+      for (int j = 0; j < TN; ++j)
+        bf[j] = *reinterpret_cast<const uint4*>(bs + (wn * (BN / WN) + j * 32 + (lane & 31)) * LROW + ko);
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j) acc[i][j] = mfma32<DT>(af[i], bf[j], acc[i][j]);
+    }
+  }
+
+  // epilogue: accumulator r of lane l is (row 8*(r/4) + 4*(l/32) + r%4, column l%32)
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+      const int n = n0 + wn * (BN / WN) + j * 32 + (lane & 31);
+      if (n >= N) continue;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int m = m0 + wm * (BM / WM) + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+        if (m >= M) continue;
+        const size_t o = (size_t)n * M + m;
+        const float y = Elem<DT>::load(Elem<DT>::store(acc[i][j][r]));
+        float v = y;
+        if (epi == 1) v = __fadd_rn(Elem<DT>::load(R[o]), y);
+        else if (epi == 2) v = __fmul_rn(Elem<DT>::load(Elem<DT>::store(silu_rn(Elem<DT>::load(R[o])))), y);
+        Y[o] = Elem<DT>::store(v);
+      }
+    }
+}
+
+template <int DT, int BM, int BN, int WM, int WN>
+static void launch_gemm(const void* X, const uint8_t* W, const uint8_t* A8, const float* AMAX,
+                        const float* CODE2, float offset, const float* LUT, void* Y, const void* R,
+                        int epi, int M, int K, int N, int bs_shift, int bs2_shift, hipStream_t st) {
+  const dim3 grid((M + BM - 1) / BM, (N + BN - 1) / BN);
+  if (A8)
+    hipLaunchKernelGGL((nf4_gemm_kernel<DT, BM, BN, WM, WN, true>), grid, dim3(GEMM_THREADS), 0, st,
+                       (const uint16_t*)X, W, A8, AMAX, CODE2, offset, LUT, (uint16_t*)Y,
+                       (const uint16_t*)R, epi, M, K, N, bs_shift, bs2_shift);
+  else
+    hipLaunchKernelGGL((nf4_gemm_kernel<DT, BM, BN, WM, WN, false>), grid, dim3(GEMM_THREADS), 0, st,
+                       (const uint16_t*)X, W, A8, AMAX, CODE2, offset, LUT, (uint16_t*)Y,
+                       (const uint16_t*)R, epi, M, K, N, bs_shift, bs2_shift);
+}
+
+int gemm_mfma(const void* X, int dt, const uint8_t* W, const uint8_t* A8, const float* AMAX,
+              const float* CODE2, float offset, const float* LUT, void* Y, const void* R, int epi,
+              int M, int K, int N, int bs_shift, int bs2_shift, hipStream_t st) {
+  if (K % KT) return (int)hipErrorInvalidValue;
+  if (dt == DT_BF16) {
+    if (N <= 32) launch_gemm<DT_BF16, 128, 32, 4, 1>(X, W, A8, AMAX, CODE2, offset, LUT, Y, R, epi, M, K, N, bs_shift, bs2_shift, st);
+    else launch_gemm<DT_BF16, 128, 128, 2, 2>(X, W, A8, AMAX, CODE2, offset, LUT, Y, R, epi, M, K, N, bs_shift, bs2_shift, st);
+  } else if (dt == DT_F16) {
+    if (N <= 32) launch_gemm<DT_F16, 128, 32, 4, 1>(X, W, A8, AMAX, CODE2, offset, LUT, Y, R, epi, M, K, N, bs_shift, bs2_shift, st);
+    else launch_gemm<DT_F16, 128, 128, 2, 2>(X, W, A8, AMAX, CODE2, offset, LUT, Y, R, epi, M, K, N, bs_shift, bs2_shift, st);
+  } else {
+    return (int)hipErrorInvalidValue;
+  }
+  TTSP_RETURN_LAUNCH();
+}
+
+int gemv_n1(const void* X, int dt, const uint8_t* W, const uint8_t* A8, const float* AMAX,
+            const float* CODE2, float offset, const float* LUT, void* Y, const void* R, int epi,
+            int M, int K, int blocksize, int blocksize2, hipStream_t st);
+
+}  // namespace ttsp
+
+using namespace ttsp;
+
+// One entry for every row count: one row takes the bandwidth-bound GEMV,
+// more rows the MFMA kernel (weights read once per BN rows).
+extern "C" int ttsp_nf4_gemm(const void* X, int x_dtype, const uint8_t* W, const uint8_t* A8,
+                             const float* AMAX, const float* CODE2, float offset, const float* LUT,
+                             void* Y, const void* R, int epi, int M, int K, int N, int blocksize,
+                             int blocksize2, hipStream_t stream) {
+  if (N <= 0 || M <= 0 || K <= 0 || !X || !W || !AMAX || !LUT || !Y) return (int)hipErrorInvalidValue;
+  if (A8 && !CODE2) return (int)hipErrorInvalidValue;
+  if (N == 1)
+    return gemv_n1(X, x_dtype, W, A8, AMAX, CODE2, offset, LUT, Y, R, epi, M, K, blocksize,
+                   blocksize2, stream);
+  int bs_shift = 0, bs2_shift = 0;
+  while ((1 << bs_shift) < blocksize) ++bs_shift;
+  if (A8)
+    while ((1 << bs2_shift) < blocksize2) ++bs2_shift;
+  if ((1 << bs_shift) != blocksize || bs_shift < 6 || (A8 && (1 << bs2_shift) != blocksize2))
+    return (int)hipErrorInvalidValue;
+  if (K % 128 || K % blocksize || epi < 0 || epi > 2 || (epi && !R)) return (int)hipErrorInvalidValue;
+  return gemm_mfma(X, x_dtype, W, A8, AMAX, CODE2, offset, LUT, Y, R, epi, M, K, N, bs_shift,
+                   bs2_shift, stream);
+}

@@ -1,0 +1,186 @@
+"""One decode position through a transformer block in ten HIP launches.
+
+Drop-in for the reference's `app/engine/fusedlayer.py` (`decode_block`,
+`install`, `stats`, `HEAD_DIM`, `CHUNK`):
+
+    rms_norm -> wqkv -> qk_rope_kv -> attn_partial -> attn_combine
+             -> wo(+x) -> rms_norm -> w1 -> w3(silu(w1) * .) -> w2(+h)
+
+`qk_rope_kv` does the head norms, rotary and KV-cache write for every head in
+one launch; attention is split-K over CHUNK-position slices of the cache (one
+workgroup per KV head and slice, the chunk's K/V staged in LDS, log-sum-exp
+merge); the residual adds and the SwiGLU gate ride on the NF4 matmul's store.
+Rounding follows the fork: wherever it produces a 16-bit tensor, so does this
+(reference: fusedlayer.py:56-159, 212-269). Every reduction has a fixed order,
+so a step's output is a deterministic function of its inputs.
+
+Only a single position (B = S = 1) takes this path; anything else returns
+None and the block's own forward runs.
+"""
+
+from __future__ import annotations
+
+import logging
+
+from ttspipe_amd import _lib
+
+logger = logging.getLogger(__name__)
+
+HEAD_DIM = 128
+#: Cache positions per attention workgroup (the kernel's ACHUNK).
+CHUNK = 64
+
+_stats = {"fused": 0, "fallback": 0}
+_installed = False
+
+
+def stats() -> dict:
+    return {**_stats, "ready": _lib.gpu_present() and _installed}
+
+
+def _eligible(block, x, mask, input_pos) -> bool:
+    import torch
+
+    from ttspipe_amd import nf4gemv
+
+    a, ff = block.attention, block.feed_forward
+    if x.dim() != 3 or x.shape[0] != 1 or x.shape[1] != 1:
+        return False
+    if x.dtype not in (torch.float16, torch.bfloat16) or x.device.type != "cuda" or not x.is_contiguous():
+        return False
+    if mask is None or input_pos is None or input_pos.numel() != 1 or a.kv_cache is None:
+        return False
+    if input_pos.dtype != torch.long or input_pos.device != x.device:
+        return False
+    if a.head_dim != HEAD_DIM or a.n_head % a.n_local_heads or a.n_head // a.n_local_heads > 16:
+        return False
+    kc, vc = a.kv_cache.k_cache, a.kv_cache.v_cache
+    if kc.dtype != x.dtype or vc.dtype != x.dtype or not (kc.is_contiguous() and vc.is_contiguous()):
+        return False
+    if kc.shape[0] != 1 or kc.shape[1] != a.n_local_heads or kc.shape[3] != HEAD_DIM:
+        return False
+    for linear in (a.wqkv, a.wo, ff.w1, ff.w2, ff.w3):
+        if getattr(linear, "bias", None) is not None or not nf4gemv.prepare(linear):
+            return False
+    return True
+
+
+def decode_block(block, x, freqs_cis, mask, input_pos, *, workspace=None):
+    """`TransformerBlock.forward` for one position, or None if it cannot.
+
+    `workspace` (optional) is a dict of preallocated buffers from
+    `make_workspace`, which lets a captured graph run without allocating.
+    """
+    import torch
+
+    from ttspipe_amd import fusedops, nf4gemv
+
+    if not _lib.gpu_present() or not _eligible(block, x, mask, input_pos):
+        return None
+    ftype = _lib.dtype_code(freqs_cis.dtype) if freqs_cis is not None else None
+    if ftype is None or not freqs_cis.is_contiguous() or freqs_cis.numel() != HEAD_DIM:
+        return None
+    a, ff = block.attention, block.feed_forward
+    nh, nkv = a.n_head, a.n_local_heads
+    max_len = a.kv_cache.k_cache.shape[2]
+    nchunk = -(-min(mask.shape[-1], max_len) // CHUNK)
+    ws = workspace if workspace is not None else make_workspace(block, x, nchunk)
+    dt = _lib.dtype_code(x.dtype)
+    lib = _lib.lib()
+    st = _lib.stream()
+
+    xn = fusedops.rms_norm(x, block.attention_norm.weight, block.attention_norm.eps, out=ws["xn"])
+    if xn is None:
+        return None
+    qkv = nf4gemv.matmul(a.wqkv, xn, out=ws["qkv"])
+    if qkv is None:
+        return None
+    qn = getattr(a, "q_norm", None) if a.attention_qk_norm else None
+    kn = getattr(a, "k_norm", None) if a.attention_qk_norm else None
+    eps = float(qn.eps if qn is not None and qn.eps is not None else 1e-6)
+    rc = lib.ttsp_qk_rope_kv(
+        qkv.data_ptr(), _lib.ptr(None if qn is None else qn.weight), _lib.ptr(None if kn is None else kn.weight),
+        eps, freqs_cis.data_ptr(), ftype, input_pos.data_ptr(), ws["q"].data_ptr(),
+        a.kv_cache.k_cache.data_ptr(), a.kv_cache.v_cache.data_ptr(), nh, nkv, max_len, dt, st)
+    _lib.check(rc, "ttsp_qk_rope_kv")
+    rc = lib.ttsp_attn_decode(
+        ws["q"].data_ptr(), a.kv_cache.k_cache.data_ptr(), a.kv_cache.v_cache.data_ptr(),
+        input_pos.data_ptr(), ws["pm"].data_ptr(), ws["pl"].data_ptr(), ws["pacc"].data_ptr(),
+        ws["y"].data_ptr(), nh, nkv, max_len, nchunk, float(HEAD_DIM**-0.5), dt, st)
+    _lib.check(rc, "ttsp_attn_decode")
+    h = nf4gemv.matmul(a.wo, ws["y"], epi=nf4gemv.EPI_RESIDUAL, operand=x, out=ws["h"])
+    hn = fusedops.rms_norm(h, block.ffn_norm.weight, block.ffn_norm.eps, out=ws["hn"])
+    g1 = nf4gemv.matmul(ff.w1, hn, out=ws["g1"])
+    g = nf4gemv.matmul(ff.w3, hn, epi=nf4gemv.EPI_SILU_GATE, operand=g1, out=ws["g"])
+    out = ws.get("out")
+    out = nf4gemv.matmul(ff.w2, g, epi=nf4gemv.EPI_RESIDUAL, operand=h, out=out)
+    if any(t is None for t in (h, hn, g1, g, out)):
+        raise RuntimeError("decode_block: a prepared layer declined mid-block")
+    _stats["fused"] += 1
+    return out.view(x.shape)
+
+
+def make_workspace(block, x, nchunk: int, *, with_out: bool = False) -> dict:
+    """Buffers one `decode_block` call uses (reusable across calls of the same shape)."""
+    import torch
+
+    a, ff = block.attention, block.feed_forward
+    nh, nkv, D = a.n_head, a.n_local_heads, x.shape[-1]
+    inter = ff.w1.out_features
+    kw = dict(dtype=x.dtype, device=x.device)
+    f32 = dict(dtype=torch.float32, device=x.device)
+    ws = {
+        "xn": torch.empty((1, 1, D), **kw),
+        "qkv": torch.empty((1, (nh + 2 * nkv) * HEAD_DIM), **kw),
+        "q": torch.empty(nh * HEAD_DIM, **kw),
+        "pm": torch.empty(nh * nchunk, **f32),
+        "pl": torch.empty(nh * nchunk, **f32),
+        "pacc": torch.empty(nh * nchunk * HEAD_DIM, **f32),
+        "y": torch.empty((1, 1, nh * HEAD_DIM), **kw),
+        "h": torch.empty((1, D), **kw),
+        "hn": torch.empty((1, 1, D), **kw),
+        "g1": torch.empty((1, inter), **kw),
+        "g": torch.empty((1, 1, inter), **kw),
+    }
+    if with_out:
+        ws["out"] = torch.empty((1, D), **kw)
+    return ws
+
+
+def _block_classes():
+    from ttspipe_amd.llama import TransformerBlock
+
+    classes = [TransformerBlock]
+    try:
+        from fish_speech.models.text2semantic.llama import TransformerBlock as ForkBlock
+
+        classes.append(ForkBlock)
+    except Exception:  # noqa: BLE001
+        pass
+    return classes
+
+
+def install() -> bool:
+    """Route single-position `TransformerBlock.forward` calls through `decode_block`."""
+    global _installed
+    if not _lib.gpu_present():
+        return False
+    _lib.load()
+    for cls in _block_classes():
+        if getattr(cls, "_fused_patched", False):
+            continue
+        original = cls.forward
+
+        def forward(self, x, freqs_cis, mask, input_pos=None, _original=original):
+            out = decode_block(self, x, freqs_cis, mask, input_pos)
+            if out is not None:
+                return out
+            if x.shape[1] == 1:
+                _stats["fallback"] += 1
+            return _original(self, x, freqs_cis, mask, input_pos)
+
+        cls.forward = forward
+        cls._fused_patched = True
+        cls._fused_original_forward = original
+    _installed = True
+    return True

@@ -1,0 +1,262 @@
+"""The NF4 matmul for decode and prefill, reading bitsandbytes-layout weights in place.
+
+Drop-in for the reference's `app/engine/nf4gemv.py` (same public names and
+behaviour: `MAX_N`, `NF4_CODE`, `EPI_*`, `available`, `prepare`, `matmul`,
+`install`, `stats`, `module._nf4_fast`, class attributes `_nf4_patched` /
+`_nf4_original_forward`). The arithmetic runs in `libttsp_hip.so`:
+
+* one activation row -> the HBM-bound GEMV (`csrc/nf4_gemv.hip`): the packed
+  weight is streamed once with coalesced 256-byte wave loads, codes resolve
+  through an LDS pair table into `v_dot2_f32_{f16,bf16}`, deterministic wave
+  reductions;
+* several rows -> the MFMA GEMM (`csrc/nf4_gemm.hip`): NF4 tiles dequantised
+  into LDS feed `v_mfma_f32_32x32x16`, so a prompt reads each weight once per
+  tile of rows rather than once per row.
+
+Unlike the reference (fp16 only, nf4gemv.py:439) both fp16 and bf16
+activations are served; anything else is declined (`None`), exactly where the
+reference declines (nf4gemv.py:328-376, 436-456), and the patched forward then
+uses the layer's own dequantise-and-matmul path. `MAX_N` is kept for callers
+that size buffers by it; a launch here takes any number of rows.
+"""
+
+from __future__ import annotations
+
+import logging
+import threading
+
+from ttspipe_amd import _lib
+from ttspipe_amd.quant import NF4_CODE
+
+logger = logging.getLogger(__name__)
+
+#: Rows the reference's kernel took per launch (nf4gemv.py:71). Kept for
+#: callers that bucket prompts by it; `matmul` takes any count in one launch.
+MAX_N = 32
+
+#: Epilogues `matmul` can fold into the kernel's store (nf4gemv.py:424).
+EPI_NONE, EPI_RESIDUAL, EPI_SILU_GATE = 0, 1, 2
+
+_lock = threading.Lock()
+_state = {"ready": None, "lut": {}}
+_stats = {"fast": 0, "fallback": 0, "layers": 0}
+
+
+def stats() -> dict:
+    """Calls served by the kernel, calls handed back to the layer's own forward, layers covered."""
+    return dict(_stats)
+
+
+def available() -> bool:
+    """Whether the kernels are usable here.
+
+    False without a GPU (nothing raises for that, nf4gemv.py:26-28 of the
+    reference's FFI). With a GPU the library must load: a missing build is an
+    error, not a slow path.
+    """
+    if _state["ready"] is not None:
+        return _state["ready"]
+    with _lock:
+        if _state["ready"] is None:
+            if not _lib.gpu_present():
+                _state["ready"] = False
+            else:
+                _lib.load()
+                _state["ready"] = True
+    return _state["ready"]
+
+
+def _lut(device):
+    import torch
+
+    key = str(device)
+    t = _state["lut"].get(key)
+    if t is None:
+        t = torch.tensor(NF4_CODE, dtype=torch.float32, device=device)
+        _state["lut"][key] = t
+    return t
+
+
+def prepare(module) -> bool:
+    """Attach what the kernel needs to one NF4 layer, or record that it cannot serve it.
+
+    Idempotent and cached on the module (`_nf4_fast`): a dict, or None for a
+    declined layer. Eligibility is the reference's (nf4gemv.py:333-376):
+    nf4, on the GPU, blocksize a power of two >= 64, in_features a multiple of
+    128 and of the blocksize, 16-byte aligned packed weight, uint8/fp32 nested
+    scales (or fp32 plain ones) forming a rectangle over the rows.
+    """
+    import torch
+
+    cached = getattr(module, "_nf4_fast", -1)
+    if cached != -1:
+        return cached is not None
+
+    def reject(why: str) -> bool:
+        module._nf4_fast = None
+        logger.debug("nf4 kernel declines %s: %s", type(module).__name__, why)
+        return False
+
+    weight = getattr(module, "weight", None)
+    quant_state = getattr(weight, "quant_state", None)
+    if quant_state is None:
+        return reject("weight is not quantised yet")
+    if getattr(quant_state, "quant_type", None) != "nf4":
+        return reject(f"quant_type={getattr(quant_state, 'quant_type', None)}")
+    if weight.device.type != "cuda":
+        return reject("weight is not on a GPU")
+
+    out_features, in_features = tuple(quant_state.shape)
+    blocksize = int(quant_state.blocksize)
+    if blocksize < 64 or blocksize & (blocksize - 1):
+        return reject(f"blocksize {blocksize} is not a power of two >= 64")
+    if in_features % blocksize or in_features % 128:
+        return reject(f"in_features {in_features} is not a multiple of 128 and {blocksize}")
+    if weight.data_ptr() % 16:
+        return reject("packed weight is not 16-byte aligned")
+
+    nblk = in_features // blocksize
+    nested = bool(getattr(quant_state, "nested", False))
+    if nested:
+        state2 = quant_state.state2
+        bs2 = int(state2.blocksize)
+        if bs2 <= 0 or bs2 & (bs2 - 1):
+            return reject(f"second-level blocksize {bs2} is not a power of two")
+        if quant_state.absmax.dtype != torch.uint8 or state2.absmax.dtype != torch.float32:
+            return reject("second-level scales are not the uint8/fp32 pair the kernel reads")
+        if state2.code.dtype != torch.float32 or state2.code.numel() != 256:
+            return reject("second-level code is not a 256-entry fp32 table")
+        scales = (quant_state.absmax, state2.absmax, state2.code)
+        offset = float(quant_state.offset)
+    else:
+        if quant_state.absmax.dtype != torch.float32:
+            return reject(f"scales are {quant_state.absmax.dtype}, not float32")
+        scales = (None, quant_state.absmax, None)
+        offset = 0.0
+        bs2 = 0
+    if quant_state.absmax.numel() != out_features * nblk:
+        return reject("scales do not form a rectangle over the weight rows")
+    for t in scales:
+        if t is not None and (t.device != weight.device or not t.is_contiguous()):
+            return reject("scales are not contiguous on the weight's device")
+
+    module._nf4_fast = {
+        "nested": nested,
+        "held": tuple(t for t in scales if t is not None),  # keeps the pointed-to tensors alive
+        "w": weight.data_ptr(),
+        "a8": _lib.ptr(scales[0]),
+        "amax": scales[1].data_ptr(),
+        "code2": _lib.ptr(scales[2]),
+        "offset": offset,
+        "lut": _lut(weight.device),
+        "bs": blocksize,
+        "bs2": bs2,
+        "M": out_features,
+        "K": in_features,
+    }
+    _stats["layers"] += 1
+    return True
+
+
+def matmul(module, x, *, epi: int = EPI_NONE, operand=None, out=None):
+    """`x @ module.weight.T` for any number of input rows, or None if not applicable.
+
+    `epi` fuses what the fork does right after: `operand + xW` (residual add)
+    or `silu(operand) * xW` (the SwiGLU gate), rounded as the unfused ops
+    round. `operand` has the output's shape and x's dtype, contiguous, on the
+    same device. `out` (optional) receives the result in place.
+    """
+    import torch
+
+    fast = getattr(module, "_nf4_fast", None)
+    if fast is None:
+        return None
+    dt = _lib.dtype_code(x.dtype)
+    if dt not in (_lib.DT_F16, _lib.DT_BF16) or x.device.type != "cuda":
+        return None
+    K, M = fast["K"], fast["M"]
+    if x.shape[-1] != K:
+        return None
+    flat = x.reshape(-1, K)
+    if not flat.is_contiguous() or flat.data_ptr() % 16:
+        flat = flat.contiguous()
+        if flat.data_ptr() % 16:
+            return None
+    rows = flat.shape[0]
+    if rows == 0:
+        return x.new_empty(*x.shape[:-1], M)
+    if epi != EPI_NONE:
+        if operand is None or operand.numel() != rows * M or operand.dtype != x.dtype:
+            return None
+        if operand.device != x.device or not operand.is_contiguous():
+            return None
+    if out is None:
+        out = torch.empty((rows, M), dtype=x.dtype, device=x.device)
+    elif out.dtype != x.dtype or out.numel() != rows * M or not out.is_contiguous():
+        return None
+    rc = _lib.lib().ttsp_nf4_gemm(
+        flat.data_ptr(), dt, fast["w"], fast["a8"], fast["amax"], fast["code2"], fast["offset"],
+        fast["lut"].data_ptr(), out.data_ptr(), _lib.ptr(operand) if epi else 0, epi, M, K, rows,
+        fast["bs"], fast["bs2"], _lib.stream())
+    if rc:
+        raise RuntimeError(f"ttsp_nf4_gemm failed: hipError_t {rc}")
+    _stats["fast"] += 1
+    return out.view(*x.shape[:-1], M)
+
+
+def _classes():
+    """Linear4bit classes to patch: ours, and bitsandbytes' where it is importable."""
+    from ttspipe_amd.quant import Linear4bit
+
+    classes = [Linear4bit]
+    try:  # a real bitsandbytes model is served the same way (same quant_state fields)
+        import bitsandbytes as bnb  # noqa: F401
+
+        classes.append(bnb.nn.Linear4bit)
+    except Exception:  # noqa: BLE001
+        pass
+    return classes
+
+
+def install(model=None) -> bool:
+    """Route fp16/bf16 NF4 `Linear4bit` calls through the kernels.
+
+    Patches the class, so it covers every instance including later ones.
+    Returns whether the fast path is live.
+    """
+    if not available():
+        return False
+    for cls in _classes():
+        if getattr(cls, "_nf4_patched", False):
+            continue
+        original_forward = cls.forward
+
+        def forward(self, x, _original=original_forward):
+            if prepare(self):
+                out = matmul(self, x)
+                if out is not None:
+                    if self.bias is not None:
+                        out = out + self.bias.to(out.dtype)
+                    return out
+            _stats["fallback"] += 1
+            return _original(self, x)
+
+        cls.forward = forward
+        cls._nf4_patched = True
+        cls._nf4_original_forward = original_forward
+    if model is not None:
+        _prepare_all(model)
+    return True
+
+
+def _prepare_all(model) -> None:
+    """Prepare every NF4 layer now, so no decode step pays for it."""
+    classes = tuple(_classes())
+    served = declined = 0
+    for module in model.modules():
+        if isinstance(module, classes):
+            if prepare(module):
+                served += 1
+            else:
+                declined += 1
+    logger.info("nf4 kernel ready for %d of %d 4-bit layers", served, served + declined)
