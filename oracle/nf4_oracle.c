@@ -123,6 +123,14 @@ float orc_exp_cw(float x) {
 
 float orc_rsqrt_rn(float x) { return 1.0f / sqrtf(x); }
 
+/* fma(a.hi, b.hi, fma(a.lo, b.lo, c)) on packed fp16 pairs, IEEE fmaf. */
+void orc_fma16_chain(const uint32_t* a, const uint32_t* b, const float* c, int n, float* out) {
+  for (int i = 0; i < n; ++i) {
+    const float t = fmaf(orc_f16_to_f32((uint16_t)(a[i] & 0xffffu)), orc_f16_to_f32((uint16_t)(b[i] & 0xffffu)), c[i]);
+    out[i] = fmaf(orc_f16_to_f32((uint16_t)(a[i] >> 16)), orc_f16_to_f32((uint16_t)(b[i] >> 16)), t);
+  }
+}
+
 static inline float silu_rn(float a) { return a / (1.0f + orc_exp_cw(-a)); }
 
 /* Sum of 64 lane values as the kernels' xor butterfly (offsets 32..1). */
@@ -196,11 +204,11 @@ static inline float epilogue(float acc, int epi, float r, int dt) {
 }
 
 /* The GPU GEMV's arithmetic, in its order (ttspipe_amd/csrc/nf4_gemv.hip):
- * lane l of K-slice ks owns dwords d = l + 64*(j*KS + ks); per dword the four
- * bytes give p_b = round(c_hi*x_2b + c_lo*x_2b+1) (codes rounded to fp16; bf16
- * activations first scaled by 2^-e per slice and converted to fp16),
- * q = (p0 + p1) + (p2 + p3), acc = fma(q, s_block, acc); lanes are summed by
- * the xor butterfly, slices left to right; then the epilogue. */
+ * lane l of K-slice ks owns dwords d = l + 64*(j*KS + ks); per dword the 8
+ * codes (rounded to fp16; bf16 activations first scaled by 2^-e per slice and
+ * converted to fp16) are chained q = fma(c_k, x_k, q) from q = +0 in code order,
+ * then acc = fma(q, s_block, acc); lanes are summed by the xor butterfly,
+ * slices left to right; then the epilogue. */
 void orc_gemv_emul(const void* X, int dt, const uint8_t* W, const uint8_t* A8, const float* AMAX,
                    const float* CODE2, float offset, const float* LUT, uint16_t* Y, const void* R,
                    int epi, int M, int K, int bs, int bs2, int KS, int J) {
@@ -247,7 +255,7 @@ void orc_gemv_emul(const void* X, int dt, const uint8_t* W, const uint8_t* A8, c
           const int d = l + 64 * (j * KS + ks);
           const int dc = d < KD ? d : KD - 1;
           const float s = scale_of((long long)m * nblk + (dc * 8) / bs, A8, AMAX, CODE2, offset, bs2);
-          float p[4];
+          float q = 0.0f;
           for (int b = 0; b < 4; ++b) {
             float x0 = 0.0f, x1 = 0.0f;
             int byte = 0;
@@ -256,10 +264,9 @@ void orc_gemv_emul(const void* X, int dt, const uint8_t* W, const uint8_t* A8, c
               x0 = xv[8 * d + 2 * b];
               x1 = xv[8 * d + 2 * b + 1];
             }
-            const float a0 = lutv[byte >> 4] * x0, a1 = lutv[byte & 15] * x1;
-            p[b] = a0 + a1;
+            q = fmaf(lutv[byte >> 4], x0, q);
+            q = fmaf(lutv[byte & 15], x1, q);
           }
-          const float q = (p[0] + p[1]) + (p[2] + p[3]);
           acc = fmaf(q, s, acc);
         }
         lanes[l] = acc;

@@ -46,6 +46,7 @@ def lib():
             "orc_f32_to_f16": ([f], ctypes.c_uint16),
             "orc_exp_cw": ([f], f),
             "orc_rsqrt_rn": ([f], f),
+            "orc_fma16_chain": ([vp, vp, vp, i, vp], None),
             "orc_nf4_dequant": ([vp, vp, vp, vp, f, vp, vp, i, ll, i, i], None),
             "orc_nf4_gemm_ref": ([vp, i, vp, vp, vp, vp, f, vp, vp, i, i, i, i, i, i], None),
             "orc_gemv_emul": ([vp, i, vp, vp, vp, vp, f, vp, vp, vp, i, i, i, i, i, i, i], None),
@@ -210,6 +211,15 @@ def attn_emul(Q, KC, VC, pos, nh, nkv, max_len, nchunk, scale, dt):
     Q, KC, VC = _c(Q), _c(KC), _c(VC)
     _lib.orc_attn_emul(_p(Q), _p(KC), _p(VC), int(pos), _p(Y), nh, nkv, max_len, nchunk, float(scale), dt)
     return Y
+
+
+def fma16_chain(a, b, c):
+    """fma(a.hi, b.hi, fma(a.lo, b.lo, c)) with IEEE fmaf, a/b packed fp16 pairs (uint32)."""
+    lib()
+    a, b, c = _c(a, np.uint32), _c(b, np.uint32), _c(c, np.float32)
+    out = np.empty(c.size, dtype=np.float32)
+    _lib.orc_fma16_chain(_p(a), _p(b), _p(c), c.size, _p(out))
+    return out
 
 
 def synth_fill(n, seed, kind, scale=1.0, offset=0.0):

@@ -16,7 +16,7 @@ import pytest
 import torch
 
 from oracle import oracle as o
-from tests.conftest import relative_error
+from tests.conftest import relative_error, ulp16
 from tests.gpuutil import bits, dt_code, first_mismatch, from_bits, gemv_shape, randn_bits
 
 pytestmark = pytest.mark.gpu
@@ -143,7 +143,8 @@ def test_qk_rope_kv_bit_exact(hip, orc, qk_norm, dtype, pos):
     kw = from_bits(kwb, dtype) if qk_norm else None
     posd = torch.tensor([pos], dtype=torch.long, device="cuda")
     fd = freqs.cuda()
-    rc = hip.ttsp_qk_rope_kv(from_bits(qkvb, dtype).data_ptr(), _lib.ptr(qw), _lib.ptr(kw), 1e-6, fd.data_ptr(),
+    qkv = from_bits(qkvb, dtype)  # held: the launch is asynchronous
+    rc = hip.ttsp_qk_rope_kv(qkv.data_ptr(), _lib.ptr(qw), _lib.ptr(kw), 1e-6, fd.data_ptr(),
                              o.DT_BF16, posd.data_ptr(), Q.data_ptr(), KC.data_ptr(), VC.data_ptr(), nh, nkv,
                              max_len, dt, _lib.stream())
     assert rc == 0
@@ -172,8 +173,8 @@ def test_decode_attention_bit_exact(hip, orc, L, dtype):
     pm, pl, pacc = torch.empty(nh * nchunk, **f32), torch.empty(nh * nchunk, **f32), torch.empty(nh * nchunk * 128, **f32)
     y = torch.empty(nh * 128, dtype=dtype, device="cuda")
     posd = torch.tensor([L - 1], dtype=torch.long, device="cuda")
-    rc = hip.ttsp_attn_decode(from_bits(qb, dtype).data_ptr(), from_bits(kcb, dtype).data_ptr(),
-                              from_bits(vcb, dtype).data_ptr(), posd.data_ptr(), pm.data_ptr(), pl.data_ptr(),
+    qd, kd, vd = from_bits(qb, dtype), from_bits(kcb, dtype), from_bits(vcb, dtype)  # held across the launch
+    rc = hip.ttsp_attn_decode(qd.data_ptr(), kd.data_ptr(), vd.data_ptr(), posd.data_ptr(), pm.data_ptr(), pl.data_ptr(),
                               pacc.data_ptr(), y.data_ptr(), nh, nkv, max_len, nchunk, float(128**-0.5), dt,
                               _lib.stream())
     assert rc == 0
@@ -201,8 +202,8 @@ def test_decode_attention_matches_torch_gqa():
     pm, pl, pacc = torch.empty(nh * nchunk, **f32), torch.empty(nh * nchunk, **f32), torch.empty(nh * nchunk * 128, **f32)
     y = torch.empty(nh * 128, dtype=torch.float16, device="cuda")
     posd = torch.tensor([L - 1], dtype=torch.long, device="cuda")
-    rc = _lib.load().ttsp_attn_decode(q.cuda().data_ptr(), k.cuda().contiguous().data_ptr(),
-                                      v.cuda().contiguous().data_ptr(), posd.data_ptr(), pm.data_ptr(), pl.data_ptr(),
+    qd, kd, vd = q.cuda(), k.cuda().contiguous(), v.cuda().contiguous()  # held across the launch
+    rc = _lib.load().ttsp_attn_decode(qd.data_ptr(), kd.data_ptr(), vd.data_ptr(), posd.data_ptr(), pm.data_ptr(), pl.data_ptr(),
                                       pacc.data_ptr(), y.data_ptr(), nh, nkv, L, nchunk, float(128**-0.5), 0,
                                       _lib.stream())
     assert rc == 0
@@ -297,8 +298,11 @@ def test_decode_block_matches_oracle_and_unfused_block(orc, qk_norm, pos, window
         before = fusedlayer.stats()["fused"]
         ours = block(x, f, mask, ip)
     assert fusedlayer.stats()["fused"] == before + 1
-    # the unfused block (fork arithmetic, torch ops) - the reference's bar
-    assert relative_error(bits_f(ours, dt), bits_f(theirs, dt)) < 5e-3
+    # the unfused block (fork arithmetic, torch ops) - the reference's bar, 5e-3 of
+    # max |y|, plus one output ulp: two separately rounded 16-bit results may sit
+    # one ulp apart, and bf16's ulp at the largest outputs is itself ~5e-3 of them
+    got, ref = bits_f(ours, dt).astype(np.float64), bits_f(theirs, dt).astype(np.float64)
+    assert np.all(np.abs(got - ref) <= 5e-3 * np.abs(ref).max() + ulp16(ref, dt))
     assert relative_error(bits_f(cache.k_cache[:, :, pos], dt), bits_f(k_ref[:, :, pos], dt)) < 1e-2
     assert torch.equal(cache.v_cache[:, :, pos], v_ref[:, :, pos])
     # the oracle composition - bit for bit

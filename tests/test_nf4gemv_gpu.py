@@ -34,30 +34,30 @@ def nf4():
 
 # ------------------------------------------------------------ numerics primitives
 
-@pytest.mark.parametrize("dtype", DTYPES)
-def test_dot2_is_one_rounding_of_two_exact_products(hip, dtype):
-    """The kernels' zero-addend dot2 is round(a0*b0 + a1*b1): checked bit for bit
-    against IEEE fp32 on random, tiny, huge and cancelling pairs."""
-    rng = np.random.default_rng(0)
-    n = 1 << 16
-    vals = np.concatenate([rng.standard_normal(n) * 10.0 ** rng.integers(-6, 4, n),
-                           rng.standard_normal(n)]).astype(np.float32)
-    a = o.from_f32(vals[:n].copy(), dt_code(dtype)).view(np.uint32)
-    b = o.from_f32(vals[n:].copy(), dt_code(dtype)).view(np.uint32).copy()
-    # exact cancellations: (x0, x1) . (x1, -x0) = 0
-    b[:1000] = ((a[:1000] >> 16) | ((a[:1000] & 0xFFFF) << 16)) ^ 0x80000000
-    at = torch.from_numpy(a.view(np.int32).copy()).cuda()
-    bt = torch.from_numpy(b.view(np.int32).copy()).cuda()
-    out = torch.empty(a.size, dtype=torch.float32, device="cuda")
+def test_fp16_fma_chain_is_ieee(hip, orc):
+    """The GEMV's inner step, fma(a.hi, b.hi, fma(a.lo, b.lo, c)) on fp16 halves
+    (v_fma_mix_f32), equals IEEE fmaf bit for bit - over random, tiny, huge and
+    exactly cancelling operands."""
     from ttspipe_amd import _lib
 
-    rc = hip.ttsp_selftest_dot2(at.data_ptr(), bt.data_ptr(), a.size, dt_code(dtype), out.data_ptr(), _lib.stream())
-    assert rc == 0
-    af = o.to_f32(a.view(np.uint16), dt_code(dtype)).reshape(-1, 2)
-    bf = o.to_f32(b.view(np.uint16), dt_code(dtype)).reshape(-1, 2)
-    expect = (af[:, 0] * bf[:, 0]).astype(np.float32) + (af[:, 1] * bf[:, 1]).astype(np.float32)
+    rng = np.random.default_rng(0)
+    n = 1 << 16
+    va = (rng.standard_normal(2 * n) * 10.0 ** rng.integers(-7, 4, 2 * n)).astype(np.float32)
+    vb = (rng.standard_normal(2 * n) * 10.0 ** rng.integers(-3, 4, 2 * n)).astype(np.float32)
+    a = o.from_f32(va, o.DT_F16).view(np.uint32).copy()
+    b = o.from_f32(vb, o.DT_F16).view(np.uint32).copy()
+    c = (rng.standard_normal(n) * 10.0 ** rng.integers(-4, 4, n)).astype(np.float32)
+    af = o.to_f32(a.view(np.uint16), o.DT_F16).reshape(-1, 2)
+    bf = o.to_f32(b.view(np.uint16), o.DT_F16).reshape(-1, 2)
+    c[:1000] = -(af[:1000, 0] * bf[:1000, 0])  # exact cancellation in the first fma
+    at = torch.from_numpy(a.view(np.int32)).cuda()
+    bt = torch.from_numpy(b.view(np.int32)).cuda()
+    ct = torch.from_numpy(c).cuda()
+    out = torch.empty(n, dtype=torch.float32, device="cuda")
+    assert hip.ttsp_selftest_fma16(at.data_ptr(), bt.data_ptr(), ct.data_ptr(), n, out.data_ptr(), _lib.stream()) == 0
     got = out.cpu().numpy()
-    assert np.array_equal(got.view(np.uint32), expect.astype(np.float32).view(np.uint32)), first_mismatch(got, expect)
+    expect = o.fma16_chain(a, b, c)
+    assert np.array_equal(got.view(np.uint32), expect.view(np.uint32)), first_mismatch(got, expect)
 
 
 @pytest.mark.parametrize("op", [0, 1, 2, 3])

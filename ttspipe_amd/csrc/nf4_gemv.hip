@@ -13,13 +13,14 @@
 //     contiguous bytes, and the 8 activations matching a dword stay in
 //     registers for every row (x is read once per wave, not once per row).
 //   * Each byte (two codes) becomes a packed pair of fp16 code values through
-//     a 256-entry LDS table, and meets the matching activation pair in one
-//     v_dot2_f32_f16 with a zero addend: round(w0*x0 + w1*x1), both products
-//     exact. bf16 activations are first rescaled per wave by a power of two
-//     and converted to fp16 exactly, so both types get 11-bit code values. Four bytes sum as (p0+p1)+(p2+p3), then one fma with
-//     the block scale into the lane accumulator. The scale multiplies the
-//     block's partial sum instead of each weight (the factored form the
-//     reference CPU kernel uses, app/engine/nf4cpu.py:115-129).
+//     a 256-entry LDS table. A dword's 8 products are chained in code order
+//     (v_fma_mix_f32 on the fp16 halves, the first onto +0, one IEEE rounding
+//     each), and the dword's partial meets its block scale in
+//     one fma into the lane accumulator: the scale multiplies the block's
+//     partial sum instead of each weight (the factored form the reference
+//     CPU kernel uses, app/engine/nf4cpu.py:115-129).
+//   * bf16 activations are first rescaled per wave by a power of two and
+//     converted to fp16 exactly, so both activation types get 11-bit codes.
 //   * The scales of a workgroup's rows are contiguous; they are loaded once,
 //     cooperatively, resolved (nested: code2 from an LDS copy) and parked in
 //     LDS, where the 8 lanes sharing a 64-code block read one broadcast word.
@@ -194,11 +195,17 @@ __global__ __launch_bounds__(GEMV_THREADS) void nf4_gemv_kernel(
       const int d = min(lane + 64 * (j * KS + ks), KD - 1);
       const float s = srr[d >> sh];
       const uint32_t wv = w[r][j];
-      const float p0 = Elem<DT_F16>::dot2(lut[wv & 0xffu], xr[j].x);
-      const float p1 = Elem<DT_F16>::dot2(lut[(wv >> 8) & 0xffu], xr[j].y);
-      const float p2 = Elem<DT_F16>::dot2(lut[(wv >> 16) & 0xffu], xr[j].z);
-      const float p3 = Elem<DT_F16>::dot2(lut[wv >> 24], xr[j].w);
-      const float q = __fadd_rn(__fadd_rn(p0, p1), __fadd_rn(p2, p3));
+      const uint32_t c0 = lut[wv & 0xffu], c1 = lut[(wv >> 8) & 0xffu];
+      const uint32_t c2 = lut[(wv >> 16) & 0xffu], c3 = lut[wv >> 24];
+      // the dword's 8 products in code order, each an fma (the first onto +0)
+      float q = __builtin_fmaf(h_lo(c0), h_lo(xr[j].x), 0.0f);
+      q = __builtin_fmaf(h_hi(c0), h_hi(xr[j].x), q);
+      q = __builtin_fmaf(h_lo(c1), h_lo(xr[j].y), q);
+      q = __builtin_fmaf(h_hi(c1), h_hi(xr[j].y), q);
+      q = __builtin_fmaf(h_lo(c2), h_lo(xr[j].z), q);
+      q = __builtin_fmaf(h_hi(c2), h_hi(xr[j].z), q);
+      q = __builtin_fmaf(h_lo(c3), h_lo(xr[j].w), q);
+      q = __builtin_fmaf(h_hi(c3), h_hi(xr[j].w), q);
       acc = __builtin_fmaf(q, s, acc);
     }
     acc = wave_sum(acc);

@@ -1,5 +1,5 @@
 // Numerics self-test entry points: evaluate the device primitives every
-// kernel relies on (exp_cw, sqrt_rn, silu_rn, the zero-addend dot2) over
+// kernel relies on (exp_cw, sqrt_rn, silu_rn, the fp16-operand fma) over
 // caller arrays, so a test can compare them bit for bit against IEEE CPU
 // arithmetic. No counterpart in the reference; used by the test suite.
 #include "ttsp_common.h"
@@ -20,12 +20,14 @@ __global__ void selftest_math_kernel(const float* __restrict__ in, int n, int op
   out[i] = y;
 }
 
-template <int DT>
-__global__ void selftest_dot2_kernel(const uint32_t* __restrict__ a, const uint32_t* __restrict__ b, int n,
-                                     float* __restrict__ out) {
+// out = fma(a.hi, b.hi, fma(a.lo, b.lo, c)) on packed fp16 pairs: the GEMV's
+// inner step (v_fma_mix_f32 with op_sel), to be checked against IEEE fmaf.
+__global__ void selftest_fma16_kernel(const uint32_t* __restrict__ a, const uint32_t* __restrict__ b,
+                                      const float* __restrict__ c, int n, float* __restrict__ out) {
   const int i = blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= n) return;
-  out[i] = Elem<DT>::dot2(a[i], b[i]);
+  const float t = __builtin_fmaf(h_lo(a[i]), h_lo(b[i]), c[i]);
+  out[i] = __builtin_fmaf(h_hi(a[i]), h_hi(b[i]), t);
 }
 
 }  // namespace ttsp
@@ -39,15 +41,10 @@ extern "C" int ttsp_selftest_math(const float* in, int n, int op, float* out, hi
   TTSP_RETURN_LAUNCH();
 }
 
-extern "C" int ttsp_selftest_dot2(const uint32_t* a, const uint32_t* b, int n, int dtype, float* out,
-                                  hipStream_t stream) {
+extern "C" int ttsp_selftest_fma16(const uint32_t* a, const uint32_t* b, const float* c, int n,
+                                   float* out, hipStream_t stream) {
   if (n < 0) return (int)hipErrorInvalidValue;
   if (n == 0) return 0;
-  if (dtype == DT_F16)
-    hipLaunchKernelGGL(selftest_dot2_kernel<DT_F16>, dim3((n + 255) / 256), dim3(256), 0, stream, a, b, n, out);
-  else if (dtype == DT_BF16)
-    hipLaunchKernelGGL(selftest_dot2_kernel<DT_BF16>, dim3((n + 255) / 256), dim3(256), 0, stream, a, b, n, out);
-  else
-    return (int)hipErrorInvalidValue;
+  hipLaunchKernelGGL(selftest_fma16_kernel, dim3((n + 255) / 256), dim3(256), 0, stream, a, b, c, n, out);
   TTSP_RETURN_LAUNCH();
 }

@@ -19,9 +19,6 @@ namespace ttsp {
 
 enum : int { DT_F16 = 0, DT_BF16 = 1, DT_F32 = 2 };
 
-typedef _Float16 half2_v __attribute__((ext_vector_type(2)));
-typedef __bf16 bf162_v __attribute__((ext_vector_type(2)));
-
 __device__ __forceinline__ float bf16_to_f32(uint32_t h) { return __uint_as_float(h << 16); }
 
 // Round to nearest even; NaN stays a (quiet) NaN.
@@ -43,31 +40,29 @@ __device__ __forceinline__ uint16_t f32_to_f16(float f) {
 
 template <int DT> struct Elem;
 
+// Rounding to a 16-bit type happens exactly where the source says, from an
+// fp32 value: `opaque` hides the value's origin from instruction selection,
+// which would otherwise fuse a preceding fp32 multiply into the conversion
+// (v_fma_mixlo_f16: one rounding of the exact product instead of two).
+__device__ __forceinline__ float opaque(float f) {
+  asm("" : "+v"(f));
+  return f;
+}
+
 template <> struct Elem<DT_F16> {
   __device__ static __forceinline__ float load(uint32_t h) { return f16_to_f32(h & 0xffffu); }
-  __device__ static __forceinline__ uint16_t store(float f) { return f32_to_f16(f); }
-  // round(a.lo*b.lo + a.hi*b.hi): both products are exact in fp32 (11x11
-  // significand bits), so with a zero addend the result is the single
-  // correctly rounded sum whatever the instruction does internally.
-  // The VOP3P form takes the zero as an inline constant; the builtin would be
-  // shrunk to v_dot2c with a v_mov of zero into the accumulator first.
-  __device__ static __forceinline__ float dot2(uint32_t a, uint32_t b) {
-    float r;
-    asm("v_dot2_f32_f16 %0, %1, %2, 0" : "=v"(r) : "v"(a), "v"(b));
-    return r;
-  }
+  __device__ static __forceinline__ uint16_t store(float f) { return f32_to_f16(opaque(f)); }
 };
 
 template <> struct Elem<DT_BF16> {
   __device__ static __forceinline__ float load(uint32_t h) { return bf16_to_f32(h & 0xffffu); }
   __device__ static __forceinline__ uint16_t store(float f) { return f32_to_bf16(f); }
-  // Same argument as fp16: 8x8 significand bits, products exact in fp32.
-  __device__ static __forceinline__ float dot2(uint32_t a, uint32_t b) {
-    float r;
-    asm("v_dot2_f32_bf16 %0, %1, %2, 0" : "=v"(r) : "v"(a), "v"(b));
-    return r;
-  }
 };
+
+// Halves of a packed fp16 pair as fp32 (exact). Fed to fmaf, they select
+// v_fma_mix_f32 with op_sel: an IEEE fma on fp16 operands, one instruction.
+__device__ __forceinline__ float h_lo(uint32_t u) { return f16_to_f32(u & 0xffffu); }
+__device__ __forceinline__ float h_hi(uint32_t u) { return f16_to_f32(u >> 16); }
 
 __device__ __forceinline__ float load_elem(const void* p, size_t i, int dt) {
   if (dt == DT_F32) return ((const float*)p)[i];
