@@ -143,6 +143,17 @@ static float butterfly64(float* v) {
   return v[0];
 }
 
+/* The same butterfly with the partner distance rising 1, 2, ..., 32 (the
+ * GEMV's DPP reduction: within 16-lane rows first, then across rows). */
+static float butterfly64_up(float* v) {
+  for (int off = 1; off <= 32; off <<= 1) {
+    float t[64];
+    for (int l = 0; l < 64; ++l) t[l] = v[l] + v[l ^ off];
+    memcpy(v, t, sizeof t);
+  }
+  return v[0];
+}
+
 /* ----------------------------------------------------------------- NF4 scale */
 
 /* Scale of flattened block b: plain absmax[b], or nested
@@ -205,9 +216,9 @@ static inline float epilogue(float acc, int epi, float r, int dt) {
 
 /* The GPU GEMV's arithmetic, in its order (ttspipe_amd/csrc/nf4_gemv.hip):
  * lane l of K-slice ks owns dwords d = l + 64*(j*KS + ks); per dword the 8
- * codes (rounded to fp16; bf16 activations first scaled by 2^-e per slice and
- * converted to fp16) are chained q = fma(c_k, x_k, q) from q = +0 in code order,
- * then acc = fma(q, s_block, acc); lanes are summed by the xor butterfly,
+ * codes (rounded to fp16; bf16 activations first scaled by 2^-e, e from the
+ * largest |x| of the vector, and converted to fp16) are chained
+ * q = fma(c_k, x_k, q) from q = +0 in code order, then acc = fma(q, s_block, acc); lanes are summed by the xor butterfly,
  * slices left to right; then the epilogue. */
 void orc_gemv_emul(const void* X, int dt, const uint8_t* W, const uint8_t* A8, const float* AMAX,
                    const float* CODE2, float offset, const float* LUT, uint16_t* Y, const void* R,
@@ -216,32 +227,20 @@ void orc_gemv_emul(const void* X, int dt, const uint8_t* W, const uint8_t* A8, c
   float lutv[16];
   for (int i = 0; i < 16; ++i) lutv[i] = rnd(LUT[i], DT_F16); /* fp16 codes for both types */
   float* xv = malloc(sizeof(float) * (size_t)K);
-  int xe[4] = {0, 0, 0, 0};
+  int xe = 0;
   for (int k = 0; k < K; ++k) xv[k] = ld(X, (size_t)k, dt);
   if (dt == DT_BF16) {
-    /* per K-slice: m = max|x| over the slice's dwords, e = ilogb(m) - 14,
-     * x <- fp16(x * 2^-e) (exact for bf16 values), partial sums * 2^e */
-    for (int ks = 0; ks < KS; ++ks) {
-      float m = 0.0f;
-      for (int l = 0; l < 64; ++l)
-        for (int j = 0; j < J; ++j) {
-          const int d = l + 64 * (j * KS + ks);
-          if (d >= KD) continue;
-          for (int i = 0; i < 8; ++i) m = fmaxf(m, fabsf(xv[8 * d + i]));
-        }
-      int e = 0;
-      if (m > 0.0f && m <= 3.402823466e38f) {
-        frexpf(m, &e);
-        e -= 15;
-      }
-      xe[ks] = e;
-      for (int l = 0; l < 64; ++l)
-        for (int j = 0; j < J; ++j) {
-          const int d = l + 64 * (j * KS + ks);
-          if (d >= KD) continue;
-          for (int i = 0; i < 8; ++i) xv[8 * d + i] = orc_f16_to_f32(orc_f32_to_f16(ldexpf(xv[8 * d + i], -e)));
-        }
+    /* m = max|x| over the whole vector, e = ilogb(m) - 14, x <- fp16(x * 2^-e)
+     * (exact for bf16 values in fp16's normal range), slice sums * 2^e */
+    float m = 0.0f;
+    for (int k = 0; k < K; ++k) m = fmaxf(m, fabsf(xv[k]));
+    int e = 0;
+    if (m > 0.0f && m <= 3.402823466e38f) {
+      frexpf(m, &e);
+      e -= 15;
     }
+    xe = e;
+    for (int k = 0; k < K; ++k) xv[k] = orc_f16_to_f32(orc_f32_to_f16(ldexpf(xv[k], -e)));
   }
 #pragma omp parallel for schedule(static)
   for (int m = 0; m < M; ++m) {
@@ -271,7 +270,7 @@ void orc_gemv_emul(const void* X, int dt, const uint8_t* W, const uint8_t* A8, c
         }
         lanes[l] = acc;
       }
-      const float ws = ldexpf(butterfly64(lanes), xe[ks]);
+      const float ws = ldexpf(butterfly64_up(lanes), xe);
       total = ks == 0 ? ws : total + ws;
     }
     const float r = epi ? ld(R, (size_t)m, dt) : 0.0f;
