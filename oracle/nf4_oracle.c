@@ -427,10 +427,11 @@ void orc_attn_emul(const uint16_t* Q, const uint16_t* KC, const uint16_t* VC, lo
   const int groups = nh / nkv;
   long long L = pos + 1;
   if (L > max_len) L = max_len;
-  float* pm = malloc(sizeof(float) * (size_t)nchunk);
-  float* pl = malloc(sizeof(float) * (size_t)nchunk);
-  float* pacc = malloc(sizeof(float) * (size_t)nchunk * 128);
+#pragma omp parallel for schedule(static)
   for (int qh = 0; qh < nh; ++qh) {
+    float* pm = malloc(sizeof(float) * (size_t)nchunk);
+    float* pl = malloc(sizeof(float) * (size_t)nchunk);
+    float* pacc = malloc(sizeof(float) * (size_t)nchunk * 128);
     const int kh = qh / groups;
     float q[128];
     for (int d = 0; d < 128; ++d) q[d] = ld(Q, (size_t)qh * 128 + d, dt) * scale;
@@ -476,10 +477,10 @@ void orc_attn_emul(const uint16_t* Q, const uint16_t* KC, const uint16_t* VC, lo
       }
       Y[(size_t)qh * 128 + d] = st16(num / den, dt);
     }
+    free(pm);
+    free(pl);
+    free(pacc);
   }
-  free(pm);
-  free(pl);
-  free(pacc);
 }
 
 /* ---------------------------------------------------- decode-loop helpers */

@@ -1,0 +1,428 @@
+"""Greedy decode of a synthetic Dual-AR (slow/fast) transformer on the NF4 kernels.
+
+The reference decodes one audio frame per step (app/engine/graphs.py:76-132,
+streamgen.py:654-715): the slow transformer (36 layers at d=2560, GQA
+32 q / 8 kv heads of 128, FFN 9728) takes the frame's summed token
+embeddings at the next position and yields the semantic token from its head;
+its final hidden state, projected to the fast width, primes the fast
+transformer at fast position 0 (every fast layer but the last in full, the
+last for its KV entries only, graphs.py:76-89); then the fast transformer
+runs once per remaining codebook, each step feeding the embedding of the
+token it just chose. This module builds that model with seeded random NF4
+weights (bitsandbytes layout, double-quant scales) and decodes it greedily -
+argmax in place of the sampler, as the benchmark specifies - so the whole
+frame is a fixed function of the weights and the starting state.
+
+Every transformer block goes through `fusedlayer.decode_block` (the drop-in
+for the reference's fused decode block) and every linear through
+`nf4gemv.matmul`; the whole frame is captured once as a HIP graph and
+replayed per step, with the position, token and history counters kept on
+the device so a replay needs nothing from the host.
+
+Weights are generated on the device by `ttsp_synth_fill` (a counter-based
+hash of (seed, index)), so a CPU restatement can regenerate the identical
+bytes from `weight_specs()` without copying 2.5 GB.
+"""
+
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass, field
+
+from ttspipe_amd import _lib
+
+#: absmax of the double-quant scales: s_b = code2[a8[b]] * absmax2 + offset
+#: with code2 in [-1, 1], so s_b stays in [offset - absmax2, offset + absmax2].
+SCALE_OFFSET = 0.02
+ABSMAX2_LO, ABSMAX2_HI = 0.004, 0.008
+
+
+@dataclass(frozen=True)
+class DualARConfig:
+    """Shapes of the synthetic frame model (defaults: the benchmark's)."""
+
+    dim: int = 2560
+    n_layer: int = 36
+    n_head: int = 32
+    n_local_heads: int = 8
+    intermediate_size: int = 9728
+    vocab_size: int = 4096
+    fast_dim: int = 1024
+    fast_n_layer: int = 4
+    fast_n_head: int = 8
+    fast_n_local_heads: int = 2
+    fast_intermediate_size: int = 3072
+    num_codebooks: int = 10
+    codebook_size: int = 4096
+    head_dim: int = 128
+    norm_eps: float = 1e-6
+    rope_base: float = 1e6
+    max_seq_len: int = 2304
+    prefill_len: int = 2048
+    qk_norm: bool = True
+    seed: int = 20260
+    fast_max_len: int = 16
+
+    @property
+    def n_tokens(self) -> int:
+        """Tokens per frame: the semantic token plus one per codebook."""
+        return 1 + self.num_codebooks
+
+
+SMALL = DualARConfig(dim=512, n_layer=3, n_head=4, n_local_heads=2, intermediate_size=1024,
+                     vocab_size=512, fast_dim=256, fast_n_layer=2, fast_n_head=2, fast_n_local_heads=1,
+                     fast_intermediate_size=512, num_codebooks=4, codebook_size=512, max_seq_len=320,
+                     prefill_len=64, seed=7)
+
+
+@dataclass
+class TensorSpec:
+    """One synthetic tensor: `ttsp_synth_fill(n, seed, kind, scale, offset)`.
+
+    kind 0: uint8 bytes; 1 / 3: u * scale + offset (u uniform in [-1, 1)) as
+    bf16 / fp32."""
+
+    name: str
+    n: int
+    seed: int
+    kind: int
+    scale: float = 1.0
+    offset: float = 0.0
+
+
+@dataclass
+class LinearSpec:
+    """An NF4 linear [out, in] with double-quant scales (blocksize 64 / 256)."""
+
+    name: str
+    out_features: int
+    in_features: int
+    packed: TensorSpec = field(init=False)
+    a8: TensorSpec = field(init=False)
+    absmax2: TensorSpec = field(init=False)
+    seed: int = 0
+    offset: float = SCALE_OFFSET
+
+    def __post_init__(self):
+        n = self.out_features * self.in_features
+        nblk = n // 64
+        mid, half = (ABSMAX2_LO + ABSMAX2_HI) / 2, (ABSMAX2_HI - ABSMAX2_LO) / 2
+        self.packed = TensorSpec(self.name + ".packed", n // 2, self.seed, 0)
+        self.a8 = TensorSpec(self.name + ".a8", nblk, self.seed + 1, 0)
+        self.absmax2 = TensorSpec(self.name + ".absmax2", -(-nblk // 256), self.seed + 2, 3, half, mid)
+
+
+def _block_specs(prefix, dim, n_head, n_local, inter, head_dim, qk_norm, seed):
+    total = (n_head + 2 * n_local) * head_dim
+    lin = [LinearSpec(f"{prefix}.wqkv", total, dim, seed=seed + 10),
+           LinearSpec(f"{prefix}.wo", dim, n_head * head_dim, seed=seed + 20),
+           LinearSpec(f"{prefix}.w1", inter, dim, seed=seed + 30),
+           LinearSpec(f"{prefix}.w3", inter, dim, seed=seed + 40),
+           LinearSpec(f"{prefix}.w2", dim, inter, seed=seed + 50)]
+    vec = [TensorSpec(f"{prefix}.attention_norm", dim, seed + 60, 1, 0.1, 1.0),
+           TensorSpec(f"{prefix}.ffn_norm", dim, seed + 61, 1, 0.1, 1.0)]
+    if qk_norm:
+        vec += [TensorSpec(f"{prefix}.q_norm", head_dim, seed + 62, 1, 0.1, 1.0),
+                TensorSpec(f"{prefix}.k_norm", head_dim, seed + 63, 1, 0.1, 1.0)]
+    return lin, vec
+
+
+def weight_specs(cfg: DualARConfig):
+    """Every synthetic tensor of the model: (linears, vectors, caches)."""
+    s = cfg.seed * 100_000
+    linears, vectors = [], []
+    for i in range(cfg.n_layer):
+        lin, vec = _block_specs(f"layers.{i}", cfg.dim, cfg.n_head, cfg.n_local_heads, cfg.intermediate_size,
+                                cfg.head_dim, cfg.qk_norm, s + 1000 * i)
+        linears += lin
+        vectors += vec
+    for i in range(cfg.fast_n_layer):
+        lin, vec = _block_specs(f"fast_layers.{i}", cfg.fast_dim, cfg.fast_n_head, cfg.fast_n_local_heads,
+                                cfg.fast_intermediate_size, cfg.head_dim, cfg.qk_norm, s + 50_000 + 1000 * i)
+        linears += lin
+        vectors += vec
+    linears += [LinearSpec("output", cfg.vocab_size, cfg.dim, seed=s + 90_000),
+                LinearSpec("fast_project_in", cfg.fast_dim, cfg.dim, seed=s + 90_100),
+                LinearSpec("fast_output", cfg.codebook_size, cfg.fast_dim, seed=s + 90_200)]
+    vectors += [TensorSpec("norm", cfg.dim, s + 90_300, 1, 0.1, 1.0),
+                TensorSpec("fast_norm", cfg.fast_dim, s + 90_301, 1, 0.1, 1.0),
+                # semantic table then one table per codebook, each [4096, dim]
+                TensorSpec("embeddings", cfg.n_tokens * cfg.vocab_size * cfg.dim, s + 90_400, 1, 1.0, 0.0),
+                TensorSpec("fast_embeddings", cfg.codebook_size * cfg.fast_dim, s + 90_500, 1, 1.0, 0.0)]
+    kv = cfg.n_local_heads * cfg.max_seq_len * cfg.head_dim
+    caches = []
+    for i in range(cfg.n_layer):
+        caches += [TensorSpec(f"layers.{i}.k_cache", kv, s + 95_000 + 2 * i, 1, 1.0, 0.0),
+                   TensorSpec(f"layers.{i}.v_cache", kv, s + 95_001 + 2 * i, 1, 1.0, 0.0)]
+    return linears, vectors, caches
+
+
+def first_tokens(cfg: DualARConfig):
+    """The frame fed at position `prefill_len` (a fixed, in-range token column)."""
+    return [(97 * (c + 1)) % (cfg.vocab_size if c == 0 else cfg.codebook_size) for c in range(cfg.n_tokens)]
+
+
+class SyntheticDualAR:
+    """The frame model on the GPU, weights materialised from `weight_specs`."""
+
+    def __init__(self, cfg: DualARConfig = DualARConfig(), device: str = "cuda"):
+        import torch
+
+        from ttspipe_amd import fusedlayer, fusedops, nf4gemv
+        from ttspipe_amd.llama import BaseModelArgs, KVCache, TransformerBlock, precompute_freqs_cis
+        from ttspipe_amd.quant import NF4_CODE, QuantState, create_dynamic_map
+
+        if not (nf4gemv.install() and fusedops.install()):
+            raise RuntimeError("the NF4 kernels are not available (no GPU or library not built)")
+        fusedlayer.install()
+        self.cfg = cfg
+        self.device = torch.device(device)
+        self.dtype = torch.bfloat16
+        self._lib = _lib.load()
+        dev, bf = self.device, self.dtype
+        linears, vectors, caches = weight_specs(cfg)
+        self.specs = {"linears": linears, "vectors": vectors, "caches": caches}
+        code = torch.tensor(NF4_CODE, dtype=torch.float32, device=dev)
+        code2 = create_dynamic_map().to(dev)
+
+        def fill(spec: TensorSpec):
+            dt = {0: torch.uint8, 1: bf, 3: torch.float32}[spec.kind]
+            t = torch.empty(spec.n, dtype=dt, device=dev)
+            rc = self._lib.ttsp_synth_fill(t.data_ptr(), spec.n, spec.seed, spec.kind, spec.scale, spec.offset,
+                                           _lib.stream())
+            _lib.check(rc, "ttsp_synth_fill")
+            return t
+
+        self.tensors = {}
+        for spec in vectors + caches:
+            self.tensors[spec.name] = fill(spec)
+        self.quant = {}
+        for spec in linears:
+            packed, a8, amax2 = fill(spec.packed), fill(spec.a8), fill(spec.absmax2)
+            state2 = QuantState(absmax=amax2, shape=(a8.numel(),), code=code2, blocksize=256,
+                                quant_type="dynamic", dtype=torch.float32)
+            state = QuantState(absmax=a8, shape=(spec.out_features, spec.in_features), code=code, blocksize=64,
+                               dtype=bf, offset=torch.tensor(spec.offset, dtype=torch.float32, device=dev),
+                               state2=state2)
+            self.quant[spec.name] = (packed.view(-1, 1), state)
+
+        def make_linear(name):
+            from ttspipe_amd.quant import Linear4bit
+
+            packed, state = self.quant[name]
+            out_f, in_f = state.shape
+            lin = Linear4bit(in_f, out_f, bias=False, compute_dtype=bf, compress_statistics=True, blocksize=64)
+            lin.set_quantized(packed, state)
+            if not nf4gemv.prepare(lin):
+                raise RuntimeError(f"the NF4 kernel declines {name}")
+            return lin
+
+        def make_blocks(prefix, n, dim, n_head, n_local, inter, max_len, k_caches):
+            args = BaseModelArgs(dim=dim, n_head=n_head, n_local_heads=n_local, head_dim=cfg.head_dim,
+                                 intermediate_size=inter, attention_qk_norm=cfg.qk_norm, norm_eps=cfg.norm_eps,
+                                 rope_base=cfg.rope_base, max_seq_len=max_len)
+            blocks = []
+            for i in range(n):
+                with torch.device("meta"):
+                    blk = TransformerBlock(args, dtype=bf)
+                p = f"{prefix}.{i}"
+                a, ff = blk.attention, blk.feed_forward
+                a.wqkv, a.wo = make_linear(f"{p}.wqkv"), make_linear(f"{p}.wo")
+                ff.w1, ff.w3, ff.w2 = make_linear(f"{p}.w1"), make_linear(f"{p}.w3"), make_linear(f"{p}.w2")
+                blk.attention_norm.weight = torch.nn.Parameter(self.tensors[f"{p}.attention_norm"], requires_grad=False)
+                blk.ffn_norm.weight = torch.nn.Parameter(self.tensors[f"{p}.ffn_norm"], requires_grad=False)
+                if cfg.qk_norm:
+                    a.q_norm.weight = torch.nn.Parameter(self.tensors[f"{p}.q_norm"], requires_grad=False)
+                    a.k_norm.weight = torch.nn.Parameter(self.tensors[f"{p}.k_norm"], requires_grad=False)
+                cache = KVCache.__new__(KVCache)
+                torch.nn.Module.__init__(cache)
+                if k_caches:
+                    kc = self.tensors[f"{p}.k_cache"].view(1, n_local, max_len, cfg.head_dim)
+                    vc = self.tensors[f"{p}.v_cache"].view(1, n_local, max_len, cfg.head_dim)
+                else:
+                    kc = torch.zeros(1, n_local, max_len, cfg.head_dim, dtype=bf, device=dev)
+                    vc = torch.zeros_like(kc)
+                cache.register_buffer("k_cache", kc)
+                cache.register_buffer("v_cache", vc)
+                a.kv_cache = cache
+                blocks.append(blk)
+            return blocks
+
+        self.layers = make_blocks("layers", cfg.n_layer, cfg.dim, cfg.n_head, cfg.n_local_heads,
+                                  cfg.intermediate_size, cfg.max_seq_len, True)
+        self.fast_layers = make_blocks("fast_layers", cfg.fast_n_layer, cfg.fast_dim, cfg.fast_n_head,
+                                       cfg.fast_n_local_heads, cfg.fast_intermediate_size, cfg.fast_max_len, False)
+        self.output = make_linear("output")
+        self.fast_project_in = make_linear("fast_project_in")
+        self.fast_output = make_linear("fast_output")
+
+        self.freqs = precompute_freqs_cis(cfg.max_seq_len, cfg.head_dim, cfg.rope_base, dtype=bf).to(dev)
+        self.fast_freqs = precompute_freqs_cis(cfg.fast_max_len, cfg.head_dim, cfg.rope_base, dtype=bf).to(dev)
+        self.mask = torch.ones(1, 1, 1, cfg.max_seq_len, dtype=torch.bool, device=dev)
+        self.fast_mask = torch.ones(1, 1, 1, cfg.fast_max_len, dtype=torch.bool, device=dev)
+
+        # device-side state of the decode loop
+        self.pos = torch.zeros(1, dtype=torch.long, device=dev)
+        self.tokens = torch.zeros(cfg.n_tokens, dtype=torch.int32, device=dev)
+        self.step_index = torch.zeros(1, dtype=torch.long, device=dev)
+        self.history = None
+        self.fast_pos = [torch.full((1,), i, dtype=torch.long, device=dev) for i in range(cfg.num_codebooks)]
+        self.freq_row = torch.empty(1, cfg.head_dim // 2, 2, dtype=bf, device=dev)
+
+        x1 = torch.empty(1, 1, cfg.dim, dtype=bf, device=dev)
+        f1 = torch.empty(1, 1, cfg.fast_dim, dtype=bf, device=dev)
+        nchunk = -(-cfg.max_seq_len // fusedlayer.CHUNK)
+        fchunk = -(-cfg.fast_max_len // fusedlayer.CHUNK)
+        self.ws = [fusedlayer.make_workspace(self.layers[0], x1, nchunk, with_out=True) for _ in range(2)]
+        self.fws = [fusedlayer.make_workspace(self.fast_layers[0], f1, fchunk, with_out=True) for _ in range(2)]
+        self.x = x1
+        self.hn = torch.empty(1, 1, cfg.dim, dtype=bf, device=dev)
+        self.logits = torch.empty(1, cfg.vocab_size, dtype=bf, device=dev)
+        self.fast_h = torch.empty(1, 1, cfg.fast_dim, dtype=bf, device=dev)
+        self.fast_hn = torch.empty(1, 1, cfg.fast_dim, dtype=bf, device=dev)
+        self.fast_logits = torch.empty(1, cfg.codebook_size, dtype=bf, device=dev)
+        self.graph = None
+        self.reset()
+
+    # ------------------------------------------------------------------ state
+
+    def reset(self, n_steps: int = 256) -> None:
+        """Position `prefill_len`, the first frame's tokens, an empty history."""
+        import torch
+
+        self.pos.fill_(self.cfg.prefill_len)
+        self.tokens.copy_(torch.tensor(first_tokens(self.cfg), dtype=torch.int32))
+        self.step_index.zero_()
+        if self.history is None or self.history.shape[0] < n_steps:
+            self.history = torch.zeros(n_steps, self.cfg.n_tokens, dtype=torch.int32, device=self.device)
+        else:
+            self.history.zero_()
+
+    # ------------------------------------------------------------------- step
+
+    def _check(self, rc, what):
+        _lib.check(rc, what)
+
+    def _fast_kv_only(self, blk, x, pos):
+        """The last fast layer at the prime position: norm, wqkv, KV write."""
+        from ttspipe_amd import fusedops, nf4gemv
+
+        a = blk.attention
+        ws = self.fws[0]
+        xn = fusedops.rms_norm(x, blk.attention_norm.weight, blk.attention_norm.eps, out=ws["xn"])
+        qkv = nf4gemv.matmul(a.wqkv, xn, out=ws["qkv"])
+        qn = a.q_norm if self.cfg.qk_norm else None
+        kn = a.k_norm if self.cfg.qk_norm else None
+        rc = self._lib.ttsp_qk_rope_kv(
+            qkv.data_ptr(), _lib.ptr(None if qn is None else qn.weight), _lib.ptr(None if kn is None else kn.weight),
+            float(self.cfg.norm_eps), self.fast_freqs[pos.item() if False else 0].data_ptr(), _lib.DT_BF16,
+            pos.data_ptr(), ws["q"].data_ptr(), a.kv_cache.k_cache.data_ptr(), a.kv_cache.v_cache.data_ptr(),
+            a.n_head, a.n_local_heads, a.kv_cache.k_cache.shape[2], _lib.DT_BF16, _lib.stream())
+        self._check(rc, "ttsp_qk_rope_kv")
+
+    def _run_blocks(self, blocks, workspaces, x, freqs, mask, pos):
+        from ttspipe_amd import fusedlayer
+
+        for i, blk in enumerate(blocks):
+            y = fusedlayer.decode_block(blk, x, freqs, mask, pos, workspace=workspaces[i % 2])
+            if y is None:
+                raise RuntimeError("decode_block declined a layer of the synthetic model")
+            x = y
+        return x
+
+    def step(self) -> None:
+        """One frame: tokens (device) at position pos -> next frame's tokens; pos += 1."""
+        import torch
+
+        from ttspipe_amd import fusedops, nf4gemv
+
+        cfg, lib, st = self.cfg, self._lib, _lib.stream()
+        # slow transformer
+        rc = lib.ttsp_embed_sum(self.tensors["embeddings"].data_ptr(), self.tokens.data_ptr(), cfg.n_tokens,
+                                cfg.vocab_size, cfg.dim, self.x.data_ptr(), _lib.DT_BF16, st)
+        self._check(rc, "ttsp_embed_sum")
+        torch.index_select(self.freqs, 0, self.pos, out=self.freq_row)
+        h = self._run_blocks(self.layers, self.ws, self.x, self.freq_row, self.mask, self.pos)
+        hn = fusedops.rms_norm(h.view(1, 1, -1), self.tensors["norm"], cfg.norm_eps, out=self.hn)
+        nf4gemv.matmul(self.output, hn, out=self.logits)
+        rc = lib.ttsp_argmax(self.logits.data_ptr(), cfg.vocab_size, _lib.DT_BF16, self.tokens.data_ptr(), st)
+        self._check(rc, "ttsp_argmax")
+        # fast transformer: prime at fast position 0 with the projected hidden state
+        fx = nf4gemv.matmul(self.fast_project_in, hn, out=self.fast_h)
+        p0 = self.fast_pos[0]
+        x = self._run_blocks(self.fast_layers[:-1], self.fws, fx, self.fast_freqs[0], self.fast_mask, p0)
+        self._fast_kv_only(self.fast_layers[-1], x, p0)
+        # codebook 0 is the semantic token (clamped into the codebook); its
+        # embedding starts the fast steps
+        torch.clamp(self.tokens[:1], 0, cfg.codebook_size - 1, out=self.tokens[1:2])
+        for i in range(1, cfg.num_codebooks):
+            rc = lib.ttsp_embed_sum(self.tensors["fast_embeddings"].data_ptr(), self.tokens[i:].data_ptr(), 1,
+                                    cfg.codebook_size, cfg.fast_dim, self.fast_h.data_ptr(), _lib.DT_BF16, st)
+            self._check(rc, "ttsp_embed_sum")
+            x = self._run_blocks(self.fast_layers, self.fws, self.fast_h, self.fast_freqs[i], self.fast_mask,
+                                 self.fast_pos[i])
+            fhn = fusedops.rms_norm(x.view(1, 1, -1), self.tensors["fast_norm"], cfg.norm_eps, out=self.fast_hn)
+            nf4gemv.matmul(self.fast_output, fhn, out=self.fast_logits)
+            rc = lib.ttsp_argmax(self.fast_logits.data_ptr(), cfg.codebook_size, _lib.DT_BF16,
+                                 self.tokens[i + 1:].data_ptr(), st)
+            self._check(rc, "ttsp_argmax")
+        # bookkeeping on the device
+        self.history.index_copy_(0, self.step_index, self.tokens.view(1, -1))
+        self.step_index.add_(1)
+        self.pos.add_(1)
+
+    def capture(self) -> None:
+        """Record one step as a HIP graph (after a warm-up step outside capture)."""
+        import torch
+
+        self.step()
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            self.step()
+        self.graph = g
+
+    def decode(self, n_steps: int, graphed: bool = True):
+        """Reset, then n_steps frames; returns the [n_steps, n_tokens] token history (host)."""
+        import torch
+
+        if graphed and self.graph is None:
+            self.capture()
+        self.reset(n_steps)
+        for _ in range(n_steps):
+            if graphed:
+                self.graph.replay()
+            else:
+                self.step()
+        torch.cuda.synchronize()
+        return self.history[:n_steps].cpu().numpy()
+
+
+def benchmark(n_steps: int = 256, warmup: int = 8, cfg: DualARConfig = DualARConfig()) -> dict:
+    """ms per frame over `n_steps` graph-replayed greedy steps (one MI355X)."""
+    import torch
+
+    model = SyntheticDualAR(cfg)
+    model.capture()
+    model.reset(max(n_steps, warmup))
+    for _ in range(warmup):
+        model.graph.replay()
+    torch.cuda.synchronize()
+    model.reset(n_steps)
+    stream = torch.cuda.current_stream()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record(stream)
+    for _ in range(n_steps):
+        model.graph.replay()
+    end.record(stream)
+    end.synchronize()
+    ms = start.elapsed_time(end) / n_steps
+    hist = model.history[:n_steps].cpu().numpy()
+    weight_bytes = sum(s.out_features * s.in_features // 2 + s.a8.n + 4 * s.absmax2.n
+                       for s in model.specs["linears"])
+    return {"ms_per_step": round(ms, 4), "steps": n_steps, "weight_bytes": weight_bytes,
+            "tokens_first_step": hist[0].tolist(), "tokens_last_step": hist[-1].tolist(),
+            "config": f"slow {cfg.n_layer}x d{cfg.dim} ({cfg.n_head}q/{cfg.n_local_heads}kv x{cfg.head_dim}, "
+                      f"FFN {cfg.intermediate_size}), fast {cfg.fast_n_layer}x d{cfg.fast_dim} "
+                      f"({cfg.fast_n_head}q/{cfg.fast_n_local_heads}kv, FFN {cfg.fast_intermediate_size}), "
+                      f"{cfg.num_codebooks} codebooks of {cfg.codebook_size}, KV from {cfg.prefill_len}"}
