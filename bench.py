@@ -32,6 +32,10 @@ sys.path.insert(0, str(ROOT))
 
 HBM_PEAK_GBS = 8000.0
 MALL_BYTES = 256 * 2**20
+#: HBM bytes one gate-shape GEMV launch moves, from rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE
+#: per dispatch (bench.py --only kernel --direct), each scaled by the same counter on a plain
+#: 64 MiB copy (FETCH_SIZE x 1.9992, WRITE_SIZE x 1.0). Re-measure when the kernel changes.
+GEMV_TRAFFIC_BYTES = 13_217_821
 
 # (name, out_features, in_features) of one decoder layer's linears
 LAYER = [("q", 4096, 2560), ("k", 1024, 2560), ("v", 1024, 2560), ("o", 2560, 4096),
@@ -138,8 +142,11 @@ def bench_layer(steps: int, warmup: int):
             "warmup": reps_w * ncopy}
 
 
-def bench_kernel(M, K, nested, dtype_name, launches_per_copy=1, min_bytes=2 * MALL_BYTES):
-    """One GEMV shape alone: average seconds per launch over > 512 MB of distinct weights."""
+def bench_kernel(M, K, nested, dtype_name, launches_per_copy=1, min_bytes=2 * MALL_BYTES, direct=False):
+    """One GEMV shape alone: average seconds per launch over > 512 MB of distinct weights.
+
+    direct=True launches each copy once without a graph (for counter runs,
+    where every dispatch is profiled on its own)."""
     import torch
 
     from ttspipe_amd import _lib
@@ -162,15 +169,41 @@ def bench_kernel(M, K, nested, dtype_name, launches_per_copy=1, min_bytes=2 * MA
 
     body()
     torch.cuda.synchronize()
-    graph = capture(body)
     stream = torch.cuda.current_stream()
-    time_graph(graph, 3, stream)
-    reps = max(3, 2000 // ncopy)
-    sec = time_graph(graph, reps, stream) / ncopy
+    if direct:
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record(stream)
+        body()
+        end.record(stream)
+        end.synchronize()
+        reps, sec = 1, start.elapsed_time(end) / 1e3 / ncopy
+    else:
+        graph = capture(body)
+        time_graph(graph, 3, stream)
+        reps = max(3, 2000 // ncopy)
+        sec = time_graph(graph, reps, stream) / ncopy
     nbytes = nf4_bytes(M, K, nested, 2)
     del lins
     return {"M": M, "K": K, "nested": nested, "dtype": dtype_name, "sec": sec, "bytes": nbytes,
             "gbs": nbytes / sec / 1e9, "launches": reps * ncopy, "copies": ncopy}
+
+
+def bench_copy(nbytes: int = 64 * 2**20, launches: int = 8):
+    """A plain device copy of known size (reads and writes `nbytes` each), the
+    calibration kernel for the HBM byte counters."""
+    import torch
+
+    src = torch.randint(0, 255, (launches, nbytes), dtype=torch.uint8, device="cuda")
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for i in range(launches):
+        dst[i].copy_(src[i])
+    end.record()
+    end.synchronize()
+    sec = start.elapsed_time(end) / 1e3 / launches
+    return {"bytes_read": nbytes, "bytes_written": nbytes, "sec": sec, "gbs_rw": 2 * nbytes / sec / 1e9}
 
 
 def cpu_baseline(seconds: float = 10.0):
@@ -190,8 +223,11 @@ def main() -> int:
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--skip-cpu", action="store_true")
     ap.add_argument("--skip-decode", action="store_true")
-    ap.add_argument("--only", choices=["layer", "kernel", "c1"], default=None,
+    ap.add_argument("--only", choices=["layer", "kernel", "c1", "copy", "decode"], default=None,
                     help="run one GPU measurement only (for profiling runs)")
+    ap.add_argument("--decode-steps", type=int, default=256, help="greedy frames the decode benchmark times")
+    ap.add_argument("--direct", action="store_true",
+                    help="with --only kernel/c1: one launch per weight copy, no graph (counter runs)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: this path has no multi-GPU mode (see DESIGN.md on sharding)",
@@ -206,21 +242,21 @@ def main() -> int:
         layer = bench_layer(args.steps, args.warmup)
         out["layer"] = layer
     if args.only in (None, "kernel"):
-        out["kernel"] = bench_kernel(9728, 2560, True, "bf16")
+        out["kernel"] = bench_kernel(9728, 2560, True, "bf16", direct=args.direct)
     if args.only in (None, "c1"):
-        out["c1"] = bench_kernel(9728, 2560, False, "fp16")
+        out["c1"] = bench_kernel(9728, 2560, False, "fp16", direct=args.direct)
+    if args.only == "copy":
+        out["copy"] = bench_copy()
+    decode = None
+    if args.only in (None, "decode") and not args.skip_decode:
+        from ttspipe_amd import dualar
+
+        decode = dualar.benchmark(n_steps=args.decode_steps)
+        decode["pct_of_hbm_peak"] = round(100 * decode["achieved_gbs"] / HBM_PEAK_GBS, 1)
+        out["decode"] = decode
     if args.only is not None:
         print(json.dumps(out))
         return 0
-
-    decode = None
-    if not args.skip_decode:
-        try:
-            from ttspipe_amd import dualar
-
-            decode = dualar.benchmark()
-        except Exception as exc:  # noqa: BLE001
-            decode = {"error": str(exc)}
     cpu = None if args.skip_cpu else cpu_baseline(args.cpu_seconds)
 
     layer, kern, c1 = out["layer"], out["kernel"], out["c1"]
@@ -253,7 +289,7 @@ def main() -> int:
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(kern["gbs"] / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            "traffic": GEMV_TRAFFIC_BYTES,
             "avg_launch_us": round(kern["sec"] * 1e6, 3),
             "bytes_per_launch": kern["bytes"],
         },

@@ -1,0 +1,154 @@
+"""The C-ABI boundary and the host-side logic, on the CPU (no GPU calls).
+
+* every function `include/ttsp_hip.h` declares is exported by the built
+  library and bound by `_lib.SIGNATURES` with the header's arity;
+* host-only entry points (`ttsp_gemv_shape`, argument validation that
+  returns before any launch) behave as documented;
+* the Python drop-ins decline without a GPU instead of raising (the
+  reference's contract, app/engine/nvrtc.py:26-28);
+* byte accounting used by the benchmark matches the closed forms.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import re
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+ROOT = Path(__file__).resolve().parent.parent
+HEADER = ROOT / "include" / "ttsp_hip.h"
+
+
+def _declared():
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    decls = {}
+    for m in re.finditer(r"\bint\s+(ttsp_\w+)\s*\(([^)]*)\)\s*;", text):
+        args = m.group(2).strip()
+        n = 0 if args in ("", "void") else args.count(",") + 1
+        decls[m.group(1)] = n
+    return decls
+
+
+def test_header_declares_the_entry_points():
+    decls = _declared()
+    for name in ("ttsp_nf4_gemm", "ttsp_nf4_dequant", "ttsp_rms_norm", "ttsp_rope", "ttsp_qk_rope_kv",
+                 "ttsp_attn_decode", "ttsp_gemv_shape"):
+        assert name in decls
+
+
+def test_library_exports_every_declared_symbol():
+    from ttspipe_amd import _lib
+
+    lib = ctypes.CDLL(str(_lib.LIB_PATH))
+    for name in _declared():
+        assert hasattr(lib, name), f"{name} declared in the header but not exported"
+
+
+def test_bindings_match_the_header():
+    from ttspipe_amd import _lib
+
+    decls = _declared()
+    assert set(_lib.SIGNATURES) == set(decls)
+    for name, n in decls.items():
+        assert len(_lib.SIGNATURES[name]) == n, name
+
+
+def _shape(M, K):
+    from ttspipe_amd import _lib
+
+    J, KS, RPW = ctypes.c_int(), ctypes.c_int(), ctypes.c_int()
+    rc = _lib.load().ttsp_gemv_shape(M, K, ctypes.byref(J), ctypes.byref(KS), ctypes.byref(RPW))
+    return rc, J.value, KS.value, RPW.value
+
+
+@pytest.mark.parametrize("M,K", [(9728, 2560), (2560, 9728), (6144, 2560), (2560, 4096), (1024, 2560),
+                                 (1536, 1024), (3072, 1024), (1024, 3072), (4096, 1024), (64, 128)])
+def test_gemv_shape_covers_every_row_and_column(M, K):
+    rc, J, KS, RPW = _shape(M, K)
+    assert rc == 0
+    assert KS in (1, 2, 4, 8) and 1 <= J <= 8 and RPW >= 1
+    assert J * KS * 64 >= K // 8 and (J - 1) * KS * 64 < K // 8  # no wholly idle chunk slot
+
+
+def test_invalid_arguments_are_rejected_before_any_launch():
+    from ttspipe_amd import _lib
+
+    lib = _lib.load()
+    # N == 0, M == 0, blocksize not a power of two, K not a multiple of 128: hipErrorInvalidValue (1)
+    assert lib.ttsp_nf4_gemm(8, 1, 8, None, 8, None, 0.0, 8, 8, None, 0, 64, 128, 0, 64, 256, None) == 1
+    assert lib.ttsp_nf4_gemm(8, 1, 8, None, 8, None, 0.0, 8, 8, None, 0, 0, 128, 1, 64, 256, None) == 1
+    assert lib.ttsp_nf4_gemm(8, 1, 8, None, 8, None, 0.0, 8, 8, None, 0, 64, 128, 1, 96, 256, None) == 1
+    assert lib.ttsp_nf4_gemm(8, 1, 8, None, 8, None, 0.0, 8, 8, None, 0, 64, 192, 1, 64, 256, None) == 1
+    # an epilogue without its operand
+    assert lib.ttsp_nf4_gemm(8, 1, 8, None, 8, None, 0.0, 8, 8, None, 1, 64, 128, 1, 64, 256, None) == 1
+    assert lib.ttsp_nf4_dequant(8, None, 8, None, 0.0, 8, 8, 1, -1, 64, 256, None) == 1
+    assert lib.ttsp_attn_decode(8, 8, 8, 8, 8, 8, 8, 8, 32, 7, 64, 1, 0.1, 1, None) == 1  # nh % nkv
+    assert lib.ttsp_attn_chunk() == 64
+
+
+def test_drop_ins_decline_without_a_gpu():
+    import torch
+
+    from ttspipe_amd import _lib, fusedlayer, fusedops, nf4gemv
+    from ttspipe_amd.quant import Linear4bit
+
+    if _lib.gpu_present():
+        pytest.skip("a GPU is present")
+    lin = Linear4bit(128, 64, compress_statistics=False, compute_dtype=torch.float16).load_weight(torch.randn(64, 128))
+    assert nf4gemv.available() is False
+    assert nf4gemv.prepare(lin) is False  # weights on the CPU
+    assert nf4gemv.matmul(lin, torch.randn(1, 128, dtype=torch.float16)) is None
+    assert nf4gemv.install() is False
+    assert fusedops.rms_norm(torch.randn(1, 64, dtype=torch.float16), torch.ones(64, dtype=torch.float16), 1e-6) is None
+    assert fusedops.install() is False and fusedlayer.install() is False
+
+
+def test_benchmark_byte_counts():
+    import bench
+
+    # the reference's CPU-runnable case (C1) and one decoder layer (C2), SURVEY-documented totals
+    assert bench.nf4_bytes(9728, 2560, False) == 14_032_896
+    assert sum(bench.nf4_bytes(M, K, True) for _, M, K in bench.LAYER) == 52_186_204
+
+
+def test_dualar_specs_and_byte_account():
+    from ttspipe_amd import dualar
+
+    cfg = dualar.DualARConfig()
+    linears, vectors, caches = dualar.weight_specs(cfg)
+    names = [s.name for s in linears + vectors + caches]
+    assert len(names) == len(set(names))
+    seeds = [t.seed for s in linears for t in (s.packed, s.a8, s.absmax2)] + [s.seed for s in vectors + caches]
+    assert len(seeds) == len(set(seeds)), "every synthetic tensor needs its own stream"
+    slow = sum(s.packed.n for s in linears if s.name.startswith("layers."))
+    assert slow == 36 * (6144 * 2560 + 2560 * 4096 + 3 * 9728 * 2560) // 2
+    b0, b1 = dualar.step_bytes(cfg, 2048), dualar.step_bytes(cfg, 2049)
+    assert 2.3e9 < b0 < 2.6e9
+    assert b1 - b0 == cfg.n_layer * cfg.n_local_heads * cfg.head_dim * 2 * 2  # one more K and V row
+
+
+def test_dualar_oracle_decode_is_deterministic_and_in_range(orc):
+    """The reduced model through the CPU restatement: same frames twice, ids in range."""
+    from oracle.dualar_oracle import OracleDualAR
+    from ttspipe_amd import dualar
+    from ttspipe_amd.llama import precompute_freqs_cis
+    from ttspipe_amd.quant import create_dynamic_map
+
+    cfg = dualar.SMALL
+    bits = lambda t: t.contiguous().view(__import__("torch").int16).numpy().view(np.uint16).reshape(-1)  # noqa: E731
+
+    def make():
+        return OracleDualAR(cfg, dualar.weight_specs(cfg), lambda M, K: _shape(M, K)[1:3],
+                            code2=create_dynamic_map().numpy(),
+                            freqs_bits=bits(precompute_freqs_cis(cfg.max_seq_len, 128, cfg.rope_base)),
+                            fast_freqs_bits=bits(precompute_freqs_cis(cfg.fast_max_len, 128, cfg.rope_base)))
+
+    a = make().decode(dualar.first_tokens(cfg), cfg.prefill_len, 6)
+    b = make().decode(dualar.first_tokens(cfg), cfg.prefill_len, 6)
+    assert np.array_equal(a, b)
+    assert (a[:, 0] < cfg.vocab_size).all() and (a[:, 1:] < cfg.codebook_size).all() and (a >= 0).all()
+    assert (a[:, 1] == np.minimum(a[:, 0], cfg.codebook_size - 1)).all()

@@ -26,7 +26,6 @@ bytes from `weight_specs()` without copying 2.5 GB.
 
 from __future__ import annotations
 
-import math
 from dataclasses import dataclass, field
 
 from ttspipe_amd import _lib
@@ -303,7 +302,7 @@ class SyntheticDualAR:
     def _check(self, rc, what):
         _lib.check(rc, what)
 
-    def _fast_kv_only(self, blk, x, pos):
+    def _fast_kv_only(self, blk, x, freqs, pos):
         """The last fast layer at the prime position: norm, wqkv, KV write."""
         from ttspipe_amd import fusedops, nf4gemv
 
@@ -315,7 +314,7 @@ class SyntheticDualAR:
         kn = a.k_norm if self.cfg.qk_norm else None
         rc = self._lib.ttsp_qk_rope_kv(
             qkv.data_ptr(), _lib.ptr(None if qn is None else qn.weight), _lib.ptr(None if kn is None else kn.weight),
-            float(self.cfg.norm_eps), self.fast_freqs[pos.item() if False else 0].data_ptr(), _lib.DT_BF16,
+            float(self.cfg.norm_eps), freqs.data_ptr(), _lib.DT_BF16,
             pos.data_ptr(), ws["q"].data_ptr(), a.kv_cache.k_cache.data_ptr(), a.kv_cache.v_cache.data_ptr(),
             a.n_head, a.n_local_heads, a.kv_cache.k_cache.shape[2], _lib.DT_BF16, _lib.stream())
         self._check(rc, "ttsp_qk_rope_kv")
@@ -351,7 +350,7 @@ class SyntheticDualAR:
         fx = nf4gemv.matmul(self.fast_project_in, hn, out=self.fast_h)
         p0 = self.fast_pos[0]
         x = self._run_blocks(self.fast_layers[:-1], self.fws, fx, self.fast_freqs[0], self.fast_mask, p0)
-        self._fast_kv_only(self.fast_layers[-1], x, p0)
+        self._fast_kv_only(self.fast_layers[-1], x, self.fast_freqs[0], p0)
         # codebook 0 is the semantic token (clamped into the codebook); its
         # embedding starts the fast steps
         torch.clamp(self.tokens[:1], 0, cfg.codebook_size - 1, out=self.tokens[1:2])
@@ -398,6 +397,32 @@ class SyntheticDualAR:
         return self.history[:n_steps].cpu().numpy()
 
 
+def linear_bytes(spec: LinearSpec) -> int:
+    """Algorithmic bytes of one batch-1 NF4 matmul: packed codes, uint8 scale
+    indices, fp32 absmax2, the 256-entry code2 and offset, x and y (bf16)."""
+    return (spec.packed.n + spec.a8.n + 4 * spec.absmax2.n + 4 * 257 + 2 * spec.in_features
+            + 2 * spec.out_features)
+
+
+def step_bytes(cfg: DualARConfig, pos: int) -> int:
+    """Algorithmic HBM bytes of one frame at slow position `pos`: every linear
+    each time it is applied, the KV rows attention reads and writes, the
+    embedding rows gathered and the norm weights."""
+    linears, _, _ = weight_specs(cfg)
+    by = {s.name: linear_bytes(s) for s in linears}
+    slow = sum(v for k, v in by.items() if k.startswith("layers."))
+    fast_layer = [sum(v for k, v in by.items() if k.startswith(f"fast_layers.{i}.")) for i in range(cfg.fast_n_layer)]
+    fast_passes = cfg.num_codebooks - 1
+    prime = sum(fast_layer[:-1]) + by[f"fast_layers.{cfg.fast_n_layer - 1}.wqkv"]
+    heads = by["output"] + by["fast_project_in"] + fast_passes * by["fast_output"]
+    kv_row = cfg.head_dim * 2
+    slow_kv = cfg.n_layer * cfg.n_local_heads * kv_row * (2 * (pos + 1) + 2)
+    fast_kv = sum(cfg.fast_n_layer * cfg.fast_n_local_heads * kv_row * (2 * (i + 1) + 2) for i in range(1, cfg.num_codebooks))
+    emb = 2 * (cfg.n_tokens * cfg.dim + fast_passes * cfg.fast_dim)
+    norms = 2 * cfg.dim * (2 * cfg.n_layer + 1) + 2 * cfg.fast_dim * (2 * cfg.fast_n_layer * (fast_passes + 1) + fast_passes)
+    return slow + fast_passes * sum(fast_layer) + prime + heads + slow_kv + fast_kv + emb + norms
+
+
 def benchmark(n_steps: int = 256, warmup: int = 8, cfg: DualARConfig = DualARConfig()) -> dict:
     """ms per frame over `n_steps` graph-replayed greedy steps (one MI355X)."""
     import torch
@@ -418,9 +443,11 @@ def benchmark(n_steps: int = 256, warmup: int = 8, cfg: DualARConfig = DualARCon
     end.synchronize()
     ms = start.elapsed_time(end) / n_steps
     hist = model.history[:n_steps].cpu().numpy()
-    weight_bytes = sum(s.out_features * s.in_features // 2 + s.a8.n + 4 * s.absmax2.n
-                       for s in model.specs["linears"])
-    return {"ms_per_step": round(ms, 4), "steps": n_steps, "weight_bytes": weight_bytes,
+    nbytes = sum(step_bytes(cfg, cfg.prefill_len + i) for i in range(n_steps)) / n_steps
+    del model
+    torch.cuda.empty_cache()
+    return {"ms_per_step": round(ms, 4), "steps": n_steps, "bytes_per_step": int(nbytes),
+            "achieved_gbs": round(nbytes / (ms * 1e-3) / 1e9, 1),
             "tokens_first_step": hist[0].tolist(), "tokens_last_step": hist[-1].tolist(),
             "config": f"slow {cfg.n_layer}x d{cfg.dim} ({cfg.n_head}q/{cfg.n_local_heads}kv x{cfg.head_dim}, "
                       f"FFN {cfg.intermediate_size}), fast {cfg.fast_n_layer}x d{cfg.fast_dim} "
