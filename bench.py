@@ -188,6 +188,53 @@ def bench_kernel(M, K, nested, dtype_name, launches_per_copy=1, min_bytes=2 * MA
             "gbs": nbytes / sec / 1e9, "launches": reps * ncopy, "copies": ncopy}
 
 
+MFMA_PEAK_TFLOPS = 2500.0  # dense bf16
+
+
+def bench_gemm(rows: int = 512, copies: int = 4, reps: int = 20):
+    """C4: a `rows`-token prefill through the seven projections of one layer
+    (X bf16 [rows, K] x NF4 nested weights -> bf16 [rows, M]), each projection
+    timed alone, graph-replayed over `copies` weight copies."""
+    import torch
+
+    from ttspipe_amd import _lib
+    from ttspipe_amd.quant import NF4_CODE
+
+    lib = _lib.load()
+    dev = torch.device("cuda", 0)
+    lut = torch.tensor(NF4_CODE, dtype=torch.float32, device=dev)
+    res, total_s, total_flop = [], 0.0, 0
+    for i, (name, M, K) in enumerate(LAYER):
+        lins = [Linear(M, K, True, seed=500 + 10 * i + c, device=dev) for c in range(copies)]
+        x = torch.randn(rows, K, device=dev).to(torch.bfloat16)
+        y = torch.empty(rows, M, dtype=torch.bfloat16, device=dev)
+
+        def body():
+            st = torch.cuda.current_stream().cuda_stream
+            for lin in lins:
+                rc = lib.ttsp_nf4_gemm(x.data_ptr(), _lib.DT_BF16, lin.w.data_ptr(), _lib.ptr(lin.a8),
+                                       lin.amax.data_ptr(), _lib.ptr(lin.code2), lin.offset, lut.data_ptr(),
+                                       y.data_ptr(), 0, 0, M, K, rows, 64, 256, st)
+                if rc:
+                    raise RuntimeError(f"ttsp_nf4_gemm failed: {rc}")
+
+        body()
+        torch.cuda.synchronize()
+        graph = capture(body)
+        stream = torch.cuda.current_stream()
+        time_graph(graph, 2, stream)
+        sec = time_graph(graph, reps, stream) / copies
+        flop = 2 * rows * M * K
+        res.append({"name": name, "M": M, "K": K, "us": round(sec * 1e6, 2),
+                    "tflops": round(flop / sec / 1e12, 1)})
+        total_s += sec
+        total_flop += flop
+        del lins
+    return {"rows": rows, "projections": res, "layer_us": round(total_s * 1e6, 1),
+            "tflops": round(total_flop / total_s / 1e12, 1),
+            "pct_of_mfma_peak": round(100 * total_flop / total_s / 1e12 / MFMA_PEAK_TFLOPS, 2)}
+
+
 def bench_copy(nbytes: int = 64 * 2**20, launches: int = 8):
     """A plain device copy of known size (reads and writes `nbytes` each), the
     calibration kernel for the HBM byte counters."""
@@ -223,7 +270,7 @@ def main() -> int:
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--skip-cpu", action="store_true")
     ap.add_argument("--skip-decode", action="store_true")
-    ap.add_argument("--only", choices=["layer", "kernel", "c1", "copy", "decode"], default=None,
+    ap.add_argument("--only", choices=["layer", "kernel", "c1", "copy", "decode", "gemm"], default=None,
                     help="run one GPU measurement only (for profiling runs)")
     ap.add_argument("--decode-steps", type=int, default=256, help="greedy frames the decode benchmark times")
     ap.add_argument("--direct", action="store_true",
@@ -247,6 +294,8 @@ def main() -> int:
         out["c1"] = bench_kernel(9728, 2560, False, "fp16", direct=args.direct)
     if args.only == "copy":
         out["copy"] = bench_copy()
+    if args.only in (None, "gemm"):
+        out["gemm"] = bench_gemm()
     decode = None
     if args.only in (None, "decode") and not args.skip_decode:
         from ttspipe_amd import dualar
@@ -301,6 +350,7 @@ def main() -> int:
             "bytes_per_launch": c1["bytes"],
         },
         "decode": decode,
+        "prefill_gemm": out["gemm"],
         "cpu_baseline": cpu,
     }
     print(json.dumps(line))

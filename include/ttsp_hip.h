@@ -45,6 +45,23 @@ int ttsp_nf4_gemm(const void* X, int x_dtype, const uint8_t* W, const uint8_t* A
                   const void* R, int epi, int M, int K, int N, int blocksize, int blocksize2,
                   void* stream);
 
+/* The batch-1 matmuls of a decode block in one launch each (K <= 10240):
+ *   W3 == NULL: Y = epi(n(X) . dequant(W1)^T), epi as ttsp_nf4_gemm;
+ *   W3 != NULL: Y = round(round(silu(round(n(X) . W1^T))) * round(n(X) . W3^T)),
+ *               W1 and W3 of one shape [M, K] (the SwiGLU gate, epi must be 0);
+ * n(X) = X, or with NORM_W != NULL the fork's RMSNorm with weight NORM_W and
+ * eps, bit-identical to ttsp_rms_norm. Scale arguments as ttsp_nf4_gemm (both
+ * weights plain or both nested). Results equal the unfused sequence
+ * ttsp_rms_norm -> ttsp_nf4_gemm (-> ttsp_nf4_gemm with epi 2) bit for bit.
+ * Replaces: the rms_norm -> nf4_mma and w1 -> w3(silu gate) launch pairs of the
+ * reference's decode block (app/engine/fusedlayer.py:222-225, 262-267). */
+int ttsp_nf4_gemv_fused(const void* X, int x_dtype, const void* NORM_W, float eps, const uint8_t* W1,
+                        const uint8_t* A8_1, const float* AMAX_1, const float* CODE2_1, float offset_1,
+                        const uint8_t* W3, const uint8_t* A8_3, const float* AMAX_3,
+                        const float* CODE2_3, float offset_3, const float* LUT, void* Y,
+                        const void* R, int epi, int M, int K, int blocksize, int blocksize2,
+                        void* stream);
+
 /* out[k] = round(LUT[q_k] * s_{k / blocksize}) for the n flattened codes, one
  * rounding, out_dtype TTSP_F16/BF16/F32. Replaces: the dequantisation inside
  * nf4_mma (app/engine/nf4gemv.py:154-188) and bitsandbytes' dequantize_4bit

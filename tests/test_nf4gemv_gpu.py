@@ -247,3 +247,75 @@ def test_gemm_epilogues(nf4, orc, epi):
     p = o.to_f32(bits(plain), 0).astype(np.float64)
     expect = r + p if epi == 1 else (r / (1 + np.exp(-r))) * p
     assert relative_error(o.to_f32(bits(y), 0), expect) < 5e-3
+
+
+# ------------------------------------------------------------ fused forms (one launch)
+
+FUSED_SHAPES = [(6144, 2560), (9728, 2560), (2560, 9728), (1536, 1024), (3072, 1024), (1544, 2560), (64, 128)]
+
+
+@pytest.mark.parametrize("shape", FUSED_SHAPES)
+@pytest.mark.parametrize("nested", [True, False])
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_norm_folded_into_the_matmul_is_bit_exact(nf4, orc, shape, nested, dtype):
+    """rmsnorm(x) . W^T in one launch == the standalone norm then the GEMV, bit for bit."""
+    M, K = shape
+    layer = random_layer(M, K, nested, seed=M + 3 * K)
+    lin = to_linear(layer, dtype)
+    assert nf4.prepare(lin)
+    dt = dt_code(dtype)
+    xb = randn_bits(K, dtype, seed=K + 1, scale=3.0)
+    gb = o.from_f32((np.random.default_rng(K).random(K) * 0.5 + 0.75).astype(np.float32), dt)
+    y = nf4.matmul_fused(lin, from_bits(xb, dtype).view(1, 1, K), norm_weight=from_bits(gb, dtype), eps=1e-6)
+    J, KS, _ = gemv_shape(M, K)
+    xn = orc.rms_norm_emul(xb, gb, 1, K, 1e-6, dt)
+    expect = orc.gemv_emul(xn, dt, **oracle_args(layer), M=M, K=K, bs=64, KS=KS, J=J, bs2=layer["bs2"] or 256)
+    assert np.array_equal(bits(y), expect), f"M={M} K={K}: {first_mismatch(bits(y), expect)}"
+
+
+@pytest.mark.parametrize("shape", [(9728, 2560), (3072, 1024), (1000, 2560), (64, 128)])
+@pytest.mark.parametrize("norm", [True, False])
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_swiglu_pair_in_one_launch_is_bit_exact(nf4, orc, shape, norm, dtype):
+    """silu(x W1) * (x W3) from one launch == w1, then w3 with the gate epilogue."""
+    M, K = shape
+    l1, l3 = random_layer(M, K, True, seed=M + 1), random_layer(M, K, True, seed=M + 2)
+    w1, w3 = to_linear(l1, dtype), to_linear(l3, dtype)
+    assert nf4.prepare(w1) and nf4.prepare(w3)
+    dt = dt_code(dtype)
+    xb = randn_bits(K, dtype, seed=K + 5)
+    gb = o.from_f32((np.random.default_rng(K + 1).random(K) + 0.5).astype(np.float32), dt)
+    y = nf4.matmul_fused(w1, from_bits(xb, dtype).view(1, 1, K), norm_weight=from_bits(gb, dtype) if norm else None,
+                         eps=1e-6, module3=w3)
+    J, KS, _ = gemv_shape(M, K)
+    xin = orc.rms_norm_emul(xb, gb, 1, K, 1e-6, dt) if norm else xb
+    g1 = orc.gemv_emul(xin, dt, **oracle_args(l1), M=M, K=K, bs=64, KS=KS, J=J)
+    expect = orc.gemv_emul(xin, dt, **oracle_args(l3), M=M, K=K, bs=64, KS=KS, J=J, R=g1, epi=2)
+    assert np.array_equal(bits(y), expect), f"M={M} K={K}: {first_mismatch(bits(y), expect)}"
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_norm_folded_with_residual_epilogue(nf4, orc, dtype):
+    M, K = 2560, 4096
+    layer = random_layer(M, K, True, seed=77)
+    lin = to_linear(layer, dtype)
+    assert nf4.prepare(lin)
+    dt = dt_code(dtype)
+    xb, rb = randn_bits(K, dtype, seed=78), randn_bits(M, dtype, seed=79)
+    gb = o.from_f32(np.full(K, 1.25, np.float32), dt)
+    y = nf4.matmul_fused(lin, from_bits(xb, dtype).view(1, K), norm_weight=from_bits(gb, dtype), eps=1e-5,
+                         epi=nf4.EPI_RESIDUAL, operand=from_bits(rb, dtype))
+    J, KS, _ = gemv_shape(M, K)
+    xn = orc.rms_norm_emul(xb, gb, 1, K, 1e-5, dt)
+    expect = orc.gemv_emul(xn, dt, **oracle_args(layer), M=M, K=K, bs=64, KS=KS, J=J, R=rb, epi=1)
+    assert np.array_equal(bits(y), expect), first_mismatch(bits(y), expect)
+
+
+def test_fused_form_declines_what_it_cannot_serve(nf4):
+    a = to_linear(random_layer(512, 2560, True, seed=1), torch.bfloat16)
+    b = to_linear(random_layer(256, 2560, True, seed=2), torch.bfloat16)
+    assert nf4.prepare(a) and nf4.prepare(b)
+    x = torch.randn(1, 2560, device="cuda", dtype=torch.bfloat16)
+    assert nf4.matmul_fused(a, x, module3=b) is None  # shapes differ
+    assert nf4.matmul_fused(a, torch.randn(2, 2560, device="cuda", dtype=torch.bfloat16)) is None  # two rows
+    assert nf4.matmul_fused(a, x, norm_weight=torch.ones(2560, device="cuda", dtype=torch.float16)) is None

@@ -1,5 +1,4 @@
-// NF4 GEMV (one activation row) and NF4 dequantisation, reading the
-// bitsandbytes layout in place:
+// NF4 GEMV (one activation row), reading the bitsandbytes layout in place:
 //   * W is the row-major flattened weight, two 4-bit codes per byte, the HIGH
 //     nibble holding the even flattened index (byte j = q[2j] << 4 | q[2j+1]);
 //   * scale block b covers flattened codes [b*bs, (b+1)*bs), bs a power of two
@@ -7,34 +6,45 @@
 //   * plain scales are fp32 absmax[b]; nested ("double-quant") scales are
 //     code2[a8[b]] * absmax2[b >> log2(bs2)] + offset, two fp32 roundings.
 //
-// GEMV design. At batch 1 every weight byte is used once, so the kernel is a
+// One kernel serves three forms of a decode-block matmul:
+//   * plain      y = epi(x . W^T)              (the reference's nf4_mma at N=1)
+//   * + norm     y = epi(rmsnorm(x) . W^T)     (the fork's RMSNorm folded in)
+//   * SwiGLU     y = round(round(silu(round(x.W1^T))) * round(x.W3^T)), two
+//                weights of one shape streamed by the same waves (w1 and w3).
+//
+// Design. At batch 1 every weight byte is used once, so the kernel is a
 // stream of W from HBM, and at decode shapes (1-25 MB) it is short enough that
-// launch ramp and the per-byte instruction count, not the bus, set its time.
-// Hence:
+// launch latency and the per-byte instruction count, not the bus, set its time.
 //   * Ownership. A row is K/8 dwords (8 codes each). Lane l of a wave owns
 //     dwords d = l + 64*(j*KS + ks) of every row the wave visits: each load
 //     instruction reads 256 contiguous bytes, and the 8 activations matching a
-//     dword stay in registers for all of the wave's rows (x is read once per
-//     wave, not once per row). KS waves split K; each wave takes RPW rows.
+//     dword stay in registers for all of the wave's rows. 8 waves per
+//     workgroup: KS of them split K, 8 / KS row groups of RPW rows.
 //   * Issue order. Everything small (code table, code2, the workgroup's
-//     scales, the residual operand, x) is requested before the weights, so
-//     waiting for it never waits for the weight stream (vector-memory counters
-//     retire in order), and all RPW*J weight dwords of a lane are in flight
-//     before the first barrier. The dot products start as rows arrive.
+//     scales, the residual operand, x, the norm weight) is requested before the
+//     weights, so waiting for it never waits for the weight stream (vector
+//     memory counters retire in order), and every weight dword of a wave is in
+//     flight before the first barrier. All loads are unconditional (clamped
+//     addresses, dummy pointers for absent operands): no branch ever separates
+//     a load from its use, which keeps the compiler's wait counts exact, so the
+//     dot products start as rows arrive.
 //   * Code lookup without bank conflicts. Each byte (two codes) becomes a
-//     packed pair of fp16 code values through a 256-entry table that is
-//     replicated 64 times in LDS, entry e of lane l at byte 256*e + 4*l: the 64
-//     lanes of a lookup always hit 64 different banks, and the address is one
-//     v_perm_b32 (the byte of W next to the lane's own offset). The 64 KiB
-//     table is built while the weights are in flight.
+//     packed pair of fp16 code values through a 256-entry table replicated 64
+//     times in LDS, entry e of lane l at byte 256*e + 4*l: the 64 lanes of a
+//     lookup always hit 64 different banks, and the address is one v_perm_b32
+//     (the byte of W next to the lane's own offset). The 64 KiB table is built
+//     while the weights are in flight.
+//   * Activations are staged once per workgroup (waves 0-3, 8 values per
+//     thread-chunk, chunk c at thread c % 256): the norm, if any - bit for bit
+//     the standalone RMSNorm kernel's sum order and roundings - then for bf16 a
+//     rescale by 2^-e (max|x| in [2^14, 2^15)) and an exact conversion to fp16,
+//     so both activation types meet 11-bit codes.
 //   * Arithmetic (fixed order, so a CPU restatement reproduces every bit): a
 //     dword's 8 products are chained in code order (v_fma_mix_f32 on fp16
 //     halves, the first onto +0), the dword's partial meets its block scale in
 //     one fma into the lane accumulator - the scale multiplies the block's
 //     partial sum, the factored form of the reference CPU kernel
-//     (app/engine/nf4cpu.py:115-129). bf16 activations are first rescaled per
-//     K-slice by a power of two and converted to fp16 exactly, so both
-//     activation types meet 11-bit codes.
+//     (app/engine/nf4cpu.py:115-129).
 //   * Reductions: lanes by a DPP butterfly inside each 16-lane row (the xor
 //     1, 2, 4, 8 tree: quad_perm, then half-mirror and mirror pair the same
 //     partial sums) and the four row sums as (r0 + r1) + (r2 + r3); K-slices
@@ -46,7 +56,41 @@ namespace ttsp {
 constexpr int LUT_REP = 64;                    // table copies, one per lane
 constexpr int LUT_BYTES = 256 * LUT_REP * 4;   // 64 KiB
 constexpr int GEMV_WAVES = 8;                  // waves per workgroup
-constexpr int GEMV_MAX_WAVES = GEMV_WAVES;
+constexpr int GEMV_THREADS = GEMV_WAVES * 64;
+constexpr int STAGE_THREADS = 256;             // threads staging x (waves 0-3)
+constexpr int XC_MAX = 5;                      // x chunks per staging thread: K <= 5 * 8 * 256
+
+// One NF4 weight. For plain scales A8 and CODE2 point at any readable memory
+// (AMAX): the kernel reads them unconditionally and discards the values.
+struct Nf4Mat {
+  const uint32_t* W;
+  const uint8_t* A8;
+  const float* AMAX;
+  const float* CODE2;
+  float offset;
+};
+
+struct GemvParams {
+  Nf4Mat mat[2];          // mat[1]: the SwiGLU form's second weight (w3)
+  const float* LUT;       // the 16 NF4 code points
+  const uint16_t* X;      // [K]
+  const uint16_t* G;      // RMSNorm weight [K], or readable dummy
+  const uint16_t* R;      // epilogue operand [M], or readable dummy
+  uint16_t* Y;            // [M]
+  float eps;
+  int M, K, KS, bs_shift, bs2_shift;
+  int dt;                 // DT_F16 / DT_BF16
+  int nested, norm, epi;  // flags; epi: 0 none, 1 residual, 2 silu gate
+};
+
+__device__ __forceinline__ int uniform(int v) { return __builtin_amdgcn_readfirstlane(v); }
+
+__device__ __forceinline__ float ld16(int dt, uint32_t h) {
+  return dt == DT_BF16 ? bf16_to_f32(h & 0xffffu) : f16_to_f32(h & 0xffffu);
+}
+__device__ __forceinline__ uint32_t st16(int dt, float f) {
+  return dt == DT_BF16 ? f32_to_bf16(f) : f32_to_f16(opaque(f));
+}
 
 // Packed fp16 code pair of table entry v: low half code[v >> 4] (the even
 // flattened index), high half code[v & 15], matching the activation pair
@@ -58,16 +102,12 @@ __device__ __forceinline__ uint32_t code_pair(float hi_code, float lo_code) {
 // Output rounding as the unfused fork: the matmul result is rounded to the
 // activation type, and so is each elementwise op after it (app/engine/
 // nf4gemv.py:215-226): residual y' = round(R + y), gate y' = round(round(silu(R)) * y).
-template <int DT>
-__device__ __forceinline__ uint16_t epilogue16(float acc, int epi, uint32_t r) {
-  const float y = Elem<DT>::load(Elem<DT>::store(acc));
+__device__ __forceinline__ uint16_t epilogue16(int dt, float acc, int epi, uint32_t r) {
+  const float y = ld16(dt, st16(dt, acc));
   float o = y;
-  if (epi == 1) {
-    o = __fadd_rn(Elem<DT>::load(r), y);
-  } else if (epi == 2) {
-    o = __fmul_rn(Elem<DT>::load(Elem<DT>::store(silu_rn(Elem<DT>::load(r)))), y);
-  }
-  return Elem<DT>::store(o);
+  if (epi == 1) o = __fadd_rn(ld16(dt, r), y);
+  else if (epi == 2) o = __fmul_rn(ld16(dt, st16(dt, silu_rn(ld16(dt, r)))), y);
+  return (uint16_t)st16(dt, o);
 }
 
 // Every lane of a 16-lane row gets the row's sum, by the xor 1, 2, 4, 8
@@ -92,11 +132,7 @@ __device__ __forceinline__ float wave_sum_dpp(float v) {
   return __fadd_rn(__fadd_rn(r0, r1), __fadd_rn(r2, r3));
 }
 
-// Largest wave-uniform value helpers: readfirstlane makes a per-wave value a
-// scalar, so row and slice offsets fold into scalar address arithmetic.
-__device__ __forceinline__ int uniform(int v) { return __builtin_amdgcn_readfirstlane(v); }
-
-// Max over the wave (every lane gets it): DPP within rows, then the 4 rows.
+// Max over the wave (every lane gets it).
 __device__ __forceinline__ float wave_max_dpp(float v) {
   v = fmaxf(v, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0xB1, 0xF, 0xF, false)));
   v = fmaxf(v, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x4E, 0xF, 0xF, false)));
@@ -117,112 +153,132 @@ __device__ __forceinline__ uint32_t bf16x2_to_f16x2(uint32_t u, int xe) {
   return lo | (hi << 16);
 }
 
-constexpr int XC_MAX = 8;  // bf16 x: 16-byte chunks a thread converts (K <= 8 * 8 * threads)
+__device__ __forceinline__ float max_abs16(int dt, uint4 v, float m) {
+  const uint32_t u[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+  for (int k = 0; k < 4; ++k) m = fmaxf(m, fmaxf(fabsf(ld16(dt, u[k])), fabsf(ld16(dt, u[k] >> 16))));
+  return m;
+}
 
-// Workgroup: 8 waves = KS * RG; wave w takes K-slice w % KS of RPW
-// consecutive rows starting at blockIdx.x * RG * RPW + (w / KS) * RPW.
-// LDS: the static code-pair table replicas at address 0 (so a lookup address
-// is the v_perm result itself), then (dynamic) pair staging [256], code2
-// [256], per-wave maxima [NW], per-wave K-slice partials [NW][RPW], the
-// workgroup's scales [RG * RPW][nblk], and for bf16 the rescaled x [K] (fp16).
-template <int DT, int J, int RPW, bool NESTED>
-__global__ __launch_bounds__(GEMV_MAX_WAVES * 64) void nf4_gemv_kernel(
-    const uint32_t* __restrict__ W, const uint8_t* __restrict__ A8,
-    const float* __restrict__ AMAX, const float* __restrict__ CODE2, float offset,
-    const float* __restrict__ LUT, const uint16_t* __restrict__ X, uint16_t* __restrict__ Y,
-    const uint16_t* R, int epi, int M, int K, int KS, int bs_shift, int bs2_shift) {
-  // Scale entries per thread: a workgroup holds (8 / KS) * RPW rows of at
-  // most 8 * J * KS blocks (bs >= 64), i.e. <= 64 * RPW * J entries.
-  constexpr int SL = (RPW * J + 7) / 8;
+// Dynamic LDS after the static table: pair staging [256], code2 [NM][256],
+// wave partials [8] and maxima [8], K-slice partials [8][NM*RPW], the
+// workgroup's scales [NM][RG*RPW][nblk] (16-byte aligned), then x as staged
+// fp16 [K].
+template <int J, int RPW, int NM>
+__global__ __launch_bounds__(GEMV_THREADS) void nf4_gemv_kernel(const GemvParams p) {
   constexpr int NW = GEMV_WAVES;
-  constexpr int nthr = NW * 64;
+  constexpr int nthr = GEMV_THREADS;
+  // Scale entries per thread: a workgroup holds (8 / KS) * RPW rows of at
+  // most 8 * J * KS blocks (bs >= 64), i.e. <= 64 * RPW * J entries per weight.
+  constexpr int SL = (NM * RPW * J + 7) / 8;
   __shared__ __align__(16) uint32_t lut_rep[256 * LUT_REP];
   extern __shared__ __align__(16) unsigned char lds_dyn[];
   uint32_t* pair_s = reinterpret_cast<uint32_t*>(lds_dyn);
-  float* code2_s = reinterpret_cast<float*>(pair_s + 256);
-  float* wmax = code2_s + 256;                      // [NW]
-  float* red = wmax + GEMV_MAX_WAVES;               // [NW][RPW]
-  float* srow = red + GEMV_MAX_WAVES * RPW;         // [RG * RPW][nblk]
+  float* code2_s = reinterpret_cast<float*>(pair_s + 256);  // [NM][256]
+  float* wpart = code2_s + NM * 256;                         // [NW]
+  float* wmax = wpart + NW;                                  // [NW]
+  float* red = wmax + NW;                                    // [NW][NM*RPW]
+  float* srow = red + NW * NM * RPW;                         // [NM][rows_wg][nblk]
+
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = uniform(tid >> 6);
-  const int ks = wave % KS, rg = wave / KS;
+  const int KS = p.KS, ks = wave % KS, rg = wave / KS;
   const int RG = NW / KS;
-  const int KD = K >> 3;
-  const int nblk = K >> bs_shift;
-  const int sh = bs_shift - 3;
+  const int M = p.M, K = p.K, KD = K >> 3;
+  const int nblk = K >> p.bs_shift, sh = p.bs_shift - 3;
   const int rows_wg = RG * RPW;
   const int wg_row0 = blockIdx.x * rows_wg;
   const int row0 = wg_row0 + rg * RPW;
-  const int nsc = min(rows_wg, M - wg_row0) * nblk;  // scale entries of this workgroup
+  const int nsc = min(rows_wg, M - wg_row0) * nblk;        // scale entries per weight
   const long long sc0 = (long long)wg_row0 * nblk;
-  uint4* xs = reinterpret_cast<uint4*>(srow + ((rows_wg * nblk + 3) & ~3));  // bf16 only: [KD]
+  const int dt = p.dt;
+  const bool nested = p.nested != 0, norm = p.norm != 0;
+  uint4* xs = reinterpret_cast<uint4*>(srow + ((NM * rows_wg * nblk + 3) & ~3));  // [KD]
+  const int XN = (KD + STAGE_THREADS - 1) / STAGE_THREADS;  // x chunks per staging thread
+  const bool stager = tid < STAGE_THREADS;
 
   // 1. small operands first: code table entries, code2, scales, residual, x
-  float chi = 0.0f, clo = 0.0f, c2v = 0.0f;
-  if (tid < 256) {
-    chi = LUT[tid >> 4];
-    clo = LUT[tid & 15];
-    if constexpr (NESTED) c2v = CODE2[tid];
+  float chi = 0.0f, clo = 0.0f, c2v[NM];
+  {
+    const int t = tid & 255;
+    chi = p.LUT[t >> 4];
+    clo = p.LUT[t & 15];
+#pragma unroll
+    for (int m = 0; m < NM; ++m) c2v[m] = p.mat[m].CODE2[nested ? t : 0];
   }
   float sv[SL];
-  uint32_t av[NESTED ? SL : 1];
+  uint32_t av[SL];
 #pragma unroll
   for (int i = 0; i < SL; ++i) {
-    const long long gb = sc0 + min(tid + i * nthr, nsc - 1);
-    if constexpr (NESTED) {
-      av[i] = A8[gb];
-      sv[i] = AMAX[gb >> bs2_shift];
-    } else {
-      sv[i] = AMAX[gb];
-    }
+    const int e = tid + i * nthr;
+    const int m = NM > 1 && e >= nsc ? 1 : 0;
+    const long long gb = sc0 + min(e - m * nsc, nsc - 1);
+    const uint8_t* a8 = m ? p.mat[NM - 1].A8 : p.mat[0].A8;
+    const float* am = m ? p.mat[NM - 1].AMAX : p.mat[0].AMAX;
+    av[i] = a8[gb];
+    sv[i] = am[nested ? gb >> p.bs2_shift : gb];
   }
-  const uint32_t rres = R[min(row0 + min(lane, RPW - 1), M - 1)];  // used by the epilogue only
-  uint4 xr[J];
-  uint4 xc[DT == DT_BF16 ? XC_MAX : 1];
-  const int XN = (KD + nthr - 1) / nthr;  // bf16: x chunks per thread (uniform)
-  if constexpr (DT == DT_BF16) {
+  const uint32_t rres = p.R[min(row0 + min(lane, RPW - 1), M - 1)];  // epilogue operand
+  uint4 xc[XC_MAX], gc[XC_MAX];
 #pragma unroll
-    for (int i = 0; i < XC_MAX; ++i) {
-      xc[i] = make_uint4(0, 0, 0, 0);
-      if (i < XN) xc[i] = *reinterpret_cast<const uint4*>(X + 8 * (size_t)min(tid + i * nthr, KD - 1));
+  for (int i = 0; i < XC_MAX; ++i) {
+    xc[i] = gc[i] = make_uint4(0, 0, 0, 0);
+    if (i < XN) {
+      const int c = min((tid & 255) + i * STAGE_THREADS, KD - 1);
+      xc[i] = *reinterpret_cast<const uint4*>(p.X + 8 * (size_t)c);
+      gc[i] = *reinterpret_cast<const uint4*>(p.G + 8 * (size_t)(norm ? c : 0));
     }
-  } else {
-#pragma unroll
-    for (int j = 0; j < J; ++j)
-      xr[j] = *reinterpret_cast<const uint4*>(X + 8 * (size_t)min(lane + 64 * (j * KS + ks), KD - 1));
   }
   // 2. the weight stream: every dword of this wave's rows, all in flight
-  uint32_t w[RPW][J];
+  uint32_t w[NM][RPW][J];
 #pragma unroll
-  for (int r = 0; r < RPW; ++r) {
-    const uint32_t* wr = W + (size_t)min(row0 + r, M - 1) * KD + 64 * ks;
+  for (int m = 0; m < NM; ++m)
 #pragma unroll
-    for (int j = 0; j < J; ++j)
-      w[r][j] = __builtin_nontemporal_load(wr + min(64 * j * KS + lane, KD - 1 - 64 * ks));
-  }
+    for (int r = 0; r < RPW; ++r) {
+      const uint32_t* wr = p.mat[m].W + (size_t)min(row0 + r, M - 1) * KD + 64 * ks;
+#pragma unroll
+      for (int j = 0; j < J; ++j)
+        w[m][r][j] = __builtin_nontemporal_load(wr + min(64 * j * KS + lane, KD - 1 - 64 * ks));
+    }
 
-
-  // 3. tables: pair staging, code2 and the x maximum, then the replicated pair
-  //    table, the resolved scales and the rescaled x
+  // 3. before the first barrier: pair staging, code2, and from the staging
+  //    waves either the norm's sum of squares (chunk order, the standalone
+  //    kernel's) or, without a norm, the bf16 maximum
   if (tid < 256) {
     pair_s[tid] = code_pair(chi, clo);
-    if constexpr (NESTED) code2_s[tid] = c2v;
+#pragma unroll
+    for (int m = 0; m < NM; ++m) code2_s[m * 256 + tid] = c2v[m];
   }
-  if constexpr (DT == DT_BF16) {
-    float m = 0.0f;
+  if (stager) {
+    float acc = 0.0f;
 #pragma unroll
     for (int i = 0; i < XC_MAX; ++i) {
-      if (i < XN) {
-        const uint32_t u[4] = {xc[i].x, xc[i].y, xc[i].z, xc[i].w};
+      if (i < XN && (tid + i * STAGE_THREADS) < KD) {
+        if (norm) {
+          const uint32_t u[4] = {xc[i].x, xc[i].y, xc[i].z, xc[i].w};
 #pragma unroll
-        for (int k = 0; k < 4; ++k)
-          m = fmaxf(m, fmaxf(fabsf(bf16_to_f32(u[k] & 0xffffu)), fabsf(bf16_to_f32(u[k] >> 16))));
+          for (int k = 0; k < 4; ++k) {
+            const float a = ld16(dt, u[k]), b = ld16(dt, u[k] >> 16);
+            acc = __builtin_fmaf(a, a, acc);
+            acc = __builtin_fmaf(b, b, acc);
+          }
+        } else {
+          acc = max_abs16(dt, xc[i], acc);
+        }
       }
     }
-    m = wave_max_dpp(m);
-    if (lane == 0) wmax[wave] = m;
+    if (norm) {
+      acc = wave_sum(acc);
+      if (lane == 0) wpart[wave] = acc;
+    } else {
+      acc = wave_max_dpp(acc);
+      if (lane == 0) wmax[wave] = acc;
+    }
   }
   __syncthreads();
+
+  // 4. the replicated pair table, the resolved scales, the normalised x and
+  //    (with a norm) its maximum
   {
     constexpr int G = (int)sizeof(lut_rep) / 1024 / NW;  // 1 KiB (4 entries) per wave store
     uint32_t v[G];
@@ -235,154 +291,140 @@ __global__ __launch_bounds__(GEMV_MAX_WAVES * 64) void nf4_gemv_kernel(
 #pragma unroll
   for (int i = 0; i < SL; ++i) {
     const int e = tid + i * nthr;
-    if (e < nsc) {
-      if constexpr (NESTED) srow[e] = __fadd_rn(__fmul_rn(code2_s[av[i]], sv[i]), offset);
-      else srow[e] = sv[i];
+    if (e < NM * nsc) {
+      const int m = NM > 1 && e >= nsc ? 1 : 0;
+      const float off = m ? p.mat[NM - 1].offset : p.mat[0].offset;
+      const float s = nested ? __fadd_rn(__fmul_rn(code2_s[m * 256 + av[i]], sv[i]), off) : sv[i];
+      srow[e + m * (rows_wg * nblk - nsc)] = s;  // weight m's block starts at m * rows_wg * nblk
     }
   }
-  // bf16 activations: rescale x by 2^-xe so max|x| lands in [2^14, 2^15) and
-  // convert to fp16 - exact, since bf16's 8 significant bits fit in fp16's 11 -
-  // then every product below is fp16 x fp16 with 11-bit codes. The row sums
-  // are scaled back by 2^xe (also exact).
-  int xe = 0;
-  if constexpr (DT == DT_BF16) {
-    float m = wmax[0];
-    for (int v = 1; v < NW; ++v) m = fmaxf(m, wmax[v]);
-    if (m > 0.0f && m <= 3.402823466e38f) xe = __builtin_amdgcn_frexp_expf(m) - 15;
+  if (norm && stager) {
+    float ss = wpart[0];
+#pragma unroll
+    for (int w2 = 1; w2 < STAGE_THREADS / 64; ++w2) ss = __fadd_rn(ss, wpart[w2]);
+    const float r = rsqrt_rn(__fadd_rn(__fdiv_rn(ss, (float)K), p.eps));
+    float m = 0.0f;
 #pragma unroll
     for (int i = 0; i < XC_MAX; ++i) {
-      const int c = tid + i * nthr;
-      if (i < XN && c < KD)
-        xs[c] = make_uint4(bf16x2_to_f16x2(xc[i].x, xe), bf16x2_to_f16x2(xc[i].y, xe),
-                           bf16x2_to_f16x2(xc[i].z, xe), bf16x2_to_f16x2(xc[i].w, xe));
+      if (i < XN) {
+        uint32_t* u = reinterpret_cast<uint32_t*>(&xc[i]);
+        const uint32_t* g = reinterpret_cast<const uint32_t*>(&gc[i]);
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          const float n0 = ld16(dt, st16(dt, __fmul_rn(ld16(dt, u[k]), r)));
+          const float n1 = ld16(dt, st16(dt, __fmul_rn(ld16(dt, u[k] >> 16), r)));
+          u[k] = st16(dt, __fmul_rn(n0, ld16(dt, g[k]))) | (st16(dt, __fmul_rn(n1, ld16(dt, g[k] >> 16))) << 16);
+        }
+        if ((tid + i * STAGE_THREADS) < KD) m = max_abs16(dt, xc[i], m);
+      }
+    }
+    m = wave_max_dpp(m);
+    if (lane == 0) wmax[wave] = m;
+  }
+  __syncthreads();
+
+  // 5. x to fp16 in LDS: bf16 is rescaled by 2^-xe so max|x| lands in
+  //    [2^14, 2^15) and converted exactly (bf16's 8 significant bits fit in
+  //    fp16's 11); the row sums are scaled back by 2^xe (also exact)
+  int xe = 0;
+  if (dt == DT_BF16) {
+    float m = wmax[0];
+#pragma unroll
+    for (int w2 = 1; w2 < STAGE_THREADS / 64; ++w2) m = fmaxf(m, wmax[w2]);
+    if (m > 0.0f && m <= 3.402823466e38f) xe = __builtin_amdgcn_frexp_expf(m) - 15;
+  }
+  if (stager) {
+#pragma unroll
+    for (int i = 0; i < XC_MAX; ++i) {
+      const int c = tid + i * STAGE_THREADS;
+      if (i < XN && c < KD) {
+        uint4 v = xc[i];
+        if (dt == DT_BF16)
+          v = make_uint4(bf16x2_to_f16x2(v.x, xe), bf16x2_to_f16x2(v.y, xe), bf16x2_to_f16x2(v.z, xe),
+                         bf16x2_to_f16x2(v.w, xe));
+        xs[c] = v;
+      }
     }
   }
   __syncthreads();
-  if constexpr (DT == DT_BF16) {
-#pragma unroll
-    for (int j = 0; j < J; ++j) xr[j] = xs[min(lane + 64 * (j * KS + ks), KD - 1)];
-  }
   // Past the row's end (K not a multiple of 512 * KS) x is zero: the clamped
-  // weight dword there is finite, so its products are exactly +0. (Only x is
-  // zeroed - the weight registers may still be in flight.)
+  // weight dword there is finite, so its products are exactly +0.
+  uint4 xr[J];
 #pragma unroll
   for (int j = 0; j < J; ++j) {
-    const bool in_row = lane + 64 * (j * KS + ks) < KD;
-    xr[j] = make_uint4(in_row ? xr[j].x : 0u, in_row ? xr[j].y : 0u, in_row ? xr[j].z : 0u,
-                       in_row ? xr[j].w : 0u);
+    const int d = lane + 64 * (j * KS + ks);
+    const uint4 v = xs[min(d, KD - 1)];
+    const bool in_row = d < KD;
+    xr[j] = make_uint4(in_row ? v.x : 0u, in_row ? v.y : 0u, in_row ? v.z : 0u, in_row ? v.w : 0u);
   }
 
-  // 4. dot products, row by row as the rows arrive
+  // 6. dot products, row by row as the rows arrive
   const uint32_t lane4 = (uint32_t)lane * 4u;
   const unsigned char* lut_b = reinterpret_cast<const unsigned char*>(lut_rep);
-  // block index of each of the lane's dwords (clamped inside the row past its end)
-  int sblk[J];
+  int sblk[J];  // block of each of the lane's dwords (clamped inside the row past its end)
 #pragma unroll
   for (int j = 0; j < J; ++j) sblk[j] = min(lane + 64 * (j * KS + ks), KD - 1) >> sh;
-  float tot[RPW];
+  float tot[NM][RPW];
 #pragma unroll
-  for (int r = 0; r < RPW; ++r) {
-    const float* srr = srow + uniform((rg * RPW + r) * nblk);
-    float acc = 0.0f;
+  for (int m = 0; m < NM; ++m)
 #pragma unroll
-    for (int j = 0; j < J; ++j) {
-      const float s = srr[sblk[j]];
-      const uint32_t wv = w[r][j];
-      const uint32_t c0 = *reinterpret_cast<const uint32_t*>(lut_b + __builtin_amdgcn_perm(wv, lane4, 0x0C0C0400u));
-      const uint32_t c1 = *reinterpret_cast<const uint32_t*>(lut_b + __builtin_amdgcn_perm(wv, lane4, 0x0C0C0500u));
-      const uint32_t c2 = *reinterpret_cast<const uint32_t*>(lut_b + __builtin_amdgcn_perm(wv, lane4, 0x0C0C0600u));
-      const uint32_t c3 = *reinterpret_cast<const uint32_t*>(lut_b + __builtin_amdgcn_perm(wv, lane4, 0x0C0C0700u));
-      // the dword's 8 products in code order, each an fma (the first onto +0)
-      float q = __builtin_fmaf(h_lo(c0), h_lo(xr[j].x), 0.0f);
-      q = __builtin_fmaf(h_hi(c0), h_hi(xr[j].x), q);
-      q = __builtin_fmaf(h_lo(c1), h_lo(xr[j].y), q);
-      q = __builtin_fmaf(h_hi(c1), h_hi(xr[j].y), q);
-      q = __builtin_fmaf(h_lo(c2), h_lo(xr[j].z), q);
-      q = __builtin_fmaf(h_hi(c2), h_hi(xr[j].z), q);
-      q = __builtin_fmaf(h_lo(c3), h_lo(xr[j].w), q);
-      q = __builtin_fmaf(h_hi(c3), h_hi(xr[j].w), q);
-      acc = __builtin_fmaf(q, s, acc);
+    for (int r = 0; r < RPW; ++r) {
+      const float* srr = srow + uniform((m * rows_wg + rg * RPW + r) * nblk);
+      float acc = 0.0f;
+#pragma unroll
+      for (int j = 0; j < J; ++j) {
+        const float s = srr[sblk[j]];
+        const uint32_t wv = w[m][r][j];
+        const uint32_t c0 = *reinterpret_cast<const uint32_t*>(lut_b + __builtin_amdgcn_perm(wv, lane4, 0x0C0C0400u));
+        const uint32_t c1 = *reinterpret_cast<const uint32_t*>(lut_b + __builtin_amdgcn_perm(wv, lane4, 0x0C0C0500u));
+        const uint32_t c2 = *reinterpret_cast<const uint32_t*>(lut_b + __builtin_amdgcn_perm(wv, lane4, 0x0C0C0600u));
+        const uint32_t c3 = *reinterpret_cast<const uint32_t*>(lut_b + __builtin_amdgcn_perm(wv, lane4, 0x0C0C0700u));
+        // the dword's 8 products in code order, each an fma (the first onto +0)
+        float q = __builtin_fmaf(h_lo(c0), h_lo(xr[j].x), 0.0f);
+        q = __builtin_fmaf(h_hi(c0), h_hi(xr[j].x), q);
+        q = __builtin_fmaf(h_lo(c1), h_lo(xr[j].y), q);
+        q = __builtin_fmaf(h_hi(c1), h_hi(xr[j].y), q);
+        q = __builtin_fmaf(h_lo(c2), h_lo(xr[j].z), q);
+        q = __builtin_fmaf(h_hi(c2), h_hi(xr[j].z), q);
+        q = __builtin_fmaf(h_lo(c3), h_lo(xr[j].w), q);
+        q = __builtin_fmaf(h_hi(c3), h_hi(xr[j].w), q);
+        acc = __builtin_fmaf(q, s, acc);
+      }
+      tot[m][r] = __builtin_ldexpf(wave_sum_dpp(acc), xe);
     }
-    acc = wave_sum_dpp(acc);
-    if constexpr (DT == DT_BF16) acc = __builtin_ldexpf(acc, xe);
-    tot[r] = acc;
-  }
 
-  // 5. K-slices left to right, epilogue, store (lane r stores row r)
+  // 7. K-slices left to right, epilogue, store (lane r stores row r)
   if (KS > 1) {
     if (lane == 0) {
 #pragma unroll
-      for (int r = 0; r < RPW; ++r) red[wave * RPW + r] = tot[r];
+      for (int m = 0; m < NM; ++m)
+#pragma unroll
+        for (int r = 0; r < RPW; ++r) red[wave * NM * RPW + m * RPW + r] = tot[m][r];
     }
     __syncthreads();
     if (ks != 0) return;
 #pragma unroll
-    for (int r = 0; r < RPW; ++r) {
-      float a = tot[r];
-      for (int k2 = 1; k2 < KS; ++k2) a = __fadd_rn(a, red[(wave + k2) * RPW + r]);
-      tot[r] = a;
-    }
-  }
-  float mine = tot[0];
+    for (int m = 0; m < NM; ++m)
 #pragma unroll
-  for (int r = 1; r < RPW; ++r) mine = lane == r ? tot[r] : mine;
-  if (lane < RPW && row0 + lane < M) Y[row0 + lane] = epilogue16<DT>(mine, epi, rres);
-}
-
-// Dequantise n codes (flattened) to fp16/bf16/fp32: out = round(code[q] * s),
-// one rounding, as bitsandbytes' dequantize_4bit. 16 codes (8 bytes) per thread.
-template <int ODT, bool NESTED>
-__global__ __launch_bounds__(256) void nf4_dequant_kernel(
-    const uint8_t* __restrict__ W, const uint8_t* __restrict__ A8, const float* __restrict__ AMAX,
-    const float* __restrict__ CODE2, float offset, const float* __restrict__ LUT,
-    void* __restrict__ OUT, long long n, int bs_shift, int bs2_shift) {
-  __shared__ float lut[16];
-  if (threadIdx.x < 16) lut[threadIdx.x] = LUT[threadIdx.x];
-  __syncthreads();
-  const long long t = (long long)blockIdx.x * blockDim.x + threadIdx.x;
-  const long long k0 = t * 16;
-  if (k0 >= n) return;
-  const long long b = k0 >> bs_shift;  // 16 codes never straddle a block (bs >= 64)
-  float s;
-  if constexpr (NESTED) {
-    s = __fadd_rn(__fmul_rn(CODE2[A8[b]], AMAX[b >> bs2_shift]), offset);
-  } else {
-    s = AMAX[b];
+      for (int r = 0; r < RPW; ++r) {
+        float a = tot[m][r];
+        for (int k2 = 1; k2 < KS; ++k2) a = __fadd_rn(a, red[(wave + k2) * NM * RPW + m * RPW + r]);
+        tot[m][r] = a;
+      }
   }
-  uint8_t bytes[8];
-  const long long nb = (n - k0 + 1) / 2 < 8 ? (n - k0 + 1) / 2 : 8;
-  if (nb == 8) {
-    const uint2 v = *reinterpret_cast<const uint2*>(W + k0 / 2);
-    *reinterpret_cast<uint2*>(bytes) = v;
-  } else {
-    for (int i = 0; i < 8; ++i) bytes[i] = i < nb ? W[k0 / 2 + i] : 0;
-  }
-  float v[16];
+  float mine[NM];
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    v[2 * i] = __fmul_rn(lut[bytes[i] >> 4], s);
-    v[2 * i + 1] = __fmul_rn(lut[bytes[i] & 15], s);
-  }
-  const int cnt = n - k0 < 16 ? (int)(n - k0) : 16;
-  if constexpr (ODT == DT_F32) {
-    float* o = (float*)OUT + k0;
-    if (cnt == 16) {
+  for (int m = 0; m < NM; ++m) {
+    mine[m] = tot[m][0];
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
-        reinterpret_cast<float4*>(o)[i] = make_float4(v[4 * i], v[4 * i + 1], v[4 * i + 2], v[4 * i + 3]);
+    for (int r = 1; r < RPW; ++r) mine[m] = lane == r ? tot[m][r] : mine[m];
+  }
+  if (lane < RPW && row0 + lane < M) {
+    if constexpr (NM == 1) {
+      p.Y[row0 + lane] = epilogue16(dt, mine[0], p.epi, rres);
     } else {
-      for (int i = 0; i < cnt; ++i) o[i] = v[i];
-    }
-  } else {
-    uint16_t* o = (uint16_t*)OUT + k0;
-    uint16_t h[16];
-#pragma unroll
-    for (int i = 0; i < 16; ++i) h[i] = Elem<ODT>::store(v[i]);
-    if (cnt == 16) {
-      reinterpret_cast<uint4*>(o)[0] = *reinterpret_cast<uint4*>(h);
-      reinterpret_cast<uint4*>(o)[1] = *reinterpret_cast<uint4*>(h + 8);
-    } else {
-      for (int i = 0; i < cnt; ++i) o[i] = h[i];
+      // SwiGLU: w1's row is the gate operand of w3's row, as the two-launch form rounds it
+      p.Y[row0 + lane] = epilogue16(dt, mine[1], 2, st16(dt, mine[0]));
     }
   }
 }
@@ -390,31 +432,30 @@ __global__ __launch_bounds__(256) void nf4_dequant_kernel(
 // ---------------------------------------------------------------------------
 // host side
 
-// Launch shape of the N == 1 GEMV for [M, K]: J 64-dword chunks per lane, K
-// split over KS waves, RPW rows per wave, NW waves per workgroup.
+// Launch shape: J 64-dword chunks per lane, K split over KS waves, RPW rows
+// per wave (8 waves per workgroup).
 struct GemvShape {
-  int J, KS, RPW, NW;
+  int J, KS, RPW;
 };
 
 static constexpr int kJ[] = {1, 2, 3, 4, 5, 6, 8};
-static constexpr int kRPW[] = {1, 2, 3, 4, 5, 6, 8};
+static constexpr int kRPW1[] = {1, 2, 3, 4, 5, 6, 8};
+static constexpr int kRPW2[] = {1, 2, 3, 4};
 static constexpr int kCUs = 256;
 static constexpr size_t kLdsPerCU = 160 * 1024;
 
 // Dynamic LDS of one workgroup (the table is static).
-static size_t gemv_dyn_lds(const GemvShape& g, int dt, int K, int bs_shift) {
-  const size_t rows_wg = (size_t)(g.NW / g.KS) * g.RPW;
-  const size_t sc = (rows_wg * (K >> bs_shift) + 3) & ~(size_t)3;
-  return 4 * (256 + 256 + GEMV_MAX_WAVES + (size_t)GEMV_MAX_WAVES * g.RPW + sc) +
-         (dt == DT_BF16 ? 2 * (size_t)K : 0);
+static size_t gemv_dyn_lds(const GemvShape& g, int nm, int K, int bs_shift) {
+  const size_t rows_wg = (size_t)(GEMV_WAVES / g.KS) * g.RPW;
+  const size_t sc = ((size_t)nm * rows_wg * (K >> bs_shift) + 3) & ~(size_t)3;
+  return 4 * (256 + 256 * (size_t)nm + 2 * GEMV_WAVES + (size_t)GEMV_WAVES * nm * g.RPW + sc) + 2 * (size_t)K;
 }
 
 // K is split (KS a power of two) so that a lane's chunks J <= 8 leave the
-// fewest slots idle; workgroups are 8 waves wide, because every workgroup
-// builds the 64 KiB table and converts x once; and RPW is the
-// smallest that fits every row into one pass of the workgroups the LDS lets
-// each CU hold.
-static GemvShape gemv_shape(int M, int K, int dt = DT_F16, int bs_shift = 6) {
+// fewest slots idle; RPW is the smallest that fits every row into one pass of
+// the workgroups the LDS lets each CU hold (every workgroup builds the 64 KiB
+// table and stages x once, so fewer, fuller workgroups pay less of that).
+static GemvShape gemv_shape(int M, int K, int nm = 1, int bs_shift = 6) {
   const int chunks = (K / 8 + 63) / 64;  // 64-dword chunks per row
   int KS = 0, J = 0, waste = 1 << 30;
   for (int ks = 1; ks <= GEMV_WAVES; ks *= 2) {
@@ -423,59 +464,50 @@ static GemvShape gemv_shape(int M, int K, int dt = DT_F16, int bs_shift = 6) {
       if (v >= (chunks + ks - 1) / ks) { j = v; break; }
     if (j && ks * j - chunks < waste) { KS = ks; J = j; waste = ks * j - chunks; }
   }
-  if (!KS) return {0, 0, 0, 0};
-  const int NW = GEMV_WAVES;
-  const int RG = NW / KS;
-  GemvShape g{J, KS, kRPW[0], NW};
-  for (int v : kRPW) {
-    g.RPW = v;
-    const size_t per_wg = LUT_BYTES + gemv_dyn_lds(g, dt, K, bs_shift);
+  if (!KS) return {0, 0, 0};
+  const int RG = GEMV_WAVES / KS;
+  GemvShape g{J, KS, 1};
+  const int* rpw = nm == 1 ? kRPW1 : kRPW2;
+  const int nrpw = nm == 1 ? (int)(sizeof(kRPW1) / sizeof(int)) : (int)(sizeof(kRPW2) / sizeof(int));
+  for (int i = 0; i < nrpw; ++i) {
+    g.RPW = rpw[i];
+    const size_t per_wg = LUT_BYTES + gemv_dyn_lds(g, nm, K, bs_shift);
     const long long slots = (long long)kCUs * (long long)(kLdsPerCU / per_wg);
-    if ((long long)(M + RG * v - 1) / (RG * v) <= slots) break;
+    if ((long long)(M + RG * g.RPW - 1) / (RG * g.RPW) <= slots) break;
   }
   return g;
 }
 
-template <int DT, int J, int RPW, bool NESTED>
-static void launch_gemv(const GemvShape& g, const void* X, const uint8_t* W, const uint8_t* A8,
-                        const float* AMAX, const float* CODE2, float offset, const float* LUT,
-                        void* Y, const void* R, int epi, int M, int K, int bs_shift, int bs2_shift,
-                        hipStream_t st) {
-  const int RG = g.NW / g.KS;
-  const int rows_wg = RG * RPW;
-  const int grid = (M + rows_wg - 1) / rows_wg;
-  const size_t shmem = gemv_dyn_lds(g, DT, K, bs_shift);
-  hipLaunchKernelGGL((nf4_gemv_kernel<DT, J, RPW, NESTED>), dim3(grid), dim3(64 * g.NW), shmem, st,
-                     (const uint32_t*)W, A8, AMAX, CODE2, offset, LUT, (const uint16_t*)X,
-                     (uint16_t*)Y, (const uint16_t*)R, epi, M, K, g.KS, bs_shift, bs2_shift);
+template <int J, int RPW, int NM>
+static void launch_gemv(const GemvShape& g, const GemvParams& p, hipStream_t st) {
+  const int rows_wg = (GEMV_WAVES / g.KS) * RPW;
+  const int grid = (p.M + rows_wg - 1) / rows_wg;
+  hipLaunchKernelGGL((nf4_gemv_kernel<J, RPW, NM>), dim3(grid), dim3(GEMV_THREADS),
+                     gemv_dyn_lds(g, NM, p.K, p.bs_shift), st, p);
 }
 
-template <int DT, int J, bool NESTED>
-static int dispatch_rpw(const GemvShape& g, const void* X, const uint8_t* W, const uint8_t* A8,
-                        const float* AMAX, const float* CODE2, float offset, const float* LUT,
-                        void* Y, const void* R, int epi, int M, int K, int bs_shift, int bs2_shift,
-                        hipStream_t st) {
-#define TTSP_R(RV)                                                                                   \
-  case RV:                                                                                           \
-    launch_gemv<DT, J, RV, NESTED>(g, X, W, A8, AMAX, CODE2, offset, LUT, Y, R, epi, M, K, bs_shift, \
-                                   bs2_shift, st);                                                   \
-    return 0;
-  switch (g.RPW) {
-    TTSP_R(1) TTSP_R(2) TTSP_R(3) TTSP_R(4) TTSP_R(5) TTSP_R(6) TTSP_R(8)
-    default: return (int)hipErrorInvalidValue;
+template <int J, int NM>
+static int dispatch_rpw(const GemvShape& g, const GemvParams& p, hipStream_t st) {
+#define TTSP_R(RV) \
+  case RV: launch_gemv<J, RV, NM>(g, p, st); return 0;
+  if constexpr (NM == 1) {
+    switch (g.RPW) {
+      TTSP_R(1) TTSP_R(2) TTSP_R(3) TTSP_R(4) TTSP_R(5) TTSP_R(6) TTSP_R(8)
+      default: return (int)hipErrorInvalidValue;
+    }
+  } else {
+    switch (g.RPW) {
+      TTSP_R(1) TTSP_R(2) TTSP_R(3) TTSP_R(4)
+      default: return (int)hipErrorInvalidValue;
+    }
   }
 #undef TTSP_R
 }
 
-template <int DT, bool NESTED>
-static int dispatch_j(const GemvShape& g, const void* X, const uint8_t* W, const uint8_t* A8,
-                      const float* AMAX, const float* CODE2, float offset, const float* LUT,
-                      void* Y, const void* R, int epi, int M, int K, int bs_shift, int bs2_shift,
-                      hipStream_t st) {
-#define TTSP_J(JV)                                                                                 \
-  case JV:                                                                                         \
-    return dispatch_rpw<DT, JV, NESTED>(g, X, W, A8, AMAX, CODE2, offset, LUT, Y, R, epi, M, K,   \
-                                        bs_shift, bs2_shift, st);
+template <int NM>
+static int dispatch_j(const GemvShape& g, const GemvParams& p, hipStream_t st) {
+#define TTSP_J(JV) \
+  case JV: return dispatch_rpw<JV, NM>(g, p, st);
   switch (g.J) {
     TTSP_J(1) TTSP_J(2) TTSP_J(3) TTSP_J(4) TTSP_J(5) TTSP_J(6) TTSP_J(8)
     default: return (int)hipErrorInvalidValue;
@@ -490,30 +522,58 @@ static int log2_exact(int v) {
   return s;
 }
 
+// Validates, fills GemvParams and launches. mat3 == nullptr: one weight with
+// epilogue `epi`; otherwise the SwiGLU pair (epi must be 0). G != nullptr
+// folds the RMSNorm prologue in.
+static int gemv_launch(const void* X, int dt, const void* G, float eps, const Nf4Mat& mat1,
+                       const Nf4Mat* mat3, bool nested, const float* LUT, void* Y, const void* R,
+                       int epi, int M, int K, int blocksize, int blocksize2, hipStream_t st) {
+  const int bs_shift = log2_exact(blocksize);
+  const int bs2_shift = nested ? log2_exact(blocksize2) : 0;
+  if (bs_shift < 6 || bs2_shift < 0 || K % 128 || K % blocksize || M <= 0) return (int)hipErrorInvalidValue;
+  if (dt != DT_F16 && dt != DT_BF16) return (int)hipErrorInvalidValue;
+  if (epi < 0 || epi > 2 || (epi && !R) || (mat3 && epi)) return (int)hipErrorInvalidValue;
+  if (K / 8 > XC_MAX * STAGE_THREADS) return (int)hipErrorInvalidValue;
+  const int nm = mat3 ? 2 : 1;
+  const GemvShape g = gemv_shape(M, K, nm, bs_shift);
+  if (!g.J) return (int)hipErrorInvalidValue;
+  if (LUT_BYTES + gemv_dyn_lds(g, nm, K, bs_shift) > kLdsPerCU) return (int)hipErrorInvalidValue;
+  GemvParams p;
+  p.mat[0] = mat1;
+  p.mat[1] = mat3 ? *mat3 : mat1;
+  for (Nf4Mat& m : p.mat) {
+    if (!nested) {  // unused operands point at readable memory
+      m.A8 = reinterpret_cast<const uint8_t*>(m.AMAX);
+      m.CODE2 = m.AMAX;
+      m.offset = 0.0f;
+    }
+  }
+  p.LUT = LUT;
+  p.X = (const uint16_t*)X;
+  p.G = G ? (const uint16_t*)G : (const uint16_t*)X;
+  p.Y = (uint16_t*)Y;
+  p.R = epi ? (const uint16_t*)R : (const uint16_t*)Y;  // read unconditionally, used by the epilogue only
+  p.eps = eps;
+  p.M = M;
+  p.K = K;
+  p.KS = g.KS;
+  p.bs_shift = bs_shift;
+  p.bs2_shift = bs2_shift;
+  p.dt = dt;
+  p.nested = nested ? 1 : 0;
+  p.norm = G ? 1 : 0;
+  p.epi = epi;
+  const int rc = nm == 1 ? dispatch_j<1>(g, p, st) : dispatch_j<2>(g, p, st);
+  if (rc) return rc;
+  TTSP_RETURN_LAUNCH();
+}
+
 int gemv_n1(const void* X, int dt, const uint8_t* W, const uint8_t* A8, const float* AMAX,
             const float* CODE2, float offset, const float* LUT, void* Y, const void* R, int epi,
             int M, int K, int blocksize, int blocksize2, hipStream_t st) {
-  const int bs_shift = log2_exact(blocksize);
-  const int bs2_shift = A8 ? log2_exact(blocksize2) : 0;
-  if (bs_shift < 6 || bs2_shift < 0 || K % 128 || K % blocksize || M <= 0) return (int)hipErrorInvalidValue;
-  if (epi < 0 || epi > 2 || (epi && !R)) return (int)hipErrorInvalidValue;
-  if (!epi) R = Y;  // the kernel reads R unconditionally (an M-element buffer); unused without an epilogue
-  const GemvShape g = gemv_shape(M, K, dt, bs_shift);
-  if (!g.J || g.KS > GEMV_MAX_WAVES) return (int)hipErrorInvalidValue;
-  // the workgroup's scales (and bf16 x) must fit next to the table
-  if (LUT_BYTES + gemv_dyn_lds(g, dt, K, bs_shift) > 160 * 1024) return (int)hipErrorInvalidValue;
-  if (dt == DT_BF16 && (K / 8 + 64 * g.NW - 1) / (64 * g.NW) > XC_MAX) return (int)hipErrorInvalidValue;
-  int rc;
-  if (dt == DT_F16)
-    rc = A8 ? dispatch_j<DT_F16, true>(g, X, W, A8, AMAX, CODE2, offset, LUT, Y, R, epi, M, K, bs_shift, bs2_shift, st)
-            : dispatch_j<DT_F16, false>(g, X, W, A8, AMAX, CODE2, offset, LUT, Y, R, epi, M, K, bs_shift, bs2_shift, st);
-  else if (dt == DT_BF16)
-    rc = A8 ? dispatch_j<DT_BF16, true>(g, X, W, A8, AMAX, CODE2, offset, LUT, Y, R, epi, M, K, bs_shift, bs2_shift, st)
-            : dispatch_j<DT_BF16, false>(g, X, W, A8, AMAX, CODE2, offset, LUT, Y, R, epi, M, K, bs_shift, bs2_shift, st);
-  else
-    return (int)hipErrorInvalidValue;
-  if (rc) return rc;
-  TTSP_RETURN_LAUNCH();
+  const Nf4Mat m{reinterpret_cast<const uint32_t*>(W), A8, AMAX, CODE2, offset};
+  return gemv_launch(X, dt, nullptr, 0.0f, m, nullptr, A8 != nullptr, LUT, Y, R, epi, M, K, blocksize,
+                     blocksize2, st);
 }
 
 }  // namespace ttsp
@@ -528,25 +588,20 @@ extern "C" int ttsp_gemv_shape(int M, int K, int* J, int* KS, int* RPW) {
   return g.J ? 0 : (int)hipErrorInvalidValue;
 }
 
-extern "C" int ttsp_nf4_dequant(const uint8_t* W, const uint8_t* A8, const float* AMAX,
-                                const float* CODE2, float offset, const float* LUT, void* out,
-                                int out_dtype, long long n, int blocksize, int blocksize2,
-                                hipStream_t stream) {
-  const int bs_shift = log2_exact(blocksize);
-  const int bs2_shift = A8 ? log2_exact(blocksize2) : 0;
-  if (bs_shift < 6 || bs2_shift < 0 || n < 0) return (int)hipErrorInvalidValue;
-  if (n == 0) return 0;
-  const long long threads = (n + 15) / 16;
-  const dim3 grid((unsigned)((threads + 255) / 256));
-#define TTSP_DQ(ODT, NESTED)                                                                  \
-  hipLaunchKernelGGL((nf4_dequant_kernel<ODT, NESTED>), grid, dim3(256), 0, stream, W, A8, AMAX, \
-                     CODE2, offset, LUT, out, n, bs_shift, bs2_shift)
-  switch (out_dtype) {
-    case DT_F16: if (A8) TTSP_DQ(DT_F16, true); else TTSP_DQ(DT_F16, false); break;
-    case DT_BF16: if (A8) TTSP_DQ(DT_BF16, true); else TTSP_DQ(DT_BF16, false); break;
-    case DT_F32: if (A8) TTSP_DQ(DT_F32, true); else TTSP_DQ(DT_F32, false); break;
-    default: return (int)hipErrorInvalidValue;
-  }
-#undef TTSP_DQ
-  TTSP_RETURN_LAUNCH();
+extern "C" int ttsp_nf4_gemv_fused(const void* X, int x_dtype, const void* NORM_W, float eps,
+                                   const uint8_t* W1, const uint8_t* A8_1, const float* AMAX_1,
+                                   const float* CODE2_1, float offset_1, const uint8_t* W3,
+                                   const uint8_t* A8_3, const float* AMAX_3, const float* CODE2_3,
+                                   float offset_3, const float* LUT, void* Y, const void* R, int epi,
+                                   int M, int K, int blocksize, int blocksize2, hipStream_t stream) {
+  if (!X || !W1 || !AMAX_1 || !LUT || !Y || M <= 0 || K <= 0) return (int)hipErrorInvalidValue;
+  const bool nested = A8_1 != nullptr;
+  if (nested && !CODE2_1) return (int)hipErrorInvalidValue;
+  const Nf4Mat m1{reinterpret_cast<const uint32_t*>(W1), A8_1, AMAX_1, CODE2_1, offset_1};
+  if (!W3) return gemv_launch(X, x_dtype, NORM_W, eps, m1, nullptr, nested, LUT, Y, R, epi, M, K, blocksize,
+                              blocksize2, stream);
+  if (!AMAX_3 || (A8_3 != nullptr) != nested || (nested && !CODE2_3)) return (int)hipErrorInvalidValue;
+  const Nf4Mat m3{reinterpret_cast<const uint32_t*>(W3), A8_3, AMAX_3, CODE2_3, offset_3};
+  return gemv_launch(X, x_dtype, NORM_W, eps, m1, &m3, nested, LUT, Y, R, epi, M, K, blocksize, blocksize2,
+                     stream);
 }

@@ -1,10 +1,15 @@
-"""One decode position through a transformer block in ten HIP launches.
+"""One decode position through a transformer block in seven HIP launches.
 
 Drop-in for the reference's `app/engine/fusedlayer.py` (`decode_block`,
 `install`, `stats`, `HEAD_DIM`, `CHUNK`):
 
-    rms_norm -> wqkv -> qk_rope_kv -> attn_partial -> attn_combine
-             -> wo(+x) -> rms_norm -> w1 -> w3(silu(w1) * .) -> w2(+h)
+    [rms_norm + wqkv] -> qk_rope_kv -> attn_partial -> attn_combine
+        -> wo(+x) -> [rms_norm + w1, w3 as silu(w1) * w3] -> w2(+h)
+
+The bracketed steps are single launches (`nf4gemv.matmul_fused`): the norm
+runs in the matmul's prologue with the standalone kernel's exact arithmetic,
+and w1/w3 stream through the same waves with the gate in the epilogue; the
+results are bit-identical to the reference's ten-launch order.
 
 `qk_rope_kv` does the head norms, rotary and KV-cache write for every head in
 one launch; attention is split-K over CHUNK-position slices of the cache (one
@@ -89,12 +94,13 @@ def decode_block(block, x, freqs_cis, mask, input_pos, *, workspace=None):
     lib = _lib.lib()
     st = _lib.stream()
 
-    xn = fusedops.rms_norm(x, block.attention_norm.weight, block.attention_norm.eps, out=ws["xn"])
-    if xn is None:
-        return None
-    qkv = nf4gemv.matmul(a.wqkv, xn, out=ws["qkv"])
-    if qkv is None:
-        return None
+    an, fn = block.attention_norm, block.ffn_norm
+    qkv = nf4gemv.matmul_fused(a.wqkv, x, norm_weight=an.weight, eps=an.eps, out=ws["qkv"])
+    if qkv is None:  # the unfused pair: norm, then matmul
+        xn = fusedops.rms_norm(x, an.weight, an.eps, out=ws["xn"])
+        qkv = None if xn is None else nf4gemv.matmul(a.wqkv, xn, out=ws["qkv"])
+        if qkv is None:
+            return None
     qn = getattr(a, "q_norm", None) if a.attention_qk_norm else None
     kn = getattr(a, "k_norm", None) if a.attention_qk_norm else None
     eps = float(qn.eps if qn is not None and qn.eps is not None else 1e-6)
@@ -109,12 +115,16 @@ def decode_block(block, x, freqs_cis, mask, input_pos, *, workspace=None):
         ws["y"].data_ptr(), nh, nkv, max_len, nchunk, float(HEAD_DIM**-0.5), dt, st)
     _lib.check(rc, "ttsp_attn_decode")
     h = nf4gemv.matmul(a.wo, ws["y"], epi=nf4gemv.EPI_RESIDUAL, operand=x, out=ws["h"])
-    hn = fusedops.rms_norm(h, block.ffn_norm.weight, block.ffn_norm.eps, out=ws["hn"])
-    g1 = nf4gemv.matmul(ff.w1, hn, out=ws["g1"])
-    g = nf4gemv.matmul(ff.w3, hn, epi=nf4gemv.EPI_SILU_GATE, operand=g1, out=ws["g"])
+    if h is None:
+        raise RuntimeError("decode_block: a prepared layer declined mid-block")
+    g = nf4gemv.matmul_fused(ff.w1, h, norm_weight=fn.weight, eps=fn.eps, module3=ff.w3, out=ws["g"])
+    if g is None:  # the unfused chain: norm, w1, w3 with the gate epilogue
+        hn = fusedops.rms_norm(h, fn.weight, fn.eps, out=ws["hn"])
+        g1 = None if hn is None else nf4gemv.matmul(ff.w1, hn, out=ws["g1"])
+        g = None if g1 is None else nf4gemv.matmul(ff.w3, hn, epi=nf4gemv.EPI_SILU_GATE, operand=g1, out=ws["g"])
     out = ws.get("out")
-    out = nf4gemv.matmul(ff.w2, g, epi=nf4gemv.EPI_RESIDUAL, operand=h, out=out)
-    if any(t is None for t in (h, hn, g1, g, out)):
+    out = None if g is None else nf4gemv.matmul(ff.w2, g, epi=nf4gemv.EPI_RESIDUAL, operand=h, out=out)
+    if g is None or out is None:
         raise RuntimeError("decode_block: a prepared layer declined mid-block")
     _stats["fused"] += 1
     return out.view(x.shape)

@@ -204,6 +204,64 @@ def matmul(module, x, *, epi: int = EPI_NONE, operand=None, out=None):
     return out.view(*x.shape[:-1], M)
 
 
+#: Widest input the fused single-row kernel stages (`ttsp_nf4_gemv_fused`).
+FUSED_MAX_K = 10240
+
+
+def matmul_fused(module, x, *, norm_weight=None, eps: float = 1e-6, module3=None, epi: int = EPI_NONE,
+                 operand=None, out=None):
+    """One input row through `module` in a single launch, or None if not applicable.
+
+    `norm_weight` folds the fork's RMSNorm of x in (bit-identical to
+    `fusedops.rms_norm` then `matmul`); `module3` (same shape and scales
+    layout as `module`) makes it the SwiGLU pair: silu(x W1) * (x W3), rounded
+    as the two-launch form `matmul(w3, epi=EPI_SILU_GATE, operand=matmul(w1))`.
+    """
+    import torch
+
+    fast = getattr(module, "_nf4_fast", None)
+    if fast is None:
+        return None
+    dt = _lib.dtype_code(x.dtype)
+    if dt not in (_lib.DT_F16, _lib.DT_BF16) or x.device.type != "cuda":
+        return None
+    K, M = fast["K"], fast["M"]
+    if x.shape[-1] != K or x.numel() != K or K > FUSED_MAX_K or not x.is_contiguous() or x.data_ptr() % 16:
+        return None
+    fast3 = None
+    if module3 is not None:
+        fast3 = getattr(module3, "_nf4_fast", None)
+        if fast3 is None or epi != EPI_NONE:
+            return None
+        if (fast3["M"], fast3["K"], fast3["nested"], fast3["bs"], fast3["bs2"]) != (M, K, fast["nested"], fast["bs"],
+                                                                                  fast["bs2"]):
+            return None
+    if norm_weight is not None:
+        if (norm_weight.dtype != x.dtype or norm_weight.numel() != K or not norm_weight.is_contiguous()
+                or norm_weight.data_ptr() % 16 or norm_weight.device != x.device):
+            return None
+    if epi != EPI_NONE:
+        if operand is None or operand.numel() != M or operand.dtype != x.dtype:
+            return None
+        if operand.device != x.device or not operand.is_contiguous():
+            return None
+    if out is None:
+        out = torch.empty((1, M), dtype=x.dtype, device=x.device)
+    elif out.dtype != x.dtype or out.numel() != M or not out.is_contiguous():
+        return None
+    f3 = fast3 or {"w": 0, "a8": 0, "amax": 0, "code2": 0, "offset": 0.0}
+    rc = _lib.lib().ttsp_nf4_gemv_fused(
+        x.data_ptr(), dt, _lib.ptr(norm_weight), float(eps),
+        fast["w"], fast["a8"], fast["amax"], fast["code2"], fast["offset"],
+        f3["w"], f3["a8"], f3["amax"], f3["code2"], f3["offset"],
+        fast["lut"].data_ptr(), out.data_ptr(), _lib.ptr(operand) if epi else 0, epi, M, K,
+        fast["bs"], fast["bs2"], _lib.stream())
+    if rc:
+        raise RuntimeError(f"ttsp_nf4_gemv_fused failed: hipError_t {rc}")
+    _stats["fast"] += 2 if fast3 is not None else 1
+    return out.view(*x.shape[:-1], M)
+
+
 def _classes():
     """Linear4bit classes to patch: ours, and bitsandbytes' where it is importable."""
     from ttspipe_amd.quant import Linear4bit
