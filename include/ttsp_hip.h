@@ -108,6 +108,20 @@ int ttsp_attn_decode(const void* Q, const void* KC, const void* VC, const long l
                      float* PL, float* PACC, void* Y, int nh, int nkv, int max_len, int nchunk,
                      float scale, int dtype, void* stream);
 
+/* qk_rope_kv and the decode attention in one pass: the head norms and rotary
+ * of the query heads are applied inside the attention workgroups (from QKV),
+ * the new position's K/V row is computed, written to KC/VC[kv][POS[0]] and used
+ * by the chunk that holds it; Y [nh*128] as ttsp_attn_decode. With nchunk == 1
+ * the merge happens in place (PM/PL/PACC may be NULL); otherwise a second
+ * launch merges the chunks. Nothing is written if POS[0] is outside
+ * [0, max_len). Results equal ttsp_qk_rope_kv followed by ttsp_attn_decode
+ * bit for bit. Replaces: qk_rope_kv + attn_partial + attn_combine,
+ * app/engine/fusedlayer.py:56-159, 233-261. */
+int ttsp_attn_decode_qkv(const void* QKV, const void* QW, const void* KW, float eps, const void* F,
+                         int ftype, const long long* POS, void* KC, void* VC, float* PM, float* PL,
+                         float* PACC, void* Y, int nh, int nkv, int max_len, int nchunk, float scale,
+                         int dtype, void* stream);
+
 /* Cache positions per attention chunk (64). Replaces: CHUNK,
  * app/engine/fusedlayer.py:40. */
 int ttsp_attn_chunk(void);

@@ -184,6 +184,48 @@ def test_decode_attention_bit_exact(hip, orc, L, dtype):
     assert relative_error(o.to_f32(bits(y), dt), ref) < 5e-3
 
 
+@pytest.mark.parametrize("qk_norm", [True, False])
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("pos,max_len,nh,nkv", [(0, 2304, 32, 8), (37, 2304, 32, 8), (63, 2304, 32, 8),
+                                                (64, 2304, 32, 8), (2047, 2304, 32, 8), (2303, 2304, 32, 8),
+                                                (0, 16, 8, 2), (9, 16, 8, 2), (15, 16, 8, 2), (100, 128, 4, 1)])
+def test_attention_from_qkv_bit_exact(hip, orc, qk_norm, dtype, pos, max_len, nh, nkv):
+    """One pass (head norms, rotary, KV write, attention, merge) == qk_rope_kv then
+    the split-K attention, through the oracle's emulations, and the cache rows."""
+    from ttspipe_amd import _lib
+    from ttspipe_amd.llama import precompute_freqs_cis
+
+    dt = dt_code(dtype)
+    nchunk = -(-max_len // 64)
+    qkvb = randn_bits((nh + 2 * nkv) * 128, dtype, seed=pos + 11, scale=2.0)
+    qwb = o.from_f32((np.random.default_rng(5).random(128) + 0.5).astype(np.float32), dt)
+    kwb = o.from_f32((np.random.default_rng(6).random(128) + 0.5).astype(np.float32), dt)
+    freqs = precompute_freqs_cis(max_len, 128, 1e6)[pos : pos + 1].contiguous()
+    kcb = randn_bits(nkv * max_len * 128, dtype, seed=pos + 12)
+    vcb = randn_bits(nkv * max_len * 128, dtype, seed=pos + 13)
+    KC, VC = from_bits(kcb, dtype), from_bits(vcb, dtype)
+    f32 = dict(dtype=torch.float32, device="cuda")
+    pm, pl, pacc = torch.empty(nh * nchunk, **f32), torch.empty(nh * nchunk, **f32), torch.empty(nh * nchunk * 128, **f32)
+    y = torch.empty(nh * 128, dtype=dtype, device="cuda")
+    qw = from_bits(qwb, dtype) if qk_norm else None
+    kw = from_bits(kwb, dtype) if qk_norm else None
+    posd = torch.tensor([pos], dtype=torch.long, device="cuda")
+    fd, qkv = freqs.cuda(), from_bits(qkvb, dtype)
+    rc = hip.ttsp_attn_decode_qkv(qkv.data_ptr(), _lib.ptr(qw), _lib.ptr(kw), 1e-6, fd.data_ptr(), o.DT_BF16,
+                                  posd.data_ptr(), KC.data_ptr(), VC.data_ptr(), pm.data_ptr(), pl.data_ptr(),
+                                  pacc.data_ptr(), y.data_ptr(), nh, nkv, max_len, nchunk, float(128**-0.5), dt,
+                                  _lib.stream())
+    assert rc == 0
+    Qo = np.zeros(nh * 128, np.uint16)
+    KCo, VCo = kcb.copy(), vcb.copy()
+    orc.qk_rope_kv(qkvb, qwb if qk_norm else None, kwb if qk_norm else None, 1e-6, bits(freqs), o.DT_BF16, pos,
+                   Qo, KCo, VCo, nh, nkv, max_len, dt)
+    expect = orc.attn_emul(Qo, KCo, VCo, pos, nh, nkv, max_len, nchunk, 128**-0.5, dt)
+    assert np.array_equal(bits(y), expect), first_mismatch(bits(y), expect)
+    assert np.array_equal(bits(KC), KCo), first_mismatch(bits(KC), KCo)
+    assert np.array_equal(bits(VC), VCo)
+
+
 def test_decode_attention_matches_torch_gqa():
     """Against torch SDPA with enable_gqa on the CPU, the reference's check
     (tests/test_nf4gemv.py:224-242)."""

@@ -12,7 +12,15 @@
 // q * 1/sqrt(128)), the wave takes the chunk max and sum of exp(s - max), and
 // lane l accumulates dims 2l, 2l+1 over the chunk's positions in order.
 // attn_combine merges chunks with the log-sum-exp rule, chunks in order.
-// Both are deterministic: no atomics, fixed orders.
+//
+// attn_qkv fuses the three: each workgroup of the split-K attention reads its
+// query heads straight from QKV and applies the head norm and rotary itself
+// (the arithmetic of qk_rope_kv, one wave per head, lane l holding elements l
+// and l + 64), the workgroup whose chunk holds the new position also computes
+// that K/V row, writes it to the cache and uses it from registers; with one
+// chunk (a short cache) the workgroup finishes the merge in place, so the
+// whole attention of a decode step is one launch (two for long caches).
+// All of these are deterministic: no atomics, fixed orders.
 #include "ttsp_common.h"
 
 namespace ttsp {
@@ -137,25 +145,203 @@ __global__ __launch_bounds__(1024) void attn_partial_kernel(
   reinterpret_cast<float2*>(PACC + slot * HD)[lane] = make_float2(a0, a1);
 }
 
+// Merge of the chunk partials of one query head: chunk weights w_c =
+// exp(m_c - max m) are computed once per chunk (one thread each) into LDS,
+// then every thread (one output dimension) folds the chunks in order:
+// den += l_c * w_c, num += acc_c[d] * w_c, y = num / den. Chunks with l = 0
+// (past the live positions) are skipped.
 template <int DT>
 __global__ __launch_bounds__(HD) void attn_combine_kernel(const float* __restrict__ PM,
                                                           const float* __restrict__ PL,
                                                           const float* __restrict__ PACC,
                                                           uint16_t* __restrict__ Y, int nchunk) {
+  extern __shared__ float cs[];  // [nchunk] m, then [nchunk] l, then [nchunk] w
+  float* pm_s = cs;
+  float* pl_s = cs + nchunk;
+  float* w_s = cs + 2 * nchunk;
   const int qh = blockIdx.x, d = threadIdx.x;
   const float* pm = PM + (size_t)qh * nchunk;
   const float* pl = PL + (size_t)qh * nchunk;
+  for (int c = d; c < nchunk; c += HD) {
+    pm_s[c] = pm[c];
+    pl_s[c] = pl[c];
+  }
+  __syncthreads();
   float M = -3.0e38f;
-  for (int c = 0; c < nchunk; ++c) M = fmaxf(M, pm[c]);
+  for (int c = 0; c < nchunk; ++c) M = fmaxf(M, pm_s[c]);
+  for (int c = d; c < nchunk; c += HD) w_s[c] = pl_s[c] == 0.0f ? 0.0f : exp_cw(__fsub_rn(pm_s[c], M));
+  __syncthreads();
+  const float* acc = PACC + (size_t)qh * nchunk * HD + d;
   float num = 0.0f, den = 0.0f;
-  for (int c = 0; c < nchunk; ++c) {
-    const float l = pl[c];
+  int c = 0;
+  for (; c + 4 <= nchunk; c += 4) {  // four independent loads in flight
+    const float a0 = acc[(size_t)c * HD], a1 = acc[(size_t)(c + 1) * HD];
+    const float a2 = acc[(size_t)(c + 2) * HD], a3 = acc[(size_t)(c + 3) * HD];
+    const float av[4] = {a0, a1, a2, a3};
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const float l = pl_s[c + k];
+      if (l == 0.0f) continue;
+      const float w = w_s[c + k];
+      den = __fadd_rn(den, __fmul_rn(l, w));
+      num = __fadd_rn(num, __fmul_rn(av[k], w));
+    }
+  }
+  for (; c < nchunk; ++c) {
+    const float l = pl_s[c];
     if (l == 0.0f) continue;
-    const float w = exp_cw(__fsub_rn(pm[c], M));
+    const float w = w_s[c];
     den = __fadd_rn(den, __fmul_rn(l, w));
-    num = __fadd_rn(num, __fmul_rn(PACC[((size_t)qh * nchunk + c) * HD + d], w));
+    num = __fadd_rn(num, __fmul_rn(acc[(size_t)c * HD], w));
   }
   Y[(size_t)qh * HD + d] = Elem<DT>::store(__fdiv_rn(num, den));
+}
+
+// Head norm and rotary of one 128-wide head held by a wave (lane l: elements
+// l and l + 64), the arithmetic of qk_rope_kv_kernel: the norm's sum is the
+// two 64-element halves (xor butterflies) added, one rounding after x * r * w;
+// rotary pairs (2i, 2i+1) with the partner in lane l ^ 1, separately rounded
+// products and sum. Returns the rotated values, not yet rounded.
+template <int DT>
+__device__ __forceinline__ void head_norm_rope(float& lo, float& hi, const uint16_t* __restrict__ NW, float eps,
+                                               const void* __restrict__ F, int ftype, int lane) {
+  if (NW != nullptr) {
+    const float ss = __fadd_rn(wave_sum(__fmul_rn(lo, lo)), wave_sum(__fmul_rn(hi, hi)));
+    const float r = rsqrt_rn(__fadd_rn(__fdiv_rn(ss, (float)HD), eps));
+    lo = Elem<DT>::load(Elem<DT>::store(__fmul_rn(__fmul_rn(lo, r), Elem<DT>::load(NW[lane]))));
+    hi = Elem<DT>::load(Elem<DT>::store(__fmul_rn(__fmul_rn(hi, r), Elem<DT>::load(NW[lane + 64]))));
+  }
+  const float plo = __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(lo), 0xB1, 0xF, 0xF, false));
+  const float phi = __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(hi), 0xB1, 0xF, 0xF, false));
+  const int e = lane & ~1;  // the pair's even element (lo half; the hi half is e + 64)
+  const float frl = load_elem(F, e, ftype), fil = load_elem(F, e + 1, ftype);
+  const float frh = load_elem(F, e + 64, ftype), fih = load_elem(F, e + 65, ftype);
+  if (lane & 1) {
+    lo = __fadd_rn(__fmul_rn(lo, frl), __fmul_rn(plo, fil));
+    hi = __fadd_rn(__fmul_rn(hi, frh), __fmul_rn(phi, fih));
+  } else {
+    lo = __fsub_rn(__fmul_rn(lo, frl), __fmul_rn(plo, fil));
+    hi = __fsub_rn(__fmul_rn(hi, frh), __fmul_rn(phi, fih));
+  }
+}
+
+// Attention of one decode position straight from QKV (see the file comment).
+// Workgroup (kv head kh, chunk c), one wave per query head of the group.
+template <int DT>
+__global__ __launch_bounds__(1024) void attn_qkv_kernel(
+    const uint16_t* __restrict__ QKV, const uint16_t* __restrict__ QW, const uint16_t* __restrict__ KW,
+    float eps, const void* __restrict__ F, int ftype, const long long* __restrict__ POS,
+    uint16_t* __restrict__ KC, uint16_t* __restrict__ VC, float* __restrict__ PM, float* __restrict__ PL,
+    float* __restrict__ PACC, uint16_t* __restrict__ Y, int nh, int nkv, int groups, int max_len, int nchunk,
+    float scale) {
+  extern __shared__ float smem[];
+  float* q_s = smem;                                                   // [groups][HD]
+  float* p_s = q_s + groups * HD;                                      // [groups][ACHUNK]
+  uint16_t* k_s = reinterpret_cast<uint16_t*>(p_s + groups * ACHUNK);  // [ACHUNK][KPAD]
+  uint16_t* v_s = k_s + ACHUNK * KPAD;                                 // [ACHUNK][HD]
+
+  const int kh = blockIdx.x, c = blockIdx.y;
+  const int tid = threadIdx.x, nthr = blockDim.x;
+  const int g = tid >> 6, lane = tid & 63;
+  const int qh = kh * groups + g;
+  const long long pos = POS[0];
+  if (pos < 0 || pos >= max_len) return;  // no cache slot for it: nothing is written
+  const long long L = pos + 1;
+  const long long j0 = (long long)c * ACHUNK;
+  const size_t slot = (size_t)qh * nchunk + c;
+  if (j0 >= L) {  // a chunk past the live positions (only with nchunk > 1)
+    if (lane == 0) {
+      PM[slot] = -1e30f;
+      PL[slot] = 0.0f;
+    }
+    return;
+  }
+  const int nvalid = (int)min((long long)ACHUNK, L - j0);
+  const int jpos = (int)(pos - j0);  // the new row's place in this chunk, if < ACHUNK
+
+  // K and V rows of the chunk from the cache, except the new position's
+  const uint16_t* kb = KC + ((size_t)kh * max_len + j0) * HD;
+  const uint16_t* vb = VC + ((size_t)kh * max_len + j0) * HD;
+  for (int t = tid; t < ACHUNK * (HD / 8); t += nthr) {
+    const int j = t / (HD / 8), e = (t % (HD / 8)) * 8;
+    if (j == jpos) continue;
+    uint4 kv = make_uint4(0, 0, 0, 0), vv = make_uint4(0, 0, 0, 0);
+    if (j < nvalid) {
+      kv = *reinterpret_cast<const uint4*>(kb + (size_t)j * HD + e);
+      vv = *reinterpret_cast<const uint4*>(vb + (size_t)j * HD + e);
+    }
+    uint32_t* kd = reinterpret_cast<uint32_t*>(k_s + j * KPAD + e);  // KPAD rows are 4-byte aligned
+    kd[0] = kv.x; kd[1] = kv.y; kd[2] = kv.z; kd[3] = kv.w;
+    *reinterpret_cast<uint4*>(v_s + j * HD + e) = vv;
+  }
+  // this wave's query head: norm, rotary, rounded as the stored Q, scaled
+  {
+    float lo = Elem<DT>::load(QKV[(size_t)qh * HD + lane]);
+    float hi = Elem<DT>::load(QKV[(size_t)qh * HD + lane + 64]);
+    head_norm_rope<DT>(lo, hi, QW, eps, F, ftype, lane);
+    q_s[g * HD + lane] = __fmul_rn(Elem<DT>::load(Elem<DT>::store(lo)), scale);
+    q_s[g * HD + lane + 64] = __fmul_rn(Elem<DT>::load(Elem<DT>::store(hi)), scale);
+  }
+  // the new position's K/V row: computed by wave 0 of the chunk that holds it
+  if (jpos < ACHUNK && g == 0) {
+    float lo = Elem<DT>::load(QKV[(size_t)(nh + kh) * HD + lane]);
+    float hi = Elem<DT>::load(QKV[(size_t)(nh + kh) * HD + lane + 64]);
+    head_norm_rope<DT>(lo, hi, KW, eps, F, ftype, lane);
+    const uint16_t klo = Elem<DT>::store(lo), khi = Elem<DT>::store(hi);
+    const uint16_t vlo = QKV[(size_t)(nh + nkv + kh) * HD + lane];
+    const uint16_t vhi = QKV[(size_t)(nh + nkv + kh) * HD + lane + 64];
+    const size_t row = ((size_t)kh * max_len + pos) * HD;
+    KC[row + lane] = klo;
+    KC[row + lane + 64] = khi;
+    VC[row + lane] = vlo;
+    VC[row + lane + 64] = vhi;
+    k_s[jpos * KPAD + lane] = klo;
+    k_s[jpos * KPAD + lane + 64] = khi;
+    v_s[jpos * HD + lane] = vlo;
+    v_s[jpos * HD + lane + 64] = vhi;
+  }
+  __syncthreads();
+
+  // score of position `lane` for query head g (as attn_partial_kernel)
+  float s = 0.0f;
+  const uint32_t* kr = reinterpret_cast<const uint32_t*>(k_s + lane * KPAD);
+  const float* qg = q_s + g * HD;
+#pragma unroll 8
+  for (int i = 0; i < HD / 2; ++i) {
+    const uint32_t kk = kr[i];
+    s = __builtin_fmaf(qg[2 * i], Elem<DT>::load(kk), s);
+    s = __builtin_fmaf(qg[2 * i + 1], Elem<DT>::load(kk >> 16), s);
+  }
+  const bool valid = lane < nvalid;
+  const float m = wave_max(valid ? s : -3.0e38f);
+  const float p = valid ? exp_cw(__fsub_rn(s, m)) : 0.0f;
+  const float l = wave_sum(p);
+  p_s[g * ACHUNK + lane] = p;
+  __syncthreads();
+
+  float a0 = 0.0f, a1 = 0.0f;
+  const float* pg = p_s + g * ACHUNK;
+  for (int j = 0; j < nvalid; ++j) {
+    const float pj = pg[j];
+    const uint32_t vv = reinterpret_cast<const uint32_t*>(v_s + j * HD)[lane];
+    a0 = __builtin_fmaf(pj, Elem<DT>::load(vv), a0);
+    a1 = __builtin_fmaf(pj, Elem<DT>::load(vv >> 16), a1);
+  }
+  if (nchunk == 1) {
+    // the merge of a single chunk, as attn_combine_kernel computes it
+    const float w = exp_cw(__fsub_rn(m, m));
+    const float den = __fadd_rn(0.0f, __fmul_rn(l, w));
+    const float y0 = __fdiv_rn(__fadd_rn(0.0f, __fmul_rn(a0, w)), den);
+    const float y1 = __fdiv_rn(__fadd_rn(0.0f, __fmul_rn(a1, w)), den);
+    reinterpret_cast<uint32_t*>(Y + (size_t)qh * HD)[lane] =
+        (uint32_t)Elem<DT>::store(y0) | ((uint32_t)Elem<DT>::store(y1) << 16);
+    return;
+  }
+  if (lane == 0) {
+    PM[slot] = m;
+    PL[slot] = l;
+  }
+  reinterpret_cast<float2*>(PACC + slot * HD)[lane] = make_float2(a0, a1);
 }
 
 }  // namespace ttsp
@@ -194,12 +380,39 @@ extern "C" int ttsp_attn_decode(const void* Q, const void* KC, const void* VC,
     hipLaunchKernelGGL(attn_partial_kernel<DTV>, dim3(nkv, nchunk), dim3(64 * groups), shmem,    \
                        stream, (const uint16_t*)Q, (const uint16_t*)KC, (const uint16_t*)VC, POS, \
                        PM, PL, PACC, groups, max_len, nchunk, scale);                           \
-    hipLaunchKernelGGL(attn_combine_kernel<DTV>, dim3(nh), dim3(HD), 0, stream, PM, PL, PACC,    \
-                       (uint16_t*)Y, nchunk);                                                   \
+    hipLaunchKernelGGL(attn_combine_kernel<DTV>, dim3(nh), dim3(HD), 3 * sizeof(float) * nchunk, \
+                       stream, PM, PL, PACC, (uint16_t*)Y, nchunk);                             \
   } while (0)
   if (dtype == DT_F16) TTSP_AT(DT_F16);
   else if (dtype == DT_BF16) TTSP_AT(DT_BF16);
   else return (int)hipErrorInvalidValue;
 #undef TTSP_AT
+  TTSP_RETURN_LAUNCH();
+}
+
+extern "C" int ttsp_attn_decode_qkv(const void* QKV, const void* QW, const void* KW, float eps,
+                                    const void* F, int ftype, const long long* POS, void* KC, void* VC,
+                                    float* PM, float* PL, float* PACC, void* Y, int nh, int nkv,
+                                    int max_len, int nchunk, float scale, int dtype, hipStream_t stream) {
+  if (nh <= 0 || nkv <= 0 || nh % nkv || nchunk <= 0 || max_len <= 0 || ftype < 0 || ftype > 2)
+    return (int)hipErrorInvalidValue;
+  const int groups = nh / nkv;
+  if (groups > 16 || (nchunk > 1 && (!PM || !PL || !PACC))) return (int)hipErrorInvalidValue;
+  const size_t shmem = sizeof(float) * (size_t)groups * (HD + ACHUNK) +
+                       sizeof(uint16_t) * (size_t)ACHUNK * (KPAD + HD);
+#define TTSP_AQ(DTV)                                                                                  \
+  do {                                                                                                \
+    hipLaunchKernelGGL(attn_qkv_kernel<DTV>, dim3(nkv, nchunk), dim3(64 * groups), shmem, stream,     \
+                       (const uint16_t*)QKV, (const uint16_t*)QW, (const uint16_t*)KW, eps, F, ftype, \
+                       POS, (uint16_t*)KC, (uint16_t*)VC, PM, PL, PACC, (uint16_t*)Y, nh, nkv, groups, \
+                       max_len, nchunk, scale);                                                       \
+    if (nchunk > 1)                                                                                   \
+      hipLaunchKernelGGL(attn_combine_kernel<DTV>, dim3(nh), dim3(HD), 3 * sizeof(float) * nchunk,    \
+                         stream, PM, PL, PACC, (uint16_t*)Y, nchunk);                                 \
+  } while (0)
+  if (dtype == DT_F16) TTSP_AQ(DT_F16);
+  else if (dtype == DT_BF16) TTSP_AQ(DT_BF16);
+  else return (int)hipErrorInvalidValue;
+#undef TTSP_AQ
   TTSP_RETURN_LAUNCH();
 }

@@ -1,15 +1,18 @@
-"""One decode position through a transformer block in seven HIP launches.
+"""One decode position through a transformer block in five or six HIP launches.
 
 Drop-in for the reference's `app/engine/fusedlayer.py` (`decode_block`,
 `install`, `stats`, `HEAD_DIM`, `CHUNK`):
 
-    [rms_norm + wqkv] -> qk_rope_kv -> attn_partial -> attn_combine
+    [rms_norm + wqkv] -> [qk norm + rope + KV write + attention (+ merge)]
         -> wo(+x) -> [rms_norm + w1, w3 as silu(w1) * w3] -> w2(+h)
 
-The bracketed steps are single launches (`nf4gemv.matmul_fused`): the norm
-runs in the matmul's prologue with the standalone kernel's exact arithmetic,
-and w1/w3 stream through the same waves with the gate in the epilogue; the
-results are bit-identical to the reference's ten-launch order.
+The bracketed steps are single launches: the norm runs in the matmul's
+prologue with the standalone kernel's exact arithmetic (`nf4gemv.
+matmul_fused`), w1/w3 stream through the same waves with the gate in the
+epilogue, and the attention workgroups apply the head norms and rotary to
+QKV themselves (`ttsp_attn_decode_qkv`; a cache longer than one 64-position
+chunk adds a merge launch). The results are bit-identical to the reference's
+ten-launch order (reference: fusedlayer.py:212-269).
 
 `qk_rope_kv` does the head norms, rotary and KV-cache write for every head in
 one launch; attention is split-K over CHUNK-position slices of the cache (one
@@ -104,16 +107,12 @@ def decode_block(block, x, freqs_cis, mask, input_pos, *, workspace=None):
     qn = getattr(a, "q_norm", None) if a.attention_qk_norm else None
     kn = getattr(a, "k_norm", None) if a.attention_qk_norm else None
     eps = float(qn.eps if qn is not None and qn.eps is not None else 1e-6)
-    rc = lib.ttsp_qk_rope_kv(
+    rc = lib.ttsp_attn_decode_qkv(
         qkv.data_ptr(), _lib.ptr(None if qn is None else qn.weight), _lib.ptr(None if kn is None else kn.weight),
-        eps, freqs_cis.data_ptr(), ftype, input_pos.data_ptr(), ws["q"].data_ptr(),
-        a.kv_cache.k_cache.data_ptr(), a.kv_cache.v_cache.data_ptr(), nh, nkv, max_len, dt, st)
-    _lib.check(rc, "ttsp_qk_rope_kv")
-    rc = lib.ttsp_attn_decode(
-        ws["q"].data_ptr(), a.kv_cache.k_cache.data_ptr(), a.kv_cache.v_cache.data_ptr(),
-        input_pos.data_ptr(), ws["pm"].data_ptr(), ws["pl"].data_ptr(), ws["pacc"].data_ptr(),
+        eps, freqs_cis.data_ptr(), ftype, input_pos.data_ptr(), a.kv_cache.k_cache.data_ptr(),
+        a.kv_cache.v_cache.data_ptr(), ws["pm"].data_ptr(), ws["pl"].data_ptr(), ws["pacc"].data_ptr(),
         ws["y"].data_ptr(), nh, nkv, max_len, nchunk, float(HEAD_DIM**-0.5), dt, st)
-    _lib.check(rc, "ttsp_attn_decode")
+    _lib.check(rc, "ttsp_attn_decode_qkv")
     h = nf4gemv.matmul(a.wo, ws["y"], epi=nf4gemv.EPI_RESIDUAL, operand=x, out=ws["h"])
     if h is None:
         raise RuntimeError("decode_block: a prepared layer declined mid-block")
