@@ -3,7 +3,11 @@
 Step (the `value`): the seven batch-1 linears of one Qwen3-4B-shaped decoder
 layer in NF4 with double-quant absmax (uint8, bs2 256, fp32 scale + offset),
 bf16 activations - q 2560->4096, k/v 2560->1024, o 4096->2560, gate/up
-2560->9728, down 9728->2560 - 52,186,204 algorithmic bytes per step.
+2560->9728, down 9728->2560 - executed as the fused decode block executes them
+(q/k/v as one wqkv GEMV, gate/up as one SwiGLU GEMV: four launches,
+52,149,332 algorithmic bytes: the same weights and scales, x read once per
+launch, one gated output instead of gate and up); the same linears as seven separate launches
+(52,186,204 bytes) are reported beside it.
 Weights rotate over enough distinct copies (> 512 MB) that every step streams
 from HBM, not from the 256 MB Infinity Cache; launches are replayed from a
 HIP graph so the GPU runs them back to back. value = bytes / time (GB/s).
@@ -74,6 +78,23 @@ class Linear:
             self.amax = torch.rand(nblk, device=device, generator=g) * 0.04 + 0.02
 
 
+# The same layer as the fused decode block executes it: q/k/v as one wqkv
+# matrix, and gate/up as one SwiGLU launch streaming both weights.
+FUSED_LAYER = [("wqkv", 6144, 2560), ("o", 2560, 4096), ("gate_up", 9728, 2560), ("down", 2560, 9728)]
+
+
+def fused_layer_bytes() -> int:
+    """Algorithmic bytes of FUSED_LAYER: every weight byte and scale once, x and
+    the code2 table once per launch (the SwiGLU launch reads two code2 tables),
+    y once."""
+    total = 0
+    for name, M, K in FUSED_LAYER:
+        n = 2 if name == "gate_up" else 1
+        nblk = M * K // 64
+        total += n * (M * K // 2 + nblk + 4 * math.ceil(nblk / 256) + 256 * 4 + 4) + 2 * K + 2 * M
+    return total
+
+
 def launch(lib, lut, lin, x, y, dt, stream):
     from ttspipe_amd import _lib
 
@@ -82,6 +103,17 @@ def launch(lib, lut, lin, x, y, dt, stream):
                            64, 256, stream)
     if rc:
         raise RuntimeError(f"ttsp_nf4_gemm failed: {rc}")
+
+
+def launch_swiglu(lib, lut, l1, l3, x, y, stream):
+    from ttspipe_amd import _lib
+
+    rc = lib.ttsp_nf4_gemv_fused(x.data_ptr(), _lib.DT_BF16, 0, 1e-6, l1.w.data_ptr(), _lib.ptr(l1.a8),
+                                 l1.amax.data_ptr(), _lib.ptr(l1.code2), l1.offset, l3.w.data_ptr(), _lib.ptr(l3.a8),
+                                 l3.amax.data_ptr(), _lib.ptr(l3.code2), l3.offset, lut.data_ptr(), y.data_ptr(), 0, 0,
+                                 l1.M, l1.K, 64, 256, stream)
+    if rc:
+        raise RuntimeError(f"ttsp_nf4_gemv_fused failed: {rc}")
 
 
 def time_graph(graph, replays: int, stream) -> float:
@@ -129,6 +161,51 @@ def bench_layer(steps: int, warmup: int):
         for layer in copies:
             for (name, M, K), lin in zip(LAYER, layer):
                 launch(lib, lut, lin, xs[K], ys[name], _lib.DT_BF16, st)
+
+    body()
+    torch.cuda.synchronize()
+    graph = capture(body)
+    stream = torch.cuda.current_stream()
+    reps_w = max(1, warmup // ncopy)
+    time_graph(graph, reps_w, stream)
+    reps = max(1, steps // ncopy)
+    sec = time_graph(graph, reps, stream) / ncopy
+    return {"step_bytes": step_bytes, "sec_per_step": sec, "steps": reps * ncopy, "copies": ncopy,
+            "warmup": reps_w * ncopy}
+
+
+def bench_fused_layer(steps: int, warmup: int):
+    """The decode block's launch structure for one layer's linears (4 launches)."""
+    import torch
+
+    from ttspipe_amd import _lib
+    from ttspipe_amd.quant import NF4_CODE
+
+    lib = _lib.load()
+    dev = torch.device("cuda", 0)
+    lut = torch.tensor(NF4_CODE, dtype=torch.float32, device=dev)
+    step_bytes = fused_layer_bytes()
+    weight_bytes = sum(M * K // 2 * (2 if n == "gate_up" else 1) for n, M, K in FUSED_LAYER)
+    ncopy = max(2, math.ceil(2 * MALL_BYTES / weight_bytes))
+    copies = []
+    for c in range(ncopy):
+        layer = {}
+        for i, (name, M, K) in enumerate(FUSED_LAYER):
+            layer[name] = Linear(M, K, True, seed=3000 + 10 * c + i, device=dev)
+            if name == "gate_up":
+                layer["up"] = Linear(M, K, True, seed=7000 + 10 * c + i, device=dev)
+        copies.append(layer)
+    xs = {K: torch.randn(K, device=dev).to(torch.bfloat16) for K in {K for _, _, K in FUSED_LAYER}}
+    ys = {name: torch.empty(M, dtype=torch.bfloat16, device=dev) for name, M, _ in FUSED_LAYER}
+
+    def body():
+        st = torch.cuda.current_stream().cuda_stream
+        for layer in copies:
+            for name, M, K in FUSED_LAYER:
+                if name == "gate_up":
+                    launch_swiglu(lib, lut, layer[name], layer["up"], xs[K], ys[name], st)
+                else:
+                    launch(lib, lut, layer[name], xs[K], ys[name], _lib.DT_BF16, st)
 
     body()
     torch.cuda.synchronize()
@@ -286,8 +363,8 @@ def main() -> int:
     torch.cuda.set_device(0)
     out = {}
     if args.only in (None, "layer"):
-        layer = bench_layer(args.steps, args.warmup)
-        out["layer"] = layer
+        out["layer_fused"] = bench_fused_layer(args.steps, args.warmup)
+        out["layer"] = bench_layer(args.steps, args.warmup)
     if args.only in (None, "kernel"):
         out["kernel"] = bench_kernel(9728, 2560, True, "bf16", direct=args.direct)
     if args.only in (None, "c1"):
@@ -308,28 +385,32 @@ def main() -> int:
         return 0
     cpu = None if args.skip_cpu else cpu_baseline(args.cpu_seconds)
 
-    layer, kern, c1 = out["layer"], out["kernel"], out["c1"]
-    value = layer["step_bytes"] / layer["sec_per_step"] / 1e9
+    layer, kern, c1, fused = out["layer"], out["kernel"], out["c1"], out["layer_fused"]
+    value = fused["step_bytes"] / fused["sec_per_step"] / 1e9
+    separate = layer["step_bytes"] / layer["sec_per_step"] / 1e9
     line = {
         "metric": "NF4 GEMV HBM GB/s (% of peak) + decode step ms/token, 4B-dim model, 1 GPU",
         "value": round(value, 1),
         "unit": "GB/s",
         "n_gpus": 1,
-        "steps": layer["steps"],
-        "warmup": layer["warmup"],
-        "ms_per_step": round(layer["sec_per_step"] * 1e3, 5),
+        "steps": fused["steps"],
+        "warmup": fused["warmup"],
+        "ms_per_step": round(fused["sec_per_step"] * 1e3, 5),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "bf16",
         "data": "synthetic",
         "config": {
-            "workload": "one Qwen3-4B-shaped decoder layer, batch 1: q 2560->4096, k/v 2560->1024, "
+            "workload": "all batch-1 linears of one Qwen3-4B-shaped decoder layer: q 2560->4096, k/v 2560->1024, "
                         "o 4096->2560, gate/up 2560->9728, down 9728->2560; NF4 bs64, double-quant absmax "
-                        "(uint8, bs2 256, fp32 scale+offset); x bf16",
-            "bytes_per_step": layer["step_bytes"],
-            "weight_copies_rotated": layer["copies"],
+                        "(uint8, bs2 256, fp32 scale+offset); x bf16; run as the fused decode block runs them "
+                        "(q/k/v as one wqkv GEMV, gate/up as one SwiGLU GEMV: 4 launches)",
+            "bytes_per_step": fused["step_bytes"],
+            "weight_copies_rotated": fused["copies"],
             "pct_of_hbm_peak": round(100 * value / HBM_PEAK_GBS, 1),
+            "seven_separate_launches": {"gbs": round(separate, 1), "ms_per_step": round(layer["sec_per_step"] * 1e3, 5),
+                                        "bytes_per_step": layer["step_bytes"]},
         },
         "roofline": {
             "bound": "hbm",

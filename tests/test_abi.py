@@ -113,6 +113,10 @@ def test_benchmark_byte_counts():
     # the reference's CPU-runnable case (C1) and one decoder layer (C2), SURVEY-documented totals
     assert bench.nf4_bytes(9728, 2560, False) == 14_032_896
     assert sum(bench.nf4_bytes(M, K, True) for _, M, K in bench.LAYER) == 52_186_204
+    # the fused launches: identical weight and scale bytes; q/k/v read x once (two fewer x reads and code2
+    # tables), gate/up read x once and write one gated output instead of two outputs
+    saved = 2 * (2560 * 2 + 1028) + 2560 * 2 + 9728 * 2
+    assert bench.fused_layer_bytes() == 52_186_204 - saved == 52_149_332
 
 
 def test_dualar_specs_and_byte_account():

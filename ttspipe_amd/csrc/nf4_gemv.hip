@@ -153,17 +153,61 @@ __device__ __forceinline__ uint32_t bf16x2_to_f16x2(uint32_t u, int xe) {
   return lo | (hi << 16);
 }
 
-__device__ __forceinline__ float max_abs16(int dt, uint4 v, float m) {
+
+// Staging steps, specialised by activation type (the kernel branches on the
+// type once per step, not per element).
+template <int DT>
+__device__ __forceinline__ float sumsq8(uint4 v, float acc) {  // element order, fma chain
   const uint32_t u[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
-  for (int k = 0; k < 4; ++k) m = fmaxf(m, fmaxf(fabsf(ld16(dt, u[k])), fabsf(ld16(dt, u[k] >> 16))));
+  for (int k = 0; k < 4; ++k) {
+    const float a = Elem<DT>::load(u[k]), b = Elem<DT>::load(u[k] >> 16);
+    acc = __builtin_fmaf(a, a, acc);
+    acc = __builtin_fmaf(b, b, acc);
+  }
+  return acc;
+}
+
+template <int DT>
+__device__ __forceinline__ float maxabs8(uint4 v, float m) {
+  const uint32_t u[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+  for (int k = 0; k < 4; ++k)
+    m = fmaxf(m, fmaxf(fabsf(Elem<DT>::load(u[k])), fabsf(Elem<DT>::load(u[k] >> 16))));
+  return m;
+}
+
+// The fork's RMSNorm of 8 values: round(round(x * r) * w), the standalone kernel's arithmetic.
+template <int DT>
+__device__ __forceinline__ uint4 norm8(uint4 v, uint4 g, float r) {
+  uint32_t u[4] = {v.x, v.y, v.z, v.w};
+  const uint32_t gw[4] = {g.x, g.y, g.z, g.w};
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const float n0 = Elem<DT>::load(Elem<DT>::store(__fmul_rn(Elem<DT>::load(u[k]), r)));
+    const float n1 = Elem<DT>::load(Elem<DT>::store(__fmul_rn(Elem<DT>::load(u[k] >> 16), r)));
+    u[k] = (uint32_t)Elem<DT>::store(__fmul_rn(n0, Elem<DT>::load(gw[k]))) |
+           ((uint32_t)Elem<DT>::store(__fmul_rn(n1, Elem<DT>::load(gw[k] >> 16))) << 16);
+  }
+  return make_uint4(u[0], u[1], u[2], u[3]);
+}
+
+// After the first barrier: normalise this thread's chunks in LDS; their max.
+template <int DT>
+__device__ __forceinline__ float norm_x(uint4* xs, const uint4* gs, int tid, int KD, float r) {
+  float m = 0.0f;
+  for (int c = tid; c < KD; c += STAGE_THREADS) {
+    const uint4 v = norm8<DT>(xs[c], gs[c], r);
+    xs[c] = v;
+    if (DT == DT_BF16) m = maxabs8<DT>(v, m);
+  }
   return m;
 }
 
 // Dynamic LDS after the static table: pair staging [256], code2 [NM][256],
 // wave partials [8] and maxima [8], K-slice partials [8][NM*RPW], the
 // workgroup's scales [NM][RG*RPW][nblk] (16-byte aligned), then x as staged
-// fp16 [K].
+// (finally fp16) [K] and the norm weight [K].
 template <int J, int RPW, int NM>
 __global__ __launch_bounds__(GEMV_THREADS) void nf4_gemv_kernel(const GemvParams p) {
   constexpr int NW = GEMV_WAVES;
@@ -193,7 +237,8 @@ __global__ __launch_bounds__(GEMV_THREADS) void nf4_gemv_kernel(const GemvParams
   const long long sc0 = (long long)wg_row0 * nblk;
   const int dt = p.dt;
   const bool nested = p.nested != 0, norm = p.norm != 0;
-  uint4* xs = reinterpret_cast<uint4*>(srow + ((NM * rows_wg * nblk + 3) & ~3));  // [KD]
+  uint4* xs = reinterpret_cast<uint4*>(srow + ((NM * rows_wg * nblk + 3) & ~3));  // [KD] x as staged
+  uint4* gs = xs + KD;                                                             // [KD] norm weight
   const int XN = (KD + STAGE_THREADS - 1) / STAGE_THREADS;  // x chunks per staging thread
   const bool stager = tid < STAGE_THREADS;
 
@@ -219,12 +264,13 @@ __global__ __launch_bounds__(GEMV_THREADS) void nf4_gemv_kernel(const GemvParams
     sv[i] = am[nested ? gb >> p.bs2_shift : gb];
   }
   const uint32_t rres = p.R[min(row0 + min(lane, RPW - 1), M - 1)];  // epilogue operand
+  const int XNw = uniform(stager ? XN : 0);  // waves 4-7 stage nothing
   uint4 xc[XC_MAX], gc[XC_MAX];
 #pragma unroll
   for (int i = 0; i < XC_MAX; ++i) {
     xc[i] = gc[i] = make_uint4(0, 0, 0, 0);
-    if (i < XN) {
-      const int c = min((tid & 255) + i * STAGE_THREADS, KD - 1);
+    if (i < XNw) {
+      const int c = min(tid + i * STAGE_THREADS, KD - 1);
       xc[i] = *reinterpret_cast<const uint4*>(p.X + 8 * (size_t)c);
       gc[i] = *reinterpret_cast<const uint4*>(p.G + 8 * (size_t)(norm ? c : 0));
     }
@@ -253,17 +299,14 @@ __global__ __launch_bounds__(GEMV_THREADS) void nf4_gemv_kernel(const GemvParams
     float acc = 0.0f;
 #pragma unroll
     for (int i = 0; i < XC_MAX; ++i) {
-      if (i < XN && (tid + i * STAGE_THREADS) < KD) {
+      const int c = tid + i * STAGE_THREADS;
+      if (i < XNw && c < KD) {
+        xs[c] = xc[i];
         if (norm) {
-          const uint32_t u[4] = {xc[i].x, xc[i].y, xc[i].z, xc[i].w};
-#pragma unroll
-          for (int k = 0; k < 4; ++k) {
-            const float a = ld16(dt, u[k]), b = ld16(dt, u[k] >> 16);
-            acc = __builtin_fmaf(a, a, acc);
-            acc = __builtin_fmaf(b, b, acc);
-          }
-        } else {
-          acc = max_abs16(dt, xc[i], acc);
+          gs[c] = gc[i];
+          acc = dt == DT_BF16 ? sumsq8<DT_BF16>(xc[i], acc) : sumsq8<DT_F16>(xc[i], acc);
+        } else if (dt == DT_BF16) {
+          acc = maxabs8<DT_BF16>(xc[i], acc);
         }
       }
     }
@@ -277,8 +320,7 @@ __global__ __launch_bounds__(GEMV_THREADS) void nf4_gemv_kernel(const GemvParams
   }
   __syncthreads();
 
-  // 4. the replicated pair table, the resolved scales, the normalised x and
-  //    (with a norm) its maximum
+  // 4. the replicated pair table, the resolved scales, and x staged
   {
     constexpr int G = (int)sizeof(lut_rep) / 1024 / NW;  // 1 KiB (4 entries) per wave store
     uint32_t v[G];
@@ -298,51 +340,34 @@ __global__ __launch_bounds__(GEMV_THREADS) void nf4_gemv_kernel(const GemvParams
       srow[e + m * (rows_wg * nblk - nsc)] = s;  // weight m's block starts at m * rows_wg * nblk
     }
   }
-  if (norm && stager) {
-    float ss = wpart[0];
+  // x to fp16 in LDS: bf16 is rescaled by 2^-xe so max|x| lands in
+  // [2^14, 2^15) and converted exactly (bf16's 8 significant bits fit in
+  // fp16's 11); the row sums are scaled back by 2^xe (also exact). Without a
+  // norm the maximum is known now; with one it needs the normalised x and a
+  // further barrier.
+  if (norm) {
+    if (stager) {
+      float ss = wpart[0];
 #pragma unroll
-    for (int w2 = 1; w2 < STAGE_THREADS / 64; ++w2) ss = __fadd_rn(ss, wpart[w2]);
-    const float r = rsqrt_rn(__fadd_rn(__fdiv_rn(ss, (float)K), p.eps));
-    float m = 0.0f;
-#pragma unroll
-    for (int i = 0; i < XC_MAX; ++i) {
-      if (i < XN) {
-        uint32_t* u = reinterpret_cast<uint32_t*>(&xc[i]);
-        const uint32_t* g = reinterpret_cast<const uint32_t*>(&gc[i]);
-#pragma unroll
-        for (int k = 0; k < 4; ++k) {
-          const float n0 = ld16(dt, st16(dt, __fmul_rn(ld16(dt, u[k]), r)));
-          const float n1 = ld16(dt, st16(dt, __fmul_rn(ld16(dt, u[k] >> 16), r)));
-          u[k] = st16(dt, __fmul_rn(n0, ld16(dt, g[k]))) | (st16(dt, __fmul_rn(n1, ld16(dt, g[k] >> 16))) << 16);
-        }
-        if ((tid + i * STAGE_THREADS) < KD) m = max_abs16(dt, xc[i], m);
-      }
+      for (int w2 = 1; w2 < STAGE_THREADS / 64; ++w2) ss = __fadd_rn(ss, wpart[w2]);
+      const float r = rsqrt_rn(__fadd_rn(__fdiv_rn(ss, (float)K), p.eps));
+      float m = dt == DT_BF16 ? norm_x<DT_BF16>(xs, gs, tid, KD, r) : norm_x<DT_F16>(xs, gs, tid, KD, r);
+      m = wave_max_dpp(m);
+      if (lane == 0) wmax[wave] = m;
     }
-    m = wave_max_dpp(m);
-    if (lane == 0) wmax[wave] = m;
+    __syncthreads();
   }
-  __syncthreads();
-
-  // 5. x to fp16 in LDS: bf16 is rescaled by 2^-xe so max|x| lands in
-  //    [2^14, 2^15) and converted exactly (bf16's 8 significant bits fit in
-  //    fp16's 11); the row sums are scaled back by 2^xe (also exact)
   int xe = 0;
   if (dt == DT_BF16) {
     float m = wmax[0];
 #pragma unroll
     for (int w2 = 1; w2 < STAGE_THREADS / 64; ++w2) m = fmaxf(m, wmax[w2]);
     if (m > 0.0f && m <= 3.402823466e38f) xe = __builtin_amdgcn_frexp_expf(m) - 15;
-  }
-  if (stager) {
-#pragma unroll
-    for (int i = 0; i < XC_MAX; ++i) {
-      const int c = tid + i * STAGE_THREADS;
-      if (i < XN && c < KD) {
-        uint4 v = xc[i];
-        if (dt == DT_BF16)
-          v = make_uint4(bf16x2_to_f16x2(v.x, xe), bf16x2_to_f16x2(v.y, xe), bf16x2_to_f16x2(v.z, xe),
-                         bf16x2_to_f16x2(v.w, xe));
-        xs[c] = v;
+    if (stager) {
+      for (int c = tid; c < KD; c += STAGE_THREADS) {
+        const uint4 v = xs[c];
+        xs[c] = make_uint4(bf16x2_to_f16x2(v.x, xe), bf16x2_to_f16x2(v.y, xe), bf16x2_to_f16x2(v.z, xe),
+                           bf16x2_to_f16x2(v.w, xe));
       }
     }
   }
@@ -440,21 +465,22 @@ struct GemvShape {
 
 static constexpr int kJ[] = {1, 2, 3, 4, 5, 6, 8};
 static constexpr int kRPW1[] = {1, 2, 3, 4, 5, 6, 8};
-static constexpr int kRPW2[] = {1, 2, 3, 4};
+static constexpr int kRPW2[] = {1, 2, 3, 4, 5};
 static constexpr int kCUs = 256;
-static constexpr size_t kLdsPerCU = 160 * 1024;
+static constexpr size_t kLdsPerCU = 160 * 1024;  // a workgroup's LDS must fit
 
 // Dynamic LDS of one workgroup (the table is static).
 static size_t gemv_dyn_lds(const GemvShape& g, int nm, int K, int bs_shift) {
   const size_t rows_wg = (size_t)(GEMV_WAVES / g.KS) * g.RPW;
   const size_t sc = ((size_t)nm * rows_wg * (K >> bs_shift) + 3) & ~(size_t)3;
-  return 4 * (256 + 256 * (size_t)nm + 2 * GEMV_WAVES + (size_t)GEMV_WAVES * nm * g.RPW + sc) + 2 * (size_t)K;
+  return 4 * (256 + 256 * (size_t)nm + 2 * GEMV_WAVES + (size_t)GEMV_WAVES * nm * g.RPW + sc) + 4 * (size_t)K;
 }
 
 // K is split (KS a power of two) so that a lane's chunks J <= 8 leave the
-// fewest slots idle; RPW is the smallest that fits every row into one pass of
-// the workgroups the LDS lets each CU hold (every workgroup builds the 64 KiB
-// table and stages x once, so fewer, fuller workgroups pay less of that).
+// fewest slots idle; RPW is the smallest that fits every row into one
+// workgroup per CU (every workgroup builds the 64 KiB table and stages x once,
+// so fewer, fuller workgroups pay less of that - measured faster than two
+// half-full workgroups per CU at every decode shape).
 static GemvShape gemv_shape(int M, int K, int nm = 1, int bs_shift = 6) {
   const int chunks = (K / 8 + 63) / 64;  // 64-dword chunks per row
   int KS = 0, J = 0, waste = 1 << 30;
@@ -471,9 +497,7 @@ static GemvShape gemv_shape(int M, int K, int nm = 1, int bs_shift = 6) {
   const int nrpw = nm == 1 ? (int)(sizeof(kRPW1) / sizeof(int)) : (int)(sizeof(kRPW2) / sizeof(int));
   for (int i = 0; i < nrpw; ++i) {
     g.RPW = rpw[i];
-    const size_t per_wg = LUT_BYTES + gemv_dyn_lds(g, nm, K, bs_shift);
-    const long long slots = (long long)kCUs * (long long)(kLdsPerCU / per_wg);
-    if ((long long)(M + RG * g.RPW - 1) / (RG * g.RPW) <= slots) break;
+    if ((long long)(M + RG * g.RPW - 1) / (RG * g.RPW) <= kCUs) break;
   }
   return g;
 }
@@ -497,7 +521,7 @@ static int dispatch_rpw(const GemvShape& g, const GemvParams& p, hipStream_t st)
     }
   } else {
     switch (g.RPW) {
-      TTSP_R(1) TTSP_R(2) TTSP_R(3) TTSP_R(4)
+      TTSP_R(1) TTSP_R(2) TTSP_R(3) TTSP_R(4) TTSP_R(5)
       default: return (int)hipErrorInvalidValue;
     }
   }

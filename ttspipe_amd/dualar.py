@@ -275,10 +275,8 @@ class SyntheticDualAR:
         self.ws = [fusedlayer.make_workspace(self.layers[0], x1, nchunk, with_out=True) for _ in range(2)]
         self.fws = [fusedlayer.make_workspace(self.fast_layers[0], f1, fchunk, with_out=True) for _ in range(2)]
         self.x = x1
-        self.hn = torch.empty(1, 1, cfg.dim, dtype=bf, device=dev)
         self.logits = torch.empty(1, cfg.vocab_size, dtype=bf, device=dev)
         self.fast_h = torch.empty(1, 1, cfg.fast_dim, dtype=bf, device=dev)
-        self.fast_hn = torch.empty(1, 1, cfg.fast_dim, dtype=bf, device=dev)
         self.fast_logits = torch.empty(1, cfg.codebook_size, dtype=bf, device=dev)
         self.graph = None
         self.reset()
@@ -304,12 +302,14 @@ class SyntheticDualAR:
 
     def _fast_kv_only(self, blk, x, freqs, pos):
         """The last fast layer at the prime position: norm, wqkv, KV write."""
-        from ttspipe_amd import fusedops, nf4gemv
+        from ttspipe_amd import nf4gemv
 
         a = blk.attention
         ws = self.fws[0]
-        xn = fusedops.rms_norm(x, blk.attention_norm.weight, blk.attention_norm.eps, out=ws["xn"])
-        qkv = nf4gemv.matmul(a.wqkv, xn, out=ws["qkv"])
+        qkv = nf4gemv.matmul_fused(a.wqkv, x, norm_weight=blk.attention_norm.weight, eps=blk.attention_norm.eps,
+                                   out=ws["qkv"])
+        if qkv is None:
+            raise RuntimeError("the fused matmul declined the fast prime's wqkv")
         qn = a.q_norm if self.cfg.qk_norm else None
         kn = a.k_norm if self.cfg.qk_norm else None
         rc = self._lib.ttsp_qk_rope_kv(
@@ -329,11 +329,19 @@ class SyntheticDualAR:
             x = y
         return x
 
+    @staticmethod
+    def _fused(linear, x, norm_weight, eps, out):
+        """RMSNorm of x folded into the matmul (one launch, the unfused pair's bits)."""
+        from ttspipe_amd import nf4gemv
+
+        y = nf4gemv.matmul_fused(linear, x, norm_weight=norm_weight, eps=eps, out=out)
+        if y is None:
+            raise RuntimeError("the fused matmul declined a head of the synthetic model")
+        return y
+
     def step(self) -> None:
         """One frame: tokens (device) at position pos -> next frame's tokens; pos += 1."""
         import torch
-
-        from ttspipe_amd import fusedops, nf4gemv
 
         cfg, lib, st = self.cfg, self._lib, _lib.stream()
         # slow transformer
@@ -341,13 +349,14 @@ class SyntheticDualAR:
                                 cfg.vocab_size, cfg.dim, self.x.data_ptr(), _lib.DT_BF16, st)
         self._check(rc, "ttsp_embed_sum")
         torch.index_select(self.freqs, 0, self.pos, out=self.freq_row)
-        h = self._run_blocks(self.layers, self.ws, self.x, self.freq_row, self.mask, self.pos)
-        hn = fusedops.rms_norm(h.view(1, 1, -1), self.tensors["norm"], cfg.norm_eps, out=self.hn)
-        nf4gemv.matmul(self.output, hn, out=self.logits)
+        h = self._run_blocks(self.layers, self.ws, self.x, self.freq_row, self.mask, self.pos).view(1, 1, -1)
+        # the final norm runs inside both consumers (head and fast projection)
+        norm, eps = self.tensors["norm"], cfg.norm_eps
+        self._fused(self.output, h, norm, eps, self.logits)
         rc = lib.ttsp_argmax(self.logits.data_ptr(), cfg.vocab_size, _lib.DT_BF16, self.tokens.data_ptr(), st)
         self._check(rc, "ttsp_argmax")
         # fast transformer: prime at fast position 0 with the projected hidden state
-        fx = nf4gemv.matmul(self.fast_project_in, hn, out=self.fast_h)
+        fx = self._fused(self.fast_project_in, h, norm, eps, self.fast_h)
         p0 = self.fast_pos[0]
         x = self._run_blocks(self.fast_layers[:-1], self.fws, fx, self.fast_freqs[0], self.fast_mask, p0)
         self._fast_kv_only(self.fast_layers[-1], x, self.fast_freqs[0], p0)
@@ -360,8 +369,7 @@ class SyntheticDualAR:
             self._check(rc, "ttsp_embed_sum")
             x = self._run_blocks(self.fast_layers, self.fws, self.fast_h, self.fast_freqs[i], self.fast_mask,
                                  self.fast_pos[i])
-            fhn = fusedops.rms_norm(x.view(1, 1, -1), self.tensors["fast_norm"], cfg.norm_eps, out=self.fast_hn)
-            nf4gemv.matmul(self.fast_output, fhn, out=self.fast_logits)
+            self._fused(self.fast_output, x.view(1, 1, -1), self.tensors["fast_norm"], cfg.norm_eps, self.fast_logits)
             rc = lib.ttsp_argmax(self.fast_logits.data_ptr(), cfg.codebook_size, _lib.DT_BF16,
                                  self.tokens[i + 1:].data_ptr(), st)
             self._check(rc, "ttsp_argmax")
