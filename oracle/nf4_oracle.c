@@ -226,22 +226,10 @@ void orc_gemv_emul(const void* X, int dt, const uint8_t* W, const uint8_t* A8, c
   const int KD = K / 8, nblk = K / bs;
   float lutv[16];
   for (int i = 0; i < 16; ++i) lutv[i] = rnd(LUT[i], DT_F16); /* fp16 codes for both types */
+  /* fp16 and bf16 activations are exact in fp32: the kernel multiplies the
+   * fp16 code by the fp32 activation (one exact product per fma) */
   float* xv = malloc(sizeof(float) * (size_t)K);
-  int xe = 0;
   for (int k = 0; k < K; ++k) xv[k] = ld(X, (size_t)k, dt);
-  if (dt == DT_BF16) {
-    /* m = max|x| over the whole vector, e = ilogb(m) - 14, x <- fp16(x * 2^-e)
-     * (exact for bf16 values in fp16's normal range), slice sums * 2^e */
-    float m = 0.0f;
-    for (int k = 0; k < K; ++k) m = fmaxf(m, fabsf(xv[k]));
-    int e = 0;
-    if (m > 0.0f && m <= 3.402823466e38f) {
-      frexpf(m, &e);
-      e -= 15;
-    }
-    xe = e;
-    for (int k = 0; k < K; ++k) xv[k] = orc_f16_to_f32(orc_f32_to_f16(ldexpf(xv[k], -e)));
-  }
 #pragma omp parallel for schedule(static)
   for (int m = 0; m < M; ++m) {
     const uint32_t* wr = (const uint32_t*)(W + (size_t)m * (K / 2));
@@ -270,7 +258,7 @@ void orc_gemv_emul(const void* X, int dt, const uint8_t* W, const uint8_t* A8, c
         }
         lanes[l] = acc;
       }
-      const float ws = ldexpf(butterfly64_up(lanes), xe);
+      const float ws = butterfly64_up(lanes);
       total = ks == 0 ? ws : total + ws;
     }
     const float r = epi ? ld(R, (size_t)m, dt) : 0.0f;
@@ -298,29 +286,29 @@ void orc_rms_norm_ref(const void* X, const void* Wt, double* Y, int rows, int D,
   }
 }
 
-/* The kernel's order (ttspipe_amd/csrc/fusedops.hip): thread t of 256 sums
- * fma(x, x, acc) over 8-element chunks t, t+256, ..., element order inside a
- * chunk; butterfly per wave; waves left to right; r = 1 / sqrt(ss/D + eps). */
+/* The kernels' order (ttspipe_amd/csrc/fusedops.hip, and the GEMV's folded
+ * norm): 64 chunks of 8 elements at a time, each chunk's squares by an fma
+ * chain in element order from 0, the 64 chunk sums by the rising-distance
+ * butterfly, these partial sums left to right; r = 1 / sqrt(ss/D + eps). */
 void orc_rms_norm_emul(const void* X, const void* Wt, uint16_t* Y, int rows, int D, float eps, int dt) {
   const int nc = D / 8;
   for (int row = 0; row < rows; ++row) {
     const size_t base = (size_t)row * D;
-    float part[4];
-    for (int w = 0; w < 4; ++w) {
+    float ss = 0.0f;
+    for (int c0 = 0; c0 < nc; c0 += 64) {
       float lanes[64];
       for (int l = 0; l < 64; ++l) {
-        const int t = w * 64 + l;
         float acc = 0.0f;
-        for (int c = t; c < nc; c += 256)
+        if (c0 + l < nc)
           for (int k = 0; k < 8; ++k) {
-            const float a = ld(X, base + 8 * (size_t)c + k, dt);
+            const float a = ld(X, base + 8 * (size_t)(c0 + l) + k, dt);
             acc = fmaf(a, a, acc);
           }
         lanes[l] = acc;
       }
-      part[w] = butterfly64(lanes);
+      const float part = butterfly64_up(lanes);
+      ss = c0 == 0 ? part : ss + part;
     }
-    const float ss = ((part[0] + part[1]) + part[2]) + part[3];
     const float r = orc_rsqrt_rn(ss / (float)D + eps);
     for (int i = 0; i < D; ++i) {
       const float n = rnd(ld(X, base + i, dt) * r, dt);

@@ -268,6 +268,9 @@ def test_norm_folded_into_the_matmul_is_bit_exact(nf4, orc, shape, nested, dtype
     gb = o.from_f32((np.random.default_rng(K).random(K) * 0.5 + 0.75).astype(np.float32), dt)
     y = nf4.matmul_fused(lin, from_bits(xb, dtype).view(1, 1, K), norm_weight=from_bits(gb, dtype), eps=1e-6)
     J, KS, _ = gemv_shape(M, K)
+    if K > nf4.NORM_MAX_K:  # too wide to fold the norm in: the caller runs it separately
+        assert y is None
+        return
     xn = orc.rms_norm_emul(xb, gb, 1, K, 1e-6, dt)
     expect = orc.gemv_emul(xn, dt, **oracle_args(layer), M=M, K=K, bs=64, KS=KS, J=J, bs2=layer["bs2"] or 256)
     assert np.array_equal(bits(y), expect), f"M={M} K={K}: {first_mismatch(bits(y), expect)}"

@@ -3,10 +3,13 @@
 //
 // rms_norm: y = round(round(x * r) * w), r = 1 / sqrt(sum(x^2) / D + eps), the
 // two roundings the fork's `_norm(x.float()).type_as(x) * weight` makes
-// (app/engine/fusedops.py:8-14, 88-93). One workgroup per row; each thread
-// owns 8-element chunks t, t+256, ... and sums their squares with fma in
-// element order; then a wave butterfly and a left-to-right sum over the 4
-// waves. Single pass over HBM: the row is re-read for the output from L1/L2.
+// (app/engine/fusedops.py:8-14, 88-93). One wave per row. The sum of squares
+// goes 64 chunks (of 8 elements) at a time: each chunk's squares by an fma
+// chain in element order from 0, the 64 chunk sums by the rising-distance DPP
+// butterfly, and these partial sums left to right - the order the GEMV's
+// folded norm uses (a wave per 64 chunks there), so the fused and unfused
+// forms agree bit for bit.
+// Single pass over HBM: the row is re-read for the output from L1/L2.
 //
 // rope: pairs (2i, 2i+1) of the last axis, y0 = x0*c - x1*s, y1 = x1*c + x0*s
 // in fp32 with each product and the sum rounded separately (no fma), then
@@ -20,34 +23,34 @@ constexpr int NORM_THREADS = 256;
 template <int DT>
 __global__ __launch_bounds__(NORM_THREADS) void rms_norm_kernel(
     const uint16_t* __restrict__ X, const uint16_t* __restrict__ Wt, uint16_t* __restrict__ Y,
-    int D, float eps) {
-  __shared__ float part[NORM_THREADS / 64];
-  const int tid = threadIdx.x;
-  const size_t base = (size_t)blockIdx.x * D;
+    int rows, int D, float eps) {
+  const int lane = threadIdx.x & 63;
+  const int row = blockIdx.x * (NORM_THREADS / 64) + (threadIdx.x >> 6);
+  if (row >= rows) return;  // whole waves
+  const size_t base = (size_t)row * D;
   const uint4* xr = reinterpret_cast<const uint4*>(X + base);
   const int nc = D >> 3;
-  float acc = 0.0f;
-  for (int c = tid; c < nc; c += NORM_THREADS) {
-    const uint4 v = xr[c];
-    const uint32_t u[4] = {v.x, v.y, v.z, v.w};
+  float ss = 0.0f;
+  for (int c0 = 0; c0 < nc; c0 += 64) {  // 64 chunks per step, steps left to right
+    float acc = 0.0f;
+    if (c0 + lane < nc) {
+      const uint4 v = xr[c0 + lane];
+      const uint32_t u[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      const float a = Elem<DT>::load(u[k]), b = Elem<DT>::load(u[k] >> 16);
-      acc = __builtin_fmaf(a, a, acc);
-      acc = __builtin_fmaf(b, b, acc);
+      for (int k = 0; k < 4; ++k) {
+        const float a = Elem<DT>::load(u[k]), b = Elem<DT>::load(u[k] >> 16);
+        acc = __builtin_fmaf(a, a, acc);
+        acc = __builtin_fmaf(b, b, acc);
+      }
     }
+    const float part = wave_sum_dpp(acc);
+    ss = c0 == 0 ? part : __fadd_rn(ss, part);
   }
-  acc = wave_sum(acc);
-  if ((tid & 63) == 0) part[tid >> 6] = acc;
-  __syncthreads();
-  float ss = part[0];
-#pragma unroll
-  for (int w = 1; w < NORM_THREADS / 64; ++w) ss = __fadd_rn(ss, part[w]);
   const float r = rsqrt_rn(__fadd_rn(__fdiv_rn(ss, (float)D), eps));
 
   const uint4* wr = reinterpret_cast<const uint4*>(Wt);
   uint4* yr = reinterpret_cast<uint4*>(Y + base);
-  for (int c = tid; c < nc; c += NORM_THREADS) {
+  for (int c = lane; c < nc; c += 64) {
     const uint4 v = xr[c], g = wr[c];
     const uint32_t u[4] = {v.x, v.y, v.z, v.w}, gw[4] = {g.x, g.y, g.z, g.w};
     uint32_t o[4];
@@ -90,12 +93,13 @@ extern "C" int ttsp_rms_norm(const void* X, const void* Wt, void* Y, int rows, i
                              int dtype, hipStream_t stream) {
   if (rows < 0 || D <= 0 || D % 8) return (int)hipErrorInvalidValue;
   if (rows == 0) return 0;
+  const unsigned grid = (unsigned)((rows + NORM_THREADS / 64 - 1) / (NORM_THREADS / 64));
   if (dtype == DT_F16)
-    hipLaunchKernelGGL(rms_norm_kernel<DT_F16>, dim3(rows), dim3(NORM_THREADS), 0, stream,
-                       (const uint16_t*)X, (const uint16_t*)Wt, (uint16_t*)Y, D, eps);
+    hipLaunchKernelGGL(rms_norm_kernel<DT_F16>, dim3(grid), dim3(NORM_THREADS), 0, stream,
+                       (const uint16_t*)X, (const uint16_t*)Wt, (uint16_t*)Y, rows, D, eps);
   else if (dtype == DT_BF16)
-    hipLaunchKernelGGL(rms_norm_kernel<DT_BF16>, dim3(rows), dim3(NORM_THREADS), 0, stream,
-                       (const uint16_t*)X, (const uint16_t*)Wt, (uint16_t*)Y, D, eps);
+    hipLaunchKernelGGL(rms_norm_kernel<DT_BF16>, dim3(grid), dim3(NORM_THREADS), 0, stream,
+                       (const uint16_t*)X, (const uint16_t*)Wt, (uint16_t*)Y, rows, D, eps);
   else
     return (int)hipErrorInvalidValue;
   TTSP_RETURN_LAUNCH();

@@ -24,31 +24,31 @@
 //     scales, the residual operand, x, the norm weight) is requested before the
 //     weights, so waiting for it never waits for the weight stream (vector
 //     memory counters retire in order), and every weight dword of a wave is in
-//     flight before the first barrier. All loads are unconditional (clamped
+//     flight before anything waits. All loads are unconditional (clamped
 //     addresses, dummy pointers for absent operands): no branch ever separates
 //     a load from its use, which keeps the compiler's wait counts exact, so the
 //     dot products start as rows arrive.
+//   * One pass of set-up while the weights stream, two barriers: each lane
+//     writes its share of the code table straight from the 16 code points (no
+//     staging), code2 goes to LDS and - with a norm - waves 0..J-1 each
+//     normalise 64 chunks of x for the workgroup (every wave holds all of x at
+//     KS == 1, so the sum of squares needs no barrier); after the first
+//     barrier the scales are resolved once per workgroup and x is read as fp32.
 //   * Code lookup without bank conflicts. Each byte (two codes) becomes a
 //     packed pair of fp16 code values through a 256-entry table replicated 64
 //     times in LDS, entry e of lane l at byte 256*e + 4*l: the 64 lanes of a
 //     lookup always hit 64 different banks, and the address is one v_perm_b32
-//     (the byte of W next to the lane's own offset). The 64 KiB table is built
-//     while the weights are in flight.
-//   * Activations are staged once per workgroup (waves 0-3, 8 values per
-//     thread-chunk, chunk c at thread c % 256): the norm, if any - bit for bit
-//     the standalone RMSNorm kernel's sum order and roundings - then for bf16 a
-//     rescale by 2^-e (max|x| in [2^14, 2^15)) and an exact conversion to fp16,
-//     so both activation types meet 11-bit codes.
+//     (the byte of W next to the lane's own offset).
 //   * Arithmetic (fixed order, so a CPU restatement reproduces every bit): a
-//     dword's 8 products are chained in code order (v_fma_mix_f32 on fp16
-//     halves, the first onto +0), the dword's partial meets its block scale in
-//     one fma into the lane accumulator - the scale multiplies the block's
-//     partial sum, the factored form of the reference CPU kernel
-//     (app/engine/nf4cpu.py:115-129).
-//   * Reductions: lanes by a DPP butterfly inside each 16-lane row (the xor
-//     1, 2, 4, 8 tree: quad_perm, then half-mirror and mirror pair the same
-//     partial sums) and the four row sums as (r0 + r1) + (r2 + r3); K-slices
-//     left to right through LDS. No atomics anywhere.
+//     dword's 8 products are chained in code order (v_fma_mix_f32: fp16 code
+//     times fp32 activation, exact, the first onto +0), the dword's partial
+//     meets its block scale in one fma into the lane accumulator - the scale
+//     multiplies the block's partial sum, the factored form of the reference
+//     CPU kernel (app/engine/nf4cpu.py:115-129). fp16 and bf16 activations are
+//     both exact in fp32, so one loop serves both.
+//   * Reductions: lanes by DPP adds (the xor 1, 2, 4, 8 tree inside 16-lane
+//     rows, then the row sums as (r3 + r2) + (r1 + r0)); K-slices left to
+//     right through LDS. No atomics anywhere.
 #include "ttsp_common.h"
 
 namespace ttsp {
@@ -57,8 +57,10 @@ constexpr int LUT_REP = 64;                    // table copies, one per lane
 constexpr int LUT_BYTES = 256 * LUT_REP * 4;   // 64 KiB
 constexpr int GEMV_WAVES = 8;                  // waves per workgroup
 constexpr int GEMV_THREADS = GEMV_WAVES * 64;
-constexpr int STAGE_THREADS = 256;             // threads staging x (waves 0-3)
-constexpr int XC_MAX = 5;                      // x chunks per staging thread: K <= 5 * 8 * 256
+constexpr int XC_MAX = 3;                      // x chunks per thread: K <= 3 * 512 * 8
+#ifndef GEMV_PREFETCH_ROWS
+#define GEMV_PREFETCH_ROWS 2                   // weight rows in flight before the barrier
+#endif
 
 // One NF4 weight. For plain scales A8 and CODE2 point at any readable memory
 // (AMAX): the kernel reads them unconditionally and discards the values.
@@ -110,52 +112,7 @@ __device__ __forceinline__ uint16_t epilogue16(int dt, float acc, int epi, uint3
   return (uint16_t)st16(dt, o);
 }
 
-// Every lane of a 16-lane row gets the row's sum, by the xor 1, 2, 4, 8
-// butterfly tree (each step adds a partner's value; fp add is commutative, so
-// the mirrored partners of steps 3 and 4 give the same bits as xor 4 and 8).
-__device__ __forceinline__ float row16_sum(float v) {
-  v = __fadd_rn(v, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0xB1, 0xF, 0xF, false)));
-  v = __fadd_rn(v, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x4E, 0xF, 0xF, false)));
-  v = __fadd_rn(v, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x141, 0xF, 0xF, false)));
-  v = __fadd_rn(v, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x140, 0xF, 0xF, false)));
-  return v;
-}
-
-// Sum over the wave: the butterfly's xor 16 and 32 steps on the row sums.
-// The result is wave-uniform.
-__device__ __forceinline__ float wave_sum_dpp(float v) {
-  v = row16_sum(v);
-  const float r0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
-  const float r1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
-  const float r2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
-  const float r3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
-  return __fadd_rn(__fadd_rn(r0, r1), __fadd_rn(r2, r3));
-}
-
-// Max over the wave (every lane gets it).
-__device__ __forceinline__ float wave_max_dpp(float v) {
-  v = fmaxf(v, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0xB1, 0xF, 0xF, false)));
-  v = fmaxf(v, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x4E, 0xF, 0xF, false)));
-  v = fmaxf(v, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x141, 0xF, 0xF, false)));
-  v = fmaxf(v, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x140, 0xF, 0xF, false)));
-  const float r0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
-  const float r1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
-  const float r2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
-  const float r3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
-  return fmaxf(fmaxf(r0, r1), fmaxf(r2, r3));
-}
-
-// bf16 pair -> fp16 pair of the same values times 2^-xe (exact for the range
-// the rescale targets; below fp16's normal range the RNE conversion rounds).
-__device__ __forceinline__ uint32_t bf16x2_to_f16x2(uint32_t u, int xe) {
-  const uint32_t lo = f32_to_f16(__builtin_ldexpf(__uint_as_float(u << 16), -xe));
-  const uint32_t hi = f32_to_f16(__builtin_ldexpf(__uint_as_float(u & 0xffff0000u), -xe));
-  return lo | (hi << 16);
-}
-
-
-// Staging steps, specialised by activation type (the kernel branches on the
-// type once per step, not per element).
+// Per-type steps on 8-value chunks (uint4 of 16-bit elements).
 template <int DT>
 __device__ __forceinline__ float sumsq8(uint4 v, float acc) {  // element order, fma chain
   const uint32_t u[4] = {v.x, v.y, v.z, v.w};
@@ -166,15 +123,6 @@ __device__ __forceinline__ float sumsq8(uint4 v, float acc) {  // element order,
     acc = __builtin_fmaf(b, b, acc);
   }
   return acc;
-}
-
-template <int DT>
-__device__ __forceinline__ float maxabs8(uint4 v, float m) {
-  const uint32_t u[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-  for (int k = 0; k < 4; ++k)
-    m = fmaxf(m, fmaxf(fabsf(Elem<DT>::load(u[k])), fabsf(Elem<DT>::load(u[k] >> 16))));
-  return m;
 }
 
 // The fork's RMSNorm of 8 values: round(round(x * r) * w), the standalone kernel's arithmetic.
@@ -192,37 +140,48 @@ __device__ __forceinline__ uint4 norm8(uint4 v, uint4 g, float r) {
   return make_uint4(u[0], u[1], u[2], u[3]);
 }
 
-// After the first barrier: normalise this thread's chunks in LDS; their max.
+struct F8 {
+  float v[8];
+};
+
 template <int DT>
-__device__ __forceinline__ float norm_x(uint4* xs, const uint4* gs, int tid, int KD, float r) {
-  float m = 0.0f;
-  for (int c = tid; c < KD; c += STAGE_THREADS) {
-    const uint4 v = norm8<DT>(xs[c], gs[c], r);
-    xs[c] = v;
-    if (DT == DT_BF16) m = maxabs8<DT>(v, m);
+__device__ __forceinline__ F8 to_f32(uint4 c) {
+  const uint32_t u[4] = {c.x, c.y, c.z, c.w};
+  F8 o;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    o.v[2 * k] = Elem<DT>::load(u[k]);
+    o.v[2 * k + 1] = Elem<DT>::load(u[k] >> 16);
   }
-  return m;
+  return o;
 }
 
-// Dynamic LDS after the static table: pair staging [256], code2 [NM][256],
-// wave partials [8] and maxima [8], K-slice partials [8][NM*RPW], the
-// workgroup's scales [NM][RG*RPW][nblk] (16-byte aligned), then x as staged
-// (finally fp16) [K] and the norm weight [K].
+// Dynamic LDS after the static table: code2 [NM][256], norm partials [8],
+// K-slice partials [8][NM*RPW], the workgroup's resolved scales
+// [NM][rows_wg][nblk] (16-byte aligned), then x as staged [K/8].
 template <int J, int RPW, int NM>
 __global__ __launch_bounds__(GEMV_THREADS) void nf4_gemv_kernel(const GemvParams p) {
   constexpr int NW = GEMV_WAVES;
   constexpr int nthr = GEMV_THREADS;
+  constexpr int G = 256 * LUT_REP / (4 * 64 * NW);  // table stores (16 bytes) per lane
+  static_assert(NW % 4 == 0, "table entry split assumes 4 | waves");
   // Scale entries per thread: a workgroup holds (8 / KS) * RPW rows of at
   // most 8 * J * KS blocks (bs >= 64), i.e. <= 64 * RPW * J entries per weight.
   constexpr int SL = (NM * RPW * J + 7) / 8;
+  constexpr int PF = RPW < GEMV_PREFETCH_ROWS ? RPW : GEMV_PREFETCH_ROWS;
   __shared__ __align__(16) uint32_t lut_rep[256 * LUT_REP];
   extern __shared__ __align__(16) unsigned char lds_dyn[];
-  uint32_t* pair_s = reinterpret_cast<uint32_t*>(lds_dyn);
-  float* code2_s = reinterpret_cast<float*>(pair_s + 256);  // [NM][256]
-  float* wpart = code2_s + NM * 256;                         // [NW]
-  float* wmax = wpart + NW;                                  // [NW]
-  float* red = wmax + NW;                                    // [NW][NM*RPW]
-  float* srow = red + NW * NM * RPW;                         // [NM][rows_wg][nblk]
+  float* code2_s = reinterpret_cast<float*>(lds_dyn);  // [NM][256]
+  float* wpart = code2_s + NM * 256;                   // [NW] norm partial sums
+  float* red = wpart + NW;                             // [NW][NM*RPW]
+  float* srow = red + NW * NM * RPW;                   // [NM][rows_wg][nblk]
+
+  // Every kernel argument is in SGPRs before anything else waits: one round
+  // trip for the argument block instead of one per first use.
+  asm volatile("" ::"s"(p.mat[0].W), "s"(p.mat[0].A8), "s"(p.mat[0].AMAX), "s"(p.mat[0].CODE2),
+               "s"(p.mat[NM - 1].W), "s"(p.mat[NM - 1].A8), "s"(p.mat[NM - 1].AMAX), "s"(p.mat[NM - 1].CODE2),
+               "s"(p.LUT), "s"(p.X), "s"(p.G), "s"(p.R), "s"(p.Y), "s"(p.M), "s"(p.K), "s"(p.KS), "s"(p.bs_shift),
+               "s"(p.bs2_shift), "s"(p.dt), "s"(p.nested), "s"(p.norm));
 
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = uniform(tid >> 6);
@@ -233,24 +192,22 @@ __global__ __launch_bounds__(GEMV_THREADS) void nf4_gemv_kernel(const GemvParams
   const int rows_wg = RG * RPW;
   const int wg_row0 = blockIdx.x * rows_wg;
   const int row0 = wg_row0 + rg * RPW;
-  const int nsc = min(rows_wg, M - wg_row0) * nblk;        // scale entries per weight
+  const int nsc = min(rows_wg, M - wg_row0) * nblk;  // scale entries per weight
   const long long sc0 = (long long)wg_row0 * nblk;
   const int dt = p.dt;
   const bool nested = p.nested != 0, norm = p.norm != 0;
-  uint4* xs = reinterpret_cast<uint4*>(srow + ((NM * rows_wg * nblk + 3) & ~3));  // [KD] x as staged
-  uint4* gs = xs + KD;                                                             // [KD] norm weight
-  const int XN = (KD + STAGE_THREADS - 1) / STAGE_THREADS;  // x chunks per staging thread
-  const bool stager = tid < STAGE_THREADS;
+  uint4* xs = reinterpret_cast<uint4*>(srow + ((NM * rows_wg * nblk + 3) & ~3));  // [KD]
 
-  // 1. small operands first: code table entries, code2, scales, residual, x
-  float chi = 0.0f, clo = 0.0f, c2v[NM];
-  {
-    const int t = tid & 255;
-    chi = p.LUT[t >> 4];
-    clo = p.LUT[t & 15];
+  // 1. small operands first. The table entries this lane writes are
+  //    e_i = 4 * (wave + NW * i) + (lane >> 4): low half code[e_i >> 4] =
+  //    code[NW / 4 * i + wave / 4] (wave-uniform, read from lane e_i >> 4 of
+  //    a load of the 16 codes), high half code[e_i & 15] = code[4 * (wave % 4)
+  //    + lane / 16].
+  const float cl16 = p.LUT[lane & 15];
+  const float clo = p.LUT[4 * (wave & 3) + (lane >> 4)];
+  uint4 c2q[NM];  // code2 entries 4 * lane .. 4 * lane + 3 (every wave writes the whole table)
 #pragma unroll
-    for (int m = 0; m < NM; ++m) c2v[m] = p.mat[m].CODE2[nested ? t : 0];
-  }
+  for (int m = 0; m < NM; ++m) c2q[m] = *reinterpret_cast<const uint4*>(p.mat[m].CODE2 + (nested ? 4 * lane : 0));
   float sv[SL];
   uint32_t av[SL];
 #pragma unroll
@@ -264,72 +221,48 @@ __global__ __launch_bounds__(GEMV_THREADS) void nf4_gemv_kernel(const GemvParams
     sv[i] = am[nested ? gb >> p.bs2_shift : gb];
   }
   const uint32_t rres = p.R[min(row0 + min(lane, RPW - 1), M - 1)];  // epilogue operand
-  const int XNw = uniform(stager ? XN : 0);  // waves 4-7 stage nothing
-  uint4 xc[XC_MAX], gc[XC_MAX];
+  // x (and the norm weight): staged once per workgroup, chunk c = tid + 512 i
+  // by thread tid (one chunk per thread unless K > 4096, where there is no norm)
+  const int XN = uniform((KD + nthr - 1) / nthr);
+  uint4 xc[XC_MAX];
+  xc[0] = *reinterpret_cast<const uint4*>(p.X + 8 * (size_t)min(tid, KD - 1));
+  const uint4 gc = *reinterpret_cast<const uint4*>(p.G + 8 * (size_t)(norm ? min(tid, KD - 1) : 0));
 #pragma unroll
-  for (int i = 0; i < XC_MAX; ++i) {
-    xc[i] = gc[i] = make_uint4(0, 0, 0, 0);
-    if (i < XNw) {
-      const int c = min(tid + i * STAGE_THREADS, KD - 1);
-      xc[i] = *reinterpret_cast<const uint4*>(p.X + 8 * (size_t)c);
-      gc[i] = *reinterpret_cast<const uint4*>(p.G + 8 * (size_t)(norm ? c : 0));
-    }
+  for (int i = 1; i < XC_MAX; ++i) {
+    xc[i] = make_uint4(0, 0, 0, 0);
+    if (i < XN) xc[i] = *reinterpret_cast<const uint4*>(p.X + 8 * (size_t)min(tid + i * nthr, KD - 1));
   }
-  // 2. the weight stream: every dword of this wave's rows, all in flight
+
+  // 2. the first PF rows of the weight stream; the rest is requested row by
+  //    row during the dot products, PF rows ahead, so no wave's barrier
+  //    waits for its whole stream to be accepted by the memory system
   uint32_t w[NM][RPW][J];
+  auto load_row = [&](int r) {
 #pragma unroll
-  for (int m = 0; m < NM; ++m)
-#pragma unroll
-    for (int r = 0; r < RPW; ++r) {
+    for (int m = 0; m < NM; ++m) {
       const uint32_t* wr = p.mat[m].W + (size_t)min(row0 + r, M - 1) * KD + 64 * ks;
 #pragma unroll
       for (int j = 0; j < J; ++j)
         w[m][r][j] = __builtin_nontemporal_load(wr + min(64 * j * KS + lane, KD - 1 - 64 * ks));
     }
-
-  // 3. before the first barrier: pair staging, code2, and from the staging
-  //    waves either the norm's sum of squares (chunk order, the standalone
-  //    kernel's) or, without a norm, the bf16 maximum
-  if (tid < 256) {
-    pair_s[tid] = code_pair(chi, clo);
+  };
 #pragma unroll
-    for (int m = 0; m < NM; ++m) code2_s[m * 256 + tid] = c2v[m];
-  }
-  if (stager) {
-    float acc = 0.0f;
-#pragma unroll
-    for (int i = 0; i < XC_MAX; ++i) {
-      const int c = tid + i * STAGE_THREADS;
-      if (i < XNw && c < KD) {
-        xs[c] = xc[i];
-        if (norm) {
-          gs[c] = gc[i];
-          acc = dt == DT_BF16 ? sumsq8<DT_BF16>(xc[i], acc) : sumsq8<DT_F16>(xc[i], acc);
-        } else if (dt == DT_BF16) {
-          acc = maxabs8<DT_BF16>(xc[i], acc);
-        }
-      }
-    }
-    if (norm) {
-      acc = wave_sum(acc);
-      if (lane == 0) wpart[wave] = acc;
-    } else {
-      acc = wave_max_dpp(acc);
-      if (lane == 0) wmax[wave] = acc;
-    }
-  }
-  __syncthreads();
+  for (int r = 0; r < PF; ++r) load_row(r);
 
-  // 4. the replicated pair table, the resolved scales, and x staged
+  // 3. set-up while those stream: the replicated code table, code2 (each wave
+  //    its own full copy: identical values, so no barrier), the resolved
+  //    scales, x staged (or, with a norm, each wave's sum of squares)
   {
-    constexpr int G = (int)sizeof(lut_rep) / 1024 / NW;  // 1 KiB (4 entries) per wave store
-    uint32_t v[G];
+    const uint32_t hi = (uint32_t)f32_to_f16(clo) << 16;
+    const uint32_t c16 = f32_to_f16(cl16);
 #pragma unroll
-    for (int i = 0; i < G; ++i) v[i] = pair_s[4 * (wave + NW * i) + (lane >> 4)];
-#pragma unroll
-    for (int i = 0; i < G; ++i)
-      reinterpret_cast<uint4*>(lut_rep)[(wave + NW * i) * 64 + lane] = make_uint4(v[i], v[i], v[i], v[i]);
+    for (int i = 0; i < G; ++i) {
+      const uint32_t v = (uint32_t)__builtin_amdgcn_readlane((int)c16, NW / 4 * i + (wave >> 2)) | hi;
+      reinterpret_cast<uint4*>(lut_rep)[(wave + NW * i) * 64 + lane] = make_uint4(v, v, v, v);
+    }
   }
+#pragma unroll
+  for (int m = 0; m < NM; ++m) reinterpret_cast<uint4*>(code2_s + m * 256)[lane] = c2q[m];
 #pragma unroll
   for (int i = 0; i < SL; ++i) {
     const int e = tid + i * nthr;
@@ -340,85 +273,87 @@ __global__ __launch_bounds__(GEMV_THREADS) void nf4_gemv_kernel(const GemvParams
       srow[e + m * (rows_wg * nblk - nsc)] = s;  // weight m's block starts at m * rows_wg * nblk
     }
   }
-  // x to fp16 in LDS: bf16 is rescaled by 2^-xe so max|x| lands in
-  // [2^14, 2^15) and converted exactly (bf16's 8 significant bits fit in
-  // fp16's 11); the row sums are scaled back by 2^xe (also exact). Without a
-  // norm the maximum is known now; with one it needs the normalised x and a
-  // further barrier.
-  if (norm) {
-    if (stager) {
-      float ss = wpart[0];
+  if (!norm) {
 #pragma unroll
-      for (int w2 = 1; w2 < STAGE_THREADS / 64; ++w2) ss = __fadd_rn(ss, wpart[w2]);
-      const float r = rsqrt_rn(__fadd_rn(__fdiv_rn(ss, (float)K), p.eps));
-      float m = dt == DT_BF16 ? norm_x<DT_BF16>(xs, gs, tid, KD, r) : norm_x<DT_F16>(xs, gs, tid, KD, r);
-      m = wave_max_dpp(m);
-      if (lane == 0) wmax[wave] = m;
+    for (int i = 0; i < XC_MAX; ++i) {
+      const int c = tid + i * nthr;
+      if (i < XN && c < KD) xs[c] = xc[i];
     }
-    __syncthreads();
-  }
-  int xe = 0;
-  if (dt == DT_BF16) {
-    float m = wmax[0];
-#pragma unroll
-    for (int w2 = 1; w2 < STAGE_THREADS / 64; ++w2) m = fmaxf(m, wmax[w2]);
-    if (m > 0.0f && m <= 3.402823466e38f) xe = __builtin_amdgcn_frexp_expf(m) - 15;
-    if (stager) {
-      for (int c = tid; c < KD; c += STAGE_THREADS) {
-        const uint4 v = xs[c];
-        xs[c] = make_uint4(bf16x2_to_f16x2(v.x, xe), bf16x2_to_f16x2(v.y, xe), bf16x2_to_f16x2(v.z, xe),
-                           bf16x2_to_f16x2(v.w, xe));
-      }
-    }
+  } else {
+    float sq = 0.0f;
+    if (tid < KD) sq = dt == DT_BF16 ? sumsq8<DT_BF16>(xc[0], 0.0f) : sumsq8<DT_F16>(xc[0], 0.0f);
+    sq = wave_sum_dpp(sq);
+    if (lane == 0) wpart[wave] = sq;
   }
   __syncthreads();
-  // Past the row's end (K not a multiple of 512 * KS) x is zero: the clamped
-  // weight dword there is finite, so its products are exactly +0.
-  uint4 xr[J];
+  if (norm) {  // the 64-chunk partial sums left to right, then each thread's chunk
+    float ss = wpart[0];
 #pragma unroll
-  for (int j = 0; j < J; ++j) {
-    const int d = lane + 64 * (j * KS + ks);
-    const uint4 v = xs[min(d, KD - 1)];
-    const bool in_row = d < KD;
-    xr[j] = make_uint4(in_row ? v.x : 0u, in_row ? v.y : 0u, in_row ? v.z : 0u, in_row ? v.w : 0u);
+    for (int w2 = 1; w2 < NW; ++w2) ss = __fadd_rn(ss, wpart[w2]);
+    const float r = rsqrt_rn(__fadd_rn(__fdiv_rn(ss, (float)K), p.eps));
+    if (tid < KD) xs[tid] = dt == DT_BF16 ? norm8<DT_BF16>(xc[0], gc, r) : norm8<DT_F16>(xc[0], gc, r);
+    __syncthreads();
   }
 
-  // 6. dot products, row by row as the rows arrive
+  // x as fp32 (zero past the row's end: the clamped weight dword there is
+  // finite, so its products are exactly +0)
+  F8 xf[J];
+  {
+    uint4 xz[J];
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+      const int d = lane + 64 * (j * KS + ks);
+      const uint4 v = xs[min(d, KD - 1)];
+      xz[j] = d < KD ? v : make_uint4(0, 0, 0, 0);
+    }
+    if (dt == DT_BF16) {
+#pragma unroll
+      for (int j = 0; j < J; ++j) xf[j] = to_f32<DT_BF16>(xz[j]);
+    } else {
+#pragma unroll
+      for (int j = 0; j < J; ++j) xf[j] = to_f32<DT_F16>(xz[j]);
+    }
+  }
+
+  // 4. dot products, row by row as the rows arrive: a dword's 8 products in
+  //    code order, each an fma (the first onto +0), then its block scale
   const uint32_t lane4 = (uint32_t)lane * 4u;
   const unsigned char* lut_b = reinterpret_cast<const unsigned char*>(lut_rep);
-  int sblk[J];  // block of each of the lane's dwords (clamped inside the row past its end)
+  const unsigned char* srow_b = reinterpret_cast<const unsigned char*>(srow);
+  int sblk4[J];  // byte offset of each dword's block in a row (clamped inside the row past its end)
 #pragma unroll
-  for (int j = 0; j < J; ++j) sblk[j] = min(lane + 64 * (j * KS + ks), KD - 1) >> sh;
+  for (int j = 0; j < J; ++j) sblk4[j] = 4 * (min(lane + 64 * (j * KS + ks), KD - 1) >> sh);
   float tot[NM][RPW];
 #pragma unroll
-  for (int m = 0; m < NM; ++m)
+  for (int r = 0; r < RPW; ++r) {
+    if (r + PF < RPW) load_row(r + PF);
 #pragma unroll
-    for (int r = 0; r < RPW; ++r) {
-      const float* srr = srow + uniform((m * rows_wg + rg * RPW + r) * nblk);
+    for (int m = 0; m < NM; ++m) {
+      const int soff = uniform(4 * (m * rows_wg + rg * RPW + r) * nblk);
       float acc = 0.0f;
 #pragma unroll
       for (int j = 0; j < J; ++j) {
-        const float s = srr[sblk[j]];
+        const float s = *reinterpret_cast<const float*>(srow_b + soff + sblk4[j]);
         const uint32_t wv = w[m][r][j];
         const uint32_t c0 = *reinterpret_cast<const uint32_t*>(lut_b + __builtin_amdgcn_perm(wv, lane4, 0x0C0C0400u));
         const uint32_t c1 = *reinterpret_cast<const uint32_t*>(lut_b + __builtin_amdgcn_perm(wv, lane4, 0x0C0C0500u));
         const uint32_t c2 = *reinterpret_cast<const uint32_t*>(lut_b + __builtin_amdgcn_perm(wv, lane4, 0x0C0C0600u));
         const uint32_t c3 = *reinterpret_cast<const uint32_t*>(lut_b + __builtin_amdgcn_perm(wv, lane4, 0x0C0C0700u));
-        // the dword's 8 products in code order, each an fma (the first onto +0)
-        float q = __builtin_fmaf(h_lo(c0), h_lo(xr[j].x), 0.0f);
-        q = __builtin_fmaf(h_hi(c0), h_hi(xr[j].x), q);
-        q = __builtin_fmaf(h_lo(c1), h_lo(xr[j].y), q);
-        q = __builtin_fmaf(h_hi(c1), h_hi(xr[j].y), q);
-        q = __builtin_fmaf(h_lo(c2), h_lo(xr[j].z), q);
-        q = __builtin_fmaf(h_hi(c2), h_hi(xr[j].z), q);
-        q = __builtin_fmaf(h_lo(c3), h_lo(xr[j].w), q);
-        q = __builtin_fmaf(h_hi(c3), h_hi(xr[j].w), q);
+        float q = __builtin_fmaf(h_lo(c0), xf[j].v[0], 0.0f);
+        q = __builtin_fmaf(h_hi(c0), xf[j].v[1], q);
+        q = __builtin_fmaf(h_lo(c1), xf[j].v[2], q);
+        q = __builtin_fmaf(h_hi(c1), xf[j].v[3], q);
+        q = __builtin_fmaf(h_lo(c2), xf[j].v[4], q);
+        q = __builtin_fmaf(h_hi(c2), xf[j].v[5], q);
+        q = __builtin_fmaf(h_lo(c3), xf[j].v[6], q);
+        q = __builtin_fmaf(h_hi(c3), xf[j].v[7], q);
         acc = __builtin_fmaf(q, s, acc);
       }
-      tot[m][r] = __builtin_ldexpf(wave_sum_dpp(acc), xe);
+      tot[m][r] = wave_sum_dpp(acc);
     }
+  }
 
-  // 7. K-slices left to right, epilogue, store (lane r stores row r)
+  // 5. K-slices left to right, epilogue, store (lane r stores row r)
   if (KS > 1) {
     if (lane == 0) {
 #pragma unroll
@@ -473,7 +408,7 @@ static constexpr size_t kLdsPerCU = 160 * 1024;  // a workgroup's LDS must fit
 static size_t gemv_dyn_lds(const GemvShape& g, int nm, int K, int bs_shift) {
   const size_t rows_wg = (size_t)(GEMV_WAVES / g.KS) * g.RPW;
   const size_t sc = ((size_t)nm * rows_wg * (K >> bs_shift) + 3) & ~(size_t)3;
-  return 4 * (256 + 256 * (size_t)nm + 2 * GEMV_WAVES + (size_t)GEMV_WAVES * nm * g.RPW + sc) + 4 * (size_t)K;
+  return 4 * (256 * (size_t)nm + GEMV_WAVES + (size_t)GEMV_WAVES * nm * g.RPW + sc) + 2 * (size_t)K;
 }
 
 // K is split (KS a power of two) so that a lane's chunks J <= 8 leave the
@@ -557,18 +492,21 @@ static int gemv_launch(const void* X, int dt, const void* G, float eps, const Nf
   if (bs_shift < 6 || bs2_shift < 0 || K % 128 || K % blocksize || M <= 0) return (int)hipErrorInvalidValue;
   if (dt != DT_F16 && dt != DT_BF16) return (int)hipErrorInvalidValue;
   if (epi < 0 || epi > 2 || (epi && !R) || (mat3 && epi)) return (int)hipErrorInvalidValue;
-  if (K / 8 > XC_MAX * STAGE_THREADS) return (int)hipErrorInvalidValue;
   const int nm = mat3 ? 2 : 1;
   const GemvShape g = gemv_shape(M, K, nm, bs_shift);
   if (!g.J) return (int)hipErrorInvalidValue;
+  if (G && K / 8 > GEMV_THREADS) return (int)hipErrorInvalidValue;  // the norm: one chunk per thread
+  if (K / 8 > XC_MAX * GEMV_THREADS) return (int)hipErrorInvalidValue;
   if (LUT_BYTES + gemv_dyn_lds(g, nm, K, bs_shift) > kLdsPerCU) return (int)hipErrorInvalidValue;
+  if (nested && ((uintptr_t)mat1.CODE2 % 16 || (mat3 && (uintptr_t)mat3->CODE2 % 16)))
+    return (int)hipErrorInvalidValue;  // code2 is read 16 bytes per lane
   GemvParams p;
   p.mat[0] = mat1;
   p.mat[1] = mat3 ? *mat3 : mat1;
   for (Nf4Mat& m : p.mat) {
     if (!nested) {  // unused operands point at readable memory
       m.A8 = reinterpret_cast<const uint8_t*>(m.AMAX);
-      m.CODE2 = m.AMAX;
+      m.CODE2 = LUT;  // 16 bytes of it are read
       m.offset = 0.0f;
     }
   }

@@ -133,6 +133,27 @@ __device__ __forceinline__ float wave_max(float v) {
   return v;
 }
 
+// v + (v of the DPP partner); rows outside ROWS add +0 and are not read after.
+template <int CTRL, int ROWS>
+__device__ __forceinline__ float dpp_add(float v) {
+  return __fadd_rn(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, ROWS, 0xF, false)));
+}
+
+// Sum over the 64 lanes with the partner distance rising: the xor 1, 2, 4, 8
+// butterfly inside each 16-lane row (quad_perm, then half-mirror and mirror,
+// which pair the same partial sums as xor 4 and 8), then row sums r1 += r0,
+// r3 += r2 and r3 += r1 by row broadcasts: lane 63 holds (r3 + r2) + (r1 + r0),
+// the same bits as the xor 16, 32 steps. The result is wave-uniform.
+__device__ __forceinline__ float wave_sum_dpp(float v) {
+  v = dpp_add<0xB1, 0xF>(v);
+  v = dpp_add<0x4E, 0xF>(v);
+  v = dpp_add<0x141, 0xF>(v);
+  v = dpp_add<0x140, 0xF>(v);
+  v = dpp_add<0x142, 0xA>(v);
+  v = dpp_add<0x143, 0xC>(v);
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+}
+
 }  // namespace ttsp
 
 // Launch-error plumbing for the extern "C" entry points: each returns the

@@ -204,8 +204,9 @@ def matmul(module, x, *, epi: int = EPI_NONE, operand=None, out=None):
     return out.view(*x.shape[:-1], M)
 
 
-#: Widest input the fused single-row kernel stages (`ttsp_nf4_gemv_fused`).
-FUSED_MAX_K = 10240
+#: Widest input whose RMSNorm the single-row kernel folds in (one 8-value
+#: chunk per thread of its 512).
+NORM_MAX_K = 4096
 
 
 def matmul_fused(module, x, *, norm_weight=None, eps: float = 1e-6, module3=None, epi: int = EPI_NONE,
@@ -226,7 +227,7 @@ def matmul_fused(module, x, *, norm_weight=None, eps: float = 1e-6, module3=None
     if dt not in (_lib.DT_F16, _lib.DT_BF16) or x.device.type != "cuda":
         return None
     K, M = fast["K"], fast["M"]
-    if x.shape[-1] != K or x.numel() != K or K > FUSED_MAX_K or not x.is_contiguous() or x.data_ptr() % 16:
+    if x.shape[-1] != K or x.numel() != K or not x.is_contiguous() or x.data_ptr() % 16:
         return None
     fast3 = None
     if module3 is not None:
@@ -237,6 +238,8 @@ def matmul_fused(module, x, *, norm_weight=None, eps: float = 1e-6, module3=None
                                                                                   fast["bs2"]):
             return None
     if norm_weight is not None:
+        if K > NORM_MAX_K:
+            return None
         if (norm_weight.dtype != x.dtype or norm_weight.numel() != K or not norm_weight.is_contiguous()
                 or norm_weight.data_ptr() % 16 or norm_weight.device != x.device):
             return None
