@@ -58,6 +58,9 @@ constexpr int LUT_BYTES = 256 * LUT_REP * 4;   // 64 KiB
 constexpr int GEMV_WAVES = 8;                  // waves per workgroup
 constexpr int GEMV_THREADS = GEMV_WAVES * 64;
 constexpr int XC_MAX = 3;                      // x chunks per thread: K <= 3 * 512 * 8
+#ifndef GEMV_LOOKAHEAD
+#define GEMV_LOOKAHEAD 3                       // (row, chunk) items whose code lookups run ahead
+#endif
 #ifndef GEMV_PREFETCH_ROWS
 #define GEMV_PREFETCH_ROWS 2                   // weight rows in flight before the barrier
 #endif
@@ -157,8 +160,8 @@ __device__ __forceinline__ F8 to_f32(uint4 c) {
 }
 
 // Dynamic LDS after the static table: code2 [NM][256], norm partials [8],
-// K-slice partials [8][NM*RPW], the workgroup's resolved scales
-// [NM][rows_wg][nblk] (16-byte aligned), then x as staged [K/8].
+// K-slice partials [8][NM*RPW], the resolved scales [8 waves][NM][RPW][8 J]
+// (16-byte aligned), then x as staged [K/8].
 template <int J, int RPW, int NM>
 __global__ __launch_bounds__(GEMV_THREADS) void nf4_gemv_kernel(const GemvParams p) {
   constexpr int NW = GEMV_WAVES;
@@ -174,7 +177,7 @@ __global__ __launch_bounds__(GEMV_THREADS) void nf4_gemv_kernel(const GemvParams
   float* code2_s = reinterpret_cast<float*>(lds_dyn);  // [NM][256]
   float* wpart = code2_s + NM * 256;                   // [NW] norm partial sums
   float* red = wpart + NW;                             // [NW][NM*RPW]
-  float* srow = red + NW * NM * RPW;                   // [NM][rows_wg][nblk]
+  float* srow = red + NW * NM * RPW;                   // [NW][NM][RPW][8 J] scale slots
 
   // Every kernel argument is in SGPRs before anything else waits: one round
   // trip for the argument block instead of one per first use.
@@ -192,11 +195,9 @@ __global__ __launch_bounds__(GEMV_THREADS) void nf4_gemv_kernel(const GemvParams
   const int rows_wg = RG * RPW;
   const int wg_row0 = blockIdx.x * rows_wg;
   const int row0 = wg_row0 + rg * RPW;
-  const int nsc = min(rows_wg, M - wg_row0) * nblk;  // scale entries per weight
-  const long long sc0 = (long long)wg_row0 * nblk;
   const int dt = p.dt;
   const bool nested = p.nested != 0, norm = p.norm != 0;
-  uint4* xs = reinterpret_cast<uint4*>(srow + ((NM * rows_wg * nblk + 3) & ~3));  // [KD]
+  uint4* xs = reinterpret_cast<uint4*>(srow + NW * NM * RPW * 8 * J);  // [KD]
 
   // 1. small operands first. The table entries this lane writes are
   //    e_i = 4 * (wave + NW * i) + (lane >> 4): low half code[e_i >> 4] =
@@ -208,13 +209,22 @@ __global__ __launch_bounds__(GEMV_THREADS) void nf4_gemv_kernel(const GemvParams
   uint4 c2q[NM];  // code2 entries 4 * lane .. 4 * lane + 3 (every wave writes the whole table)
 #pragma unroll
   for (int m = 0; m < NM; ++m) c2q[m] = *reinterpret_cast<const uint4*>(p.mat[m].CODE2 + (nested ? 4 * lane : 0));
+  // Scales, per wave and read by that wave only (no barrier): slot
+  // (m, r, 8 j + g) holds the scale of block g of the wave's chunk j in row r
+  // of weight m (8 slots per chunk; with bs > 64 the chunk has 64 / (bs / 8)
+  // blocks and the other slots go unread), so a lane's scale sits at a fixed
+  // offset per row and chunk. Lane l loads slots l + 64 i.
+  constexpr int SW = NM * RPW * 8 * J;  // slots per wave
+  const int spc = sh <= 6 ? 64 >> sh : 1;  // blocks per 64-dword chunk
   float sv[SL];
   uint32_t av[SL];
 #pragma unroll
   for (int i = 0; i < SL; ++i) {
-    const int e = tid + i * nthr;
-    const int m = NM > 1 && e >= nsc ? 1 : 0;
-    const long long gb = sc0 + min(e - m * nsc, nsc - 1);
+    const int sl = min(lane + 64 * i, SW - 1);
+    const int mr = sl / (8 * J), jg = sl % (8 * J);
+    const int m = mr / RPW, r = mr % RPW, j = jg >> 3, g = min(jg & 7, spc - 1);
+    const int d = min(64 * (j * KS + ks) + (g << sh), KD - 1);
+    const uint32_t gb = (uint32_t)min(row0 + r, M - 1) * (uint32_t)nblk + (uint32_t)(d >> sh);
     const uint8_t* a8 = m ? p.mat[NM - 1].A8 : p.mat[0].A8;
     const float* am = m ? p.mat[NM - 1].AMAX : p.mat[0].AMAX;
     av[i] = a8[gb];
@@ -237,13 +247,16 @@ __global__ __launch_bounds__(GEMV_THREADS) void nf4_gemv_kernel(const GemvParams
   //    row during the dot products, PF rows ahead, so no wave's barrier
   //    waits for its whole stream to be accepted by the memory system
   uint32_t w[NM][RPW][J];
+  uint32_t woff[J];  // byte offset of the lane's dword j in the wave's K-slice (clamped inside the row)
+#pragma unroll
+  for (int j = 0; j < J; ++j) woff[j] = 4u * (uint32_t)min(64 * j * KS + lane, KD - 1 - 64 * ks);
   auto load_row = [&](int r) {
 #pragma unroll
     for (int m = 0; m < NM; ++m) {
-      const uint32_t* wr = p.mat[m].W + (size_t)min(row0 + r, M - 1) * KD + 64 * ks;
+      const char* wr = reinterpret_cast<const char*>(p.mat[m].W + (size_t)uniform(min(row0 + r, M - 1)) * KD + 64 * ks);
 #pragma unroll
       for (int j = 0; j < J; ++j)
-        w[m][r][j] = __builtin_nontemporal_load(wr + min(64 * j * KS + lane, KD - 1 - 64 * ks));
+        w[m][r][j] = __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(wr + woff[j]));
     }
   };
 #pragma unroll
@@ -265,13 +278,10 @@ __global__ __launch_bounds__(GEMV_THREADS) void nf4_gemv_kernel(const GemvParams
   for (int m = 0; m < NM; ++m) reinterpret_cast<uint4*>(code2_s + m * 256)[lane] = c2q[m];
 #pragma unroll
   for (int i = 0; i < SL; ++i) {
-    const int e = tid + i * nthr;
-    if (e < NM * nsc) {
-      const int m = NM > 1 && e >= nsc ? 1 : 0;
-      const float off = m ? p.mat[NM - 1].offset : p.mat[0].offset;
-      const float s = nested ? __fadd_rn(__fmul_rn(code2_s[m * 256 + av[i]], sv[i]), off) : sv[i];
-      srow[e + m * (rows_wg * nblk - nsc)] = s;  // weight m's block starts at m * rows_wg * nblk
-    }
+    const int sl = lane + 64 * i;
+    const int m = sl / (8 * J * RPW);
+    const float off = m ? p.mat[NM - 1].offset : p.mat[0].offset;
+    if (sl < SW) srow[wave * SW + sl] = nested ? __fadd_rn(__fmul_rn(code2_s[m * 256 + av[i]], sv[i]), off) : sv[i];
   }
   if (!norm) {
 #pragma unroll
@@ -320,38 +330,49 @@ __global__ __launch_bounds__(GEMV_THREADS) void nf4_gemv_kernel(const GemvParams
   const uint32_t lane4 = (uint32_t)lane * 4u;
   const unsigned char* lut_b = reinterpret_cast<const unsigned char*>(lut_rep);
   const unsigned char* srow_b = reinterpret_cast<const unsigned char*>(srow);
-  int sblk4[J];  // byte offset of each dword's block in a row (clamped inside the row past its end)
+  int sblk4[J];  // byte offset of each of the lane's chunks' scale slot in row 0 of weight 0
 #pragma unroll
-  for (int j = 0; j < J; ++j) sblk4[j] = 4 * (min(lane + 64 * (j * KS + ks), KD - 1) >> sh);
+  for (int j = 0; j < J; ++j) sblk4[j] = 4 * (wave * SW + 8 * j + (lane >> sh));
+  // The (row, chunk) items in order, the code lookups LA items ahead of the
+  // arithmetic (sched_barrier keeps the compiler from pulling them back), the
+  // next weight row requested at each row's start.
+  constexpr int T = NM * RPW * J;
+  constexpr int LA = GEMV_LOOKAHEAD < T ? GEMV_LOOKAHEAD : T;
+  float sc[T];
+  uint32_t cp[T][4];
+  auto lookup = [&](int t) {
+    const int j = t % J, mr = t / J, m = mr / RPW, r = mr % RPW;
+    sc[t] = *reinterpret_cast<const float*>(srow_b + sblk4[j] + 4 * 8 * J * (m * RPW + r));
+#pragma unroll
+    for (int b = 0; b < 4; ++b)
+      cp[t][b] = *reinterpret_cast<const uint32_t*>(lut_b + __builtin_amdgcn_perm(w[m][r][j], lane4, 0x0C0C0400u + (b << 8)));
+  };
+#pragma unroll
+  for (int t = 0; t < LA; ++t) lookup(t);
   float tot[NM][RPW];
 #pragma unroll
-  for (int r = 0; r < RPW; ++r) {
-    if (r + PF < RPW) load_row(r + PF);
+  for (int m = 0; m < NM; ++m)
 #pragma unroll
-    for (int m = 0; m < NM; ++m) {
-      const int soff = uniform(4 * (m * rows_wg + rg * RPW + r) * nblk);
+    for (int r = 0; r < RPW; ++r) {
+      if (m == 0 && r + PF < RPW) load_row(r + PF);
       float acc = 0.0f;
 #pragma unroll
       for (int j = 0; j < J; ++j) {
-        const float s = *reinterpret_cast<const float*>(srow_b + soff + sblk4[j]);
-        const uint32_t wv = w[m][r][j];
-        const uint32_t c0 = *reinterpret_cast<const uint32_t*>(lut_b + __builtin_amdgcn_perm(wv, lane4, 0x0C0C0400u));
-        const uint32_t c1 = *reinterpret_cast<const uint32_t*>(lut_b + __builtin_amdgcn_perm(wv, lane4, 0x0C0C0500u));
-        const uint32_t c2 = *reinterpret_cast<const uint32_t*>(lut_b + __builtin_amdgcn_perm(wv, lane4, 0x0C0C0600u));
-        const uint32_t c3 = *reinterpret_cast<const uint32_t*>(lut_b + __builtin_amdgcn_perm(wv, lane4, 0x0C0C0700u));
-        float q = __builtin_fmaf(h_lo(c0), xf[j].v[0], 0.0f);
-        q = __builtin_fmaf(h_hi(c0), xf[j].v[1], q);
-        q = __builtin_fmaf(h_lo(c1), xf[j].v[2], q);
-        q = __builtin_fmaf(h_hi(c1), xf[j].v[3], q);
-        q = __builtin_fmaf(h_lo(c2), xf[j].v[4], q);
-        q = __builtin_fmaf(h_hi(c2), xf[j].v[5], q);
-        q = __builtin_fmaf(h_lo(c3), xf[j].v[6], q);
-        q = __builtin_fmaf(h_hi(c3), xf[j].v[7], q);
-        acc = __builtin_fmaf(q, s, acc);
+        const int t = (m * RPW + r) * J + j;
+        if (t + LA < T) lookup(t + LA);
+        __builtin_amdgcn_sched_barrier(0);
+        float q = __builtin_fmaf(h_lo(cp[t][0]), xf[j].v[0], 0.0f);
+        q = __builtin_fmaf(h_hi(cp[t][0]), xf[j].v[1], q);
+        q = __builtin_fmaf(h_lo(cp[t][1]), xf[j].v[2], q);
+        q = __builtin_fmaf(h_hi(cp[t][1]), xf[j].v[3], q);
+        q = __builtin_fmaf(h_lo(cp[t][2]), xf[j].v[4], q);
+        q = __builtin_fmaf(h_hi(cp[t][2]), xf[j].v[5], q);
+        q = __builtin_fmaf(h_lo(cp[t][3]), xf[j].v[6], q);
+        q = __builtin_fmaf(h_hi(cp[t][3]), xf[j].v[7], q);
+        acc = __builtin_fmaf(q, sc[t], acc);
       }
       tot[m][r] = wave_sum_dpp(acc);
     }
-  }
 
   // 5. K-slices left to right, epilogue, store (lane r stores row r)
   if (KS > 1) {
@@ -401,13 +422,15 @@ struct GemvShape {
 static constexpr int kJ[] = {1, 2, 3, 4, 5, 6, 8};
 static constexpr int kRPW1[] = {1, 2, 3, 4, 5, 6, 8};
 static constexpr int kRPW2[] = {1, 2, 3, 4, 5};
-static constexpr int kCUs = 256;
+#ifndef GEMV_WG_SLOTS
+#define GEMV_WG_SLOTS 256
+#endif
+static constexpr int kCUs = GEMV_WG_SLOTS;  // workgroups resident at once
 static constexpr size_t kLdsPerCU = 160 * 1024;  // a workgroup's LDS must fit
 
 // Dynamic LDS of one workgroup (the table is static).
 static size_t gemv_dyn_lds(const GemvShape& g, int nm, int K, int bs_shift) {
-  const size_t rows_wg = (size_t)(GEMV_WAVES / g.KS) * g.RPW;
-  const size_t sc = ((size_t)nm * rows_wg * (K >> bs_shift) + 3) & ~(size_t)3;
+  const size_t sc = (size_t)GEMV_WAVES * nm * g.RPW * 8 * g.J;  // scale slots
   return 4 * (256 * (size_t)nm + GEMV_WAVES + (size_t)GEMV_WAVES * nm * g.RPW + sc) + 2 * (size_t)K;
 }
 
