@@ -6,13 +6,16 @@
 //   * dequantise BM x 64 weights, 16 packed bytes (32 codes) each, as
 //     round(code * scale) in the activation type - the exact value
 //     bitsandbytes' dequantize_4bit produces, so the product is the dense
-//     fork's matmul on identical weights - straight into an LDS A tile;
+//     fork's matmul on identical weights - straight into an LDS A tile (the
+//     16 code points in LDS: 64 lanes hit at most 16 banks, no conflicts; one
+//     hardware pack-convert rounds two products);
 //   * copy BN x 64 activations into an LDS B tile;
 // and the 4 waves run v_mfma_f32_32x32x16 over their sub-tiles, fp32
-// accumulate. LDS is double-buffered; the next step's packed weights and
-// activations are already in registers while the current step multiplies.
-// Rows are padded to 72 elements (144 B) so the 16-byte operand reads of 16
-// consecutive rows hit disjoint banks.
+// accumulate. The packed weights, scales and activations of the next PF
+// steps are in flight in registers while a step multiplies (the K loop is
+// latency-bound otherwise: a lone workgroup waits a memory round trip per
+// step), and LDS is double-buffered. Rows are padded to 72 elements (144 B) so
+// the 16-byte operand reads of 16 consecutive rows hit disjoint banks.
 //
 // MFMA 32x32x16 operand layout: lane l supplies row (l % 32) of A and column
 // (l % 32) of B, each as 8 consecutive k at 8 * (l / 32); accumulator r of
@@ -25,6 +28,9 @@ namespace ttsp {
 typedef __bf16 bf16x8_v __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x8_v __attribute__((ext_vector_type(8)));
 typedef float f32x16_v __attribute__((ext_vector_type(16)));
+typedef __bf16 bf16x2_v __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2_v __attribute__((ext_vector_type(2)));
+typedef float f32x2_v __attribute__((ext_vector_type(2)));
 
 constexpr int GEMM_THREADS = 256;
 constexpr int KT = 64;        // codes per K-step (one bs=64 scale block)
@@ -40,8 +46,20 @@ __device__ __forceinline__ f32x16_v mfma32(uint4 a, uint4 b, f32x16_v c) {
                                                   __builtin_bit_cast(f16x8_v, b), c, 0, 0, 0);
 }
 
-// WM x WN waves; each wave covers (BM/WM) x (BN/WN) with 32x32 MFMA blocks.
-template <int DT, int BM, int BN, int WM, int WN, bool NESTED>
+// Two fp32 values, each already rounded to fp32, to the activation type
+// (round to nearest even, one hardware pack-convert); lo in the low half.
+template <int DT>
+__device__ __forceinline__ uint32_t pack2(float lo, float hi) {
+  const f32x2_v v = {opaque(lo), opaque(hi)};
+  if constexpr (DT == DT_BF16)
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2_v));
+  else
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, f16x2_v));
+}
+
+// WM x WN waves; each wave covers (BM/WM) x (BN/WN) with 32x32 MFMA blocks;
+// PF K-steps of operands in flight (nsteps a multiple of PF).
+template <int DT, int BM, int BN, int WM, int WN, bool NESTED, int PF>
 __global__ __launch_bounds__(GEMM_THREADS) void nf4_gemm_kernel(
     const uint16_t* __restrict__ X, const uint8_t* __restrict__ W, const uint8_t* __restrict__ A8,
     const float* __restrict__ AMAX, const float* __restrict__ CODE2, float offset,
@@ -49,9 +67,10 @@ __global__ __launch_bounds__(GEMM_THREADS) void nf4_gemm_kernel(
     int epi, int M, int K, int N, int bs_shift, int bs2_shift) {
   static_assert(WM * WN == GEMM_THREADS / 64, "4 waves");
   constexpr int TM = BM / WM / 32, TN = BN / WN / 32;  // MFMA blocks per wave
-  constexpr int A_PER_T = BM * (KT / 32) / GEMM_THREADS;  // 16-byte packed chunks per thread
-  constexpr int B_PER_T = BN * (KT / 8) / GEMM_THREADS;   // 16-byte activation chunks per thread
-  static_assert(A_PER_T >= 1 && B_PER_T >= 1, "tile too small for the workgroup");
+  constexpr int A_CH = BM * (KT / 32);                                  // 16-byte packed chunks per step
+  constexpr int A_PER_T = (A_CH + GEMM_THREADS - 1) / GEMM_THREADS;     // per thread (the last partly idle)
+  constexpr int B_PER_T = BN * (KT / 8) / GEMM_THREADS;                 // 16-byte activation chunks per thread
+  static_assert(B_PER_T >= 1 && BN * (KT / 8) % GEMM_THREADS == 0, "tile too small for the workgroup");
 
   __shared__ uint16_t As[2][BM * LROW];
   __shared__ uint16_t Bs[2][BN * LROW];
@@ -67,66 +86,63 @@ __global__ __launch_bounds__(GEMM_THREADS) void nf4_gemm_kernel(
   if (tid < 16) lut_s[tid] = LUT[tid];
   if constexpr (NESTED) code2_s[tid] = CODE2[tid];
 
-  uint4 wraw[A_PER_T];
-  float wsc[A_PER_T];
-  uint4 xraw[B_PER_T];
+  struct Stage {
+    uint4 w[A_PER_T];
+    float s[A_PER_T];
+    uint32_t a8[NESTED ? A_PER_T : 1];
+    uint4 x[B_PER_T];
+  };
+  Stage stg[PF];
 
-  auto load_step = [&](int step) {
-    const int k0 = step * KT;
+  // step clamped into range: the loads past the last step repeat it and go unused
+  auto load_step = [&](Stage& sg, int step) {
+    const int k0 = min(step, nsteps - 1) * KT;
 #pragma unroll
     for (int i = 0; i < A_PER_T; ++i) {
-      const int c = tid + i * GEMM_THREADS;  // chunk: row c/2, half c%2
+      const int c = min(tid + i * GEMM_THREADS, A_CH - 1);  // chunk: row c/2, half c%2
       const int row = min(m0 + c / 2, M - 1);
       const int kc = k0 + (c & 1) * 32;
       typedef uint32_t u32x4_v __attribute__((ext_vector_type(4)));
       const u32x4_v v = __builtin_nontemporal_load(
           reinterpret_cast<const u32x4_v*>(W + (size_t)row * rowbytes + kc / 2));
-      wraw[i] = make_uint4(v.x, v.y, v.z, v.w);
+      sg.w[i] = make_uint4(v.x, v.y, v.z, v.w);
       const long long b = ((long long)row * K + kc) >> bs_shift;
       if constexpr (NESTED) {
-        wsc[i] = AMAX[b >> bs2_shift];  // absmax2; the code2 index comes from load_a8
+        sg.a8[i] = A8[b];
+        sg.s[i] = AMAX[b >> bs2_shift];
       } else {
-        wsc[i] = AMAX[b];
+        sg.s[i] = AMAX[b];
       }
     }
 #pragma unroll
     for (int i = 0; i < B_PER_T; ++i) {
       const int c = tid + i * GEMM_THREADS;  // chunk: row c/8, 8 elements at (c%8)*8
-      const int n = n0 + c / (KT / 8);
-      xraw[i] = n < N ? *reinterpret_cast<const uint4*>(X + (size_t)n * K + k0 + (c % (KT / 8)) * 8)
-                      : make_uint4(0, 0, 0, 0);
+      const int n = min(n0 + c / (KT / 8), N - 1);
+      sg.x[i] = *reinterpret_cast<const uint4*>(X + (size_t)n * K + k0 + (c % (KT / 8)) * 8);
     }
   };
-  uint32_t a8raw[NESTED ? A_PER_T : 1];
-  auto load_a8 = [&](int step) {
-    if constexpr (NESTED) {
-      const int k0 = step * KT;
-#pragma unroll
-      for (int i = 0; i < A_PER_T; ++i) {
-        const int c = tid + i * GEMM_THREADS;
-        const int row = min(m0 + c / 2, M - 1);
-        const long long b = ((long long)row * K + k0 + (c & 1) * 32) >> bs_shift;
-        a8raw[i] = A8[b];
-      }
-    }
-  };
-  auto store_step = [&](int buf) {
+  auto store_step = [&](const Stage& sg, int buf) {
 #pragma unroll
     for (int i = 0; i < A_PER_T; ++i) {
       const int c = tid + i * GEMM_THREADS;
-      float s = wsc[i];
-      if constexpr (NESTED) s = __fadd_rn(__fmul_rn(code2_s[a8raw[i]], s), offset);
-      const uint32_t wv[4] = {wraw[i].x, wraw[i].y, wraw[i].z, wraw[i].w};
-      uint32_t o[16];
+      if (A_CH % GEMM_THREADS && c >= A_CH) break;
+      float s = sg.s[i];
+      if constexpr (NESTED) s = __fadd_rn(__fmul_rn(code2_s[sg.a8[i]], s), offset);
+      const uint32_t wv[4] = {sg.w[i].x, sg.w[i].y, sg.w[i].z, sg.w[i].w};
+      // all 32 code lookups in flight before the first is used (one LDS
+      // round trip per step instead of one per byte)
+      float cv[32];
 #pragma unroll
       for (int q = 0; q < 4; ++q)
 #pragma unroll
         for (int bb = 0; bb < 4; ++bb) {
           const uint32_t byte = (wv[q] >> (8 * bb)) & 0xffu;
-          const uint32_t lo = Elem<DT>::store(__fmul_rn(lut_s[byte >> 4], s));
-          const uint32_t hi = Elem<DT>::store(__fmul_rn(lut_s[byte & 15u], s));
-          o[q * 4 + bb] = lo | (hi << 16);
+          cv[2 * (q * 4 + bb)] = lut_s[byte >> 4];
+          cv[2 * (q * 4 + bb) + 1] = lut_s[byte & 15u];
         }
+      uint32_t o[16];
+#pragma unroll
+      for (int e = 0; e < 16; ++e) o[e] = pack2<DT>(__fmul_rn(cv[2 * e], s), __fmul_rn(cv[2 * e + 1], s));
       uint4* dst = reinterpret_cast<uint4*>(&As[buf][(c / 2) * LROW + (c & 1) * 32]);
 #pragma unroll
       for (int q = 0; q < 4; ++q) dst[q] = make_uint4(o[4 * q], o[4 * q + 1], o[4 * q + 2], o[4 * q + 3]);
@@ -134,7 +150,9 @@ __global__ __launch_bounds__(GEMM_THREADS) void nf4_gemm_kernel(
 #pragma unroll
     for (int i = 0; i < B_PER_T; ++i) {
       const int c = tid + i * GEMM_THREADS;
-      *reinterpret_cast<uint4*>(&Bs[buf][(c / (KT / 8)) * LROW + (c % (KT / 8)) * 8]) = xraw[i];
+      const int n = n0 + c / (KT / 8);
+      *reinterpret_cast<uint4*>(&Bs[buf][(c / (KT / 8)) * LROW + (c % (KT / 8)) * 8]) =
+          n < N ? sg.x[i] : make_uint4(0, 0, 0, 0);
     }
   };
 
@@ -146,33 +164,40 @@ __global__ __launch_bounds__(GEMM_THREADS) void nf4_gemm_kernel(
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
 
-  load_a8(0);
-  load_step(0);
+#pragma unroll
+  for (int i = 0; i < PF; ++i) load_step(stg[i], i);
   __syncthreads();  // lut_s / code2_s
-  for (int step = 0; step < nsteps; ++step) {
-    const int buf = step & 1;
-    store_step(buf);
-    __syncthreads();
-    if (step + 1 < nsteps) {
-      load_a8(step + 1);
-      load_step(step + 1);
-    }
-    const uint16_t* as = As[buf];
-    const uint16_t* bs = Bs[buf];
+  store_step(stg[0], 0);
+  __syncthreads();
+  load_step(stg[0], PF);
+  // Step s multiplies buffer s & 1 while the same waves dequantise step s + 1
+  // into the other buffer (read by nobody since the previous barrier); one
+  // barrier per step. The last step stages a repeat of itself, unread.
+  for (int s0 = 0; s0 < nsteps; s0 += PF) {
 #pragma unroll
-    for (int kk = 0; kk < KT / 16; ++kk) {
-      const int ko = kk * 16 + (lane >> 5) * 8;
-      uint4 af[TM], bf[TN];
+    for (int i = 0; i < PF; ++i) {
+      const int step = s0 + i;
+      const int buf = step & 1;
+      const uint16_t* as = As[buf];
+      const uint16_t* bs = Bs[buf];
 #pragma unroll
-      for (int i = 0; i < TM; ++i)
-        af[i] = *reinterpret_cast<const uint4*>(as + (wm * (BM / WM) + i * 32 + (lane & 31)) * LROW + ko);
+      for (int kk = 0; kk < KT / 16; ++kk) {
+        const int ko = kk * 16 + (lane >> 5) * 8;
+        uint4 af[TM], bf[TN];
 #pragma unroll
-      for (int j = 0; j < TN; ++j)
-        bf[j] = *reinterpret_cast<const uint4*>(bs + (wn * (BN / WN) + j * 32 + (lane & 31)) * LROW + ko);
+        for (int a = 0; a < TM; ++a)
+          af[a] = *reinterpret_cast<const uint4*>(as + (wm * (BM / WM) + a * 32 + (lane & 31)) * LROW + ko);
 #pragma unroll
-      for (int i = 0; i < TM; ++i)
+        for (int b = 0; b < TN; ++b)
+          bf[b] = *reinterpret_cast<const uint4*>(bs + (wn * (BN / WN) + b * 32 + (lane & 31)) * LROW + ko);
 #pragma unroll
-        for (int j = 0; j < TN; ++j) acc[i][j] = mfma32<DT>(af[i], bf[j], acc[i][j]);
+        for (int a = 0; a < TM; ++a)
+#pragma unroll
+          for (int b = 0; b < TN; ++b) acc[a][b] = mfma32<DT>(af[a], bf[b], acc[a][b]);
+      }
+      store_step(stg[(i + 1) % PF], buf ^ 1);
+      __syncthreads();
+      load_step(stg[(i + 1) % PF], step + 1 + PF);
     }
   }
 
@@ -197,17 +222,17 @@ __global__ __launch_bounds__(GEMM_THREADS) void nf4_gemm_kernel(
     }
 }
 
-template <int DT, int BM, int BN, int WM, int WN>
+template <int DT, int BM, int BN, int WM, int WN, int PF>
 static void launch_gemm(const void* X, const uint8_t* W, const uint8_t* A8, const float* AMAX,
                         const float* CODE2, float offset, const float* LUT, void* Y, const void* R,
                         int epi, int M, int K, int N, int bs_shift, int bs2_shift, hipStream_t st) {
   const dim3 grid((M + BM - 1) / BM, (N + BN - 1) / BN);
   if (A8)
-    hipLaunchKernelGGL((nf4_gemm_kernel<DT, BM, BN, WM, WN, true>), grid, dim3(GEMM_THREADS), 0, st,
+    hipLaunchKernelGGL((nf4_gemm_kernel<DT, BM, BN, WM, WN, true, PF>), grid, dim3(GEMM_THREADS), 0, st,
                        (const uint16_t*)X, W, A8, AMAX, CODE2, offset, LUT, (uint16_t*)Y,
                        (const uint16_t*)R, epi, M, K, N, bs_shift, bs2_shift);
   else
-    hipLaunchKernelGGL((nf4_gemm_kernel<DT, BM, BN, WM, WN, false>), grid, dim3(GEMM_THREADS), 0, st,
+    hipLaunchKernelGGL((nf4_gemm_kernel<DT, BM, BN, WM, WN, false, PF>), grid, dim3(GEMM_THREADS), 0, st,
                        (const uint16_t*)X, W, A8, AMAX, CODE2, offset, LUT, (uint16_t*)Y,
                        (const uint16_t*)R, epi, M, K, N, bs_shift, bs2_shift);
 }
@@ -215,16 +240,31 @@ static void launch_gemm(const void* X, const uint8_t* W, const uint8_t* A8, cons
 int gemm_mfma(const void* X, int dt, const uint8_t* W, const uint8_t* A8, const float* AMAX,
               const float* CODE2, float offset, const float* LUT, void* Y, const void* R, int epi,
               int M, int K, int N, int bs_shift, int bs2_shift, hipStream_t st) {
-  if (K % KT) return (int)hipErrorInvalidValue;
+  if (K % (2 * KT)) return (int)hipErrorInvalidValue;
+  const bool pf4 = (K / KT) % 4 == 0;
+#define TTSP_G(DTV, BMV, BNV, WMV, WNV)                                                                     \
+  (pf4 ? launch_gemm<DTV, BMV, BNV, WMV, WNV, 4>(X, W, A8, AMAX, CODE2, offset, LUT, Y, R, epi, M, K, N,    \
+                                                 bs_shift, bs2_shift, st)                                   \
+       : launch_gemm<DTV, BMV, BNV, WMV, WNV, 2>(X, W, A8, AMAX, CODE2, offset, LUT, Y, R, epi, M, K, N,    \
+                                                 bs_shift, bs2_shift, st))
+  // the largest tile that still gives every CU a workgroup (small M: more,
+  // smaller tiles, so the K loops of several workgroups overlap per CU)
+  const auto tiles = [&](int bm, int bn) { return (long long)((M + bm - 1) / bm) * ((N + bn - 1) / bn); };
+  const int shape = N <= 32 ? 0 : tiles(128, 128) >= 256 ? 1 : tiles(64, 128) >= 256 ? 2 : 3;
   if (dt == DT_BF16) {
-    if (N <= 32) launch_gemm<DT_BF16, 128, 32, 4, 1>(X, W, A8, AMAX, CODE2, offset, LUT, Y, R, epi, M, K, N, bs_shift, bs2_shift, st);
-    else launch_gemm<DT_BF16, 128, 128, 2, 2>(X, W, A8, AMAX, CODE2, offset, LUT, Y, R, epi, M, K, N, bs_shift, bs2_shift, st);
+    if (shape == 0) TTSP_G(DT_BF16, 128, 32, 4, 1);
+    else if (shape == 1) TTSP_G(DT_BF16, 128, 128, 2, 2);
+    else if (shape == 2) TTSP_G(DT_BF16, 64, 128, 2, 2);
+    else TTSP_G(DT_BF16, 64, 64, 2, 2);
   } else if (dt == DT_F16) {
-    if (N <= 32) launch_gemm<DT_F16, 128, 32, 4, 1>(X, W, A8, AMAX, CODE2, offset, LUT, Y, R, epi, M, K, N, bs_shift, bs2_shift, st);
-    else launch_gemm<DT_F16, 128, 128, 2, 2>(X, W, A8, AMAX, CODE2, offset, LUT, Y, R, epi, M, K, N, bs_shift, bs2_shift, st);
+    if (shape == 0) TTSP_G(DT_F16, 128, 32, 4, 1);
+    else if (shape == 1) TTSP_G(DT_F16, 128, 128, 2, 2);
+    else if (shape == 2) TTSP_G(DT_F16, 64, 128, 2, 2);
+    else TTSP_G(DT_F16, 64, 64, 2, 2);
   } else {
     return (int)hipErrorInvalidValue;
   }
+#undef TTSP_G
   TTSP_RETURN_LAUNCH();
 }
 
