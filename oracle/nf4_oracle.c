@@ -133,18 +133,9 @@ void orc_fma16_chain(const uint32_t* a, const uint32_t* b, const float* c, int n
 
 static inline float silu_rn(float a) { return a / (1.0f + orc_exp_cw(-a)); }
 
-/* Sum of 64 lane values as the kernels' xor butterfly (offsets 32..1). */
-static float butterfly64(float* v) {
-  for (int off = 32; off >= 1; off >>= 1) {
-    float t[64];
-    for (int l = 0; l < 64; ++l) t[l] = v[l] + v[l ^ off];
-    memcpy(v, t, sizeof t);
-  }
-  return v[0];
-}
-
-/* The same butterfly with the partner distance rising 1, 2, ..., 32 (the
- * GEMV's DPP reduction: within 16-lane rows first, then across rows). */
+/* Sum of 64 lane values as the kernels' xor butterfly with the partner
+ * distance rising 1, 2, ..., 32 (their DPP reduction: within 16-lane rows
+ * first, then across rows). */
 static float butterfly64_up(float* v) {
   for (int off = 1; off <= 32; off <<= 1) {
     float t[64];
@@ -337,7 +328,8 @@ void orc_rope(const void* X, const void* F, int ftype, uint16_t* Y, long long pa
 /* --------------------------------------------------- qk norm + rope + KV write */
 
 /* app/engine/fusedlayer.py:56-92: per head, optional norm over 128 with one
- * rounding round((x * r) * w) (r from the two-wave butterfly sum of x*x),
+ * rounding round((x * r) * w) (r from the sum of x*x: each 64-element half by
+ * the rising butterfly, then the halves added),
  * rotary, then Q or the K cache at pos; V heads copied to the V cache. */
 void orc_qk_rope_kv(const uint16_t* QKV, const uint16_t* QW, const uint16_t* KW, float eps,
                     const void* F, int ftype, long long pos, uint16_t* Q, uint16_t* KC, uint16_t* VC,
@@ -359,7 +351,7 @@ void orc_qk_rope_kv(const uint16_t* QKV, const uint16_t* QW, const uint16_t* KW,
         v0[l] = x[l] * x[l];
         v1[l] = x[64 + l] * x[64 + l];
       }
-      const float ss = butterfly64(v0) + butterfly64(v1);
+      const float ss = butterfly64_up(v0) + butterfly64_up(v1);
       const float r = orc_rsqrt_rn(ss / 128.0f + eps);
       for (int d = 0; d < 128; ++d) x[d] = rnd((x[d] * r) * ld(w, (size_t)d, dt), dt);
     }
@@ -407,9 +399,12 @@ void orc_attn_ref(const uint16_t* Q, const uint16_t* KC, const uint16_t* VC, lon
 }
 
 /* The kernels' order (ttspipe_amd/csrc/fusedlayer.hip): chunks of 64
- * positions; q * scale rounded; score = fma chain over d; chunk max; p =
- * exp_cw(s - max); l = butterfly sum; acc[d] = fma chain over positions;
- * chunks merged in order with w = exp_cw(m_c - M), den += l*w, num += acc*w. */
+ * positions; q * scale rounded; score = four fma chains, chain c over the
+ * element pairs i = c, c + 4, ... (elements 2i, 2i + 1), summed (s0 + s1) +
+ * (s2 + s3); chunk max; p = exp_cw(s - max); l = rising butterfly sum;
+ * acc[d] = four fma chains, chain c over positions j = c, c + 4, ..., summed
+ * (a0 + a1) + (a2 + a3); chunks merged in order with w = exp_cw(m_c - M),
+ * den += l*w, num += acc*w. */
 void orc_attn_emul(const uint16_t* Q, const uint16_t* KC, const uint16_t* VC, long long pos, uint16_t* Y,
                    int nh, int nkv, int max_len, int nchunk, float scale, int dt) {
   const int groups = nh / nkv;
@@ -436,7 +431,12 @@ void orc_attn_emul(const uint16_t* Q, const uint16_t* KC, const uint16_t* VC, lo
         float acc = 0.0f;
         if (l < nvalid) {
           const uint16_t* kr = KC + ((size_t)kh * max_len + j0 + l) * 128;
-          for (int d = 0; d < 128; ++d) acc = fmaf(q[d], ld(kr, (size_t)d, dt), acc);
+          float ch[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+          for (int i = 0; i < 64; ++i) {
+            ch[i & 3] = fmaf(q[2 * i], ld(kr, (size_t)(2 * i), dt), ch[i & 3]);
+            ch[i & 3] = fmaf(q[2 * i + 1], ld(kr, (size_t)(2 * i + 1), dt), ch[i & 3]);
+          }
+          acc = (ch[0] + ch[1]) + (ch[2] + ch[3]);
         }
         s[l] = acc;
         if (l < nvalid && acc > mx) mx = acc;
@@ -445,12 +445,12 @@ void orc_attn_emul(const uint16_t* Q, const uint16_t* KC, const uint16_t* VC, lo
       float pw[64];
       memcpy(pw, p, sizeof pw);
       pm[c] = mx;
-      pl[c] = butterfly64(pw);
+      pl[c] = butterfly64_up(pw);
       for (int d = 0; d < 128; ++d) {
-        float a = 0.0f;
+        float ch[4] = {0.0f, 0.0f, 0.0f, 0.0f};
         for (int j = 0; j < nvalid; ++j)
-          a = fmaf(p[j], ld(VC, ((size_t)kh * max_len + j0 + j) * 128 + d, dt), a);
-        pacc[(size_t)c * 128 + d] = a;
+          ch[j & 3] = fmaf(p[j], ld(VC, ((size_t)kh * max_len + j0 + j) * 128 + d, dt), ch[j & 3]);
+        pacc[(size_t)c * 128 + d] = (ch[0] + ch[1]) + (ch[2] + ch[3]);
       }
     }
     float M = -3.0e38f;

@@ -28,6 +28,59 @@ namespace ttsp {
 constexpr int HD = 128;        // head dim
 constexpr int ACHUNK = 64;     // positions per attention chunk
 constexpr int KPAD = HD + 2;   // LDS row stride (elements): 65 dwords, conflict-free columns
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+// Max over the wave by DPP steps and row broadcasts (exact in any order);
+// the result is wave-uniform.
+__device__ __forceinline__ float wave_max_u(float v) {
+  v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(v), __float_as_int(v), 0xB1, 0xF, 0xF, false)));
+  v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(v), __float_as_int(v), 0x4E, 0xF, 0xF, false)));
+  v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(v), __float_as_int(v), 0x141, 0xF, 0xF, false)));
+  v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(v), __float_as_int(v), 0x140, 0xF, 0xF, false)));
+  v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(v), __float_as_int(v), 0x142, 0xA, 0xF, false)));
+  v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(v), __float_as_int(v), 0x143, 0xC, 0xF, false)));
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+}
+
+// q . k of one position: four fma chains over the element pairs i = c, c + 4,
+// ... (pair i = elements 2i, 2i + 1 in order), then (s0 + s1) + (s2 + s3).
+template <int DT>
+__device__ __forceinline__ float score4(const float* __restrict__ qg, const uint32_t* __restrict__ kr) {
+  float a[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+  for (int i = 0; i < HD / 2; ++i) {
+    const uint32_t kk = kr[i];
+    a[i & 3] = __builtin_fmaf(qg[2 * i], Elem<DT>::load(kk), a[i & 3]);
+    a[i & 3] = __builtin_fmaf(qg[2 * i + 1], Elem<DT>::load(kk >> 16), a[i & 3]);
+  }
+  return __fadd_rn(__fadd_rn(a[0], a[1]), __fadd_rn(a[2], a[3]));
+}
+
+// p . V for dims 2 lane, 2 lane + 1: four fma chains over the positions
+// j = c, c + 4, ... below nvalid, then (a0 + a1) + (a2 + a3).
+template <int DT>
+__device__ __forceinline__ void pv4(const float* __restrict__ pg, const uint16_t* __restrict__ v_s, int nvalid,
+                                    int lane, float& y0, float& y1) {
+  float a[4] = {0.0f, 0.0f, 0.0f, 0.0f}, b[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  int j = 0;
+  for (; j + 4 <= nvalid; j += 4) {
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const float pj = pg[j + c];
+      const uint32_t vv = reinterpret_cast<const uint32_t*>(v_s + (j + c) * HD)[lane];
+      a[c] = __builtin_fmaf(pj, Elem<DT>::load(vv), a[c]);
+      b[c] = __builtin_fmaf(pj, Elem<DT>::load(vv >> 16), b[c]);
+    }
+  }
+  for (int c = 0; j + c < nvalid; ++c) {
+    const float pj = pg[j + c];
+    const uint32_t vv = reinterpret_cast<const uint32_t*>(v_s + (j + c) * HD)[lane];
+    a[c] = __builtin_fmaf(pj, Elem<DT>::load(vv), a[c]);
+    b[c] = __builtin_fmaf(pj, Elem<DT>::load(vv >> 16), b[c]);
+  }
+  y0 = __fadd_rn(__fadd_rn(a[0], a[1]), __fadd_rn(a[2], a[3]));
+  y1 = __fadd_rn(__fadd_rn(b[0], b[1]), __fadd_rn(b[2], b[3]));
+}
 
 template <int DT>
 __global__ __launch_bounds__(HD) void qk_rope_kv_kernel(
@@ -49,7 +102,7 @@ __global__ __launch_bounds__(HD) void qk_rope_kv_kernel(
   float x = Elem<DT>::load(QKV[(size_t)head * HD + d]);
   const uint16_t* w = is_q ? QW : KW;
   if (w != nullptr) {
-    const float v = wave_sum(__fmul_rn(x, x));
+    const float v = wave_sum_dpp(__fmul_rn(x, x));
     if ((d & 63) == 0) part[d >> 6] = v;
     __syncthreads();
     const float ss = __fadd_rn(part[0], part[1]);
@@ -114,30 +167,16 @@ __global__ __launch_bounds__(1024) void attn_partial_kernel(
   __syncthreads();
 
   // score of position `lane` for query head g
-  float s = 0.0f;
-  const uint32_t* kr = reinterpret_cast<const uint32_t*>(k_s + lane * KPAD);
-  const float* qg = q_s + g * HD;
-#pragma unroll 8
-  for (int i = 0; i < HD / 2; ++i) {
-    const uint32_t kk = kr[i];
-    s = __builtin_fmaf(qg[2 * i], Elem<DT>::load(kk), s);
-    s = __builtin_fmaf(qg[2 * i + 1], Elem<DT>::load(kk >> 16), s);
-  }
+  const float s = score4<DT>(q_s + g * HD, reinterpret_cast<const uint32_t*>(k_s + lane * KPAD));
   const bool valid = lane < nvalid;
-  const float m = wave_max(valid ? s : -3.0e38f);
+  const float m = wave_max_u(valid ? s : -3.0e38f);
   const float p = valid ? exp_cw(__fsub_rn(s, m)) : 0.0f;
-  const float l = wave_sum(p);
+  const float l = wave_sum_dpp(p);
   p_s[g * ACHUNK + lane] = p;
   __syncthreads();
 
-  float a0 = 0.0f, a1 = 0.0f;
-  const float* pg = p_s + g * ACHUNK;
-  for (int j = 0; j < nvalid; ++j) {
-    const float pj = pg[j];
-    const uint32_t vv = reinterpret_cast<const uint32_t*>(v_s + j * HD)[lane];
-    a0 = __builtin_fmaf(pj, Elem<DT>::load(vv), a0);
-    a1 = __builtin_fmaf(pj, Elem<DT>::load(vv >> 16), a1);
-  }
+  float a0, a1;
+  pv4<DT>(p_s + g * ACHUNK, v_s, nvalid, lane, a0, a1);
   if (lane == 0) {
     PM[slot] = m;
     PL[slot] = l;
@@ -197,25 +236,35 @@ __global__ __launch_bounds__(HD) void attn_combine_kernel(const float* __restric
   Y[(size_t)qh * HD + d] = Elem<DT>::store(__fdiv_rn(num, den));
 }
 
+// Rotary factors of the pair that holds lanes l and l + 64 of a head: the
+// pair's (cos, sin) for the low half, then for the high half.
+struct RopeF {
+  float rl, il, rh, ih;
+};
+__device__ __forceinline__ RopeF load_rope(const void* __restrict__ F, int ftype, int lane) {
+  const int e = lane & ~1;  // the pair's even element (lo half; the hi half is e + 64)
+  return RopeF{load_elem(F, e, ftype), load_elem(F, e + 1, ftype), load_elem(F, e + 64, ftype),
+               load_elem(F, e + 65, ftype)};
+}
+
 // Head norm and rotary of one 128-wide head held by a wave (lane l: elements
 // l and l + 64), the arithmetic of qk_rope_kv_kernel: the norm's sum is the
-// two 64-element halves (xor butterflies) added, one rounding after x * r * w;
+// two 64-element halves (rising DPP sums) added, one rounding after x * r * w;
 // rotary pairs (2i, 2i+1) with the partner in lane l ^ 1, separately rounded
-// products and sum. Returns the rotated values, not yet rounded.
+// products and sum. Returns the rotated values, not yet rounded. nwl, nwh
+// are the norm weights of elements l and l + 64 (unused when norm is false).
 template <int DT>
-__device__ __forceinline__ void head_norm_rope(float& lo, float& hi, const uint16_t* __restrict__ NW, float eps,
-                                               const void* __restrict__ F, int ftype, int lane) {
-  if (NW != nullptr) {
-    const float ss = __fadd_rn(wave_sum(__fmul_rn(lo, lo)), wave_sum(__fmul_rn(hi, hi)));
+__device__ __forceinline__ void head_norm_rope(float& lo, float& hi, bool norm, uint16_t nwl, uint16_t nwh,
+                                               float eps, const RopeF& f, int lane) {
+  if (norm) {
+    const float ss = __fadd_rn(wave_sum_dpp(__fmul_rn(lo, lo)), wave_sum_dpp(__fmul_rn(hi, hi)));
     const float r = rsqrt_rn(__fadd_rn(__fdiv_rn(ss, (float)HD), eps));
-    lo = Elem<DT>::load(Elem<DT>::store(__fmul_rn(__fmul_rn(lo, r), Elem<DT>::load(NW[lane]))));
-    hi = Elem<DT>::load(Elem<DT>::store(__fmul_rn(__fmul_rn(hi, r), Elem<DT>::load(NW[lane + 64]))));
+    lo = Elem<DT>::load(Elem<DT>::store(__fmul_rn(__fmul_rn(lo, r), Elem<DT>::load(nwl))));
+    hi = Elem<DT>::load(Elem<DT>::store(__fmul_rn(__fmul_rn(hi, r), Elem<DT>::load(nwh))));
   }
   const float plo = __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(lo), 0xB1, 0xF, 0xF, false));
   const float phi = __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(hi), 0xB1, 0xF, 0xF, false));
-  const int e = lane & ~1;  // the pair's even element (lo half; the hi half is e + 64)
-  const float frl = load_elem(F, e, ftype), fil = load_elem(F, e + 1, ftype);
-  const float frh = load_elem(F, e + 64, ftype), fih = load_elem(F, e + 65, ftype);
+  const float frl = f.rl, fil = f.il, frh = f.rh, fih = f.ih;
   if (lane & 1) {
     lo = __fadd_rn(__fmul_rn(lo, frl), __fmul_rn(plo, fil));
     hi = __fadd_rn(__fmul_rn(hi, frh), __fmul_rn(phi, fih));
@@ -259,74 +308,103 @@ __global__ __launch_bounds__(1024) void attn_qkv_kernel(
   const int nvalid = (int)min((long long)ACHUNK, L - j0);
   const int jpos = (int)(pos - j0);  // the new row's place in this chunk, if < ACHUNK
 
-  // K and V rows of the chunk from the cache, except the new position's
+  // Every global load of the workgroup is issued up front: this wave's query
+  // head with its norm weights and rotary factors, the new position's K/V row
+  // (wave 0 of the chunk that holds it), then the chunk's cached K and V rows
+  // (rows clamped into the live range: rows past it are never read).
+  const bool newrow = jpos < ACHUNK && g == 0;
+  const bool qn = QW != nullptr, kn = KW != nullptr;
+  const uint16_t* qr = QKV + (size_t)qh * HD;
+  const uint16_t* kr_ = QKV + (size_t)(nh + kh) * HD;
+  const uint16_t* vr = QKV + (size_t)(nh + nkv + kh) * HD;
+  const uint16_t q0 = qr[lane], q1 = qr[lane + 64];
+  const uint16_t qw0 = qn ? QW[lane] : 0, qw1 = qn ? QW[lane + 64] : 0;
+  const RopeF rf = load_rope(F, ftype, lane);
+  uint16_t k0 = 0, k1 = 0, v0 = 0, v1 = 0, kw0 = 0, kw1 = 0;
+  if (newrow) {
+    k0 = kr_[lane];
+    k1 = kr_[lane + 64];
+    v0 = vr[lane];
+    v1 = vr[lane + 64];
+    if (kn) {
+      kw0 = KW[lane];
+      kw1 = KW[lane + 64];
+    }
+  }
   const uint16_t* kb = KC + ((size_t)kh * max_len + j0) * HD;
   const uint16_t* vb = VC + ((size_t)kh * max_len + j0) * HD;
-  for (int t = tid; t < ACHUNK * (HD / 8); t += nthr) {
-    const int j = t / (HD / 8), e = (t % (HD / 8)) * 8;
-    if (j == jpos) continue;
-    uint4 kv = make_uint4(0, 0, 0, 0), vv = make_uint4(0, 0, 0, 0);
-    if (j < nvalid) {
-      kv = *reinterpret_cast<const uint4*>(kb + (size_t)j * HD + e);
-      vv = *reinterpret_cast<const uint4*>(vb + (size_t)j * HD + e);
+  constexpr int NT = ACHUNK * (HD / 8);  // 16-byte pieces of the chunk's K (and of its V)
+  constexpr int PER = NT / 256;          // pieces per thread with 4 or more waves
+  const bool upfront = nthr >= 256;      // fewer waves stage the chunk in a loop below
+  u32x4 kq[PER], vq[PER];
+  if (upfront) {
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+      const int t = min(tid + i * nthr, NT - 1);
+      const int j = min(t / (HD / 8), nvalid - 1), e = (t % (HD / 8)) * 8;
+      kq[i] = *reinterpret_cast<const u32x4*>(kb + (size_t)j * HD + e);
+      vq[i] = *reinterpret_cast<const u32x4*>(vb + (size_t)j * HD + e);
     }
-    uint32_t* kd = reinterpret_cast<uint32_t*>(k_s + j * KPAD + e);  // KPAD rows are 4-byte aligned
-    kd[0] = kv.x; kd[1] = kv.y; kd[2] = kv.z; kd[3] = kv.w;
-    *reinterpret_cast<uint4*>(v_s + j * HD + e) = vv;
   }
+
   // this wave's query head: norm, rotary, rounded as the stored Q, scaled
   {
-    float lo = Elem<DT>::load(QKV[(size_t)qh * HD + lane]);
-    float hi = Elem<DT>::load(QKV[(size_t)qh * HD + lane + 64]);
-    head_norm_rope<DT>(lo, hi, QW, eps, F, ftype, lane);
+    float lo = Elem<DT>::load(q0), hi = Elem<DT>::load(q1);
+    head_norm_rope<DT>(lo, hi, qn, qw0, qw1, eps, rf, lane);
     q_s[g * HD + lane] = __fmul_rn(Elem<DT>::load(Elem<DT>::store(lo)), scale);
     q_s[g * HD + lane + 64] = __fmul_rn(Elem<DT>::load(Elem<DT>::store(hi)), scale);
   }
-  // the new position's K/V row: computed by wave 0 of the chunk that holds it
-  if (jpos < ACHUNK && g == 0) {
-    float lo = Elem<DT>::load(QKV[(size_t)(nh + kh) * HD + lane]);
-    float hi = Elem<DT>::load(QKV[(size_t)(nh + kh) * HD + lane + 64]);
-    head_norm_rope<DT>(lo, hi, KW, eps, F, ftype, lane);
+  // the new position's K/V row: into the cache and into the staged chunk
+  if (newrow) {
+    float lo = Elem<DT>::load(k0), hi = Elem<DT>::load(k1);
+    head_norm_rope<DT>(lo, hi, kn, kw0, kw1, eps, rf, lane);
     const uint16_t klo = Elem<DT>::store(lo), khi = Elem<DT>::store(hi);
-    const uint16_t vlo = QKV[(size_t)(nh + nkv + kh) * HD + lane];
-    const uint16_t vhi = QKV[(size_t)(nh + nkv + kh) * HD + lane + 64];
     const size_t row = ((size_t)kh * max_len + pos) * HD;
     KC[row + lane] = klo;
     KC[row + lane + 64] = khi;
-    VC[row + lane] = vlo;
-    VC[row + lane + 64] = vhi;
+    VC[row + lane] = v0;
+    VC[row + lane + 64] = v1;
     k_s[jpos * KPAD + lane] = klo;
     k_s[jpos * KPAD + lane + 64] = khi;
-    v_s[jpos * HD + lane] = vlo;
-    v_s[jpos * HD + lane + 64] = vhi;
+    v_s[jpos * HD + lane] = v0;
+    v_s[jpos * HD + lane + 64] = v1;
+  }
+  if (upfront) {
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+      const int t = tid + i * nthr;
+      const int j = t / (HD / 8), e = (t % (HD / 8)) * 8;
+      if (t < NT && j != jpos) {
+        uint32_t* kd = reinterpret_cast<uint32_t*>(k_s + j * KPAD + e);  // KPAD rows are 4-byte aligned
+        kd[0] = kq[i].x; kd[1] = kq[i].y; kd[2] = kq[i].z; kd[3] = kq[i].w;
+        *reinterpret_cast<u32x4*>(v_s + j * HD + e) = vq[i];
+      }
+    }
+  } else {
+    for (int t = tid; t < NT; t += nthr) {
+      const int j = t / (HD / 8), e = (t % (HD / 8)) * 8;
+      if (j == jpos) continue;
+      const int jr = min(j, nvalid - 1);
+      const uint4 kv = *reinterpret_cast<const uint4*>(kb + (size_t)jr * HD + e);
+      const uint4 vv = *reinterpret_cast<const uint4*>(vb + (size_t)jr * HD + e);
+      uint32_t* kd = reinterpret_cast<uint32_t*>(k_s + j * KPAD + e);
+      kd[0] = kv.x; kd[1] = kv.y; kd[2] = kv.z; kd[3] = kv.w;
+      *reinterpret_cast<uint4*>(v_s + j * HD + e) = vv;
+    }
   }
   __syncthreads();
 
   // score of position `lane` for query head g (as attn_partial_kernel)
-  float s = 0.0f;
-  const uint32_t* kr = reinterpret_cast<const uint32_t*>(k_s + lane * KPAD);
-  const float* qg = q_s + g * HD;
-#pragma unroll 8
-  for (int i = 0; i < HD / 2; ++i) {
-    const uint32_t kk = kr[i];
-    s = __builtin_fmaf(qg[2 * i], Elem<DT>::load(kk), s);
-    s = __builtin_fmaf(qg[2 * i + 1], Elem<DT>::load(kk >> 16), s);
-  }
+  const float s = score4<DT>(q_s + g * HD, reinterpret_cast<const uint32_t*>(k_s + lane * KPAD));
   const bool valid = lane < nvalid;
-  const float m = wave_max(valid ? s : -3.0e38f);
+  const float m = wave_max_u(valid ? s : -3.0e38f);
   const float p = valid ? exp_cw(__fsub_rn(s, m)) : 0.0f;
-  const float l = wave_sum(p);
+  const float l = wave_sum_dpp(p);
   p_s[g * ACHUNK + lane] = p;
   __syncthreads();
 
-  float a0 = 0.0f, a1 = 0.0f;
-  const float* pg = p_s + g * ACHUNK;
-  for (int j = 0; j < nvalid; ++j) {
-    const float pj = pg[j];
-    const uint32_t vv = reinterpret_cast<const uint32_t*>(v_s + j * HD)[lane];
-    a0 = __builtin_fmaf(pj, Elem<DT>::load(vv), a0);
-    a1 = __builtin_fmaf(pj, Elem<DT>::load(vv >> 16), a1);
-  }
+  float a0, a1;
+  pv4<DT>(p_s + g * ACHUNK, v_s, nvalid, lane, a0, a1);
   if (nchunk == 1) {
     // the merge of a single chunk, as attn_combine_kernel computes it
     const float w = exp_cw(__fsub_rn(m, m));

@@ -118,21 +118,6 @@ __device__ __forceinline__ float silu_rn(float a) {
   return __fdiv_rn(a, __fadd_rn(1.0f, exp_cw(-a)));
 }
 
-// Sum over the 64 lanes of a wavefront, xor butterfly 32,16,8,4,2,1. Each step
-// adds a lane's value to its partner's, which is commutative, so every lane
-// ends with the same bits; the order is a fixed binary tree.
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) v = __fadd_rn(v, __shfl_xor(v, off, 64));
-  return v;
-}
-
-__device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
-  return v;
-}
-
 // v + (v of the DPP partner); rows outside ROWS add +0 and are not read after.
 template <int CTRL, int ROWS>
 __device__ __forceinline__ float dpp_add(float v) {
