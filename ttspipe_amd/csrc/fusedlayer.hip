@@ -27,8 +27,11 @@ namespace ttsp {
 
 constexpr int HD = 128;        // head dim
 constexpr int ACHUNK = 64;     // positions per attention chunk
-constexpr int KPAD = HD + 2;   // LDS row stride (elements): 65 dwords, conflict-free columns
+// LDS row stride of the staged K rows (elements): 272 bytes, so rows are
+// 16-byte aligned and the 16 lanes of a 16-byte read hit 64 distinct banks.
+constexpr int KPAD = HD + 8;
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 // Max over the wave by DPP steps and row broadcasts (exact in any order);
 // the result is wave-uniform.
@@ -44,39 +47,69 @@ __device__ __forceinline__ float wave_max_u(float v) {
 
 // q . k of one position: four fma chains over the element pairs i = c, c + 4,
 // ... (pair i = elements 2i, 2i + 1 in order), then (s0 + s1) + (s2 + s3).
+// qg (the wave's query, broadcast) and kr (this lane's K row) are LDS rows,
+// read 16 bytes at a time; each 32-element block's reads are issued together.
 template <int DT>
-__device__ __forceinline__ float score4(const float* __restrict__ qg, const uint32_t* __restrict__ kr) {
+__device__ __forceinline__ float score4(const float* __restrict__ qg, const uint16_t* __restrict__ kr) {
+  const f32x4* q4 = reinterpret_cast<const f32x4*>(qg);
+  const u32x4* k4 = reinterpret_cast<const u32x4*>(kr);
   float a[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-  for (int i = 0; i < HD / 2; ++i) {
-    const uint32_t kk = kr[i];
-    a[i & 3] = __builtin_fmaf(qg[2 * i], Elem<DT>::load(kk), a[i & 3]);
-    a[i & 3] = __builtin_fmaf(qg[2 * i + 1], Elem<DT>::load(kk >> 16), a[i & 3]);
+  for (int b = 0; b < HD / 32; ++b) {
+    u32x4 kk[4];
+    f32x4 qq[8];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) kk[i] = k4[4 * b + i];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) qq[i] = q4[8 * b + i];
+#pragma unroll
+    for (int t = 0; t < 16; ++t) {  // pair i = 16 b + t
+      const uint32_t k2 = kk[t >> 2][t & 3];
+      const f32x4 q = qq[t >> 1];
+      const float qa = (t & 1) ? q[2] : q[0], qb = (t & 1) ? q[3] : q[1];
+      a[t & 3] = __builtin_fmaf(qa, Elem<DT>::load(k2), a[t & 3]);
+      a[t & 3] = __builtin_fmaf(qb, Elem<DT>::load(k2 >> 16), a[t & 3]);
+    }
   }
   return __fadd_rn(__fadd_rn(a[0], a[1]), __fadd_rn(a[2], a[3]));
 }
 
 // p . V for dims 2 lane, 2 lane + 1: four fma chains over the positions
-// j = c, c + 4, ... below nvalid, then (a0 + a1) + (a2 + a3).
+// j = c, c + 4, ... below nvalid, then (a0 + a1) + (a2 + a3). pg is the
+// wave's own probability row (LDS, broadcast), v_s the staged V rows; each
+// block of 16 positions has its reads issued together.
 template <int DT>
 __device__ __forceinline__ void pv4(const float* __restrict__ pg, const uint16_t* __restrict__ v_s, int nvalid,
                                     int lane, float& y0, float& y1) {
   float a[4] = {0.0f, 0.0f, 0.0f, 0.0f}, b[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-  int j = 0;
-  for (; j + 4 <= nvalid; j += 4) {
+  const uint32_t* vcol = reinterpret_cast<const uint32_t*>(v_s) + lane;
+  const f32x4* p4 = reinterpret_cast<const f32x4*>(pg);
 #pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      const float pj = pg[j + c];
-      const uint32_t vv = reinterpret_cast<const uint32_t*>(v_s + (j + c) * HD)[lane];
-      a[c] = __builtin_fmaf(pj, Elem<DT>::load(vv), a[c]);
-      b[c] = __builtin_fmaf(pj, Elem<DT>::load(vv >> 16), b[c]);
+  for (int jb = 0; jb < ACHUNK; jb += 16) {
+    if (jb >= nvalid) break;
+    uint32_t vv[16];
+    f32x4 pp[4];
+#pragma unroll
+    for (int t = 0; t < 16; ++t) vv[t] = vcol[(jb + t) * (HD / 2)];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) pp[t] = p4[jb / 4 + t];
+    if (jb + 16 <= nvalid) {
+#pragma unroll
+      for (int t = 0; t < 16; ++t) {
+        const float pj = pp[t >> 2][t & 3];
+        a[t & 3] = __builtin_fmaf(pj, Elem<DT>::load(vv[t]), a[t & 3]);
+        b[t & 3] = __builtin_fmaf(pj, Elem<DT>::load(vv[t] >> 16), b[t & 3]);
+      }
+    } else {
+#pragma unroll
+      for (int t = 0; t < 16; ++t) {
+        if (jb + t < nvalid) {
+          const float pj = pp[t >> 2][t & 3];
+          a[t & 3] = __builtin_fmaf(pj, Elem<DT>::load(vv[t]), a[t & 3]);
+          b[t & 3] = __builtin_fmaf(pj, Elem<DT>::load(vv[t] >> 16), b[t & 3]);
+        }
+      }
     }
-  }
-  for (int c = 0; j + c < nvalid; ++c) {
-    const float pj = pg[j + c];
-    const uint32_t vv = reinterpret_cast<const uint32_t*>(v_s + (j + c) * HD)[lane];
-    a[c] = __builtin_fmaf(pj, Elem<DT>::load(vv), a[c]);
-    b[c] = __builtin_fmaf(pj, Elem<DT>::load(vv >> 16), b[c]);
   }
   y0 = __fadd_rn(__fadd_rn(a[0], a[1]), __fadd_rn(a[2], a[3]));
   y1 = __fadd_rn(__fadd_rn(b[0], b[1]), __fadd_rn(b[2], b[3]));
@@ -155,25 +188,23 @@ __global__ __launch_bounds__(1024) void attn_partial_kernel(
   const uint16_t* vb = VC + ((size_t)kh * max_len + j0) * HD;
   for (int t = tid; t < ACHUNK * (HD / 8); t += nthr) {
     const int j = t / (HD / 8), e = (t % (HD / 8)) * 8;
-    uint4 kv = make_uint4(0, 0, 0, 0), vv = make_uint4(0, 0, 0, 0);
+    u32x4 kv = {0u, 0u, 0u, 0u}, vv = {0u, 0u, 0u, 0u};
     if (j < nvalid) {
-      kv = *reinterpret_cast<const uint4*>(kb + (size_t)j * HD + e);
-      vv = *reinterpret_cast<const uint4*>(vb + (size_t)j * HD + e);
+      kv = *reinterpret_cast<const u32x4*>(kb + (size_t)j * HD + e);
+      vv = *reinterpret_cast<const u32x4*>(vb + (size_t)j * HD + e);
     }
-    uint32_t* kd = reinterpret_cast<uint32_t*>(k_s + j * KPAD + e);  // KPAD rows are 4-byte aligned
-    kd[0] = kv.x; kd[1] = kv.y; kd[2] = kv.z; kd[3] = kv.w;
-    *reinterpret_cast<uint4*>(v_s + j * HD + e) = vv;
+    *reinterpret_cast<u32x4*>(k_s + j * KPAD + e) = kv;
+    *reinterpret_cast<u32x4*>(v_s + j * HD + e) = vv;
   }
   __syncthreads();
 
   // score of position `lane` for query head g
-  const float s = score4<DT>(q_s + g * HD, reinterpret_cast<const uint32_t*>(k_s + lane * KPAD));
+  const float s = score4<DT>(q_s + g * HD, k_s + lane * KPAD);
   const bool valid = lane < nvalid;
   const float m = wave_max_u(valid ? s : -3.0e38f);
   const float p = valid ? exp_cw(__fsub_rn(s, m)) : 0.0f;
   const float l = wave_sum_dpp(p);
-  p_s[g * ACHUNK + lane] = p;
-  __syncthreads();
+  p_s[g * ACHUNK + lane] = p;  // read back by this wave only: no barrier
 
   float a0, a1;
   pv4<DT>(p_s + g * ACHUNK, v_s, nvalid, lane, a0, a1);
@@ -241,10 +272,22 @@ __global__ __launch_bounds__(HD) void attn_combine_kernel(const float* __restric
 struct RopeF {
   float rl, il, rh, ih;
 };
+// Branch-free: the pair is one dword of a 16-bit table or two of an fp32 one,
+// so every lane issues the same two dword loads per half whatever ftype is.
 __device__ __forceinline__ RopeF load_rope(const void* __restrict__ F, int ftype, int lane) {
+  const uint32_t* fw = reinterpret_cast<const uint32_t*>(F);
+  const int es = ftype == DT_F32 ? 1 : 0;
   const int e = lane & ~1;  // the pair's even element (lo half; the hi half is e + 64)
-  return RopeF{load_elem(F, e, ftype), load_elem(F, e + 1, ftype), load_elem(F, e + 64, ftype),
-               load_elem(F, e + 65, ftype)};
+  const int wl = (e << es) >> 1, wh = ((e + 64) << es) >> 1;
+  const uint32_t l0 = fw[wl], l1 = fw[wl + es], h0 = fw[wh], h1 = fw[wh + es];
+  const bool f16 = ftype == DT_F16;
+  // all three decodings computed, one selected (no branch on the loaded data)
+  auto dec = [&](uint32_t a, uint32_t b, bool second) {
+    const uint32_t h = second ? a >> 16 : a & 0xffffu;
+    const float x16 = f16_to_f32(h), xb = __uint_as_float(h << 16), x32 = __uint_as_float(second ? b : a);
+    return es ? x32 : (f16 ? x16 : xb);
+  };
+  return RopeF{dec(l0, l1, false), dec(l0, l1, true), dec(h0, h1, false), dec(h0, h1, true)};
 }
 
 // Head norm and rotary of one 128-wide head held by a wave (lane l: elements
@@ -292,11 +335,51 @@ __global__ __launch_bounds__(1024) void attn_qkv_kernel(
   const int kh = blockIdx.x, c = blockIdx.y;
   const int tid = threadIdx.x, nthr = blockDim.x;
   const int g = tid >> 6, lane = tid & 63;
+  // All kernel arguments the loads need are fetched at once, here (otherwise
+  // the compiler fetches them one branch at a time, each with its own wait).
+  const long long pos0 = POS[0];  // issued first, waited for only after the loads below are issued
+  asm volatile("" ::"s"(QKV), "s"(QW), "s"(KW), "s"(F), "s"(ftype), "s"(KC), "s"(VC), "s"(nh), "s"(nkv),
+               "s"(max_len));
   const int qh = kh * groups + g;
-  const long long pos = POS[0];
+  const long long j0 = (long long)c * ACHUNK;
+
+  // Every global load of the workgroup is issued before the position is
+  // known: this wave's query head with its norm weights and rotary factors,
+  // the new K/V row (wave 0; used by the chunk that holds the position), then
+  // the chunk's cached K and V rows, clamped into the cache allocation (rows
+  // at or past the live range are staged but never read).
+  // No load depends on a branch: absent norm weights read QKV instead (and
+  // are not used), every wave reads the new K/V row.
+  const bool qn = QW != nullptr, kn = KW != nullptr;
+  const uint16_t* qwp = qn ? QW : QKV;
+  const uint16_t* kwp = kn ? KW : QKV;
+  const uint16_t* qr = QKV + (size_t)qh * HD;
+  const uint16_t* kr_ = QKV + (size_t)(nh + kh) * HD;
+  const uint16_t* vr = QKV + (size_t)(nh + nkv + kh) * HD;
+  const uint16_t q0 = qr[lane], q1 = qr[lane + 64];
+  const uint16_t qw0 = qwp[lane], qw1 = qwp[lane + 64];
+  const RopeF rf = load_rope(F, ftype, lane);
+  const uint16_t k0 = kr_[lane], k1 = kr_[lane + 64];
+  const uint16_t v0 = vr[lane], v1 = vr[lane + 64];
+  const uint16_t kw0 = kwp[lane], kw1 = kwp[lane + 64];
+  const uint16_t* kb = KC + (size_t)kh * max_len * HD;
+  const uint16_t* vb = VC + (size_t)kh * max_len * HD;
+  constexpr int NT = ACHUNK * (HD / 8);  // 16-byte pieces of the chunk's K (and of its V)
+  constexpr int PER = NT / 256;  // pieces per thread issued here: all of them with 4 or more waves
+  u32x4 kq[PER], vq[PER];
+#pragma unroll
+  for (int i = 0; i < PER; ++i) {
+    const int t = min(tid + i * nthr, NT - 1);
+    const long long row = min(j0 + t / (HD / 8), (long long)max_len - 1);
+    const int e = (t % (HD / 8)) * 8;
+    kq[i] = *reinterpret_cast<const u32x4*>(kb + (size_t)row * HD + e);
+    vq[i] = *reinterpret_cast<const u32x4*>(vb + (size_t)row * HD + e);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  const long long pos = pos0;
+
   if (pos < 0 || pos >= max_len) return;  // no cache slot for it: nothing is written
   const long long L = pos + 1;
-  const long long j0 = (long long)c * ACHUNK;
   const size_t slot = (size_t)qh * nchunk + c;
   if (j0 >= L) {  // a chunk past the live positions (only with nchunk > 1)
     if (lane == 0) {
@@ -307,45 +390,7 @@ __global__ __launch_bounds__(1024) void attn_qkv_kernel(
   }
   const int nvalid = (int)min((long long)ACHUNK, L - j0);
   const int jpos = (int)(pos - j0);  // the new row's place in this chunk, if < ACHUNK
-
-  // Every global load of the workgroup is issued up front: this wave's query
-  // head with its norm weights and rotary factors, the new position's K/V row
-  // (wave 0 of the chunk that holds it), then the chunk's cached K and V rows
-  // (rows clamped into the live range: rows past it are never read).
   const bool newrow = jpos < ACHUNK && g == 0;
-  const bool qn = QW != nullptr, kn = KW != nullptr;
-  const uint16_t* qr = QKV + (size_t)qh * HD;
-  const uint16_t* kr_ = QKV + (size_t)(nh + kh) * HD;
-  const uint16_t* vr = QKV + (size_t)(nh + nkv + kh) * HD;
-  const uint16_t q0 = qr[lane], q1 = qr[lane + 64];
-  const uint16_t qw0 = qn ? QW[lane] : 0, qw1 = qn ? QW[lane + 64] : 0;
-  const RopeF rf = load_rope(F, ftype, lane);
-  uint16_t k0 = 0, k1 = 0, v0 = 0, v1 = 0, kw0 = 0, kw1 = 0;
-  if (newrow) {
-    k0 = kr_[lane];
-    k1 = kr_[lane + 64];
-    v0 = vr[lane];
-    v1 = vr[lane + 64];
-    if (kn) {
-      kw0 = KW[lane];
-      kw1 = KW[lane + 64];
-    }
-  }
-  const uint16_t* kb = KC + ((size_t)kh * max_len + j0) * HD;
-  const uint16_t* vb = VC + ((size_t)kh * max_len + j0) * HD;
-  constexpr int NT = ACHUNK * (HD / 8);  // 16-byte pieces of the chunk's K (and of its V)
-  constexpr int PER = NT / 256;          // pieces per thread with 4 or more waves
-  const bool upfront = nthr >= 256;      // fewer waves stage the chunk in a loop below
-  u32x4 kq[PER], vq[PER];
-  if (upfront) {
-#pragma unroll
-    for (int i = 0; i < PER; ++i) {
-      const int t = min(tid + i * nthr, NT - 1);
-      const int j = min(t / (HD / 8), nvalid - 1), e = (t % (HD / 8)) * 8;
-      kq[i] = *reinterpret_cast<const u32x4*>(kb + (size_t)j * HD + e);
-      vq[i] = *reinterpret_cast<const u32x4*>(vb + (size_t)j * HD + e);
-    }
-  }
 
   // this wave's query head: norm, rotary, rounded as the stored Q, scaled
   {
@@ -354,57 +399,54 @@ __global__ __launch_bounds__(1024) void attn_qkv_kernel(
     q_s[g * HD + lane] = __fmul_rn(Elem<DT>::load(Elem<DT>::store(lo)), scale);
     q_s[g * HD + lane + 64] = __fmul_rn(Elem<DT>::load(Elem<DT>::store(hi)), scale);
   }
-  // the new position's K/V row: into the cache and into the staged chunk
+  // the new position's K/V row: into the staged chunk now, into the cache
+  // at the end (no later step of this launch reads it from there)
+  uint16_t klo = 0, khi = 0;
   if (newrow) {
     float lo = Elem<DT>::load(k0), hi = Elem<DT>::load(k1);
     head_norm_rope<DT>(lo, hi, kn, kw0, kw1, eps, rf, lane);
-    const uint16_t klo = Elem<DT>::store(lo), khi = Elem<DT>::store(hi);
-    const size_t row = ((size_t)kh * max_len + pos) * HD;
-    KC[row + lane] = klo;
-    KC[row + lane + 64] = khi;
-    VC[row + lane] = v0;
-    VC[row + lane + 64] = v1;
+    klo = Elem<DT>::store(lo);
+    khi = Elem<DT>::store(hi);
     k_s[jpos * KPAD + lane] = klo;
     k_s[jpos * KPAD + lane + 64] = khi;
     v_s[jpos * HD + lane] = v0;
     v_s[jpos * HD + lane + 64] = v1;
   }
-  if (upfront) {
 #pragma unroll
-    for (int i = 0; i < PER; ++i) {
-      const int t = tid + i * nthr;
-      const int j = t / (HD / 8), e = (t % (HD / 8)) * 8;
-      if (t < NT && j != jpos) {
-        uint32_t* kd = reinterpret_cast<uint32_t*>(k_s + j * KPAD + e);  // KPAD rows are 4-byte aligned
-        kd[0] = kq[i].x; kd[1] = kq[i].y; kd[2] = kq[i].z; kd[3] = kq[i].w;
-        *reinterpret_cast<u32x4*>(v_s + j * HD + e) = vq[i];
-      }
+  for (int i = 0; i < PER; ++i) {
+    const int t = tid + i * nthr;
+    const int j = t / (HD / 8), e = (t % (HD / 8)) * 8;
+    if (t < NT && j != jpos) {
+      *reinterpret_cast<u32x4*>(k_s + j * KPAD + e) = kq[i];
+      *reinterpret_cast<u32x4*>(v_s + j * HD + e) = vq[i];
     }
-  } else {
-    for (int t = tid; t < NT; t += nthr) {
-      const int j = t / (HD / 8), e = (t % (HD / 8)) * 8;
-      if (j == jpos) continue;
-      const int jr = min(j, nvalid - 1);
-      const uint4 kv = *reinterpret_cast<const uint4*>(kb + (size_t)jr * HD + e);
-      const uint4 vv = *reinterpret_cast<const uint4*>(vb + (size_t)jr * HD + e);
-      uint32_t* kd = reinterpret_cast<uint32_t*>(k_s + j * KPAD + e);
-      kd[0] = kv.x; kd[1] = kv.y; kd[2] = kv.z; kd[3] = kv.w;
-      *reinterpret_cast<uint4*>(v_s + j * HD + e) = vv;
-    }
+  }
+  for (int t = tid + PER * nthr; t < NT; t += nthr) {  // the rest, with fewer than 4 waves
+    const int j = t / (HD / 8), e = (t % (HD / 8)) * 8;
+    if (j == jpos) continue;
+    const long long jr = j0 + min(j, nvalid - 1);
+    *reinterpret_cast<u32x4*>(k_s + j * KPAD + e) = *reinterpret_cast<const u32x4*>(kb + (size_t)jr * HD + e);
+    *reinterpret_cast<u32x4*>(v_s + j * HD + e) = *reinterpret_cast<const u32x4*>(vb + (size_t)jr * HD + e);
   }
   __syncthreads();
 
   // score of position `lane` for query head g (as attn_partial_kernel)
-  const float s = score4<DT>(q_s + g * HD, reinterpret_cast<const uint32_t*>(k_s + lane * KPAD));
+  const float s = score4<DT>(q_s + g * HD, k_s + lane * KPAD);
   const bool valid = lane < nvalid;
   const float m = wave_max_u(valid ? s : -3.0e38f);
   const float p = valid ? exp_cw(__fsub_rn(s, m)) : 0.0f;
   const float l = wave_sum_dpp(p);
-  p_s[g * ACHUNK + lane] = p;
-  __syncthreads();
+  p_s[g * ACHUNK + lane] = p;  // read back by this wave only: no barrier
 
   float a0, a1;
   pv4<DT>(p_s + g * ACHUNK, v_s, nvalid, lane, a0, a1);
+  if (newrow) {
+    const size_t row = ((size_t)kh * max_len + pos) * HD;
+    KC[row + lane] = klo;
+    KC[row + lane + 64] = khi;
+    VC[row + lane] = v0;
+    VC[row + lane + 64] = v1;
+  }
   if (nchunk == 1) {
     // the merge of a single chunk, as attn_combine_kernel computes it
     const float w = exp_cw(__fsub_rn(m, m));
