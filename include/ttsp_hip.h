@@ -102,7 +102,8 @@ int ttsp_qk_rope_kv(const void* QKV, const void* QW, const void* KW, float eps, 
  * [0, min(POS[0] + 1, max_len)), split into nchunk chunks of
  * ttsp_attn_chunk() positions, then merged: Y [nh*128]. Scratch (caller's):
  * PM, PL [nh * nchunk] and PACC [nh * nchunk * 128], fp32. nh % nkv == 0,
- * nh / nkv <= 16. Replaces: attn_partial + attn_combine,
+ * nh / nkv <= 16, nchunk <= 512 (a 32768-position cache); larger values
+ * return hipErrorInvalidValue. Replaces: attn_partial + attn_combine,
  * app/engine/fusedlayer.py:95-159, 244-261. */
 int ttsp_attn_decode(const void* Q, const void* KC, const void* VC, const long long* POS, float* PM,
                      float* PL, float* PACC, void* Y, int nh, int nkv, int max_len, int nchunk,

@@ -215,54 +215,70 @@ __global__ __launch_bounds__(1024) void attn_partial_kernel(
   reinterpret_cast<float2*>(PACC + slot * HD)[lane] = make_float2(a0, a1);
 }
 
-// Merge of the chunk partials of one query head: chunk weights w_c =
-// exp(m_c - max m) are computed once per chunk (one thread each) into LDS,
-// then every thread (one output dimension) folds the chunks in order:
-// den += l_c * w_c, num += acc_c[d] * w_c, y = num / den. Chunks with l = 0
-// (past the live positions) are skipped.
+// Merge of the chunk partials of one query head: with M the largest chunk
+// maximum, chunk weights w_c = exp(m_c - M) (0 for chunks with l = 0, past
+// the live positions) are computed once per chunk into LDS, then every
+// thread (one output dimension) folds the chunks in order: den += l_c * w_c,
+// num += acc_c[d] * w_c, skipping chunks with l = 0; y = num / den. The
+// partial sums are read in batches of CMB chunks, each batch requested
+// before the previous one is folded (the first before the chunk maxima).
+constexpr int CMB = 16;
+constexpr int CMAX = 4 * HD;  // chunks the merge takes (a 32768-position cache)
 template <int DT>
 __global__ __launch_bounds__(HD) void attn_combine_kernel(const float* __restrict__ PM,
                                                           const float* __restrict__ PL,
                                                           const float* __restrict__ PACC,
                                                           uint16_t* __restrict__ Y, int nchunk) {
-  extern __shared__ float cs[];  // [nchunk] m, then [nchunk] l, then [nchunk] w
-  float* pm_s = cs;
-  float* pl_s = cs + nchunk;
-  float* w_s = cs + 2 * nchunk;
-  const int qh = blockIdx.x, d = threadIdx.x;
+  __shared__ __align__(16) float wl_s[CMAX][2];  // per chunk: w_c, l_c
+  __shared__ float mx_s[2];
+  const int qh = blockIdx.x, d = threadIdx.x, lane = d & 63;
+  const float* acc = PACC + (size_t)qh * nchunk * HD + d;
+  float cur[CMB];
+#pragma unroll
+  for (int k = 0; k < CMB; ++k) cur[k] = acc[(size_t)min(k, nchunk - 1) * HD];
   const float* pm = PM + (size_t)qh * nchunk;
   const float* pl = PL + (size_t)qh * nchunk;
-  for (int c = d; c < nchunk; c += HD) {
-    pm_s[c] = pm[c];
-    pl_s[c] = pl[c];
-  }
-  __syncthreads();
-  float M = -3.0e38f;
-  for (int c = 0; c < nchunk; ++c) M = fmaxf(M, pm_s[c]);
-  for (int c = d; c < nchunk; c += HD) w_s[c] = pl_s[c] == 0.0f ? 0.0f : exp_cw(__fsub_rn(pm_s[c], M));
-  __syncthreads();
-  const float* acc = PACC + (size_t)qh * nchunk * HD + d;
-  float num = 0.0f, den = 0.0f;
-  int c = 0;
-  for (; c + 4 <= nchunk; c += 4) {  // four independent loads in flight
-    const float a0 = acc[(size_t)c * HD], a1 = acc[(size_t)(c + 1) * HD];
-    const float a2 = acc[(size_t)(c + 2) * HD], a3 = acc[(size_t)(c + 3) * HD];
-    const float av[4] = {a0, a1, a2, a3};
+  constexpr int PC = CMAX / HD;  // chunks per thread
+  float m[PC], l[PC];
 #pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      const float l = pl_s[c + k];
-      if (l == 0.0f) continue;
-      const float w = w_s[c + k];
-      den = __fadd_rn(den, __fmul_rn(l, w));
-      num = __fadd_rn(num, __fmul_rn(av[k], w));
+  for (int k = 0; k < PC; ++k) {
+    const int c = d + k * HD;
+    m[k] = c < nchunk ? pm[c] : -3.0e38f;
+    l[k] = c < nchunk ? pl[c] : 0.0f;
+  }
+  float mx = fmaxf(fmaxf(m[0], m[1]), fmaxf(m[2], m[3]));
+  mx = wave_max_u(mx);
+  if (lane == 0) mx_s[d >> 6] = mx;
+  __syncthreads();
+  const float M = fmaxf(mx_s[0], mx_s[1]);  // a max: exact in any order
+#pragma unroll
+  for (int k = 0; k < PC; ++k) {
+    const int c = d + k * HD;
+    if (c < nchunk) {
+      wl_s[c][0] = l[k] == 0.0f ? 0.0f : exp_cw(__fsub_rn(m[k], M));
+      wl_s[c][1] = l[k];
     }
   }
-  for (; c < nchunk; ++c) {
-    const float l = pl_s[c];
-    if (l == 0.0f) continue;
-    const float w = w_s[c];
-    den = __fadd_rn(den, __fmul_rn(l, w));
-    num = __fadd_rn(num, __fmul_rn(acc[(size_t)c * HD], w));
+  __syncthreads();
+  float num = 0.0f, den = 0.0f;
+  for (int c0 = 0; c0 < nchunk; c0 += CMB) {
+    float nxt[CMB];
+#pragma unroll
+    for (int k = 0; k < CMB; ++k) nxt[k] = acc[(size_t)min(c0 + CMB + k, nchunk - 1) * HD];
+    f32x4 wl[CMB / 2];
+#pragma unroll
+    for (int k = 0; k < CMB / 2; ++k) wl[k] = *reinterpret_cast<const f32x4*>(&wl_s[min(c0 + 2 * k, CMAX - 2)][0]);
+#pragma unroll
+    for (int k = 0; k < CMB; ++k) {
+      const float w = wl[k >> 1][(k & 1) * 2], lc = wl[k >> 1][(k & 1) * 2 + 1];
+      const bool take = c0 + k < nchunk && lc != 0.0f;
+      const float den1 = __fadd_rn(den, __fmul_rn(lc, w));
+      const float num1 = __fadd_rn(num, __fmul_rn(cur[k], w));
+      den = take ? den1 : den;
+      num = take ? num1 : num;
+    }
+#pragma unroll
+    for (int k = 0; k < CMB; ++k) cur[k] = nxt[k];
   }
   Y[(size_t)qh * HD + d] = Elem<DT>::store(__fdiv_rn(num, den));
 }
@@ -492,7 +508,7 @@ extern "C" int ttsp_attn_decode(const void* Q, const void* KC, const void* VC,
                                 hipStream_t stream) {
   if (nh <= 0 || nkv <= 0 || nh % nkv || nchunk <= 0 || max_len <= 0) return (int)hipErrorInvalidValue;
   const int groups = nh / nkv;
-  if (groups > 16 || (long long)nchunk * ACHUNK < 1) return (int)hipErrorInvalidValue;
+  if (groups > 16 || nchunk > CMAX) return (int)hipErrorInvalidValue;
   const size_t shmem = sizeof(float) * (size_t)groups * (HD + ACHUNK) +
                        sizeof(uint16_t) * (size_t)ACHUNK * (KPAD + HD);
 #define TTSP_AT(DTV)                                                                            \
@@ -500,8 +516,8 @@ extern "C" int ttsp_attn_decode(const void* Q, const void* KC, const void* VC,
     hipLaunchKernelGGL(attn_partial_kernel<DTV>, dim3(nkv, nchunk), dim3(64 * groups), shmem,    \
                        stream, (const uint16_t*)Q, (const uint16_t*)KC, (const uint16_t*)VC, POS, \
                        PM, PL, PACC, groups, max_len, nchunk, scale);                           \
-    hipLaunchKernelGGL(attn_combine_kernel<DTV>, dim3(nh), dim3(HD), 3 * sizeof(float) * nchunk, \
-                       stream, PM, PL, PACC, (uint16_t*)Y, nchunk);                             \
+    hipLaunchKernelGGL(attn_combine_kernel<DTV>, dim3(nh), dim3(HD), 0, stream, PM, PL, PACC,   \
+                       (uint16_t*)Y, nchunk);                                                   \
   } while (0)
   if (dtype == DT_F16) TTSP_AT(DT_F16);
   else if (dtype == DT_BF16) TTSP_AT(DT_BF16);
@@ -517,7 +533,7 @@ extern "C" int ttsp_attn_decode_qkv(const void* QKV, const void* QW, const void*
   if (nh <= 0 || nkv <= 0 || nh % nkv || nchunk <= 0 || max_len <= 0 || ftype < 0 || ftype > 2)
     return (int)hipErrorInvalidValue;
   const int groups = nh / nkv;
-  if (groups > 16 || (nchunk > 1 && (!PM || !PL || !PACC))) return (int)hipErrorInvalidValue;
+  if (groups > 16 || nchunk > CMAX || (nchunk > 1 && (!PM || !PL || !PACC))) return (int)hipErrorInvalidValue;
   const size_t shmem = sizeof(float) * (size_t)groups * (HD + ACHUNK) +
                        sizeof(uint16_t) * (size_t)ACHUNK * (KPAD + HD);
 #define TTSP_AQ(DTV)                                                                                  \
@@ -527,8 +543,8 @@ extern "C" int ttsp_attn_decode_qkv(const void* QKV, const void* QW, const void*
                        POS, (uint16_t*)KC, (uint16_t*)VC, PM, PL, PACC, (uint16_t*)Y, nh, nkv, groups, \
                        max_len, nchunk, scale);                                                       \
     if (nchunk > 1)                                                                                   \
-      hipLaunchKernelGGL(attn_combine_kernel<DTV>, dim3(nh), dim3(HD), 3 * sizeof(float) * nchunk,    \
-                         stream, PM, PL, PACC, (uint16_t*)Y, nchunk);                                 \
+      hipLaunchKernelGGL(attn_combine_kernel<DTV>, dim3(nh), dim3(HD), 0, stream, PM, PL, PACC,       \
+                         (uint16_t*)Y, nchunk);                                                       \
   } while (0)
   if (dtype == DT_F16) TTSP_AQ(DT_F16);
   else if (dtype == DT_BF16) TTSP_AQ(DT_BF16);
