@@ -188,7 +188,9 @@ def test_decode_attention_bit_exact(hip, orc, L, dtype):
 @pytest.mark.parametrize("dtype", DTYPES)
 @pytest.mark.parametrize("pos,max_len,nh,nkv", [(0, 2304, 32, 8), (37, 2304, 32, 8), (63, 2304, 32, 8),
                                                 (64, 2304, 32, 8), (2047, 2304, 32, 8), (2303, 2304, 32, 8),
-                                                (0, 16, 8, 2), (9, 16, 8, 2), (15, 16, 8, 2), (100, 128, 4, 1)])
+                                                (0, 16, 8, 2), (9, 16, 8, 2), (15, 16, 8, 2), (100, 128, 4, 1),
+                                                (70, 256, 8, 8), (130, 256, 4, 2), (200, 1024, 16, 1),
+                                                (5000, 8192, 16, 1)])
 def test_attention_from_qkv_bit_exact(hip, orc, qk_norm, dtype, pos, max_len, nh, nkv):
     """One pass (head norms, rotary, KV write, attention, merge) == qk_rope_kv then
     the split-K attention, through the oracle's emulations, and the cache rows."""

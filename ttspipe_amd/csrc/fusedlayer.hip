@@ -158,7 +158,7 @@ __global__ __launch_bounds__(1024) void attn_partial_kernel(
     const uint16_t* __restrict__ VC, const long long* __restrict__ POS, float* __restrict__ PM,
     float* __restrict__ PL, float* __restrict__ PACC, int groups, int max_len, int nchunk,
     float scale) {
-  extern __shared__ float smem[];
+  extern __shared__ __align__(16) float smem[];
   float* q_s = smem;                                         // [groups][HD]
   float* p_s = q_s + groups * HD;                            // [groups][ACHUNK]
   uint16_t* k_s = reinterpret_cast<uint16_t*>(p_s + groups * ACHUNK);  // [ACHUNK][KPAD]
@@ -342,7 +342,7 @@ __global__ __launch_bounds__(1024) void attn_qkv_kernel(
     uint16_t* __restrict__ KC, uint16_t* __restrict__ VC, float* __restrict__ PM, float* __restrict__ PL,
     float* __restrict__ PACC, uint16_t* __restrict__ Y, int nh, int nkv, int groups, int max_len, int nchunk,
     float scale) {
-  extern __shared__ float smem[];
+  extern __shared__ __align__(16) float smem[];
   float* q_s = smem;                                                   // [groups][HD]
   float* p_s = q_s + groups * HD;                                      // [groups][ACHUNK]
   uint16_t* k_s = reinterpret_cast<uint16_t*>(p_s + groups * ACHUNK);  // [ACHUNK][KPAD]
