@@ -10,6 +10,11 @@ source tree. Flags that matter for results:
 * `-Xclang -target-feature -Xclang -packed-fp32-ops`: no packed fp32
   instructions are generated.
 
+And one for speed: `-mllvm -amdgpu-kernarg-preload-count=16` has the command
+processor place the first kernel-argument dwords in SGPRs at wave launch, so
+a kernel's first loads do not wait for a fetch of its argument block (the
+code keeps a prologue that fetches them, for firmware without preloading).
+
 Usage: `python -m ttspipe_amd.build` (or `build()` from Python).
 """
 
@@ -38,6 +43,8 @@ COMMON_FLAGS = [
     "-target-feature",
     "-Xclang",
     "-packed-fp32-ops",
+    "-mllvm",
+    "-amdgpu-kernarg-preload-count=16",
     f"-I{CSRC}",
 ]
 
