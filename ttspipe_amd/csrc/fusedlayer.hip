@@ -30,8 +30,6 @@ constexpr int ACHUNK = 64;     // positions per attention chunk
 // LDS row stride of the staged K rows (elements): 272 bytes, so rows are
 // 16-byte aligned and the 16 lanes of a 16-byte read hit 64 distinct banks.
 constexpr int KPAD = HD + 8;
-typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 // Max over the wave by DPP steps and row broadcasts (exact in any order);
 // the result is wave-uniform.

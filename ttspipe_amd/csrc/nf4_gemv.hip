@@ -162,8 +162,17 @@ __device__ __forceinline__ F8 to_f32(uint4 c) {
 // Dynamic LDS after the static table: code2 [NM][256], norm partials [8],
 // K-slice partials [8][NM*RPW], the resolved scales [8 waves][NM][RPW][8 J]
 // (16-byte aligned), then x as staged [K/8].
+// The leading scalar arguments are what the first loads need (weight 0's
+// stream and scales, x, the code tables, the sizes): the command processor
+// preloads them into SGPRs, so those loads issue at wave start; the rest of
+// GemvParams is fetched once they are in flight. mk = M | (K / 128) << 20,
+// cfg = KS | bs_shift << 4 | bs2_shift << 8 | dt << 12 | nested << 14 |
+// norm << 15.
 template <int J, int RPW, int NM>
-__global__ __launch_bounds__(GEMV_THREADS) void nf4_gemv_kernel(const GemvParams p) {
+__global__ __launch_bounds__(GEMV_THREADS) void nf4_gemv_kernel(
+    const uint32_t* __restrict__ W0, const uint16_t* __restrict__ X, const float* __restrict__ LUT,
+    const uint8_t* __restrict__ A80, const float* __restrict__ AM0, const float* __restrict__ C20, uint32_t mk,
+    uint32_t cfg, const GemvParams p) {
   constexpr int NW = GEMV_WAVES;
   constexpr int nthr = GEMV_THREADS;
   constexpr int G = 256 * LUT_REP / (4 * 64 * NW);  // table stores (16 bytes) per lane
@@ -179,24 +188,24 @@ __global__ __launch_bounds__(GEMV_THREADS) void nf4_gemv_kernel(const GemvParams
   float* red = wpart + NW;                             // [NW][NM*RPW]
   float* srow = red + NW * NM * RPW;                   // [NW][NM][RPW][8 J] scale slots
 
-  // Every kernel argument is in SGPRs before anything else waits: one round
-  // trip for the argument block instead of one per first use.
-  asm volatile("" ::"s"(p.mat[0].W), "s"(p.mat[0].A8), "s"(p.mat[0].AMAX), "s"(p.mat[0].CODE2),
-               "s"(p.mat[NM - 1].W), "s"(p.mat[NM - 1].A8), "s"(p.mat[NM - 1].AMAX), "s"(p.mat[NM - 1].CODE2),
-               "s"(p.LUT), "s"(p.X), "s"(p.G), "s"(p.R), "s"(p.Y), "s"(p.M), "s"(p.K), "s"(p.KS), "s"(p.bs_shift),
-               "s"(p.bs2_shift), "s"(p.dt), "s"(p.nested), "s"(p.norm));
-
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = uniform(tid >> 6);
-  const int KS = p.KS, ks = wave % KS, rg = wave / KS;
+  const int KS = (int)(cfg & 15u), ks = wave % KS, rg = wave / KS;
+  const int bs_shift = (int)((cfg >> 4) & 15u), bs2_shift = (int)((cfg >> 8) & 15u);
   const int RG = NW / KS;
-  const int M = p.M, K = p.K, KD = K >> 3;
-  const int nblk = K >> p.bs_shift, sh = p.bs_shift - 3;
+  const int M = (int)(mk & 0xfffffu), K = (int)(mk >> 20) * 128, KD = K >> 3;
+  const int nblk = K >> bs_shift, sh = bs_shift - 3;
   const int rows_wg = RG * RPW;
   const int wg_row0 = blockIdx.x * rows_wg;
   const int row0 = wg_row0 + rg * RPW;
-  const int dt = p.dt;
-  const bool nested = p.nested != 0, norm = p.norm != 0;
+  const int dt = (int)((cfg >> 12) & 3u);
+  const bool nested = (cfg >> 14) & 1u, norm = (cfg >> 15) & 1u;
+  // weight m's operands: m = 0 from the preloaded arguments (the SwiGLU
+  // form's second weight comes from GemvParams, fetched here)
+  const uint32_t* W1 = NM == 2 ? p.mat[1].W : W0;
+  const uint8_t* A81 = NM == 2 ? p.mat[1].A8 : A80;
+  const float* AM1 = NM == 2 ? p.mat[1].AMAX : AM0;
+  const float* C21 = NM == 2 ? p.mat[1].CODE2 : C20;
   uint4* xs = reinterpret_cast<uint4*>(srow + NW * NM * RPW * 8 * J);  // [KD]
 
   // 1. small operands first. The table entries this lane writes are
@@ -204,11 +213,11 @@ __global__ __launch_bounds__(GEMV_THREADS) void nf4_gemv_kernel(const GemvParams
   //    code[NW / 4 * i + wave / 4] (wave-uniform, read from lane e_i >> 4 of
   //    a load of the 16 codes), high half code[e_i & 15] = code[4 * (wave % 4)
   //    + lane / 16].
-  const float cl16 = p.LUT[lane & 15];
-  const float clo = p.LUT[4 * (wave & 3) + (lane >> 4)];
-  uint4 c2q[NM];  // code2 entries 4 * lane .. 4 * lane + 3 (every wave writes the whole table)
+  const float cl16 = LUT[lane & 15];
+  const float clo = LUT[4 * (wave & 3) + (lane >> 4)];
+  u32x4 c2q[NM];  // code2 entries 4 * lane .. 4 * lane + 3 (every wave writes the whole table)
 #pragma unroll
-  for (int m = 0; m < NM; ++m) c2q[m] = *reinterpret_cast<const uint4*>(p.mat[m].CODE2 + (nested ? 4 * lane : 0));
+  for (int m = 0; m < NM; ++m) c2q[m] = *reinterpret_cast<const u32x4*>((m ? C21 : C20) + (nested ? 4 * lane : 0));
   // Scales, per wave and read by that wave only (no barrier): slot
   // (m, r, 8 j + g) holds the scale of block g of the wave's chunk j in row r
   // of weight m (8 slots per chunk; with bs > 64 the chunk has 64 / (bs / 8)
@@ -225,23 +234,19 @@ __global__ __launch_bounds__(GEMV_THREADS) void nf4_gemv_kernel(const GemvParams
     const int m = mr / RPW, r = mr % RPW, j = jg >> 3, g = min(jg & 7, spc - 1);
     const int d = min(64 * (j * KS + ks) + (g << sh), KD - 1);
     const uint32_t gb = (uint32_t)min(row0 + r, M - 1) * (uint32_t)nblk + (uint32_t)(d >> sh);
-    const uint8_t* a8 = m ? p.mat[NM - 1].A8 : p.mat[0].A8;
-    const float* am = m ? p.mat[NM - 1].AMAX : p.mat[0].AMAX;
-    av[i] = a8[gb];
-    sv[i] = am[nested ? gb >> p.bs2_shift : gb];
+    av[i] = (m ? A81 : A80)[gb];
+    sv[i] = (m ? AM1 : AM0)[nested ? gb >> bs2_shift : gb];
   }
-  const uint32_t rres = p.R[min(row0 + min(lane, RPW - 1), M - 1)];  // epilogue operand
   // x (and the norm weight): staged once per workgroup, chunk c = tid + 512 i
   // by thread tid (one chunk per thread unless K > 4096, where there is no norm)
   const int XN = uniform((KD + nthr - 1) / nthr);
   uint4 xc[XC_MAX];
-  xc[0] = *reinterpret_cast<const uint4*>(p.X + 8 * (size_t)min(tid, KD - 1));
-  const uint4 gc = *reinterpret_cast<const uint4*>(p.G + 8 * (size_t)(norm ? min(tid, KD - 1) : 0));
+  // (chunks past XN stay unset and unread: a zero-initialised chunk would make
+  // the branch's join wait for the load)
+  xc[0] = *reinterpret_cast<const uint4*>(X + 8 * (size_t)min(tid, KD - 1));
 #pragma unroll
-  for (int i = 1; i < XC_MAX; ++i) {
-    xc[i] = make_uint4(0, 0, 0, 0);
-    if (i < XN) xc[i] = *reinterpret_cast<const uint4*>(p.X + 8 * (size_t)min(tid + i * nthr, KD - 1));
-  }
+  for (int i = 1; i < XC_MAX; ++i)
+    if (i < XN) xc[i] = *reinterpret_cast<const uint4*>(X + 8 * (size_t)min(tid + i * nthr, KD - 1));
 
   // 2. the first PF rows of the weight stream; the rest is requested row by
   //    row during the dot products, PF rows ahead, so no wave's barrier
@@ -253,7 +258,7 @@ __global__ __launch_bounds__(GEMV_THREADS) void nf4_gemv_kernel(const GemvParams
   auto load_row = [&](int r) {
 #pragma unroll
     for (int m = 0; m < NM; ++m) {
-      const char* wr = reinterpret_cast<const char*>(p.mat[m].W + (size_t)uniform(min(row0 + r, M - 1)) * KD + 64 * ks);
+      const char* wr = reinterpret_cast<const char*>((m ? W1 : W0) + (size_t)uniform(min(row0 + r, M - 1)) * KD + 64 * ks);
 #pragma unroll
       for (int j = 0; j < J; ++j)
         w[m][r][j] = __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(wr + woff[j]));
@@ -261,6 +266,10 @@ __global__ __launch_bounds__(GEMV_THREADS) void nf4_gemv_kernel(const GemvParams
   };
 #pragma unroll
   for (int r = 0; r < PF; ++r) load_row(r);
+  // the remaining arguments, in one round trip while those loads fly
+  asm volatile("" ::"s"(p.G), "s"(p.R), "s"(p.Y), "s"(p.mat[0].offset), "s"(p.mat[NM - 1].offset), "s"(p.eps));
+  const uint32_t rres = p.R[min(row0 + min(lane, RPW - 1), M - 1)];  // epilogue operand
+  const uint4 gc = *reinterpret_cast<const uint4*>(p.G + 8 * (size_t)(norm ? min(tid, KD - 1) : 0));
 
   // 3. set-up while those stream: the replicated code table, code2 (each wave
   //    its own full copy: identical values, so no barrier), the resolved
@@ -275,7 +284,7 @@ __global__ __launch_bounds__(GEMV_THREADS) void nf4_gemv_kernel(const GemvParams
     }
   }
 #pragma unroll
-  for (int m = 0; m < NM; ++m) reinterpret_cast<uint4*>(code2_s + m * 256)[lane] = c2q[m];
+  for (int m = 0; m < NM; ++m) reinterpret_cast<u32x4*>(code2_s + m * 256)[lane] = c2q[m];
 #pragma unroll
   for (int i = 0; i < SL; ++i) {
     const int sl = lane + 64 * i;
@@ -464,8 +473,12 @@ template <int J, int RPW, int NM>
 static void launch_gemv(const GemvShape& g, const GemvParams& p, hipStream_t st) {
   const int rows_wg = (GEMV_WAVES / g.KS) * RPW;
   const int grid = (p.M + rows_wg - 1) / rows_wg;
+  const uint32_t mk = (uint32_t)p.M | ((uint32_t)(p.K / 128) << 20);
+  const uint32_t cfg = (uint32_t)g.KS | ((uint32_t)p.bs_shift << 4) | ((uint32_t)p.bs2_shift << 8) |
+                       ((uint32_t)p.dt << 12) | ((uint32_t)p.nested << 14) | ((uint32_t)p.norm << 15);
   hipLaunchKernelGGL((nf4_gemv_kernel<J, RPW, NM>), dim3(grid), dim3(GEMV_THREADS),
-                     gemv_dyn_lds(g, NM, p.K, p.bs_shift), st, p);
+                     gemv_dyn_lds(g, NM, p.K, p.bs_shift), st, p.mat[0].W, p.X, p.LUT, p.mat[0].A8,
+                     p.mat[0].AMAX, p.mat[0].CODE2, mk, cfg, p);
 }
 
 template <int J, int NM>
@@ -512,7 +525,9 @@ static int gemv_launch(const void* X, int dt, const void* G, float eps, const Nf
                        int epi, int M, int K, int blocksize, int blocksize2, hipStream_t st) {
   const int bs_shift = log2_exact(blocksize);
   const int bs2_shift = nested ? log2_exact(blocksize2) : 0;
-  if (bs_shift < 6 || bs2_shift < 0 || K % 128 || K % blocksize || M <= 0) return (int)hipErrorInvalidValue;
+  if (bs_shift < 6 || bs_shift > 15 || bs2_shift < 0 || bs2_shift > 15 || K % 128 || K % blocksize || M <= 0 ||
+      M >= (1 << 20) || K / 128 >= (1 << 12))
+    return (int)hipErrorInvalidValue;  // the sizes travel packed: M < 2^20, K / 128 < 2^12
   if (dt != DT_F16 && dt != DT_BF16) return (int)hipErrorInvalidValue;
   if (epi < 0 || epi > 2 || (epi && !R) || (mat3 && epi)) return (int)hipErrorInvalidValue;
   const int nm = mat3 ? 2 : 1;

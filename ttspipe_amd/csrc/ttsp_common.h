@@ -19,6 +19,11 @@ namespace ttsp {
 
 enum : int { DT_F16 = 0, DT_BF16 = 1, DT_F32 = 2 };
 
+// Plain vector types for 16-byte values held in registers (HIP's uint4 is a
+// union-backed struct that can keep a small local array out of registers).
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
 __device__ __forceinline__ float bf16_to_f32(uint32_t h) { return __uint_as_float(h << 16); }
 
 // Round to nearest even; NaN stays a (quiet) NaN.
