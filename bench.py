@@ -39,7 +39,7 @@ MALL_BYTES = 256 * 2**20
 #: HBM bytes one gate-shape GEMV launch moves, from rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE
 #: per dispatch (bench.py --only kernel --direct), each scaled by the same counter on a plain
 #: 64 MiB copy (FETCH_SIZE x 1.9992, WRITE_SIZE x 1.0). Re-measure when the kernel changes.
-GEMV_TRAFFIC_BYTES = 13_188_319
+GEMV_TRAFFIC_BYTES = 13_211_842
 
 # (name, out_features, in_features) of one decoder layer's linears
 LAYER = [("q", 4096, 2560), ("k", 1024, 2560), ("v", 1024, 2560), ("o", 2560, 4096),
