@@ -123,6 +123,23 @@ int ttsp_attn_decode_qkv(const void* QKV, const void* QW, const void* KW, float 
                          float* PACC, void* Y, int nh, int nkv, int max_len, int nchunk, float scale,
                          int dtype, void* stream);
 
+/* ttsp_attn_decode_qkv for a cache of at most one chunk, and the attention
+ * output projection, in one launch: every workgroup of the NF4 GEMV that
+ * computes Y = epi(attention . W^T) first computes the whole attention (all
+ * nh <= 8 query heads; nkv * max_len <= 128, max_len <= 64) in its own LDS,
+ * with ttsp_attn_decode_qkv's arithmetic, rounds it to dtype as x, and the
+ * first workgroup writes the new K/V row to KC/VC[kv][POS[0]]. W/A8/AMAX/
+ * CODE2/offset/LUT/R/epi/M/blocksize/blocksize2 as ttsp_nf4_gemm with K =
+ * nh * 128. Results equal ttsp_attn_decode_qkv followed by ttsp_nf4_gemm
+ * (N = 1) bit for bit; with POS[0] outside [0, max_len) nothing is written to
+ * the cache and Y is unspecified. Replaces: attention + wo in decode_block,
+ * app/engine/fusedlayer.py:233-261 (the fast transformer's short caches). */
+int ttsp_attn_nf4_gemv(const void* QKV, const void* QW, const void* KW, float eps, const void* F,
+                       int ftype, const long long* POS, void* KC, void* VC, int nh, int nkv, int max_len,
+                       float scale, const uint8_t* W, const uint8_t* A8, const float* AMAX,
+                       const float* CODE2, float offset, const float* LUT, void* Y, const void* R, int epi,
+                       int M, int blocksize, int blocksize2, int dtype, void* stream);
+
 /* Cache positions per attention chunk (64). Replaces: CHUNK,
  * app/engine/fusedlayer.py:40. */
 int ttsp_attn_chunk(void);

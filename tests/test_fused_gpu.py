@@ -228,6 +228,83 @@ def test_attention_from_qkv_bit_exact(hip, orc, qk_norm, dtype, pos, max_len, nh
     assert np.array_equal(bits(VC), VCo)
 
 
+@pytest.mark.parametrize("nested", [True, False])
+@pytest.mark.parametrize("qk_norm", [True, False])
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("pos,max_len,nh,nkv,M", [(0, 16, 8, 2, 1024), (9, 16, 8, 2, 1024), (15, 16, 8, 2, 1024),
+                                                  (37, 64, 4, 1, 640), (63, 64, 8, 2, 2048), (5, 8, 2, 2, 256),
+                                                  (20, 32, 8, 4, 1024), (0, 1, 1, 1, 64)])
+def test_attention_and_wo_in_one_launch(hip, nested, qk_norm, dtype, pos, max_len, nh, nkv, M):
+    """ttsp_attn_nf4_gemv (every wo workgroup recomputes the one-chunk attention)
+    == ttsp_attn_decode_qkv then the wo GEMV with the residual, bit for bit,
+    and the same KV-cache rows."""
+    from tests.nf4data import random_layer
+    from ttspipe_amd import _lib
+    from ttspipe_amd.llama import precompute_freqs_cis
+    from ttspipe_amd.quant import NF4_CODE
+
+    dt = dt_code(dtype)
+    K = nh * 128
+    layer = random_layer(M, K, nested, seed=M + K + pos)
+    W = torch.from_numpy(layer["W"]).cuda()
+    A8 = torch.from_numpy(layer["A8"]).cuda() if nested else None
+    AM = torch.from_numpy(layer["AMAX"]).cuda()
+    C2 = torch.from_numpy(layer["CODE2"]).cuda() if nested else None
+    lut = torch.tensor(NF4_CODE, dtype=torch.float32, device="cuda")
+    qkvb = randn_bits((nh + 2 * nkv) * 128, dtype, seed=pos + 21, scale=2.0)
+    qwb = o.from_f32((np.random.default_rng(5).random(128) + 0.5).astype(np.float32), dt)
+    kwb = o.from_f32((np.random.default_rng(6).random(128) + 0.5).astype(np.float32), dt)
+    freqs = precompute_freqs_cis(max(max_len, pos + 1), 128, 1e6)[pos : pos + 1].contiguous().cuda()
+    kcb = randn_bits(nkv * max_len * 128, dtype, seed=pos + 22)
+    vcb = randn_bits(nkv * max_len * 128, dtype, seed=pos + 23)
+    rb = randn_bits(M, dtype, seed=pos + 24)
+    qkv, R = from_bits(qkvb, dtype), from_bits(rb, dtype)
+    qw = from_bits(qwb, dtype) if qk_norm else None
+    kw = from_bits(kwb, dtype) if qk_norm else None
+    posd = torch.tensor([pos], dtype=torch.long, device="cuda")
+    scale = float(128**-0.5)
+    offset = float(layer["offset"])
+    bs2 = layer["bs2"] or 0
+
+    # two launches
+    KC1, VC1 = from_bits(kcb, dtype), from_bits(vcb, dtype)
+    y = torch.empty(nh * 128, dtype=dtype, device="cuda")
+    h1 = torch.empty(M, dtype=dtype, device="cuda")
+    rc = hip.ttsp_attn_decode_qkv(qkv.data_ptr(), _lib.ptr(qw), _lib.ptr(kw), 1e-6, freqs.data_ptr(), o.DT_BF16,
+                                  posd.data_ptr(), KC1.data_ptr(), VC1.data_ptr(), None, None, None, y.data_ptr(),
+                                  nh, nkv, max_len, 1, scale, dt, _lib.stream())
+    assert rc == 0
+    rc = hip.ttsp_nf4_gemm(y.data_ptr(), dt, W.data_ptr(), _lib.ptr(A8), AM.data_ptr(), _lib.ptr(C2), offset,
+                           lut.data_ptr(), h1.data_ptr(), R.data_ptr(), 1, M, K, 1, 64, bs2, _lib.stream())
+    assert rc == 0
+    # one launch
+    KC2, VC2 = from_bits(kcb, dtype), from_bits(vcb, dtype)
+    h2 = torch.empty(M, dtype=dtype, device="cuda")
+    rc = hip.ttsp_attn_nf4_gemv(qkv.data_ptr(), _lib.ptr(qw), _lib.ptr(kw), 1e-6, freqs.data_ptr(), o.DT_BF16,
+                                posd.data_ptr(), KC2.data_ptr(), VC2.data_ptr(), nh, nkv, max_len, scale,
+                                W.data_ptr(), _lib.ptr(A8), AM.data_ptr(), _lib.ptr(C2), offset, lut.data_ptr(),
+                                h2.data_ptr(), R.data_ptr(), 1, M, 64, bs2, dt, _lib.stream())
+    assert rc == 0
+    assert np.array_equal(bits(h2), bits(h1)), first_mismatch(bits(h2), bits(h1))
+    assert np.array_equal(bits(KC2), bits(KC1)), first_mismatch(bits(KC2), bits(KC1))
+    assert np.array_equal(bits(VC2), bits(VC1))
+
+
+def test_attention_and_wo_declines_what_it_cannot_serve(hip):
+    """Shapes outside the one-launch form are rejected with an error code (the
+    caller then runs the two-launch form), never launched."""
+    from ttspipe_amd import _lib
+
+    d = torch.zeros(1 << 16, dtype=torch.float32, device="cuda")
+    p = d.data_ptr()
+    st = _lib.stream()
+    # (nh, nkv, max_len): too many heads, a cache longer than one chunk, too many staged rows
+    for nh, nkv, max_len in ((16, 2, 16), (8, 2, 65), (8, 4, 64), (6, 4, 16)):
+        rc = hip.ttsp_attn_nf4_gemv(p, None, None, 1e-6, p, o.DT_F32, p, p, p, nh, nkv, max_len, 0.088, p, None, p,
+                                    None, 0.0, p, p, p, 1, 64, 64, 0, o.DT_BF16, st)
+        assert rc != 0, (nh, nkv, max_len)
+
+
 def test_decode_attention_matches_torch_gqa():
     """Against torch SDPA with enable_gqa on the CPU, the reference's check
     (tests/test_nf4gemv.py:224-242)."""

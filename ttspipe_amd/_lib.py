@@ -42,6 +42,8 @@ SIGNATURES: dict[str, list] = {
     "ttsp_attn_decode": [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _f, _i, _vp],
     "ttsp_attn_decode_qkv": [_vp, _vp, _vp, _f, _vp, _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _f,
                              _i, _vp],
+    "ttsp_attn_nf4_gemv": [_vp, _vp, _vp, _f, _vp, _i, _vp, _vp, _vp, _i, _i, _i, _f, _vp, _vp, _vp, _vp, _f,
+                           _vp, _vp, _vp, _i, _i, _i, _i, _i, _vp],
     "ttsp_attn_chunk": [],
     "ttsp_embed_sum": [_vp, _vp, _i, _i, _i, _vp, _i, _vp],
     "ttsp_argmax": [_vp, _i, _i, _vp, _vp],

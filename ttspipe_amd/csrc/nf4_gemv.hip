@@ -49,7 +49,7 @@
 //   * Reductions: lanes by DPP adds (the xor 1, 2, 4, 8 tree inside 16-lane
 //     rows, then the row sums as (r3 + r2) + (r1 + r0)); K-slices left to
 //     right through LDS. No atomics anywhere.
-#include "ttsp_common.h"
+#include "attn_common.h"
 
 namespace ttsp {
 
@@ -75,6 +75,21 @@ struct Nf4Mat {
   float offset;
 };
 
+// The attention whose output is the GEMV's x (the attention-prologue form):
+// one decode position, all query heads, a cache of at most one chunk.
+struct AttnSrc {
+  const uint16_t* QKV;    // [nh + 2 nkv][128]
+  const uint16_t* QW;     // q / k head-norm weights, or QKV (hcfg says which are used)
+  const uint16_t* KW;
+  const void* F;          // the position's rotary row
+  const long long* POS;
+  uint16_t* KC;           // [nkv][max_len][128]
+  uint16_t* VC;
+  float eps, scale;
+  int max_len;            // <= 64
+  uint32_t hcfg;          // nh | nkv << 8 | groups << 16 | ftype << 24 | qn << 28 | kn << 29
+};
+
 struct GemvParams {
   Nf4Mat mat[2];          // mat[1]: the SwiGLU form's second weight (w3)
   const float* LUT;       // the 16 NF4 code points
@@ -86,7 +101,18 @@ struct GemvParams {
   int M, K, KS, bs_shift, bs2_shift;
   int dt;                 // DT_F16 / DT_BF16
   int nested, norm, epi;  // flags; epi: 0 none, 1 residual, 2 silu gate
+  AttnSrc att;            // the attention-prologue form only
 };
+
+// LDS of the attention prologue after x: q [8][128] fp32, p [8][64] fp32,
+// then per kv head R16 staged K rows (KPAD stride) and R16 V rows, R16 the
+// cache length rounded up to 16 (the PV loop reads rows 16 at a time).
+static constexpr int ATT_MAX_HEADS = 8;
+__host__ __device__ constexpr int att_r16(int max_len) { return (max_len + 15) & ~15; }
+__host__ __device__ constexpr size_t att_lds(int nkv, int max_len) {
+  return 4 * (size_t)ATT_MAX_HEADS * (HD + ACHUNK) + 2 * (size_t)nkv * att_r16(max_len) * (KPAD + HD);
+}
+constexpr int ATT_PER = 4;  // staged 16-byte pieces per thread: nkv * R16 * 16 <= 4 * 512
 
 __device__ __forceinline__ int uniform(int v) { return __builtin_amdgcn_readfirstlane(v); }
 
@@ -168,7 +194,7 @@ __device__ __forceinline__ F8 to_f32(uint4 c) {
 // GemvParams is fetched once they are in flight. mk = M | (K / 128) << 20,
 // cfg = KS | bs_shift << 4 | bs2_shift << 8 | dt << 12 | nested << 14 |
 // norm << 15.
-template <int J, int RPW, int NM>
+template <int J, int RPW, int NM, bool ATT = false>
 __global__ __launch_bounds__(GEMV_THREADS) void nf4_gemv_kernel(
     const uint32_t* __restrict__ W0, const uint16_t* __restrict__ X, const float* __restrict__ LUT,
     const uint8_t* __restrict__ A80, const float* __restrict__ AM0, const float* __restrict__ C20, uint32_t mk,
@@ -243,10 +269,12 @@ __global__ __launch_bounds__(GEMV_THREADS) void nf4_gemv_kernel(
   uint4 xc[XC_MAX];
   // (chunks past XN stay unset and unread: a zero-initialised chunk would make
   // the branch's join wait for the load)
-  xc[0] = *reinterpret_cast<const uint4*>(X + 8 * (size_t)min(tid, KD - 1));
+  if constexpr (!ATT) {
+    xc[0] = *reinterpret_cast<const uint4*>(X + 8 * (size_t)min(tid, KD - 1));
 #pragma unroll
-  for (int i = 1; i < XC_MAX; ++i)
-    if (i < XN) xc[i] = *reinterpret_cast<const uint4*>(X + 8 * (size_t)min(tid + i * nthr, KD - 1));
+    for (int i = 1; i < XC_MAX; ++i)
+      if (i < XN) xc[i] = *reinterpret_cast<const uint4*>(X + 8 * (size_t)min(tid + i * nthr, KD - 1));
+  }
 
   // 2. the first PF rows of the weight stream; the rest is requested row by
   //    row during the dot products, PF rows ahead, so no wave's barrier
@@ -271,6 +299,48 @@ __global__ __launch_bounds__(GEMV_THREADS) void nf4_gemv_kernel(
   const uint32_t rres = p.R[min(row0 + min(lane, RPW - 1), M - 1)];  // epilogue operand
   const uint4 gc = *reinterpret_cast<const uint4*>(p.G + 8 * (size_t)(norm ? min(tid, KD - 1) : 0));
 
+  // 2b. (attention prologue) every load of the attention, before any waits:
+  //     wave w takes query head min(w, nh - 1) (waves past nh duplicate the
+  //     last head's loads and compute nothing), its kv head's new K/V row and
+  //     norm weights, and the workgroup stages all nkv * max_len cached rows
+  //     (row pos, stale, is replaced by the computed row).
+  const AttnSrc& at = p.att;
+  const int a_nh = (int)(at.hcfg & 255u), a_nkv = (int)((at.hcfg >> 8) & 255u);
+  const int a_groups = (int)((at.hcfg >> 16) & 255u), a_ftype = (int)((at.hcfg >> 24) & 15u);
+  const bool a_qn = (at.hcfg >> 28) & 1u, a_kn = (at.hcfg >> 29) & 1u;
+  const int a_R = att_r16(at.max_len);
+  const int a_head = min(wave, a_nh - 1), a_kvh = a_head / a_groups;
+  uint16_t aq0 = 0, aq1 = 0, aqw0 = 0, aqw1 = 0, ak0 = 0, ak1 = 0, av0 = 0, av1 = 0, akw0 = 0, akw1 = 0;
+  RopeF arf{};
+  u32x4 akq[ATT_PER], avq[ATT_PER];
+  long long apos0 = 0;
+  if constexpr (ATT) {
+    apos0 = at.POS[0];
+    const uint16_t* qr = at.QKV + (size_t)a_head * HD;
+    const uint16_t* kr = at.QKV + (size_t)(a_nh + a_kvh) * HD;
+    const uint16_t* vr = at.QKV + (size_t)(a_nh + a_nkv + a_kvh) * HD;
+    aq0 = qr[lane];
+    aq1 = qr[lane + 64];
+    aqw0 = at.QW[lane];
+    aqw1 = at.QW[lane + 64];
+    arf = load_rope(at.F, a_ftype, lane);
+    ak0 = kr[lane];
+    ak1 = kr[lane + 64];
+    av0 = vr[lane];
+    av1 = vr[lane + 64];
+    akw0 = at.KW[lane];
+    akw1 = at.KW[lane + 64];
+    const int npc = a_nkv * at.max_len * (HD / 8);  // pieces to stage
+#pragma unroll
+    for (int i = 0; i < ATT_PER; ++i) {
+      const int t = min(tid + i * nthr, npc - 1);
+      const int kvh = t / (at.max_len * (HD / 8)), j = (t / (HD / 8)) % at.max_len, e = (t % (HD / 8)) * 8;
+      const size_t off = ((size_t)kvh * at.max_len + j) * HD + e;
+      akq[i] = *reinterpret_cast<const u32x4*>(at.KC + off);
+      avq[i] = *reinterpret_cast<const u32x4*>(at.VC + off);
+    }
+  }
+
   // 3. set-up while those stream: the replicated code table, code2 (each wave
   //    its own full copy: identical values, so no barrier), the resolved
   //    scales, x staged (or, with a norm, each wave's sum of squares)
@@ -292,7 +362,77 @@ __global__ __launch_bounds__(GEMV_THREADS) void nf4_gemv_kernel(
     const float off = m ? p.mat[NM - 1].offset : p.mat[0].offset;
     if (sl < SW) srow[wave * SW + sl] = nested ? __fadd_rn(__fmul_rn(code2_s[m * 256 + av[i]], sv[i]), off) : sv[i];
   }
-  if (!norm) {
+  if constexpr (ATT) {
+    // 3b. the attention (attn_qkv_kernel's arithmetic, one chunk), its
+    //     output rounded into x
+    float* q_s = reinterpret_cast<float*>(xs + KD);                         // [8][128]
+    float* p_s = q_s + ATT_MAX_HEADS * HD;                                  // [8][64]
+    uint16_t* k_s = reinterpret_cast<uint16_t*>(p_s + ATT_MAX_HEADS * ACHUNK);  // [nkv][R16][KPAD]
+    uint16_t* v_s = k_s + (size_t)a_nkv * a_R * KPAD;                       // [nkv][R16][HD]
+    const long long pos = apos0;
+    const bool pos_ok = pos >= 0 && pos < at.max_len;
+    const int jpos = pos_ok ? (int)pos : 0, nvalid = jpos + 1;
+    const bool qwave = wave < a_nh, newrow = qwave && wave % a_groups == 0;
+    uint16_t klo = 0, khi = 0;
+    if (qwave) {
+      float lo = ld16(dt, aq0), hi = ld16(dt, aq1);
+      if (dt == DT_BF16) head_norm_rope<DT_BF16>(lo, hi, a_qn, aqw0, aqw1, at.eps, arf, lane);
+      else head_norm_rope<DT_F16>(lo, hi, a_qn, aqw0, aqw1, at.eps, arf, lane);
+      q_s[wave * HD + lane] = __fmul_rn(ld16(dt, st16(dt, lo)), at.scale);
+      q_s[wave * HD + lane + 64] = __fmul_rn(ld16(dt, st16(dt, hi)), at.scale);
+    }
+    if (newrow) {
+      float lo = ld16(dt, ak0), hi = ld16(dt, ak1);
+      if (dt == DT_BF16) head_norm_rope<DT_BF16>(lo, hi, a_kn, akw0, akw1, at.eps, arf, lane);
+      else head_norm_rope<DT_F16>(lo, hi, a_kn, akw0, akw1, at.eps, arf, lane);
+      klo = (uint16_t)st16(dt, lo);
+      khi = (uint16_t)st16(dt, hi);
+      uint16_t* kd = k_s + ((size_t)a_kvh * a_R + jpos) * KPAD;
+      uint16_t* vd = v_s + ((size_t)a_kvh * a_R + jpos) * HD;
+      kd[lane] = klo;
+      kd[lane + 64] = khi;
+      vd[lane] = av0;
+      vd[lane + 64] = av1;
+    }
+    const int npc = a_nkv * at.max_len * (HD / 8);
+#pragma unroll
+    for (int i = 0; i < ATT_PER; ++i) {
+      const int t = tid + i * nthr;
+      const int kvh = t / (at.max_len * (HD / 8)), j = (t / (HD / 8)) % at.max_len, e = (t % (HD / 8)) * 8;
+      if (t < npc && j != jpos) {
+        *reinterpret_cast<u32x4*>(k_s + ((size_t)kvh * a_R + j) * KPAD + e) = akq[i];
+        *reinterpret_cast<u32x4*>(v_s + ((size_t)kvh * a_R + j) * HD + e) = avq[i];
+      }
+    }
+    __syncthreads();
+    if (qwave) {
+      const uint16_t* kr = k_s + ((size_t)a_kvh * a_R + min(lane, at.max_len - 1)) * KPAD;
+      const float sc = dt == DT_BF16 ? score4<DT_BF16>(q_s + wave * HD, kr) : score4<DT_F16>(q_s + wave * HD, kr);
+      const bool valid = lane < nvalid;
+      const float m = wave_max_u(valid ? sc : -3.0e38f);
+      const float pr = valid ? exp_cw(__fsub_rn(sc, m)) : 0.0f;
+      const float l = wave_sum_dpp(pr);
+      p_s[wave * ACHUNK + lane] = pr;  // read back by this wave only
+      float a0, a1;
+      const uint16_t* vs = v_s + (size_t)a_kvh * a_R * HD;
+      if (dt == DT_BF16) pv4<DT_BF16>(p_s + wave * ACHUNK, vs, nvalid, lane, a0, a1);
+      else pv4<DT_F16>(p_s + wave * ACHUNK, vs, nvalid, lane, a0, a1);
+      // the merge of a single chunk, as attn_combine_kernel computes it
+      const float wt = exp_cw(__fsub_rn(m, m));
+      const float den = __fadd_rn(0.0f, __fmul_rn(l, wt));
+      const float y0 = __fdiv_rn(__fadd_rn(0.0f, __fmul_rn(a0, wt)), den);
+      const float y1 = __fdiv_rn(__fadd_rn(0.0f, __fmul_rn(a1, wt)), den);
+      reinterpret_cast<uint32_t*>(xs)[wave * 64 + lane] = st16(dt, y0) | (st16(dt, y1) << 16);
+    }
+    // the new row into the cache, once (workgroup 0)
+    if (newrow && pos_ok && blockIdx.x == 0) {
+      const size_t row = ((size_t)a_kvh * at.max_len + pos) * HD;
+      at.KC[row + lane] = klo;
+      at.KC[row + lane + 64] = khi;
+      at.VC[row + lane] = av0;
+      at.VC[row + lane + 64] = av1;
+    }
+  } else if (!norm) {
 #pragma unroll
     for (int i = 0; i < XC_MAX; ++i) {
       const int c = tid + i * nthr;
@@ -469,16 +609,16 @@ static GemvShape gemv_shape(int M, int K, int nm = 1, int bs_shift = 6) {
   return g;
 }
 
-template <int J, int RPW, int NM>
-static void launch_gemv(const GemvShape& g, const GemvParams& p, hipStream_t st) {
+template <int J, int RPW, int NM, bool ATT = false>
+static void launch_gemv(const GemvShape& g, const GemvParams& p, hipStream_t st, size_t extra_lds = 0) {
   const int rows_wg = (GEMV_WAVES / g.KS) * RPW;
   const int grid = (p.M + rows_wg - 1) / rows_wg;
   const uint32_t mk = (uint32_t)p.M | ((uint32_t)(p.K / 128) << 20);
   const uint32_t cfg = (uint32_t)g.KS | ((uint32_t)p.bs_shift << 4) | ((uint32_t)p.bs2_shift << 8) |
                        ((uint32_t)p.dt << 12) | ((uint32_t)p.nested << 14) | ((uint32_t)p.norm << 15);
-  hipLaunchKernelGGL((nf4_gemv_kernel<J, RPW, NM>), dim3(grid), dim3(GEMV_THREADS),
-                     gemv_dyn_lds(g, NM, p.K, p.bs_shift), st, p.mat[0].W, p.X, p.LUT, p.mat[0].A8,
-                     p.mat[0].AMAX, p.mat[0].CODE2, mk, cfg, p);
+  hipLaunchKernelGGL((nf4_gemv_kernel<J, RPW, NM, ATT>), dim3(grid), dim3(GEMV_THREADS),
+                     gemv_dyn_lds(g, NM, p.K, p.bs_shift) + extra_lds, st, p.mat[0].W, p.X, p.LUT,
+                     p.mat[0].A8, p.mat[0].AMAX, p.mat[0].CODE2, mk, cfg, p);
 }
 
 template <int J, int NM>
@@ -510,6 +650,18 @@ static int dispatch_j(const GemvShape& g, const GemvParams& p, hipStream_t st) {
 #undef TTSP_J
 }
 
+// The attention-prologue form: one weight, K = nh * 128 <= 1024, so KS = 1,
+// J <= 2 and any RPW the row count needs up to 4 (beyond that: declined).
+static int dispatch_att(const GemvShape& g, const GemvParams& p, hipStream_t st, size_t extra) {
+  if (g.KS != 1) return (int)hipErrorInvalidValue;
+#define TTSP_A(JV, RV) \
+  if (g.J == JV && g.RPW == RV) { launch_gemv<JV, RV, 1, true>(g, p, st, extra); return 0; }
+  TTSP_A(1, 1) TTSP_A(1, 2) TTSP_A(1, 3) TTSP_A(1, 4)
+  TTSP_A(2, 1) TTSP_A(2, 2) TTSP_A(2, 3) TTSP_A(2, 4)
+#undef TTSP_A
+  return (int)hipErrorInvalidValue;
+}
+
 static int log2_exact(int v) {
   if (v <= 0 || (v & (v - 1))) return -1;
   int s = 0;
@@ -522,7 +674,8 @@ static int log2_exact(int v) {
 // folds the RMSNorm prologue in.
 static int gemv_launch(const void* X, int dt, const void* G, float eps, const Nf4Mat& mat1,
                        const Nf4Mat* mat3, bool nested, const float* LUT, void* Y, const void* R,
-                       int epi, int M, int K, int blocksize, int blocksize2, hipStream_t st) {
+                       int epi, int M, int K, int blocksize, int blocksize2, hipStream_t st,
+                       const AttnSrc* att = nullptr) {
   const int bs_shift = log2_exact(blocksize);
   const int bs2_shift = nested ? log2_exact(blocksize2) : 0;
   if (bs_shift < 6 || bs_shift > 15 || bs2_shift < 0 || bs2_shift > 15 || K % 128 || K % blocksize || M <= 0 ||
@@ -535,7 +688,9 @@ static int gemv_launch(const void* X, int dt, const void* G, float eps, const Nf
   if (!g.J) return (int)hipErrorInvalidValue;
   if (G && K / 8 > GEMV_THREADS) return (int)hipErrorInvalidValue;  // the norm: one chunk per thread
   if (K / 8 > XC_MAX * GEMV_THREADS) return (int)hipErrorInvalidValue;
-  if (LUT_BYTES + gemv_dyn_lds(g, nm, K, bs_shift) > kLdsPerCU) return (int)hipErrorInvalidValue;
+  const size_t att_bytes = att ? att_lds((int)((att->hcfg >> 8) & 255u), att->max_len) : 0;
+  if (LUT_BYTES + gemv_dyn_lds(g, nm, K, bs_shift) + att_bytes > kLdsPerCU) return (int)hipErrorInvalidValue;
+  if (att && (G || mat3)) return (int)hipErrorInvalidValue;
   if (nested && ((uintptr_t)mat1.CODE2 % 16 || (mat3 && (uintptr_t)mat3->CODE2 % 16)))
     return (int)hipErrorInvalidValue;  // code2 is read 16 bytes per lane
   GemvParams p;
@@ -563,7 +718,8 @@ static int gemv_launch(const void* X, int dt, const void* G, float eps, const Nf
   p.nested = nested ? 1 : 0;
   p.norm = G ? 1 : 0;
   p.epi = epi;
-  const int rc = nm == 1 ? dispatch_j<1>(g, p, st) : dispatch_j<2>(g, p, st);
+  p.att = att ? *att : AttnSrc{};
+  const int rc = att ? dispatch_att(g, p, st, att_bytes) : nm == 1 ? dispatch_j<1>(g, p, st) : dispatch_j<2>(g, p, st);
   if (rc) return rc;
   TTSP_RETURN_LAUNCH();
 }
@@ -604,4 +760,34 @@ extern "C" int ttsp_nf4_gemv_fused(const void* X, int x_dtype, const void* NORM_
   const Nf4Mat m3{reinterpret_cast<const uint32_t*>(W3), A8_3, AMAX_3, CODE2_3, offset_3};
   return gemv_launch(X, x_dtype, NORM_W, eps, m1, &m3, nested, LUT, Y, R, epi, M, K, blocksize, blocksize2,
                      stream);
+}
+
+extern "C" int ttsp_attn_nf4_gemv(const void* QKV, const void* QW, const void* KW, float eps, const void* F,
+                                  int ftype, const long long* POS, void* KC, void* VC, int nh, int nkv,
+                                  int max_len, float scale, const uint8_t* W, const uint8_t* A8,
+                                  const float* AMAX, const float* CODE2, float offset, const float* LUT,
+                                  void* Y, const void* R, int epi, int M, int blocksize, int blocksize2,
+                                  int dtype, hipStream_t stream) {
+  if (!QKV || !F || !POS || !KC || !VC || !W || !AMAX || !LUT || !Y) return (int)hipErrorInvalidValue;
+  if (nh <= 0 || nkv <= 0 || nh > ATT_MAX_HEADS || nh % nkv || ftype < 0 || ftype > 2) return (int)hipErrorInvalidValue;
+  if (max_len <= 0 || max_len > ACHUNK || nkv * max_len * (HD / 8) > ATT_PER * GEMV_THREADS)
+    return (int)hipErrorInvalidValue;
+  const bool nested = A8 != nullptr;
+  if (nested && !CODE2) return (int)hipErrorInvalidValue;
+  AttnSrc a;
+  a.QKV = (const uint16_t*)QKV;
+  a.QW = QW ? (const uint16_t*)QW : (const uint16_t*)QKV;
+  a.KW = KW ? (const uint16_t*)KW : (const uint16_t*)QKV;
+  a.F = F;
+  a.POS = POS;
+  a.KC = (uint16_t*)KC;
+  a.VC = (uint16_t*)VC;
+  a.eps = eps;
+  a.scale = scale;
+  a.max_len = max_len;
+  a.hcfg = (uint32_t)nh | ((uint32_t)nkv << 8) | ((uint32_t)(nh / nkv) << 16) | ((uint32_t)ftype << 24) |
+           ((QW ? 1u : 0u) << 28) | ((KW ? 1u : 0u) << 29);
+  const Nf4Mat m{reinterpret_cast<const uint32_t*>(W), A8, AMAX, CODE2, offset};
+  return gemv_launch(QKV, dtype, nullptr, 0.0f, m, nullptr, nested, LUT, Y, R, epi, M, nh * HD, blocksize,
+                     blocksize2, stream, &a);
 }

@@ -1,4 +1,4 @@
-"""One decode position through a transformer block in five or six HIP launches.
+"""One decode position through a transformer block in four to six HIP launches.
 
 Drop-in for the reference's `app/engine/fusedlayer.py` (`decode_block`,
 `install`, `stats`, `HEAD_DIM`, `CHUNK`):
@@ -11,8 +11,11 @@ prologue with the standalone kernel's exact arithmetic (`nf4gemv.
 matmul_fused`), w1/w3 stream through the same waves with the gate in the
 epilogue, and the attention workgroups apply the head norms and rotary to
 QKV themselves (`ttsp_attn_decode_qkv`; a cache longer than one 64-position
-chunk adds a merge launch). The results are bit-identical to the reference's
-ten-launch order (reference: fusedlayer.py:212-269).
+chunk adds a merge launch). With a cache of at most one chunk (the fast
+transformer's), the attention and wo are one launch: every wo workgroup
+computes the small attention itself (`ttsp_attn_nf4_gemv`). The results are
+bit-identical to the reference's ten-launch order (reference:
+fusedlayer.py:212-269).
 
 `qk_rope_kv` does the head norms, rotary and KV-cache write for every head in
 one launch; attention is split-K over CHUNK-position slices of the cache (one
@@ -88,7 +91,7 @@ def decode_block(block, x, freqs_cis, mask, input_pos, *, workspace=None):
     ftype = _lib.dtype_code(freqs_cis.dtype) if freqs_cis is not None else None
     if ftype is None or not freqs_cis.is_contiguous() or freqs_cis.numel() != HEAD_DIM:
         return None
-    a, ff = block.attention, block.feed_forward
+    a = block.attention
     nh, nkv = a.n_head, a.n_local_heads
     max_len = a.kv_cache.k_cache.shape[2]
     nchunk = -(-min(mask.shape[-1], max_len) // CHUNK)
@@ -97,7 +100,7 @@ def decode_block(block, x, freqs_cis, mask, input_pos, *, workspace=None):
     lib = _lib.lib()
     st = _lib.stream()
 
-    an, fn = block.attention_norm, block.ffn_norm
+    an = block.attention_norm
     qkv = nf4gemv.matmul_fused(a.wqkv, x, norm_weight=an.weight, eps=an.eps, out=ws["qkv"])
     if qkv is None:  # the unfused pair: norm, then matmul
         xn = fusedops.rms_norm(x, an.weight, an.eps, out=ws["xn"])
@@ -107,6 +110,9 @@ def decode_block(block, x, freqs_cis, mask, input_pos, *, workspace=None):
     qn = getattr(a, "q_norm", None) if a.attention_qk_norm else None
     kn = getattr(a, "k_norm", None) if a.attention_qk_norm else None
     eps = float(qn.eps if qn is not None and qn.eps is not None else 1e-6)
+    h = _attn_wo(a, qkv, qn, kn, eps, freqs_cis, ftype, input_pos, x, ws, nchunk, dt, st)
+    if h is not None:  # attention and wo (+ residual) in one launch (short caches)
+        return _ffn(block, h, ws, x.shape)
     rc = lib.ttsp_attn_decode_qkv(
         qkv.data_ptr(), _lib.ptr(None if qn is None else qn.weight), _lib.ptr(None if kn is None else kn.weight),
         eps, freqs_cis.data_ptr(), ftype, input_pos.data_ptr(), a.kv_cache.k_cache.data_ptr(),
@@ -116,6 +122,41 @@ def decode_block(block, x, freqs_cis, mask, input_pos, *, workspace=None):
     h = nf4gemv.matmul(a.wo, ws["y"], epi=nf4gemv.EPI_RESIDUAL, operand=x, out=ws["h"])
     if h is None:
         raise RuntimeError("decode_block: a prepared layer declined mid-block")
+    return _ffn(block, h, ws, x.shape)
+
+
+def _attn_wo(a, qkv, qn, kn, eps, freqs_cis, ftype, input_pos, x, ws, nchunk, dt, st):
+    """`ttsp_attn_nf4_gemv`: the attention of a cache of at most one chunk and
+    wo with the residual in one launch (every GEMV workgroup recomputes the
+    small attention), or None where it does not apply (the two-launch form
+    runs; both give the same bits)."""
+    from ttspipe_amd import nf4gemv
+
+    fast = getattr(a.wo, "_nf4_fast", None)
+    nh, nkv = a.n_head, a.n_local_heads
+    max_len = a.kv_cache.k_cache.shape[2]
+    D = x.shape[-1]
+    if fast is None or nchunk != 1 or nh > 8 or max_len > CHUNK or nkv * max_len > 128:
+        return None
+    if fast["K"] != nh * HEAD_DIM or fast["M"] != D or x.numel() != D or not x.is_contiguous():
+        return None
+    h = ws["h"]
+    rc = _lib.lib().ttsp_attn_nf4_gemv(
+        qkv.data_ptr(), _lib.ptr(None if qn is None else qn.weight), _lib.ptr(None if kn is None else kn.weight),
+        eps, freqs_cis.data_ptr(), ftype, input_pos.data_ptr(), a.kv_cache.k_cache.data_ptr(),
+        a.kv_cache.v_cache.data_ptr(), nh, nkv, max_len, float(HEAD_DIM**-0.5),
+        fast["w"], fast["a8"], fast["amax"], fast["code2"], fast["offset"], fast["lut"].data_ptr(),
+        h.data_ptr(), x.data_ptr(), nf4gemv.EPI_RESIDUAL, D, fast["bs"], fast["bs2"], dt, st)
+    _lib.check(rc, "ttsp_attn_nf4_gemv")
+    nf4gemv._stats["fast"] += 1
+    return h
+
+
+def _ffn(block, h, ws, shape):
+    """The block's second half: norm + w1/w3 (SwiGLU) and w2 with the residual."""
+    from ttspipe_amd import fusedops, nf4gemv
+
+    ff, fn = block.feed_forward, block.ffn_norm
     g = nf4gemv.matmul_fused(ff.w1, h, norm_weight=fn.weight, eps=fn.eps, module3=ff.w3, out=ws["g"])
     if g is None:  # the unfused chain: norm, w1, w3 with the gate epilogue
         hn = fusedops.rms_norm(h, fn.weight, fn.eps, out=ws["hn"])
@@ -126,7 +167,7 @@ def decode_block(block, x, freqs_cis, mask, input_pos, *, workspace=None):
     if g is None or out is None:
         raise RuntimeError("decode_block: a prepared layer declined mid-block")
     _stats["fused"] += 1
-    return out.view(x.shape)
+    return out.view(shape)
 
 
 def make_workspace(block, x, nchunk: int, *, with_out: bool = False) -> dict:
