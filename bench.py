@@ -16,7 +16,8 @@ Also reported: the dominant kernel (gate 9728x2560) timed alone with HIP
 events on its stream -> `roofline`; the single fp16 GEMV of the reference's
 CPU-runnable case (plain fp32 absmax) -> `gemv_fp16_plain`; the synthetic
 Dual-AR decode step -> `decode`; and the CPU baseline (the reference's CPU
-NF4 GEMV algorithm restated in C++, on this host's cores) -> `cpu_baseline`.
+NF4 GEMV algorithm restated in C++, on this host's cores) -> `cpu_baseline`,
+with the same Dual-AR frame on the CPU through it -> `cpu_baseline.decode`.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
 """
@@ -330,13 +331,17 @@ def bench_copy(nbytes: int = 64 * 2**20, launches: int = 8):
     return {"bytes_read": nbytes, "bytes_written": nbytes, "sec": sec, "gbs_rw": 2 * nbytes / sec / 1e9}
 
 
-def cpu_baseline(seconds: float = 10.0):
-    """The reference's CPU NF4 GEMV algorithm (restated in C++) on this host."""
+def cpu_baseline(seconds: float = 10.0, decode_frames: int = 3):
+    """The reference's CPU NF4 GEMV algorithm (restated in C++) on this host,
+    and the synthetic Dual-AR frame through the same kernels (`decode`)."""
     try:
         from oracle import cpu_baseline as cb
     except Exception as exc:  # noqa: BLE001
         return {"value": None, "unit": "GB/s", "cores": None, "kind": "port", "sample": f"unavailable: {exc}"}
-    return cb.run(LAYER, seconds=seconds)
+    out = cb.run(LAYER, seconds=seconds)
+    if decode_frames > 0:
+        out["decode"] = cb.run_decode(frames=decode_frames)
+    return out
 
 
 def main() -> int:
@@ -350,6 +355,7 @@ def main() -> int:
     ap.add_argument("--only", choices=["layer", "kernel", "c1", "copy", "decode", "gemm"], default=None,
                     help="run one GPU measurement only (for profiling runs)")
     ap.add_argument("--decode-steps", type=int, default=256, help="greedy frames the decode benchmark times")
+    ap.add_argument("--cpu-decode-frames", type=int, default=3, help="frames the CPU baseline's decode times")
     ap.add_argument("--direct", action="store_true",
                     help="with --only kernel/c1: one launch per weight copy, no graph (counter runs)")
     args = ap.parse_args()
@@ -383,7 +389,7 @@ def main() -> int:
     if args.only is not None:
         print(json.dumps(out))
         return 0
-    cpu = None if args.skip_cpu else cpu_baseline(args.cpu_seconds)
+    cpu = None if args.skip_cpu else cpu_baseline(args.cpu_seconds, 0 if args.skip_decode else args.cpu_decode_frames)
 
     layer, kern, c1, fused = out["layer"], out["kernel"], out["c1"], out["layer_fused"]
     value = fused["step_bytes"] / fused["sec_per_step"] / 1e9

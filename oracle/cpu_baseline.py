@@ -111,3 +111,98 @@ def run(layer_shapes, seconds: float = 10.0, threads: int | None = None) -> dict
                   f"{'AVX512-BF16 kernel' if avx else 'scalar fallback (no AVX512-BF16 on this host)'}; "
                   f"{_cpu_model()}, {os.cpu_count()} logical CPUs",
     }
+
+
+def run_decode(frames: int = 3, threads: int | None = None) -> dict:
+    """One synthetic Dual-AR frame on the CPU (the GPU decode's structure): 36
+    slow blocks at position 2048+, the semantic head, the fast projection, the
+    fast prime (4 blocks at fast position 0), then 9 codebooks of 4 fast
+    blocks + head each, every block through `cpu_decode_block` (the reference
+    CPU path's decode_block structure, nf4cpu.py:479-617) and every linear
+    through the port's AVX512-BF16 GEMV. Random NF4 bytes and bf16 scales,
+    distinct per layer (2 GB, past any last-level cache)."""
+    from ttspipe_amd.dualar import DualARConfig
+
+    cfg = DualARConfig()
+    lib = _lib()
+    threads = threads or len(os.sched_getaffinity(0))
+    u16p, u8p, fp, i64 = ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64
+    lib.cpu_decode_block.argtypes = ([u16p, u16p, i64, i64, i64, i64, u16p, u16p, u16p, u16p, ctypes.c_float]
+                                     + [u8p, u16p] * 4 + [u16p, u16p, u16p, i64, i64, fp, ctypes.c_int])
+    lib.cpu_decode_block.restype = None
+    lib.cpu_argmax_bf16.argtypes = [u16p, i64]
+    lib.cpu_argmax_bf16.restype = i64
+    rng = np.random.default_rng(1)
+    from oracle import oracle as o
+
+    code = o.from_f32(o.NF4_CODE, o.DT_BF16)
+
+    def lin(M, K):
+        return (rng.integers(0, 256, M * K // 2, dtype=np.uint8),
+                (0x3C00 + rng.integers(0, 0x80, M * K // 64, dtype=np.uint16)).astype(np.uint16))
+
+    def vec(n):
+        return (0x3F80 + rng.integers(0, 0x40, n, dtype=np.uint16)).astype(np.uint16)
+
+    def cache(nkv, max_len):
+        r = rng.integers(0, 0x80, nkv * max_len * 128, dtype=np.uint16)
+        return ((r | 0x3F00) ^ (r << 8 & 0x8000)).astype(np.uint16)
+
+    def block(D, nh, nkv, inter, max_len):
+        hd = cfg.head_dim
+        return {"D": D, "nh": nh, "nkv": nkv, "inter": inter, "max_len": max_len,
+                "an": vec(D), "fn": vec(D), "qn": vec(hd), "kn": vec(hd),
+                "qkv": lin((nh + 2 * nkv) * hd, D), "wo": lin(D, nh * hd), "w13": lin(2 * inter, D),
+                "w2": lin(D, inter), "kc": cache(nkv, max_len), "vc": cache(nkv, max_len)}
+
+    slow = [block(cfg.dim, cfg.n_head, cfg.n_local_heads, cfg.intermediate_size, cfg.max_seq_len)
+            for _ in range(cfg.n_layer)]
+    fast = [block(cfg.fast_dim, cfg.fast_n_head, cfg.fast_n_local_heads, cfg.fast_intermediate_size,
+                  cfg.fast_max_len) for _ in range(cfg.fast_n_layer)]
+    head, proj, fhead = lin(cfg.vocab_size, cfg.dim), lin(cfg.fast_dim, cfg.dim), lin(cfg.codebook_size, cfg.fast_dim)
+    freqs = np.stack([np.cos(np.arange(64) * 0.01), np.sin(np.arange(64) * 0.01)], -1).astype(np.float32).ravel()
+    x = vec(cfg.dim)
+    bufs = {D: (np.empty(D, np.uint16), np.empty(D, np.uint16)) for D in (cfg.dim, cfg.fast_dim)}
+    logits = np.empty(max(cfg.vocab_size, cfg.codebook_size), np.uint16)
+    fx = np.empty(cfg.fast_dim, np.uint16)
+
+    def run_block(b, xin, out, pos):
+        p = lambda a: a.ctypes.data  # noqa: E731
+        lib.cpu_decode_block(p(xin), p(out), b["D"], b["nh"], b["nkv"], b["inter"], p(b["an"]), p(b["fn"]),
+                             p(b["qn"]), p(b["kn"]), cfg.norm_eps, p(b["qkv"][0]), p(b["qkv"][1]), p(b["wo"][0]),
+                             p(b["wo"][1]), p(b["w13"][0]), p(b["w13"][1]), p(b["w2"][0]), p(b["w2"][1]), p(code),
+                             p(b["kc"]), p(b["vc"]), pos, b["max_len"], p(freqs), threads)
+
+    def gemv_into(w, xin, M, K, out):
+        lib.cpu_nf4_gemv(xin.ctypes.data, K, w[0].ctypes.data, w[1].ctypes.data, code.ctypes.data, M,
+                         out.ctypes.data, threads, 0)
+
+    def blocks(stack, xin, D, pos):
+        cur = xin
+        for i, blk in enumerate(stack):  # outputs alternate between two buffers
+            out = bufs[D][i % 2]
+            run_block(blk, cur, out, pos)
+            cur = out
+        return cur
+
+    def frame(pos):
+        cur = blocks(slow, x, cfg.dim, pos)
+        gemv_into(head, cur, cfg.vocab_size, cfg.dim, logits)
+        lib.cpu_argmax_bf16(logits.ctypes.data, cfg.vocab_size)
+        gemv_into(proj, cur, cfg.fast_dim, cfg.dim, fx)
+        for cb in range(cfg.num_codebooks):  # the prime at fast position 0, then one step per codebook
+            fcur = blocks(fast, fx, cfg.fast_dim, cb)
+            if cb:
+                gemv_into(fhead, fcur, cfg.codebook_size, cfg.fast_dim, logits)
+                lib.cpu_argmax_bf16(logits.ctypes.data, cfg.codebook_size)
+
+    frame(cfg.prefill_len)  # warm up threads and pages
+    t0 = time.perf_counter()
+    for i in range(frames):
+        frame(cfg.prefill_len + 1 + i)
+    el = time.perf_counter() - t0
+    return {"ms_per_step": round(el / frames * 1e3, 2), "frames": frames, "cores": threads,
+            "sample": f"{frames} synthetic Dual-AR frames after one warm-up (36 slow blocks at positions 2049+, "
+                      f"semantic head, fast projection, fast prime + 9 codebooks of 4 fast blocks and head), "
+                      f"distinct random NF4 weights per layer (dense bf16 absmax), "
+                      f"{'AVX512-BF16 GEMV' if lib.cpu_has_avx512bf16() else 'scalar GEMV'}"}
