@@ -322,3 +322,28 @@ def test_fused_form_declines_what_it_cannot_serve(nf4):
     assert nf4.matmul_fused(a, x, module3=b) is None  # shapes differ
     assert nf4.matmul_fused(a, torch.randn(2, 2560, device="cuda", dtype=torch.bfloat16)) is None  # two rows
     assert nf4.matmul_fused(a, x, norm_weight=torch.ones(2560, device="cuda", dtype=torch.float16)) is None
+
+
+@pytest.mark.parametrize("nested", [True, False])
+def test_prequantised_checkpoint_serves_the_same_bits(nf4, nested):
+    """A layer saved in bitsandbytes' serialised layout, read back with the safe
+    loader and loaded into a fresh Linear4bit on the GPU, computes bit for bit
+    what the original does (GEMV and GEMM paths)."""
+    import io
+
+    from ttspipe_amd import quant
+
+    M, K, dtype = 1536, 1024, torch.bfloat16
+    layer = random_layer(M, K, nested, seed=5)
+    src = to_linear(layer, dtype)
+    buf = io.BytesIO()
+    torch.save({k: v.cpu() for k, v in quant.quant_state_to_dict(src.weight.data, src.weight.quant_state).items()},
+               buf)
+    buf.seek(0)
+    sd = torch.load(buf, weights_only=True)
+    dst = quant.Linear4bit(K, M, bias=False, compute_dtype=dtype, compress_statistics=nested, device="cuda")
+    quant.load_nf4_state_dict(dst, sd)
+    assert dst.weight.device.type == "cuda"
+    for rows in (1, 24):
+        x = from_bits(randn_bits(rows * K, dtype, seed=rows), dtype).view(rows, K)
+        assert torch.equal(src(x).view(torch.int16), dst(x).view(torch.int16))

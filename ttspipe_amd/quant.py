@@ -210,6 +210,7 @@ class Linear4bit(torch.nn.Module):
         self.quant_type = quant_type
         self.compress_statistics = compress_statistics
         self.blocksize = blocksize
+        self.device = torch.device(device) if device is not None else None  # where loaded weights go
         self.weight = None
         self.bias = (torch.nn.Parameter(torch.zeros(out_features, device=device,
                                                     dtype=compute_dtype or torch.float16),
@@ -237,3 +238,132 @@ class Linear4bit(torch.nn.Module):
         out = torch.nn.functional.linear(x.to(dt), w.view(self.out_features, self.in_features),
                                          None if self.bias is None else self.bias.to(dt))
         return out.to(x.dtype)
+
+
+# --------------------------------------------------------------------------
+# bitsandbytes' serialised form of a 4-bit weight (what a prequantised
+# checkpoint such as the reference's NF4 `model.pth` holds, loaded by the
+# fork through bitsandbytes' Params4bit / QuantState): for a Linear4bit at
+# `prefix`,
+#   prefix + "weight"                       packed uint8 codes [n/2, 1]
+#   prefix + "weight.absmax"                fp32 [nblocks], or uint8 when nested
+#   prefix + "weight.quant_map"             the 16 NF4 code points, fp32
+#   prefix + "weight.nested_absmax"         fp32 [nblocks / bs2]          (nested)
+#   prefix + "weight.nested_quant_map"      the 256-point dynamic map     (nested)
+#   prefix + "weight.quant_state.bitsandbytes__nf4"
+#       uint8 bytes of a JSON object: quant_type, blocksize, dtype, shape and,
+#       nested, nested_blocksize, nested_dtype, nested_offset.
+
+_PACKED_KEY = "quant_state.bitsandbytes__"
+
+
+def _dtype_name(dt) -> str:
+    return str(dt).replace("torch.", "")
+
+
+def _dtype_from(name: str):
+    dt = getattr(torch, name, None)
+    if not isinstance(dt, torch.dtype):
+        raise ValueError(f"unknown dtype {name!r} in a 4-bit weight's state")
+    return dt
+
+
+def quant_state_to_dict(packed, state) -> dict:
+    """The tensors bitsandbytes stores for one 4-bit weight, keyed relative to
+    the module prefix ("weight", "weight.absmax", ...)."""
+    import json
+
+    meta = {"quant_type": state.quant_type, "blocksize": int(state.blocksize),
+            "dtype": _dtype_name(state.dtype or torch.float16), "shape": list(state.shape)}
+    out = {"weight": packed, "weight.absmax": state.absmax, "weight.quant_map": state.code}
+    if state.nested:
+        out["weight.nested_absmax"] = state.state2.absmax
+        out["weight.nested_quant_map"] = state.state2.code
+        meta.update({"nested_blocksize": int(state.state2.blocksize),
+                     "nested_dtype": _dtype_name(state.state2.dtype or torch.float32),
+                     "nested_offset": float(state.offset)})
+    blob = json.dumps(meta).encode("utf-8")
+    out["weight." + _PACKED_KEY + state.quant_type] = torch.tensor(list(blob), dtype=torch.uint8)
+    return out
+
+
+def quant_state_from_dict(tensors: dict, device=None):
+    """(packed, QuantState) from the tensors `quant_state_to_dict` names (the
+    bitsandbytes layout). Raises ValueError on a malformed entry."""
+    import json
+
+    packed_key = [k for k in tensors if k.startswith("weight." + _PACKED_KEY)]
+    if len(packed_key) != 1:
+        raise ValueError("a 4-bit weight needs exactly one packed quant_state entry")
+    qt = packed_key[0][len("weight." + _PACKED_KEY):]
+    if qt != "nf4":
+        raise ValueError(f"quant_type {qt!r} is not served (nf4 only)")
+    meta = json.loads(bytes(tensors[packed_key[0]].to("cpu", torch.uint8).tolist()).decode("utf-8"))
+    dev = device if device is not None else tensors["weight"].device
+    shape = tuple(int(v) for v in meta["shape"])
+    code = tensors["weight.quant_map"].to(dev, torch.float32)
+    packed = tensors["weight"].to(dev)
+    if packed.dtype != torch.uint8 or packed.numel() * 2 != math.prod(shape):
+        raise ValueError("packed codes do not match the weight's shape")
+    nested = "weight.nested_absmax" in tensors
+    state2 = offset = None
+    absmax = tensors["weight.absmax"].to(dev)
+    if nested:
+        state2 = QuantState(absmax=tensors["weight.nested_absmax"].to(dev, torch.float32),
+                            shape=(absmax.numel(),), code=tensors["weight.nested_quant_map"].to(dev, torch.float32),
+                            blocksize=int(meta["nested_blocksize"]), quant_type="dynamic",
+                            dtype=_dtype_from(meta.get("nested_dtype", "float32")))
+        offset = torch.tensor(float(meta["nested_offset"]), device=dev)
+    state = QuantState(absmax=absmax, shape=shape, code=code, blocksize=int(meta["blocksize"]), quant_type=qt,
+                       dtype=_dtype_from(meta["dtype"]), offset=offset, state2=state2)
+    return packed.view(-1, 1), state
+
+
+def nf4_state_dict(model) -> dict:
+    """`model.state_dict()` with every Linear4bit's weight in bitsandbytes'
+    serialised form (the layout of a prequantised checkpoint)."""
+    sd = {}
+    lin = {name: m for name, m in model.named_modules() if isinstance(m, Linear4bit)}
+    for k, v in model.state_dict().items():
+        owner = k.rsplit(".", 1)[0] if "." in k else ""
+        if owner in lin and k.endswith("weight"):
+            continue
+        sd[k] = v
+    for name, m in lin.items():
+        prefix = f"{name}." if name else ""
+        for k, v in quant_state_to_dict(m.weight.data, m.weight.quant_state).items():
+            sd[prefix + k] = v
+    return sd
+
+
+def load_nf4_state_dict(model, state_dict: dict, strict: bool = True):
+    """Load a prequantised checkpoint's state dict (bitsandbytes' 4-bit layout)
+    into `model`, whose quantised linears are `Linear4bit`s (no bitsandbytes
+    needed). A layer's tensors go to the device it was built on (else where its
+    current weight lives, else where the state dict's tensors are). Every other
+    entry goes through `load_state_dict`. Returns the (missing, unexpected) keys
+    of that remainder. Read a checkpoint file with `torch.load(path,
+    weights_only=True)` first."""
+    lin = {name: m for name, m in model.named_modules() if isinstance(m, Linear4bit)}
+    used = set()
+    for name, m in lin.items():
+        prefix = f"{name}." if name else ""
+        sub = {k[len(prefix):]: v for k, v in state_dict.items()
+               if k == prefix + "weight" or k.startswith(prefix + "weight.")}
+        if "weight" not in sub:
+            if strict:
+                raise KeyError(f"{prefix}weight missing from the state dict")
+            continue
+        dev = m.device if getattr(m, "device", None) is not None else (
+            m.weight.device if m.weight is not None else None)
+        packed, state = quant_state_from_dict(sub, device=dev)
+        if tuple(state.shape) != (m.out_features, m.in_features):
+            raise ValueError(f"{prefix}weight: shape {state.shape} for a {m.out_features}x{m.in_features} layer")
+        m.set_quantized(packed, state)
+        used.update(prefix + k for k in sub)
+    rest = {k: v for k, v in state_dict.items() if k not in used}
+    missing, unexpected = model.load_state_dict(rest, strict=False)
+    missing = [k for k in missing if not any(k == (f"{n}." if n else "") + "weight" for n in lin)]
+    if strict and (missing or unexpected):
+        raise KeyError(f"missing {missing}, unexpected {unexpected}")
+    return missing, unexpected
