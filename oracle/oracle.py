@@ -246,3 +246,30 @@ def argmax(X, dt) -> int:
     lib()
     X = _c(X)
     return int(_lib.orc_argmax(_p(X), X.size, dt))
+
+
+def sample_topk_ref(logits, temperature: float, top_p: float, top_k: int, u):
+    """The fork's top-k / top-p draw as the reference's fused sampler computes
+    it (app/engine/fusedsample.py:55-223), in float64: the top_k largest
+    logits (ties by lowest index) sorted descending; the first and every one
+    whose inclusive cumulative probability under softmax(logits) is <= top_p
+    kept; returns (index, kept indices, cumulative probabilities, scores) with
+    index = argmax over the kept of l / max(temperature, 1e-5) -
+    log(-log(max(u, 1e-20))), ties to the lowest index."""
+    l = np.asarray(logits, np.float64)
+    V = l.size
+    k = int(min(max(int(top_k), 1), 64, V))
+    order = np.lexsort((np.arange(V), -l))[:k]  # value descending, then index ascending
+    m = l.max()
+    p = np.exp(l[order] - m) / np.exp(l - m).sum()
+    c = np.cumsum(p)
+    keep = np.zeros(k, bool)
+    keep[0] = True
+    keep[1:] = c[1:] <= top_p
+    kept = order[keep]
+    uu = np.maximum(np.asarray(u, np.float64)[kept], 1e-20)
+    scores = l[kept] / max(float(temperature), 1e-5) - np.log(-np.log(uu))
+    mx = scores.max()
+    cand = kept[scores == mx]
+    best = int(cand.min())
+    return best, kept, c, scores

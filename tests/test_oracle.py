@@ -360,3 +360,39 @@ def test_embed_sum_and_argmax(orc):
     assert np.array_equal(got, expect)
     x = o.from_f32(np.float32([1, 5, 3, 5, -2]), o.DT_F16)
     assert orc.argmax(x, o.DT_F16) == 1
+
+
+# ------------------------------------------------------------------ sampler
+
+
+def test_sampler_ref_closed_forms():
+    """top_k = 1 and top_p = 0 keep only the largest logit (first index among
+    ties); equal uniforms make the draw the largest kept logit."""
+    rng = np.random.default_rng(0)
+    l = rng.standard_normal(300)
+    l[17] = l[200] = l.max() + 1.0
+    u = rng.random(300)
+    assert o.sample_topk_ref(l, 0.7, 0.9, 1, u)[0] == 17
+    assert o.sample_topk_ref(l, 0.7, 0.0, 40, u)[0] == 17
+    best, kept, c, _ = o.sample_topk_ref(l, 1.0, 1.0, 64, np.full(300, 0.5))
+    assert best == 17 and kept.size == 64 and np.all(np.diff(l[kept]) <= 0)
+
+
+def test_sampler_ref_draws_from_the_truncated_tempered_softmax():
+    """Gumbel-max over the kept set with fresh uniforms: empirical frequencies
+    match softmax(l / T) restricted to the kept candidates (a dropped
+    temperature or a wrong cut fails this)."""
+    rng = np.random.default_rng(1)
+    l = np.array([2.0, 1.5, 1.0, 0.5, 0.0, -0.5, -1.0, -3.0])
+    T, top_p, top_k, n = 0.8, 0.93, 6, 40000
+    counts = np.zeros(l.size)
+    for _ in range(n):
+        counts[o.sample_topk_ref(l, T, top_p, top_k, rng.random(l.size))[0]] += 1
+    _, kept, _, _ = o.sample_topk_ref(l, T, top_p, top_k, np.full(l.size, 0.5))
+    q = np.zeros(l.size)
+    q[kept] = np.exp(l[kept] / T)
+    q /= q.sum()
+    assert np.abs(counts / n - q).max() < 0.01
+    # the cut: softmax(l) cumulative <= top_p, first always kept
+    p = np.exp(l - l.max()) / np.exp(l - l.max()).sum()
+    assert set(kept) == {i for i in range(top_k) if i == 0 or np.cumsum(p)[i] <= top_p}

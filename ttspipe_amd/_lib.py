@@ -45,6 +45,8 @@ SIGNATURES: dict[str, list] = {
     "ttsp_attn_nf4_gemv": [_vp, _vp, _vp, _f, _vp, _i, _vp, _vp, _vp, _i, _i, _i, _f, _vp, _vp, _vp, _vp, _f,
                            _vp, _vp, _vp, _i, _i, _i, _i, _i, _vp],
     "ttsp_attn_chunk": [],
+    "ttsp_sample_topk": [_vp, _i, _i, _vp, _vp, _vp, _vp, _vp, _vp],
+    "ttsp_sample_max_top_k": [],
     "ttsp_embed_sum": [_vp, _vp, _i, _i, _i, _vp, _i, _vp],
     "ttsp_argmax": [_vp, _i, _i, _vp, _vp],
     "ttsp_synth_fill": [_vp, _ll, ctypes.c_ulonglong, _i, _f, _f, _vp],
