@@ -158,6 +158,28 @@ int ttsp_sample_max_top_k(void);
  * app/engine/fusedlayer.py:40. */
 int ttsp_attn_chunk(void);
 
+/* Grouped-query attention of S new positions at once (a prefill): for query
+ * i and head hd (kv head hd / (nh / nkv)),
+ *   Y[i][hd][:] = softmax_j(Q[i][hd] . K[j] * scale, over j < L with
+ *                 mask[i][j] != 0) . V[j].
+ * Q element (i, hd, d) at Q + i*q_seq_stride + hd*q_head_stride + d, K/V
+ * (j, kv, d) likewise with their strides (elements; all multiples of 8),
+ * mask one byte per (i, j) at mask + i*mask_row_stride + j (a multiple of
+ * 16, >= L), Y [S][nh][128] contiguous; head dim 128, fp16 or bf16 (dtype),
+ * nh / nkv <= ttsp_prefill_max_groups(), S <= 2^20, 16-byte aligned bases;
+ * other values return hipErrorInvalidValue. A row with no allowed key gives
+ * NaN (0/0), as a softmax over all -inf. Replaces: decode_attention for
+ * S <= 64 and scaled_dot_product_attention(attn_mask=mask, enable_gqa=True)
+ * beyond, app/engine/fastpath.py:133-174 and 244-268. */
+int ttsp_prefill_attention(const void* Q, long long q_seq_stride, long long q_head_stride,
+                           const void* K, long long k_seq_stride, long long k_head_stride,
+                           const void* V, long long v_seq_stride, long long v_head_stride,
+                           const void* mask, long long mask_row_stride, void* Y, int S, int nh,
+                           int nkv, int L, float scale, int dtype, hipStream_t stream);
+
+/* Largest query heads per kv head ttsp_prefill_attention takes (8). */
+int ttsp_prefill_max_groups(void);
+
 /* out[d] = round(sum_{c < ntok} E[(c*vocab + tok[c]) * D + d]) (tok int32 on the
  * device, clamped into [0, vocab)). Replaces: the codebook-embedding lookup of
  * a decode step (app/engine/graphs.py:124-131 via the fork's _fast_embed /

@@ -1,0 +1,214 @@
+"""Prefill attention (`fastpath.prefill_attention`, one HIP launch) against
+fp64 attention on the CPU and against the reference's formula
+(`fastpath.decode_attention`, app/engine/fastpath.py:133-174) on the GPU.
+
+Bar: a floating-point kernel (scores on the matrix cores, probabilities
+rounded to the activation type before the second product), so within 5e-3
+of fp64 in the reference's measure, max |got - ref| / max |ref| (the bar of
+the decode attention, tests/test_nf4gemv.py:224-242); NaN exactly where the
+reference's softmax gives NaN (a row with no allowed key).
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from tests.conftest import relative_error
+
+pytestmark = pytest.mark.gpu
+
+TOL = 5e-3
+D = 128
+
+
+def _setup(S, prefix, nh, nkv, dtype, max_len=None, seed=0):
+    """q as `llama.Attention` hands it over (a transposed view of the wqkv
+    output), k/v as the KV cache sliced to the live length L = prefix + S, and
+    the fork's mask: rows input_pos of tril(max_len), cut to L."""
+    L = prefix + S
+    max_len = max_len or ((L + 255) // 256) * 256
+    g = torch.Generator().manual_seed(seed)
+    total = (nh + 2 * nkv) * D
+    qkv = torch.randn(1, S, total, generator=g).to(dtype).cuda()
+    q = qkv[..., : nh * D].view(1, S, nh, D).transpose(1, 2)
+    kc = torch.zeros(1, nkv, max_len, D, dtype=dtype, device="cuda")
+    vc = torch.zeros_like(kc)
+    kc[:, :, :L] = torch.randn(1, nkv, L, D, generator=g).to(dtype).cuda()
+    vc[:, :, :L] = torch.randn(1, nkv, L, D, generator=g).to(dtype).cuda()
+    causal = torch.tril(torch.ones(max_len, max_len, dtype=torch.bool, device="cuda"))
+    pos = torch.arange(prefix, L, device="cuda")
+    mask = causal[None, None, pos, :max_len][..., :L]
+    return q, kc[:, :, :L], vc[:, :, :L], mask
+
+
+def _fp64(q, k, v, mask):
+    """Exact attention: q (1, nh, S, D), k/v (1, nkv, L, D), mask (1, 1, S, L)."""
+    qn = q[0].double().cpu().numpy()
+    kn, vn = k[0].double().cpu().numpy(), v[0].double().cpu().numpy()
+    m = mask[0, 0].cpu().numpy()
+    nh, nkv = qn.shape[0], kn.shape[0]
+    out = np.empty_like(qn)
+    for hd in range(nh):
+        kv = hd // (nh // nkv)
+        s = qn[hd] @ kn[kv].T * D**-0.5
+        s = np.where(m, s, -np.inf)
+        with np.errstate(invalid="ignore"):
+            p = np.exp(s - s.max(axis=1, keepdims=True))
+            out[hd] = (p / p.sum(axis=1, keepdims=True)) @ vn[kv]
+    return out
+
+
+def _run(q, k, v, mask, nh, nkv):
+    from ttspipe_amd import fastpath
+
+    before = fastpath.stats()["prefill_attn"]
+    y = fastpath.prefill_attention(q, k, v, mask, nh, nkv, D)
+    assert y is not None, "declined"
+    assert fastpath.stats()["prefill_attn"] == before + 1
+    assert y.shape == q.shape and y.dtype == q.dtype
+    assert y.transpose(1, 2).is_contiguous()
+    return y
+
+
+CASES = [  # (S, prefix, nh, nkv)
+    (512, 0, 32, 8),      # the 512-token prompt prefill of the 4B-dim layer
+    (512, 1536, 32, 8),   # the same after a cached prefix
+    (64, 0, 32, 8),       # the reference's largest decode_attention prefill
+    (7, 0, 4, 2),         # the test block of the reference (4 q / 2 kv heads)
+    (33, 100, 8, 2),      # ragged: S and L off every tile size
+    (1, 300, 32, 8),      # one position (a declined decode step)
+    (100, 0, 16, 16),     # one query head per kv head
+    (65, 5, 8, 1),        # eight query heads per kv head
+    (200, 2900, 8, 2),    # the fast transformer's head shape over a long cache
+]
+
+
+@pytest.mark.parametrize("S,prefix,nh,nkv", CASES)
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_prefill_attention_matches_fp64_and_the_reference_formula(S, prefix, nh, nkv, dtype):
+    from ttspipe_amd.fastpath import decode_attention
+
+    q, k, v, mask = _setup(S, prefix, nh, nkv, dtype, seed=S + prefix + nh)
+    y = _run(q, k, v, mask, nh, nkv)
+    exact = _fp64(q, k, v, mask)
+    got = y[0].float().cpu().numpy()
+    assert np.isfinite(got).all()
+    assert relative_error(got, exact) < TOL
+    theirs = decode_attention(q, k, v, mask, nh, nkv, D)[0].float().cpu().numpy()
+    assert relative_error(got, theirs) < TOL
+
+
+def test_arbitrary_mask_and_rows_with_no_key():
+    """Any boolean mask (not only causal), including rows that allow no key:
+    NaN there, as the reference's softmax; every other row exact to the bar."""
+    S, L, nh, nkv = 70, 90, 8, 2
+    q, k, v, _ = _setup(S, L - S, nh, nkv, torch.bfloat16, seed=5)
+    g = torch.Generator().manual_seed(9)
+    store = torch.rand(S, 96, generator=g) < 0.3  # row stride 96: 16-byte rows, cut to L
+    store[3] = False
+    store[40, :] = False
+    store[40, 89] = True  # only the last key
+    mask = store.cuda()[None, None, :, :L]
+    y = _run(q, k, v, mask, nh, nkv)[0].float().cpu().numpy()
+    exact = _fp64(q, k, v, mask)
+    assert np.isnan(y[:, 3]).all()
+    keep = [i for i in range(S) if i != 3]
+    assert np.isfinite(y[:, keep]).all()
+    assert relative_error(y[:, keep], exact[:, keep]) < TOL
+
+
+def test_declines_what_it_does_not_take():
+    from ttspipe_amd import fastpath
+
+    q, k, v, mask = _setup(40, 8, 8, 2, torch.bfloat16)
+    before = fastpath.stats()["prefill_declined"]
+    assert fastpath.prefill_attention(q.float(), k.float(), v.float(), mask, 8, 2, D) is None
+    assert fastpath.prefill_attention(q, k, v, None, 8, 2, D) is None
+    assert fastpath.prefill_attention(q[..., :64], k[..., :64], v[..., :64], mask, 8, 2, 64) is None
+    loose = mask.contiguous()[..., :47].contiguous()  # 48 keys cut to 47: row stride 47
+    assert fastpath.prefill_attention(q, k[:, :, :47], v[:, :, :47], loose, 8, 2, D) is None
+    q16, k16, v16, m16 = _setup(40, 8, 32, 2, torch.bfloat16)  # 16 query heads per kv head
+    assert fastpath.prefill_attention(q16, k16, v16, m16, 32, 2, D) is None
+    assert fastpath.stats()["prefill_declined"] == before + 5
+
+
+def test_rejected_arguments_return_an_error():
+    from ttspipe_amd import _lib
+
+    hip, st = _lib.load(), _lib.stream()
+    buf = torch.zeros(1 << 16, dtype=torch.bfloat16, device="cuda")
+    p = buf.data_ptr()
+    ok = dict(S=4, nh=8, nkv=2, L=16)
+    bad = [dict(ok, nh=7), dict(ok, nh=32, nkv=2), dict(ok, S=0), dict(ok, L=0), dict(ok, L=100)]
+    for a in bad:  # L=100 exceeds the mask row stride of 64
+        rc = hip.ttsp_prefill_attention(p, 1024, 128, p, 256, 4096, p, 256, 4096, p, 64, p, a["S"], a["nh"],
+                                        a["nkv"], a["L"], 0.088, 1, st)
+        assert rc != 0, a
+    rc = hip.ttsp_prefill_attention(p + 2, 1024, 128, p, 256, 4096, p, 256, 4096, p, 64, p, 4, 8, 2, 16, 0.088,
+                                    1, st)
+    assert rc != 0  # misaligned Q
+    rc = hip.ttsp_prefill_attention(p, 1024, 128, p, 256, 4096, p, 256, 4096, p, 40, p, 4, 8, 2, 16, 0.088, 1,
+                                    st)
+    assert rc != 0  # mask rows not 16-byte aligned
+    torch.cuda.synchronize()
+
+
+def test_captured_in_a_graph_replays_identically():
+    from ttspipe_amd import fastpath
+
+    q, k, v, mask = _setup(96, 40, 8, 2, torch.bfloat16, seed=3)
+    out = torch.empty(1, 96, 8 * D, dtype=torch.bfloat16, device="cuda")
+    eager = fastpath.prefill_attention(q, k, v, mask, 8, 2, D).clone()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        fastpath.prefill_attention(q, k, v, mask, 8, 2, D, out=out)
+    for _ in range(3):
+        out.zero_()
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out.view(1, 96, 8, D).transpose(1, 2), eager)
+
+
+def test_attention_forward_takes_the_kernel_for_a_prefill():
+    """`llama.Attention.forward` over 40 new positions after 24 cached ones:
+    the HIP prefill attention runs, and the layer output (after wo) agrees
+    with the same layer run through the reference's formula."""
+    from ttspipe_amd import fastpath
+    from ttspipe_amd.llama import Attention, BaseModelArgs, KVCache, precompute_freqs_cis
+    from tests.nf4data import random_layer, to_linear
+
+    torch.manual_seed(0)
+    args = BaseModelArgs(dim=512, n_head=4, n_local_heads=2, head_dim=128, intermediate_size=1024,
+                         attention_qk_norm=True)
+    att = Attention(args, dtype=torch.bfloat16, device="cuda")
+    att.wqkv = to_linear(random_layer(8 * 128, 512, True, seed=1), torch.bfloat16)
+    att.wo = to_linear(random_layer(512, 4 * 128, True, seed=2), torch.bfloat16)
+    max_len = 128
+    att.kv_cache = KVCache(1, max_len, 2, 128, dtype=torch.bfloat16, device="cuda")
+    att.kv_cache.k_cache.normal_()
+    att.kv_cache.v_cache.normal_()
+    freqs = precompute_freqs_cis(max_len, 128, 1e6).cuda()
+    pos = torch.arange(24, 64, device="cuda")
+    causal = torch.tril(torch.ones(max_len, max_len, dtype=torch.bool, device="cuda"))
+    mask = causal[None, None, pos][..., :64]
+    x = torch.randn(1, 40, 512, dtype=torch.bfloat16, device="cuda")
+    saved = (att.kv_cache.k_cache.clone(), att.kv_cache.v_cache.clone())
+    before = fastpath.stats()["prefill_attn"]
+    ours = att(x, freqs[pos], mask, pos)
+    assert fastpath.stats()["prefill_attn"] == before + 1
+    att.kv_cache.k_cache.copy_(saved[0])
+    att.kv_cache.v_cache.copy_(saved[1])
+    orig = fastpath.prefill_attention
+    fastpath.prefill_attention = lambda *a, **kw: None
+    try:
+        theirs = att(x, freqs[pos], mask, pos)
+    finally:
+        fastpath.prefill_attention = orig
+    # the layer-level bar of the reference's prefill block test, rel-norm < 2e-2
+    # (tests/test_nf4cpu.py:175-191): the attention outputs differ by bf16
+    # roundings, which wo then mixes
+    rel = ((ours.float() - theirs.float()).norm() / theirs.float().norm()).item()
+    assert rel < 2e-2

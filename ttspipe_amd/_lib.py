@@ -45,6 +45,9 @@ SIGNATURES: dict[str, list] = {
     "ttsp_attn_nf4_gemv": [_vp, _vp, _vp, _f, _vp, _i, _vp, _vp, _vp, _i, _i, _i, _f, _vp, _vp, _vp, _vp, _f,
                            _vp, _vp, _vp, _i, _i, _i, _i, _i, _vp],
     "ttsp_attn_chunk": [],
+    "ttsp_prefill_attention": [_vp, _ll, _ll, _vp, _ll, _ll, _vp, _ll, _ll, _vp, _ll, _vp, _i, _i, _i, _i, _f, _i,
+                               _vp],
+    "ttsp_prefill_max_groups": [],
     "ttsp_sample_topk": [_vp, _i, _i, _vp, _vp, _vp, _vp, _vp, _vp],
     "ttsp_sample_max_top_k": [],
     "ttsp_embed_sum": [_vp, _vp, _i, _i, _i, _vp, _i, _vp],

@@ -1,0 +1,467 @@
+// Grouped-query attention over a run of new positions (a prefill), flash
+// style on the matrix cores. It computes what the reference computes for
+// S > 1 queries with a boolean mask (app/engine/fastpath.py:133-174 for
+// S <= 64 and torch's scaled_dot_product_attention with attn_mask beyond,
+// fastpath.py:244-268): softmax over the keys the mask allows of
+// q . k * scale, times v, query head h reading kv head h / (nh / nkv).
+//
+// Workgroup = (kv head kh, block of 32 queries): one wave per query head of
+// the group, times NS key splits (split s takes key blocks s, s + NS, ...;
+// the splits merge through LDS at the end). Keys go through LDS in blocks of
+// 32: the K rows as they are, V transposed (dims x keys) and the 32 x 32
+// mask tile. Each wave computes the transposed score tile S^T = K Q^T (32
+// keys x 32 queries, 8 MFMA 32x32x16 over the 128 dims; Q stays in
+// registers), so one lane holds 16 keys of one query and a query's online
+// softmax needs only its own lane and lane ^ 32. P^T then feeds
+// O^T += V^T P^T straight from registers: the V^T fragments are read in the
+// key order the score layout gives P^T, so no transpose of P goes through
+// LDS. Scores, running max and sum are fp32 (in log2 units: the scale and
+// log2 e fold into one multiply-add before the hardware exp2);
+// probabilities are rounded to the activation type for the matrix core; O
+// is divided by the sum once at the end.
+//
+// Staging is a two-deep pipeline: block group t + 2 is loaded into registers
+// (buffer loads, never under a branch, so the waits count them exactly)
+// while group t is computed, and group t + 1 is written to the other LDS
+// buffer after it. A group whose mask tile allows every key is flagged while
+// it is staged, and skips the per-key masking. A first pass over the
+// workgroup's 32 mask rows finds the last key any of them may see, so a
+// causal mask costs only the blocks on and below the diagonal.
+//
+// MFMA 32x32x16 layout: lane l supplies row (l % 32) of A and column (l % 32)
+// of B, each as 8 consecutive k at 8 * (l / 32) (any k permutation both
+// operands agree on is fine); accumulator r of lane l is
+// D[8*(r/4) + 4*(l/32) + r%4][l % 32].
+#include "attn_common.h"
+
+namespace ttsp {
+
+typedef __bf16 pa_bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 pa_f16x8 __attribute__((ext_vector_type(8)));
+typedef float pa_f32x16 __attribute__((ext_vector_type(16)));
+
+constexpr int PA_QB = 32;            // queries per workgroup
+constexpr int PA_KB = 32;            // keys per block
+constexpr int PA_KROW = HD + 8;      // K tile row stride (elements): 272 B
+constexpr int PA_VROW = PA_KB + 8;   // V^T tile row stride (elements): 80 B
+constexpr int PA_MROW = PA_KB + 16;  // mask tile row stride (bytes)
+constexpr int PA_MAX_GROUPS = 8;
+#define PA_SPLITS(G) ((G) == 1 || (G) == 2 || (G) == 4 ? 2 : 1)
+
+template <int DT>
+__device__ __forceinline__ pa_f32x16 pa_mfma(u32x4 a, u32x4 b, pa_f32x16 c) {
+  if constexpr (DT == DT_BF16)
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(pa_bf16x8, a),
+                                                   __builtin_bit_cast(pa_bf16x8, b), c, 0, 0, 0);
+  else
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(pa_f16x8, a),
+                                                  __builtin_bit_cast(pa_f16x8, b), c, 0, 0, 0);
+}
+
+constexpr float PA_LOG2E = 1.4426950408889634f;
+
+__device__ __forceinline__ float pa_exp2(float x) { return __builtin_amdgcn_exp2f(x); }  // -inf -> 0
+
+// two fp32 values rounded to nearest-even into a packed pair of DT (the
+// hardware conversion: one instruction for the pair on gfx950)
+template <int DT>
+__device__ __forceinline__ uint32_t pa_pack(float lo, float hi) {
+  typedef float f32x2 __attribute__((ext_vector_type(2)));
+  if constexpr (DT == DT_BF16) {
+    typedef __bf16 b16x2 __attribute__((ext_vector_type(2)));
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){lo, hi}, b16x2));
+  } else {
+    typedef _Float16 h16x2 __attribute__((ext_vector_type(2)));
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){lo, hi}, h16x2));
+  }
+}
+
+// A raw buffer over [base, base + bytes): 32-bit byte offsets, and loads past
+// the end return zeros instead of touching memory.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t pa_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+}
+__device__ __forceinline__ u32x4 pa_ld16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
+}
+
+// Mask bytes past column L cleared, for the 16 bytes from column c; applied
+// where the value is used, so the load's wait is not pulled forward.
+__device__ __forceinline__ u32x4 pa_mask_tail(u32x4 v, int c, int L) {
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {
+    const int valid = L - c - 4 * w;  // bytes of this word before L
+    v[w] &= valid >= 4 ? 0xffffffffu : valid <= 0 ? 0u : (1u << (8 * valid)) - 1u;
+  }
+  return v;
+}
+// whether all 16 bytes are nonzero
+__device__ __forceinline__ bool pa_all_set(u32x4 v) {
+  uint32_t z = 0;
+#pragma unroll
+  for (int w = 0; w < 4; ++w) z |= (v[w] - 0x01010101u) & ~v[w] & 0x80808080u;
+  return z == 0;
+}
+
+struct PrefillArgs {
+  const uint16_t* Q;   // [S][nh][128] via q_ss / q_sh
+  const uint16_t* K;   // [L][nkv][128] via k_ss / k_sh
+  const uint16_t* V;   // via v_ss / v_sh
+  const uint8_t* M;    // [S][L] bytes (nonzero: allowed), row stride m_ss
+  uint16_t* Y;         // [S][nh][128], contiguous
+  long long q_ss, q_sh;
+  int k_ss, k_sh, v_ss, v_sh, m_ss;  // elements (bytes for the mask); the host bounds them
+  int S, nh, nkv, L;
+  float scale2;  // scale * log2(e): scores in log2 units
+};
+
+// LDS of one staged key block: K rows, V^T, mask tile (bytes)
+constexpr int PA_KT = PA_KB * PA_KROW * 2;
+constexpr int PA_VT = HD * PA_VROW * 2;
+constexpr int PA_MT = PA_QB * PA_MROW;
+constexpr int PA_BLK = PA_KT + PA_VT + PA_MT;
+
+template <int DT, int G, int NS>
+__global__ __launch_bounds__(64 * G * NS) void prefill_attn_kernel(const PrefillArgs a) {
+  constexpr int NT = 64 * G * NS, NW = NT / 64;
+  constexpr int NKP = NS * PA_KB * (HD / 8), NVP = NS * (PA_KB / 2) * (HD / 8), NMP = NS * PA_QB * 2;
+  constexpr int KPT = (NKP + NT - 1) / NT, VPT = (NVP + NT - 1) / NT, MPT = (NMP + NT - 1) / NT;
+  constexpr int STAGE = 2 * NS * PA_BLK;
+  constexpr int MERGE = NS > 1 ? G * 66 * 64 * 4 : 0;  // split 1's o (64 floats), m, l per lane
+  __shared__ __align__(16) uint8_t lds[STAGE > MERGE ? STAGE : MERGE];
+  __shared__ int wmax[NW];  // the mask scan's per-wave result
+  __shared__ int full[3];   // per block group (mod 3): every key of its mask tiles allowed
+  const int kh = blockIdx.x, q0 = blockIdx.y * PA_QB;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int gw = wave % G, split = wave / G;
+  const int h = lane >> 5, ql = lane & 31;
+  const int head = kh * G + gw;
+  const int i = q0 + ql;  // this lane's query
+  const int nq = min(PA_QB, a.S - q0);
+  const int L = a.L;
+  const __amdgpu_buffer_rsrc_t kr = pa_rsrc(a.K + (size_t)kh * a.k_sh, (uint32_t)((L - 1) * a.k_ss + HD) * 2);
+  const __amdgpu_buffer_rsrc_t vr = pa_rsrc(a.V + (size_t)kh * a.v_sh, (uint32_t)((L - 1) * a.v_ss + HD) * 2);
+  // the mask buffer ends with the 16-byte piece holding the last row's byte
+  // L - 1 (bounds are checked per dword; the piece lies in the same page as
+  // that byte, and its bytes past L are cleared)
+  const __amdgpu_buffer_rsrc_t mr =
+      pa_rsrc(a.M + (size_t)q0 * a.m_ss, (uint32_t)((nq - 1) * a.m_ss + ((L + 15) & ~15)));
+
+  // the mask scan's first step, issued before everything else: thread
+  // (row r, k) reads the k-th 16-byte piece from the end of row r
+  constexpr int PER = NT / PA_QB;
+  const int ncg = (L + 15) / 16, srow = tid % PA_QB, scg0 = ncg - 1 - tid / PA_QB;
+  const u32x4 scan0 = pa_ld16(mr, (uint32_t)(min(srow, nq - 1) * a.m_ss + 16 * max(scg0, 0)));
+  __builtin_amdgcn_sched_barrier(0);  // keep it first, so waiting for it waits for nothing else
+
+  // Q^T fragments (B operand): column = query ql, dims 16 kc + 8 h .. + 7
+  u32x4 qf[HD / 16];
+  {
+    const uint16_t* qr = a.Q + (size_t)min(i, a.S - 1) * a.q_ss + (size_t)head * a.q_sh;
+#pragma unroll
+    for (int kc = 0; kc < HD / 16; ++kc) qf[kc] = *reinterpret_cast<const u32x4*>(qr + 16 * kc + 8 * h);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+
+  // staging of block group t (blocks NS t .. NS t + NS - 1): K rows (16-byte
+  // pieces), V as pairs of keys x 8 dims (written transposed as 8 dwords),
+  // mask pieces. Group t is loaded into register set t % 2 two groups ahead
+  // and written to LDS buffer t % 2 at the end of the iteration before it.
+  // Rows are clamped into [0, L): keys past L then hold finite values, which
+  // their zero probabilities cancel.
+  struct Regs {
+    u32x4 k[KPT], v[VPT][2], m[MPT];
+  };
+  Regs rs[2];
+  auto load = [&](Regs& r, int t) {
+#pragma unroll
+    for (int n = 0; n < KPT; ++n) {
+      const int p = min(tid + n * NT, NKP - 1), blk = p / (PA_KB * (HD / 8)), q = p % (PA_KB * (HD / 8));
+      const int j = min(NS * t * PA_KB + blk * PA_KB + q / (HD / 8), L - 1), e = (q % (HD / 8)) * 8;
+      r.k[n] = pa_ld16(kr, (uint32_t)(j * a.k_ss + e) * 2);
+    }
+#pragma unroll
+    for (int n = 0; n < VPT; ++n) {
+      const int p = min(tid + n * NT, NVP - 1), blk = p / ((PA_KB / 2) * (HD / 8)), q = p % ((PA_KB / 2) * (HD / 8));
+      const int j = NS * t * PA_KB + blk * PA_KB + 2 * (q % (PA_KB / 2)), e = (q / (PA_KB / 2)) * 8;
+      r.v[n][0] = pa_ld16(vr, (uint32_t)(min(j, L - 1) * a.v_ss + e) * 2);
+      r.v[n][1] = pa_ld16(vr, (uint32_t)(min(j + 1, L - 1) * a.v_ss + e) * 2);
+    }
+#pragma unroll
+    for (int n = 0; n < MPT; ++n) {
+      const int p = min(tid + n * NT, NMP - 1), blk = p / (PA_QB * 2), q = p % (PA_QB * 2);
+      const int c = min(NS * t * PA_KB + blk * PA_KB + 16 * (q & 1), 16 * (ncg - 1));
+      r.m[n] = pa_ld16(mr, (uint32_t)(min(q >> 1, nq - 1) * a.m_ss + c));
+    }
+  };
+  auto store = [&](const Regs& r, int t) {
+    const int buf = t & 1;
+#pragma unroll
+    for (int n = 0; n < KPT; ++n) {
+      const int p = tid + n * NT, blk = p / (PA_KB * (HD / 8)), q = p % (PA_KB * (HD / 8));
+      if (NKP % NT == 0 || p < NKP) {
+        uint8_t* base = lds + (size_t)(buf * NS + blk) * PA_BLK;
+        *reinterpret_cast<u32x4*>(base + 2 * ((q / (HD / 8)) * PA_KROW + (q % (HD / 8)) * 8)) = r.k[n];
+      }
+    }
+#pragma unroll
+    for (int n = 0; n < VPT; ++n) {
+      const int p = tid + n * NT, blk = p / ((PA_KB / 2) * (HD / 8)), q = p % ((PA_KB / 2) * (HD / 8));
+      if (NVP % NT == 0 || p < NVP) {
+        const int jp = q % (PA_KB / 2), e = (q / (PA_KB / 2)) * 8;
+        uint32_t* vt = reinterpret_cast<uint32_t*>(lds + (size_t)(buf * NS + blk) * PA_BLK + PA_KT +
+                                                   2 * (e * PA_VROW + 2 * jp));
+        const u32x4 v0 = r.v[n][0], v1 = r.v[n][1];
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+          vt[(2 * w) * (PA_VROW / 2)] = (v0[w] & 0xffffu) | (v1[w] << 16);
+          vt[(2 * w + 1) * (PA_VROW / 2)] = (v0[w] >> 16) | (v1[w] & 0xffff0000u);
+        }
+      }
+    }
+#pragma unroll
+    for (int n = 0; n < MPT; ++n) {
+      const int p = tid + n * NT, blk = p / (PA_QB * 2), q = p % (PA_QB * 2);
+      if (NMP % NT == 0 || p < NMP) {
+        const u32x4 m = pa_mask_tail(r.m[n], NS * t * PA_KB + blk * PA_KB + 16 * (q & 1), L);
+        *reinterpret_cast<u32x4*>(lds + (size_t)(buf * NS + blk) * PA_BLK + PA_KT + PA_VT + (q >> 1) * PA_MROW +
+                                  16 * (q & 1)) = m;
+        if ((q >> 1) < nq && !pa_all_set(m)) full[t % 3] = 0;  // rows past nq are never used
+      }
+    }
+  };
+  load(rs[0], 0);
+  __builtin_amdgcn_sched_barrier(0);
+  load(rs[1], 1);
+  __builtin_amdgcn_sched_barrier(0);
+
+  // the last key any of the workgroup's queries may see: the first step's
+  // piece, then (only where it holds no allowed key) the rest of the row
+  // backwards; the maximum over the workgroup through one slot per wave
+  int hit = -1;
+  if (srow < nq && scg0 >= 0) {
+    u32x4 v = pa_mask_tail(scan0, 16 * scg0, L);
+    for (int cg = scg0;;) {
+#pragma unroll
+      for (int w = 3; w >= 0; --w)
+        if (hit < 0 && v[w]) hit = 16 * cg + 4 * w + (31 - __builtin_clz(v[w])) / 8;
+      cg -= PER;
+      if (hit >= 0 || cg < 0) break;
+      v = pa_mask_tail(pa_ld16(mr, (uint32_t)(srow * a.m_ss + 16 * cg)), 16 * cg, L);
+    }
+  }
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) hit = max(hit, __shfl_xor(hit, o, 64));
+  if (lane == 0) wmax[wave] = hit;
+  if (tid == 0) full[0] = full[1] = 1;
+  __syncthreads();
+  int last = -1;
+#pragma unroll
+  for (int w = 0; w < NW; ++w) last = max(last, wmax[w]);
+  const int nkb = (last + PA_KB) / PA_KB;  // blocks holding keys 0 .. last
+  const int nit = (nkb + NS - 1) / NS;
+  // wait for Q here: a wait inside the loop would also wait for the
+  // prefetch loads issued after it
+#pragma unroll
+  for (int kc = 0; kc < HD / 16; ++kc) asm volatile("" ::"v"(qf[kc]));
+
+  pa_f32x16 o[HD / 32];
+#pragma unroll
+  for (int d = 0; d < HD / 32; ++d)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) o[d][r] = 0.0f;
+  float mrun = -__builtin_inff(), lrun = 0.0f;
+
+  if (nit > 0) store(rs[0], 0);
+  __syncthreads();
+  // one step of the pipeline: load group t + 2 into set rl, compute group t,
+  // write group t + 1 (set rw) to the other LDS buffer
+  auto step = [&](int t, Regs& rl, const Regs& rw) {
+    const int buf = t & 1, b = NS * t + split;
+    load(rl, t + 2);  // also past the last group: clamped rows, never stored
+    if (tid == 0) full[(t + 2) % 3] = 1;  // group t - 1 used this slot before the last barrier
+    if (b < nkb) {
+      const uint8_t* base = lds + (size_t)(buf * NS + split) * PA_BLK;
+      const uint16_t* ks = reinterpret_cast<const uint16_t*>(base);
+      const uint16_t* vs = reinterpret_cast<const uint16_t*>(base + PA_KT);
+      const uint8_t* ms = base + PA_KT + PA_VT;
+      const bool all = __builtin_amdgcn_readfirstlane(full[t % 3]) != 0;
+      // S^T = K Q^T for keys 32 b .. 32 b + 31
+      pa_f32x16 s;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) s[r] = 0.0f;
+      const uint16_t* krow = ks + ql * PA_KROW + 8 * h;
+#pragma unroll
+      for (int kc = 0; kc < HD / 16; ++kc)
+        s = pa_mfma<DT>(*reinterpret_cast<const u32x4*>(krow + 16 * kc), qf[kc], s);
+      // V^T fragments (A operand of the second product), read while the
+      // scores are computed
+      u32x4 vf[HD / 32][2];
+#pragma unroll
+      for (int d = 0; d < HD / 32; ++d) {
+        const uint16_t* vrow = vs + (32 * d + ql) * PA_VROW + 4 * h;
+#pragma unroll
+        for (int c = 0; c < 2; ++c) {
+          const uint2 lo = *reinterpret_cast<const uint2*>(vrow + 16 * c);
+          const uint2 hi = *reinterpret_cast<const uint2*>(vrow + 16 * c + 8);
+          vf[d][c] = (u32x4){lo.x, lo.y, hi.x, hi.y};
+        }
+      }
+      // keys 8 g + 4 h + 0..3 of the block (g = r / 4) masked to -inf unless
+      // the whole group is allowed; the online softmax of query ql over this
+      // lane and lane ^ 32, in log2 units
+      if (!all) {
+        const uint8_t* mrow = ms + ql * PA_MROW + 4 * h;
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const uint32_t mw = *reinterpret_cast<const uint32_t*>(mrow + 8 * g);
+#pragma unroll
+          for (int c = 0; c < 4; ++c)
+            if (((mw >> (8 * c)) & 0xffu) == 0) s[4 * g + c] = -__builtin_inff();
+        }
+      }
+      float bm = -__builtin_inff();
+#pragma unroll
+      for (int r = 0; r < 16; ++r) bm = fmaxf(bm, s[r]);
+      bm = fmaxf(bm, __shfl_xor(bm, 32, 64)) * a.scale2;
+      const float mnew = fmaxf(mrun, bm);
+      const float mref = mnew == -__builtin_inff() ? 0.0f : mnew;  // nothing seen yet: all terms 0
+      const float alpha = pa_exp2(mrun - mref);
+      float ps = 0.0f;
+      u32x4 pf[2];  // P^T fragments (B operand): keys 16 c + {4h .. 4h + 3, 8 + 4h .. 8 + 4h + 3}
+#pragma unroll
+      for (int c = 0; c < 2; ++c) {
+        float pv[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+          pv[u] = pa_exp2(__builtin_fmaf(s[8 * c + u], a.scale2, -mref));
+          ps += pv[u];
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u) pf[c][u] = pa_pack<DT>(pv[2 * u], pv[2 * u + 1]);
+      }
+      ps += __shfl_xor(ps, 32, 64);
+      lrun = lrun * alpha + ps;
+      mrun = mnew;
+      // O^T = alpha O^T + V^T P^T (the rescale skipped while no lane's max moved)
+      if (__any(alpha != 1.0f)) {
+#pragma unroll
+        for (int d = 0; d < HD / 32; ++d)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) o[d][r] *= alpha;
+      }
+#pragma unroll
+      for (int d = 0; d < HD / 32; ++d)
+#pragma unroll
+        for (int c = 0; c < 2; ++c) o[d] = pa_mfma<DT>(vf[d][c], pf[c], o[d]);
+    }
+    if (t + 1 < nit) store(rw, t + 1);  // the other buffer: last read before the previous barrier
+    __syncthreads();
+  };
+  for (int t = 0; t < nit; t += 2) {
+    step(t, rs[0], rs[1]);
+    if (t + 1 < nit) step(t + 1, rs[1], rs[0]);
+  }
+  if constexpr (NS > 1) {
+    // merge split 1 into split 0 through LDS (same lane layout in both), then
+    // split 0 writes; the staging buffers are free after the loop's last barrier
+    static_assert(NS == 2, "one merge round");
+    float* mg = reinterpret_cast<float*>(lds) + gw * 66 * 64 + lane;
+    if (split == 1) {
+#pragma unroll
+      for (int d = 0; d < HD / 32; ++d)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) mg[(16 * d + r) * 64] = o[d][r];
+      mg[64 * 64] = mrun;
+      mg[65 * 64] = lrun;
+    }
+    __syncthreads();
+    if (split == 1) return;
+    const float m2 = mg[64 * 64], l2 = mg[65 * 64];
+    const float mm = fmaxf(mrun, m2);
+    const float mref = mm == -__builtin_inff() ? 0.0f : mm;
+    const float f1 = pa_exp2(mrun - mref), f2 = pa_exp2(m2 - mref);
+    lrun = lrun * f1 + l2 * f2;
+#pragma unroll
+    for (int d = 0; d < HD / 32; ++d)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) o[d][r] = o[d][r] * f1 + mg[(16 * d + r) * 64] * f2;
+  }
+  // Y[i][head][dim] = O^T[dim][i] / l (a row with no allowed key: 0 / 0, as the reference's softmax)
+  if (i < a.S) {
+    const float inv = 1.0f / lrun;
+    uint16_t* yr = a.Y + ((size_t)i * a.nh + head) * HD;
+#pragma unroll
+    for (int d = 0; d < HD / 32; ++d)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        uint2 w;
+        w.x = pa_pack<DT>(o[d][4 * g] * inv, o[d][4 * g + 1] * inv);
+        w.y = pa_pack<DT>(o[d][4 * g + 2] * inv, o[d][4 * g + 3] * inv);
+        *reinterpret_cast<uint2*>(yr + 32 * d + 8 * g + 4 * h) = w;
+      }
+  }
+}
+
+}  // namespace ttsp
+
+using namespace ttsp;
+
+extern "C" int ttsp_prefill_max_groups() { return PA_MAX_GROUPS; }
+
+extern "C" int ttsp_prefill_attention(const void* Q, long long q_seq_stride, long long q_head_stride,
+                                      const void* K, long long k_seq_stride, long long k_head_stride,
+                                      const void* V, long long v_seq_stride, long long v_head_stride,
+                                      const void* mask, long long mask_row_stride, void* Y, int S, int nh,
+                                      int nkv, int L, float scale, int dtype, hipStream_t stream) {
+  if (!Q || !K || !V || !mask || !Y || S <= 0 || nh <= 0 || nkv <= 0 || nh % nkv || L <= 0 ||
+      nh / nkv > PA_MAX_GROUPS || S > (1 << 20) || mask_row_stride < L)
+    return (int)hipErrorInvalidValue;
+  // 16-byte pieces: every row start and the bases aligned
+  const long long st[6] = {q_seq_stride, q_head_stride, k_seq_stride, k_head_stride, v_seq_stride, v_head_stride};
+  for (long long s : st)
+    if (s < 0 || s % 8) return (int)hipErrorInvalidValue;
+  if (mask_row_stride % 16 || (uintptr_t)Q % 16 || (uintptr_t)K % 16 || (uintptr_t)V % 16 ||
+      (uintptr_t)mask % 16 || (uintptr_t)Y % 16)
+    return (int)hipErrorInvalidValue;
+  // K, V (one kv head) and the mask rows of one workgroup are addressed with
+  // 32-bit byte offsets
+  const long long lim = (1LL << 31) - 1;
+  if (((L - 1) * k_seq_stride + 128) * 2 > lim || ((L - 1) * v_seq_stride + 128) * 2 > lim ||
+      k_head_stride > lim || v_head_stride > lim || 31 * mask_row_stride + L > lim)
+    return (int)hipErrorInvalidValue;
+  PrefillArgs a{(const uint16_t*)Q, (const uint16_t*)K, (const uint16_t*)V, (const uint8_t*)mask, (uint16_t*)Y,
+                q_seq_stride, q_head_stride, (int)k_seq_stride, (int)k_head_stride, (int)v_seq_stride,
+                (int)v_head_stride, (int)mask_row_stride, S, nh, nkv, L, scale * PA_LOG2E};
+  const int groups = nh / nkv;
+  const dim3 grid(nkv, (S + PA_QB - 1) / PA_QB);
+  // two key splits for 1, 2 and 4 heads per kv head (at most 8 waves, two a
+  // SIMD at ~240 registers), one otherwise
+#define TTSP_PA_G(DTV, G)                                                                                   \
+  case G:                                                                                                   \
+    hipLaunchKernelGGL((prefill_attn_kernel<DTV, G, PA_SPLITS(G)>), grid, dim3(64 * G * PA_SPLITS(G)), 0, \
+                       stream, a);                                                                          \
+    break;
+#define TTSP_PA(DTV)                           \
+  switch (groups) {                            \
+    TTSP_PA_G(DTV, 1)                          \
+    TTSP_PA_G(DTV, 2)                          \
+    TTSP_PA_G(DTV, 3)                          \
+    TTSP_PA_G(DTV, 4)                          \
+    TTSP_PA_G(DTV, 5)                          \
+    TTSP_PA_G(DTV, 6)                          \
+    TTSP_PA_G(DTV, 7)                          \
+    TTSP_PA_G(DTV, 8)                          \
+    default: return (int)hipErrorInvalidValue; \
+  }
+  if (dtype == DT_F16) {
+    TTSP_PA(DT_F16)
+  } else if (dtype == DT_BF16) {
+    TTSP_PA(DT_BF16)
+  } else {
+    return (int)hipErrorInvalidValue;
+  }
+#undef TTSP_PA
+#undef TTSP_PA_G
+  TTSP_RETURN_LAUNCH();
+}

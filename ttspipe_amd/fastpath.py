@@ -6,11 +6,80 @@ query head i reads KV head i // groups (the grouping `repeat_interleave` and
 applied with -inf, softmax in fp32, probabilities cast to V's dtype before the
 second matmul. This is the unfused attention of `llama.Attention` (prefill and
 declined decode calls); a decode step takes the HIP kernels in `fusedlayer`.
+
+`prefill_attention` is the same computation in one HIP launch (flash form on
+the matrix cores) for any number of new positions: the reference runs
+`decode_attention` for up to `GROUPED_MAX_QUERY` queries and torch's
+`scaled_dot_product_attention` with the boolean mask beyond
+(app/engine/fastpath.py:244-268). It declines (returns None) what it does not
+take, and the caller then runs `decode_attention`.
 """
 
 from __future__ import annotations
 
 GROUPED_MAX_QUERY = 64
+HEAD_DIM = 128
+
+_stats = {"prefill_attn": 0, "prefill_declined": 0}
+
+
+def stats() -> dict:
+    return dict(_stats)
+
+
+def _prefill_eligible(q, k, v, mask, n_head, n_local_heads, head_dim) -> bool:
+    import torch
+
+    from ttspipe_amd import _lib
+
+    if head_dim != HEAD_DIM or mask is None or not q.is_cuda or q.dim() != 4 or k.dim() != 4 or v.dim() != 4:
+        return False
+    if q.dtype not in (torch.float16, torch.bfloat16) or k.dtype != q.dtype or v.dtype != q.dtype:
+        return False
+    bsz, nh, seqlen, d = q.shape
+    if bsz != 1 or nh != n_head or d != head_dim or n_head % n_local_heads:
+        return False
+    if n_head // n_local_heads > _lib.lib().ttsp_prefill_max_groups():
+        return False
+    L = k.shape[2]
+    if k.shape != (1, n_local_heads, L, head_dim) or v.shape != k.shape:
+        return False
+    if mask.dtype != torch.bool or mask.dim() != 4 or tuple(mask.shape) != (1, 1, seqlen, L) or not mask.is_cuda:
+        return False
+    for t in (q, k, v):
+        if t.stride(3) != 1 or t.stride(1) % 8 or t.stride(2) % 8 or t.data_ptr() % 16:
+            return False
+    return mask.stride(3) == 1 and mask.stride(2) % 16 == 0 and mask.stride(2) >= L and mask.data_ptr() % 16 == 0
+
+
+def prefill_attention(q, k, v, mask, n_head, n_local_heads, head_dim, out=None):
+    """`decode_attention` in one launch: q (1, n_head, S, 128), k/v (1,
+    n_local_heads, L, 128) with the last dim contiguous (any seq/head strides
+    that keep rows 16-byte aligned, e.g. the KV cache sliced to L), mask bool
+    (1, 1, S, L) with 16-byte aligned rows. Returns (1, n_head, S, 128) as a
+    transposed view of a contiguous (1, S, n_head * 128) tensor (`out=` may
+    supply that tensor), so the caller's `transpose(1, 2).contiguous()` is free;
+    None when declined. A query whose mask row allows no key gets NaN, as the
+    reference's softmax over all -inf scores."""
+    import torch
+
+    from ttspipe_amd import _lib
+
+    if not _lib.gpu_present() or not _prefill_eligible(q, k, v, mask, n_head, n_local_heads, head_dim):
+        _stats["prefill_declined"] += 1
+        return None
+    seqlen, L = q.shape[2], k.shape[2]
+    if out is None:
+        out = torch.empty(1, seqlen, n_head * head_dim, dtype=q.dtype, device=q.device)
+    elif out.shape != (1, seqlen, n_head * head_dim) or out.dtype != q.dtype or not out.is_contiguous():
+        raise ValueError("out must be a contiguous (1, S, n_head * head_dim) tensor of q's dtype")
+    rc = _lib.lib().ttsp_prefill_attention(
+        q.data_ptr(), q.stride(2), q.stride(1), k.data_ptr(), k.stride(2), k.stride(1), v.data_ptr(), v.stride(2),
+        v.stride(1), mask.data_ptr(), mask.stride(2), out.data_ptr(), seqlen, n_head, n_local_heads, L,
+        float(head_dim**-0.5), _lib.dtype_code(q.dtype), _lib.stream())
+    _lib.check(rc, "ttsp_prefill_attention")
+    _stats["prefill_attn"] += 1
+    return out.view(1, seqlen, n_head, head_dim).transpose(1, 2)
 
 
 def decode_attention(q, k, v, mask, n_head, n_local_heads, head_dim):

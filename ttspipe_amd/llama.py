@@ -123,7 +123,7 @@ class Attention(nn.Module):
 
     def forward(self, x, freqs_cis, mask, input_pos=None):
         from ttspipe_amd import fusedops
-        from ttspipe_amd.fastpath import decode_attention
+        from ttspipe_amd.fastpath import decode_attention, prefill_attention
 
         bsz, seqlen, _ = x.shape
         q_size = self.n_head * self.head_dim
@@ -149,7 +149,9 @@ class Attention(nn.Module):
         if mask is not None and mask.shape[-1] < k.shape[2]:
             k = k[:, :, : mask.shape[-1]]
             v = v[:, :, : mask.shape[-1]]
-        y = decode_attention(q, k, v, mask, self.n_head, self.n_local_heads, self.head_dim)
+        y = prefill_attention(q, k, v, mask, self.n_head, self.n_local_heads, self.head_dim)
+        if y is None:
+            y = decode_attention(q, k, v, mask, self.n_head, self.n_local_heads, self.head_dim)
         y = y.transpose(1, 2).contiguous().view(bsz, seqlen, q_size)
         return self.wo(y)
 
