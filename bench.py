@@ -313,6 +313,55 @@ def bench_gemm(rows: int = 512, copies: int = 4, reps: int = 20):
             "pct_of_mfma_peak": round(100 * total_flop / total_s / 1e12 / MFMA_PEAK_TFLOPS, 2)}
 
 
+def bench_prefill_attention(rows: int = 512, prefixes=(0, 1536), n_head: int = 32, n_kv: int = 8, reps: int = 20):
+    """Prefill attention of `rows` new positions (32 q / 8 kv heads of 128,
+    bf16) over a cached prefix, with the fork's causal mask, as one HIP
+    launch; torch's scaled_dot_product_attention with the same boolean mask
+    (the reference's path beyond 64 positions) timed beside it. FLOPs count
+    the allowed (query, key) pairs: 4 * 128 per pair and head."""
+    import torch
+    import torch.nn.functional as F
+
+    from ttspipe_amd import fastpath
+
+    dev = torch.device("cuda", 0)
+    g = torch.Generator(device=dev).manual_seed(11)
+    out = []
+    for prefix in prefixes:
+        L = prefix + rows
+        max_len = ((L + 255) // 256) * 256
+        q = torch.randn(1, rows, n_head, 128, device=dev, generator=g).to(torch.bfloat16).transpose(1, 2)
+        kc = torch.randn(1, n_kv, max_len, 128, device=dev, generator=g).to(torch.bfloat16)
+        vc = torch.randn(1, n_kv, max_len, 128, device=dev, generator=g).to(torch.bfloat16)
+        k, v = kc[:, :, :L], vc[:, :, :L]
+        causal = torch.tril(torch.ones(max_len, max_len, dtype=torch.bool, device=dev))
+        mask = causal[None, None, torch.arange(prefix, L, device=dev)][..., :L]
+        y = torch.empty(1, rows, n_head * 128, dtype=torch.bfloat16, device=dev)
+
+        def ours():
+            if fastpath.prefill_attention(q, k, v, mask, n_head, n_kv, 128, out=y) is None:
+                raise RuntimeError("prefill attention declined")
+
+        def sdpa():
+            F.scaled_dot_product_attention(q, k, v, attn_mask=mask, enable_gqa=True)
+
+        times = {}
+        for name, fn in (("hip", ours), ("sdpa", sdpa)):
+            fn()
+            torch.cuda.synchronize()
+            graph = capture(lambda fn=fn: [fn() for _ in range(4)])
+            stream = torch.cuda.current_stream()
+            time_graph(graph, 2, stream)
+            times[name] = time_graph(graph, reps, stream) / 4
+        pairs = rows * prefix + rows * (rows + 1) // 2
+        flop = 4 * 128 * pairs * n_head
+        out.append({"rows": rows, "prefix": prefix, "us": round(times["hip"] * 1e6, 2),
+                    "tflops": round(flop / times["hip"] / 1e12, 1),
+                    "pct_of_mfma_peak": round(100 * flop / times["hip"] / 1e12 / MFMA_PEAK_TFLOPS, 2),
+                    "torch_sdpa_us": round(times["sdpa"] * 1e6, 1)})
+    return out
+
+
 def bench_copy(nbytes: int = 64 * 2**20, launches: int = 8):
     """A plain device copy of known size (reads and writes `nbytes` each), the
     calibration kernel for the HBM byte counters."""
@@ -352,7 +401,7 @@ def main() -> int:
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--skip-cpu", action="store_true")
     ap.add_argument("--skip-decode", action="store_true")
-    ap.add_argument("--only", choices=["layer", "kernel", "c1", "copy", "decode", "gemm"], default=None,
+    ap.add_argument("--only", choices=["layer", "kernel", "c1", "copy", "decode", "gemm", "pattn"], default=None,
                     help="run one GPU measurement only (for profiling runs)")
     ap.add_argument("--decode-steps", type=int, default=256, help="greedy frames the decode benchmark times")
     ap.add_argument("--cpu-decode-frames", type=int, default=3, help="frames the CPU baseline's decode times")
@@ -379,6 +428,8 @@ def main() -> int:
         out["copy"] = bench_copy()
     if args.only in (None, "gemm"):
         out["gemm"] = bench_gemm()
+    if args.only in (None, "pattn"):
+        out["pattn"] = bench_prefill_attention()
     decode = None
     if args.only in (None, "decode") and not args.skip_decode:
         from ttspipe_amd import dualar
@@ -438,6 +489,7 @@ def main() -> int:
         },
         "decode": decode,
         "prefill_gemm": out["gemm"],
+        "prefill_attention": out["pattn"],
         "cpu_baseline": cpu,
     }
     print(json.dumps(line))

@@ -8,14 +8,13 @@
 // Workgroup = (kv head kh, block of 32 queries): one wave per query head of
 // the group, times NS key splits (split s takes key blocks s, s + NS, ...;
 // the splits merge through LDS at the end). Keys go through LDS in blocks of
-// 32: the K rows as they are, V transposed (dims x keys) and the 32 x 32
-// mask tile. Each wave computes the transposed score tile S^T = K Q^T (32
+// 32: the K and V rows as they are and the 32 x 32 mask tile. Each wave computes the transposed score tile S^T = K Q^T (32
 // keys x 32 queries, 8 MFMA 32x32x16 over the 128 dims; Q stays in
 // registers), so one lane holds 16 keys of one query and a query's online
 // softmax needs only its own lane and lane ^ 32. P^T then feeds
-// O^T += V^T P^T straight from registers: the V^T fragments are read in the
-// key order the score layout gives P^T, so no transpose of P goes through
-// LDS. Scores, running max and sum are fp32 (in log2 units: the scale and
+// O^T += V^T P^T straight from registers: the V^T fragments come from V's
+// row-major tile through the transposing LDS read, in the key order the
+// score layout gives P^T, so neither V nor P is transposed by hand. Scores, running max and sum are fp32 (in log2 units: the scale and
 // log2 e fold into one multiply-add before the hardware exp2);
 // probabilities are rounded to the activation type for the matrix core; O
 // is divided by the sum once at the end.
@@ -39,11 +38,13 @@ namespace ttsp {
 typedef __bf16 pa_bf16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 pa_f16x8 __attribute__((ext_vector_type(8)));
 typedef float pa_f32x16 __attribute__((ext_vector_type(16)));
+typedef short pa_s16x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) pa_s16x4 pa_lds_s16x4;
 
 constexpr int PA_QB = 32;            // queries per workgroup
 constexpr int PA_KB = 32;            // keys per block
 constexpr int PA_KROW = HD + 8;      // K tile row stride (elements): 272 B
-constexpr int PA_VROW = PA_KB + 8;   // V^T tile row stride (elements): 80 B
+constexpr int PA_VROW = HD + 32;     // V tile row stride (elements): 320 B, see the transposed reads
 constexpr int PA_MROW = PA_KB + 16;  // mask tile row stride (bytes)
 constexpr int PA_MAX_GROUPS = 8;
 #define PA_SPLITS(G) ((G) == 1 || (G) == 2 || (G) == 4 ? 2 : 1)
@@ -76,6 +77,16 @@ __device__ __forceinline__ uint32_t pa_pack(float lo, float hi) {
   }
 }
 
+// ds_read_b64_tr_b16 (gfx950): within each group of 16 lanes, lane j's result
+// element k is element j % 4 of the 8 bytes lane 4 k + j / 4 addresses. Four
+// lanes addressing 4 consecutive dims of one key row, for 4 key rows, thus
+// hand each lane of the group one dim at 4 consecutive keys: a column of V
+// read straight from V's row-major tile.
+__device__ __forceinline__ uint2 pa_ld_tr(const uint8_t* lds_base, uint32_t off) {
+  const pa_lds_s16x4* p = (const pa_lds_s16x4*)((__attribute__((address_space(3))) const uint8_t*)lds_base + off);
+  return __builtin_bit_cast(uint2, __builtin_amdgcn_ds_read_tr16_b64_v4i16(const_cast<pa_lds_s16x4*>(p)));
+}
+
 // A raw buffer over [base, base + bytes): 32-bit byte offsets, and loads past
 // the end return zeros instead of touching memory.
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t pa_rsrc(const void* base, uint32_t bytes) {
@@ -88,10 +99,12 @@ __device__ __forceinline__ u32x4 pa_ld16(__amdgpu_buffer_rsrc_t r, uint32_t off)
 // Mask bytes past column L cleared, for the 16 bytes from column c; applied
 // where the value is used, so the load's wait is not pulled forward.
 __device__ __forceinline__ u32x4 pa_mask_tail(u32x4 v, int c, int L) {
+  if (c + 16 > L) {  // rare: the piece reaches past L
 #pragma unroll
-  for (int w = 0; w < 4; ++w) {
-    const int valid = L - c - 4 * w;  // bytes of this word before L
-    v[w] &= valid >= 4 ? 0xffffffffu : valid <= 0 ? 0u : (1u << (8 * valid)) - 1u;
+    for (int w = 0; w < 4; ++w) {
+      const int valid = L - c - 4 * w;  // bytes of this word before L
+      v[w] &= valid >= 4 ? 0xffffffffu : valid <= 0 ? 0u : (1u << (8 * valid)) - 1u;
+    }
   }
   return v;
 }
@@ -115,16 +128,16 @@ struct PrefillArgs {
   float scale2;  // scale * log2(e): scores in log2 units
 };
 
-// LDS of one staged key block: K rows, V^T, mask tile (bytes)
+// LDS of one staged key block: K rows, V rows, mask tile (bytes)
 constexpr int PA_KT = PA_KB * PA_KROW * 2;
-constexpr int PA_VT = HD * PA_VROW * 2;
+constexpr int PA_VT = PA_KB * PA_VROW * 2;
 constexpr int PA_MT = PA_QB * PA_MROW;
 constexpr int PA_BLK = PA_KT + PA_VT + PA_MT;
 
 template <int DT, int G, int NS>
 __global__ __launch_bounds__(64 * G * NS) void prefill_attn_kernel(const PrefillArgs a) {
   constexpr int NT = 64 * G * NS, NW = NT / 64;
-  constexpr int NKP = NS * PA_KB * (HD / 8), NVP = NS * (PA_KB / 2) * (HD / 8), NMP = NS * PA_QB * 2;
+  constexpr int NKP = NS * PA_KB * (HD / 8), NVP = NKP, NMP = NS * PA_QB * 2;
   constexpr int KPT = (NKP + NT - 1) / NT, VPT = (NVP + NT - 1) / NT, MPT = (NMP + NT - 1) / NT;
   constexpr int STAGE = 2 * NS * PA_BLK;
   constexpr int MERGE = NS > 1 ? G * 66 * 64 * 4 : 0;  // split 1's o (64 floats), m, l per lane
@@ -163,14 +176,13 @@ __global__ __launch_bounds__(64 * G * NS) void prefill_attn_kernel(const Prefill
   }
   __builtin_amdgcn_sched_barrier(0);
 
-  // staging of block group t (blocks NS t .. NS t + NS - 1): K rows (16-byte
-  // pieces), V as pairs of keys x 8 dims (written transposed as 8 dwords),
-  // mask pieces. Group t is loaded into register set t % 2 two groups ahead
+  // staging of block group t (blocks NS t .. NS t + NS - 1): K and V rows
+  // (16-byte pieces), mask pieces. Group t is loaded into register set t % 2 two groups ahead
   // and written to LDS buffer t % 2 at the end of the iteration before it.
   // Rows are clamped into [0, L): keys past L then hold finite values, which
   // their zero probabilities cancel.
   struct Regs {
-    u32x4 k[KPT], v[VPT][2], m[MPT];
+    u32x4 k[KPT], v[VPT], m[MPT];
   };
   Regs rs[2];
   auto load = [&](Regs& r, int t) {
@@ -182,10 +194,9 @@ __global__ __launch_bounds__(64 * G * NS) void prefill_attn_kernel(const Prefill
     }
 #pragma unroll
     for (int n = 0; n < VPT; ++n) {
-      const int p = min(tid + n * NT, NVP - 1), blk = p / ((PA_KB / 2) * (HD / 8)), q = p % ((PA_KB / 2) * (HD / 8));
-      const int j = NS * t * PA_KB + blk * PA_KB + 2 * (q % (PA_KB / 2)), e = (q / (PA_KB / 2)) * 8;
-      r.v[n][0] = pa_ld16(vr, (uint32_t)(min(j, L - 1) * a.v_ss + e) * 2);
-      r.v[n][1] = pa_ld16(vr, (uint32_t)(min(j + 1, L - 1) * a.v_ss + e) * 2);
+      const int p = min(tid + n * NT, NVP - 1), blk = p / (PA_KB * (HD / 8)), q = p % (PA_KB * (HD / 8));
+      const int j = min(NS * t * PA_KB + blk * PA_KB + q / (HD / 8), L - 1), e = (q % (HD / 8)) * 8;
+      r.v[n] = pa_ld16(vr, (uint32_t)(j * a.v_ss + e) * 2);
     }
 #pragma unroll
     for (int n = 0; n < MPT; ++n) {
@@ -206,17 +217,10 @@ __global__ __launch_bounds__(64 * G * NS) void prefill_attn_kernel(const Prefill
     }
 #pragma unroll
     for (int n = 0; n < VPT; ++n) {
-      const int p = tid + n * NT, blk = p / ((PA_KB / 2) * (HD / 8)), q = p % ((PA_KB / 2) * (HD / 8));
+      const int p = tid + n * NT, blk = p / (PA_KB * (HD / 8)), q = p % (PA_KB * (HD / 8));
       if (NVP % NT == 0 || p < NVP) {
-        const int jp = q % (PA_KB / 2), e = (q / (PA_KB / 2)) * 8;
-        uint32_t* vt = reinterpret_cast<uint32_t*>(lds + (size_t)(buf * NS + blk) * PA_BLK + PA_KT +
-                                                   2 * (e * PA_VROW + 2 * jp));
-        const u32x4 v0 = r.v[n][0], v1 = r.v[n][1];
-#pragma unroll
-        for (int w = 0; w < 4; ++w) {
-          vt[(2 * w) * (PA_VROW / 2)] = (v0[w] & 0xffffu) | (v1[w] << 16);
-          vt[(2 * w + 1) * (PA_VROW / 2)] = (v0[w] >> 16) | (v1[w] & 0xffff0000u);
-        }
+        uint8_t* base = lds + (size_t)(buf * NS + blk) * PA_BLK + PA_KT;
+        *reinterpret_cast<u32x4*>(base + 2 * ((q / (HD / 8)) * PA_VROW + (q % (HD / 8)) * 8)) = r.v[n];
       }
     }
 #pragma unroll
@@ -283,7 +287,6 @@ __global__ __launch_bounds__(64 * G * NS) void prefill_attn_kernel(const Prefill
     if (b < nkb) {
       const uint8_t* base = lds + (size_t)(buf * NS + split) * PA_BLK;
       const uint16_t* ks = reinterpret_cast<const uint16_t*>(base);
-      const uint16_t* vs = reinterpret_cast<const uint16_t*>(base + PA_KT);
       const uint8_t* ms = base + PA_KT + PA_VT;
       const bool all = __builtin_amdgcn_readfirstlane(full[t % 3]) != 0;
       // S^T = K Q^T for keys 32 b .. 32 b + 31
@@ -294,18 +297,22 @@ __global__ __launch_bounds__(64 * G * NS) void prefill_attn_kernel(const Prefill
 #pragma unroll
       for (int kc = 0; kc < HD / 16; ++kc)
         s = pa_mfma<DT>(*reinterpret_cast<const u32x4*>(krow + 16 * kc), qf[kc], s);
-      // V^T fragments (A operand of the second product), read while the
-      // scores are computed
+      // V^T fragments (A operand of the second product: dim 32 d + ql at keys
+      // 16 c + {4h .. 4h + 3, 8 + 4h .. 8 + 4h + 3}), read transposed while
+      // the scores are computed: lane 4 k + q of each 16-lane group (dims
+      // 16 db .. 16 db + 15) addresses key 16 c + 4 h + k (+ 8), dims 4 q ..
       u32x4 vf[HD / 32][2];
+      {
+        const int g = lane >> 4, li = lane & 15;
+        const uint32_t vo = (uint32_t)(PA_KT + ((4 * (g >> 1) + (li >> 2)) * PA_VROW + 16 * (g & 1) + 4 * (li & 3)) * 2);
 #pragma unroll
-      for (int d = 0; d < HD / 32; ++d) {
-        const uint16_t* vrow = vs + (32 * d + ql) * PA_VROW + 4 * h;
+        for (int d = 0; d < HD / 32; ++d)
 #pragma unroll
-        for (int c = 0; c < 2; ++c) {
-          const uint2 lo = *reinterpret_cast<const uint2*>(vrow + 16 * c);
-          const uint2 hi = *reinterpret_cast<const uint2*>(vrow + 16 * c + 8);
-          vf[d][c] = (u32x4){lo.x, lo.y, hi.x, hi.y};
-        }
+          for (int c = 0; c < 2; ++c) {
+            const uint2 lo = pa_ld_tr(base, vo + (16 * c * PA_VROW + 32 * d) * 2);
+            const uint2 hi = pa_ld_tr(base, vo + ((16 * c + 8) * PA_VROW + 32 * d) * 2);
+            vf[d][c] = (u32x4){lo.x, lo.y, hi.x, hi.y};
+          }
       }
       // keys 8 g + 4 h + 0..3 of the block (g = r / 4) masked to -inf unless
       // the whole group is allowed; the online softmax of query ql over this
