@@ -67,13 +67,18 @@ __global__ __launch_bounds__(GEMM_THREADS) void nf4_gemm_kernel(
     int epi, int M, int K, int N, int bs_shift, int bs2_shift) {
   static_assert(WM * WN == GEMM_THREADS / 64, "4 waves");
   constexpr int TM = BM / WM / 32, TN = BN / WN / 32;  // MFMA blocks per wave
-  constexpr int A_CH = BM * (KT / 32);                                  // 16-byte packed chunks per step
+  constexpr int A_CH = BM * (KT / 16);                                  // 8-byte packed chunks (16 codes) per step
   constexpr int A_PER_T = (A_CH + GEMM_THREADS - 1) / GEMM_THREADS;     // per thread (the last partly idle)
   constexpr int B_PER_T = BN * (KT / 8) / GEMM_THREADS;                 // 16-byte activation chunks per thread
   static_assert(B_PER_T >= 1 && BN * (KT / 8) % GEMM_THREADS == 0, "tile too small for the workgroup");
 
-  __shared__ uint16_t As[2][BM * LROW];
-  __shared__ uint16_t Bs[2][BN * LROW];
+  // the operand tiles (two buffers each); after the K loop the same memory
+  // holds the output tile, BN rows of BM + 8 elements
+  constexpr int YROW = BM + 8;
+  constexpr int OPS = 2 * (BM + BN) * LROW, YS = BN * YROW;
+  __shared__ __align__(16) uint16_t smem[OPS > YS ? OPS : YS];
+  uint16_t (*As)[BM * LROW] = reinterpret_cast<uint16_t (*)[BM * LROW]>(smem);
+  uint16_t (*Bs)[BN * LROW] = reinterpret_cast<uint16_t (*)[BN * LROW]>(smem + 2 * BM * LROW);
   __shared__ float lut_s[16];
   __shared__ float code2_s[NESTED ? 256 : 1];
 
@@ -87,7 +92,7 @@ __global__ __launch_bounds__(GEMM_THREADS) void nf4_gemm_kernel(
   if constexpr (NESTED) code2_s[tid] = CODE2[tid];
 
   struct Stage {
-    uint4 w[A_PER_T];
+    uint2 w[A_PER_T];
     float s[A_PER_T];
     uint32_t a8[NESTED ? A_PER_T : 1];
     uint4 x[B_PER_T];
@@ -99,13 +104,13 @@ __global__ __launch_bounds__(GEMM_THREADS) void nf4_gemm_kernel(
     const int k0 = min(step, nsteps - 1) * KT;
 #pragma unroll
     for (int i = 0; i < A_PER_T; ++i) {
-      const int c = min(tid + i * GEMM_THREADS, A_CH - 1);  // chunk: row c/2, half c%2
-      const int row = min(m0 + c / 2, M - 1);
-      const int kc = k0 + (c & 1) * 32;
-      typedef uint32_t u32x4_v __attribute__((ext_vector_type(4)));
-      const u32x4_v v = __builtin_nontemporal_load(
-          reinterpret_cast<const u32x4_v*>(W + (size_t)row * rowbytes + kc / 2));
-      sg.w[i] = make_uint4(v.x, v.y, v.z, v.w);
+      const int c = min(tid + i * GEMM_THREADS, A_CH - 1);  // chunk: row c / 4, codes 16 (c % 4) ..
+      const int row = min(m0 + c / (KT / 16), M - 1);
+      const int kc = k0 + (c % (KT / 16)) * 16;
+      typedef uint32_t u32x2_v __attribute__((ext_vector_type(2)));
+      const u32x2_v v = __builtin_nontemporal_load(
+          reinterpret_cast<const u32x2_v*>(W + (size_t)row * rowbytes + kc / 2));
+      sg.w[i] = make_uint2(v.x, v.y);
       const long long b = ((long long)row * K + kc) >> bs_shift;
       if constexpr (NESTED) {
         sg.a8[i] = A8[b];
@@ -128,24 +133,24 @@ __global__ __launch_bounds__(GEMM_THREADS) void nf4_gemm_kernel(
       if (A_CH % GEMM_THREADS && c >= A_CH) break;
       float s = sg.s[i];
       if constexpr (NESTED) s = __fadd_rn(__fmul_rn(code2_s[sg.a8[i]], s), offset);
-      const uint32_t wv[4] = {sg.w[i].x, sg.w[i].y, sg.w[i].z, sg.w[i].w};
-      // all 32 code lookups in flight before the first is used (one LDS
+      const uint32_t wv[2] = {sg.w[i].x, sg.w[i].y};
+      // all 16 code lookups in flight before the first is used (one LDS
       // round trip per step instead of one per byte)
-      float cv[32];
+      float cv[16];
 #pragma unroll
-      for (int q = 0; q < 4; ++q)
+      for (int q = 0; q < 2; ++q)
 #pragma unroll
         for (int bb = 0; bb < 4; ++bb) {
           const uint32_t byte = (wv[q] >> (8 * bb)) & 0xffu;
           cv[2 * (q * 4 + bb)] = lut_s[byte >> 4];
           cv[2 * (q * 4 + bb) + 1] = lut_s[byte & 15u];
         }
-      uint32_t o[16];
+      uint32_t o[8];
 #pragma unroll
-      for (int e = 0; e < 16; ++e) o[e] = pack2<DT>(__fmul_rn(cv[2 * e], s), __fmul_rn(cv[2 * e + 1], s));
-      uint4* dst = reinterpret_cast<uint4*>(&As[buf][(c / 2) * LROW + (c & 1) * 32]);
+      for (int e = 0; e < 8; ++e) o[e] = pack2<DT>(__fmul_rn(cv[2 * e], s), __fmul_rn(cv[2 * e + 1], s));
+      uint4* dst = reinterpret_cast<uint4*>(&As[buf][(c / (KT / 16)) * LROW + (c % (KT / 16)) * 16]);
 #pragma unroll
-      for (int q = 0; q < 4; ++q) dst[q] = make_uint4(o[4 * q], o[4 * q + 1], o[4 * q + 2], o[4 * q + 3]);
+      for (int q = 0; q < 2; ++q) dst[q] = make_uint4(o[4 * q], o[4 * q + 1], o[4 * q + 2], o[4 * q + 3]);
     }
 #pragma unroll
     for (int i = 0; i < B_PER_T; ++i) {
@@ -201,25 +206,67 @@ __global__ __launch_bounds__(GEMM_THREADS) void nf4_gemm_kernel(
     }
   }
 
-  // epilogue: accumulator r of lane l is (row 8*(r/4) + 4*(l/32) + r%4, column l%32)
+  // epilogue: accumulator r of lane l is (row 8*(r/4) + 4*(l/32) + r%4, column
+  // l%32); each value is rounded to the activation type and the tile goes
+  // through LDS as Y rows (the operand buffers are free after the last
+  // barrier), so the stores and the operand reads are 16 bytes per lane
 #pragma unroll
   for (int i = 0; i < TM; ++i)
 #pragma unroll
     for (int j = 0; j < TN; ++j) {
-      const int n = n0 + wn * (BN / WN) + j * 32 + (lane & 31);
-      if (n >= N) continue;
+      const int nl = wn * (BN / WN) + j * 32 + (lane & 31);
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int m = m0 + wm * (BM / WM) + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-        if (m >= M) continue;
-        const size_t o = (size_t)n * M + m;
-        const float y = Elem<DT>::load(Elem<DT>::store(acc[i][j][r]));
-        float v = y;
-        if (epi == 1) v = __fadd_rn(Elem<DT>::load(R[o]), y);
-        else if (epi == 2) v = __fmul_rn(Elem<DT>::load(Elem<DT>::store(silu_rn(Elem<DT>::load(R[o])))), y);
-        Y[o] = Elem<DT>::store(v);
+      for (int g = 0; g < 4; ++g) {
+        const int ml = wm * (BM / WM) + i * 32 + 8 * g + 4 * (lane >> 5);
+        const uint32_t lo = (uint32_t)Elem<DT>::store(acc[i][j][4 * g]) |
+                            ((uint32_t)Elem<DT>::store(acc[i][j][4 * g + 1]) << 16);
+        const uint32_t hi = (uint32_t)Elem<DT>::store(acc[i][j][4 * g + 2]) |
+                            ((uint32_t)Elem<DT>::store(acc[i][j][4 * g + 3]) << 16);
+        *reinterpret_cast<uint2*>(&smem[nl * YROW + ml]) = make_uint2(lo, hi);
       }
     }
+  __syncthreads();
+  const bool vec = (epi & 4) != 0;  // M % 8 == 0 and Y, R 16-byte aligned (host)
+  const int ep = epi & 3;
+  for (int cc = tid; cc < BN * (BM / 8); cc += GEMM_THREADS) {
+    const int nl = cc / (BM / 8), ml = (cc % (BM / 8)) * 8;
+    const int n = n0 + nl, m = m0 + ml;
+    if (n >= N || m >= M) continue;
+    const uint4 yv = *reinterpret_cast<const uint4*>(&smem[nl * YROW + ml]);
+    const uint32_t yw[4] = {yv.x, yv.y, yv.z, yv.w};
+    const size_t o = (size_t)n * M + m;
+    if (vec && m + 8 <= M) {
+      uint32_t rw[4] = {0u, 0u, 0u, 0u};
+      if (ep) {
+        const uint4 rv = *reinterpret_cast<const uint4*>(R + o);
+        rw[0] = rv.x, rw[1] = rv.y, rw[2] = rv.z, rw[3] = rv.w;
+      }
+      uint32_t ow[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        uint32_t h2[2];
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+          const float y = Elem<DT>::load(yw[q] >> (16 * u));
+          const float r = Elem<DT>::load(rw[q] >> (16 * u));
+          float v = y;
+          if (ep == 1) v = __fadd_rn(r, y);
+          else if (ep == 2) v = __fmul_rn(Elem<DT>::load(Elem<DT>::store(silu_rn(r))), y);
+          h2[u] = Elem<DT>::store(v);
+        }
+        ow[q] = h2[0] | (h2[1] << 16);
+      }
+      *reinterpret_cast<uint4*>(Y + o) = make_uint4(ow[0], ow[1], ow[2], ow[3]);
+    } else {
+      for (int u = 0; u < 8 && m + u < M; ++u) {
+        const float y = Elem<DT>::load(yw[u >> 1] >> (16 * (u & 1)));
+        float v = y;
+        if (ep == 1) v = __fadd_rn(Elem<DT>::load(R[o + u]), y);
+        else if (ep == 2) v = __fmul_rn(Elem<DT>::load(Elem<DT>::store(silu_rn(Elem<DT>::load(R[o + u])))), y);
+        Y[o + u] = Elem<DT>::store(v);
+      }
+    }
+  }
 }
 
 template <int DT, int BM, int BN, int WM, int WN, int PF>
@@ -294,6 +341,8 @@ extern "C" int ttsp_nf4_gemm(const void* X, int x_dtype, const uint8_t* W, const
   if ((1 << bs_shift) != blocksize || bs_shift < 6 || (A8 && (1 << bs2_shift) != blocksize2))
     return (int)hipErrorInvalidValue;
   if (K % 128 || K % blocksize || epi < 0 || epi > 2 || (epi && !R)) return (int)hipErrorInvalidValue;
-  return gemm_mfma(X, x_dtype, W, A8, AMAX, CODE2, offset, LUT, Y, R, epi, M, K, N, bs_shift,
+  // vectorised output rows: 8 elements per 16-byte store
+  const bool vec = M % 8 == 0 && (uintptr_t)Y % 16 == 0 && (!epi || (uintptr_t)R % 16 == 0);
+  return gemm_mfma(X, x_dtype, W, A8, AMAX, CODE2, offset, LUT, Y, R, epi | (vec ? 4 : 0), M, K, N, bs_shift,
                    bs2_shift, stream);
 }
