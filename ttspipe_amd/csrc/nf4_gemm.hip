@@ -2,20 +2,23 @@
 // with W the bitsandbytes NF4 weight (nf4_gemv.hip gives the layout).
 //
 // Each workgroup owns a BM x BN tile of the output (BM weight rows, BN input
-// rows). Per K-step of 64 codes, the 256 threads
-//   * dequantise BM x 64 weights, 16 packed bytes (32 codes) each, as
+// rows), WM x WN waves of 32x32 MFMA blocks. Per K-step of 64 codes, the
+// workgroup's threads
+//   * dequantise BM x 64 weights, 8 packed bytes (16 codes) each, as
 //     round(code * scale) in the activation type - the exact value
 //     bitsandbytes' dequantize_4bit produces, so the product is the dense
 //     fork's matmul on identical weights - straight into an LDS A tile (the
 //     16 code points in LDS: 64 lanes hit at most 16 banks, no conflicts; one
 //     hardware pack-convert rounds two products);
 //   * copy BN x 64 activations into an LDS B tile;
-// and the 4 waves run v_mfma_f32_32x32x16 over their sub-tiles, fp32
+// and the waves run v_mfma_f32_32x32x16 over their sub-tiles, fp32
 // accumulate. The packed weights, scales and activations of the next PF
 // steps are in flight in registers while a step multiplies (the K loop is
 // latency-bound otherwise: a lone workgroup waits a memory round trip per
 // step), and LDS is double-buffered. Rows are padded to 72 elements (144 B) so
-// the 16-byte operand reads of 16 consecutive rows hit disjoint banks.
+// the 16-byte operand reads of 16 consecutive rows hit disjoint banks. The
+// output tile is rounded, staged in LDS and written (with the epilogue) as
+// 16-byte row pieces.
 //
 // MFMA 32x32x16 operand layout: lane l supplies row (l % 32) of A and column
 // (l % 32) of B, each as 8 consecutive k at 8 * (l / 32); accumulator r of
@@ -32,7 +35,6 @@ typedef __bf16 bf16x2_v __attribute__((ext_vector_type(2)));
 typedef _Float16 f16x2_v __attribute__((ext_vector_type(2)));
 typedef float f32x2_v __attribute__((ext_vector_type(2)));
 
-constexpr int GEMM_THREADS = 256;
 constexpr int KT = 64;        // codes per K-step (one bs=64 scale block)
 constexpr int LROW = KT + 8;  // LDS row stride in elements
 
@@ -60,12 +62,12 @@ __device__ __forceinline__ uint32_t pack2(float lo, float hi) {
 // WM x WN waves; each wave covers (BM/WM) x (BN/WN) with 32x32 MFMA blocks;
 // PF K-steps of operands in flight (nsteps a multiple of PF).
 template <int DT, int BM, int BN, int WM, int WN, bool NESTED, int PF>
-__global__ __launch_bounds__(GEMM_THREADS) void nf4_gemm_kernel(
+__global__ __launch_bounds__(64 * WM * WN) void nf4_gemm_kernel(
     const uint16_t* __restrict__ X, const uint8_t* __restrict__ W, const uint8_t* __restrict__ A8,
     const float* __restrict__ AMAX, const float* __restrict__ CODE2, float offset,
     const float* __restrict__ LUT, uint16_t* __restrict__ Y, const uint16_t* __restrict__ R,
     int epi, int M, int K, int N, int bs_shift, int bs2_shift) {
-  static_assert(WM * WN == GEMM_THREADS / 64, "4 waves");
+  constexpr int GEMM_THREADS = 64 * WM * WN;
   constexpr int TM = BM / WM / 32, TN = BN / WN / 32;  // MFMA blocks per wave
   constexpr int A_CH = BM * (KT / 16);                                  // 8-byte packed chunks (16 codes) per step
   constexpr int A_PER_T = (A_CH + GEMM_THREADS - 1) / GEMM_THREADS;     // per thread (the last partly idle)
@@ -89,7 +91,8 @@ __global__ __launch_bounds__(GEMM_THREADS) void nf4_gemm_kernel(
   const size_t rowbytes = (size_t)K / 2;
 
   if (tid < 16) lut_s[tid] = LUT[tid];
-  if constexpr (NESTED) code2_s[tid] = CODE2[tid];
+  if constexpr (NESTED)
+    if (tid < 256) code2_s[tid] = CODE2[tid];
 
   struct Stage {
     uint2 w[A_PER_T];
@@ -275,11 +278,11 @@ static void launch_gemm(const void* X, const uint8_t* W, const uint8_t* A8, cons
                         int epi, int M, int K, int N, int bs_shift, int bs2_shift, hipStream_t st) {
   const dim3 grid((M + BM - 1) / BM, (N + BN - 1) / BN);
   if (A8)
-    hipLaunchKernelGGL((nf4_gemm_kernel<DT, BM, BN, WM, WN, true, PF>), grid, dim3(GEMM_THREADS), 0, st,
+    hipLaunchKernelGGL((nf4_gemm_kernel<DT, BM, BN, WM, WN, true, PF>), grid, dim3(64 * WM * WN), 0, st,
                        (const uint16_t*)X, W, A8, AMAX, CODE2, offset, LUT, (uint16_t*)Y,
                        (const uint16_t*)R, epi, M, K, N, bs_shift, bs2_shift);
   else
-    hipLaunchKernelGGL((nf4_gemm_kernel<DT, BM, BN, WM, WN, false, PF>), grid, dim3(GEMM_THREADS), 0, st,
+    hipLaunchKernelGGL((nf4_gemm_kernel<DT, BM, BN, WM, WN, false, PF>), grid, dim3(64 * WM * WN), 0, st,
                        (const uint16_t*)X, W, A8, AMAX, CODE2, offset, LUT, (uint16_t*)Y,
                        (const uint16_t*)R, epi, M, K, N, bs_shift, bs2_shift);
 }
@@ -295,18 +298,20 @@ int gemm_mfma(const void* X, int dt, const uint8_t* W, const uint8_t* A8, const 
        : launch_gemm<DTV, BMV, BNV, WMV, WNV, 2>(X, W, A8, AMAX, CODE2, offset, LUT, Y, R, epi, M, K, N,    \
                                                  bs_shift, bs2_shift, st))
   // the largest tile that still gives every CU a workgroup (small M: more,
-  // smaller tiles, so the K loops of several workgroups overlap per CU)
+  // smaller tiles, so the K loops of several workgroups overlap per CU);
+  // 8 waves for the 128 x 128 and 64 x 128 tiles (two a SIMD: one wave's
+  // dequantisation runs while the other's matrix products do)
   const auto tiles = [&](int bm, int bn) { return (long long)((M + bm - 1) / bm) * ((N + bn - 1) / bn); };
   const int shape = N <= 32 ? 0 : tiles(128, 128) >= 256 ? 1 : tiles(64, 128) >= 256 ? 2 : 3;
   if (dt == DT_BF16) {
     if (shape == 0) TTSP_G(DT_BF16, 128, 32, 4, 1);
-    else if (shape == 1) TTSP_G(DT_BF16, 128, 128, 2, 2);
-    else if (shape == 2) TTSP_G(DT_BF16, 64, 128, 2, 2);
+    else if (shape == 1) TTSP_G(DT_BF16, 128, 128, 4, 2);
+    else if (shape == 2) TTSP_G(DT_BF16, 64, 128, 2, 4);
     else TTSP_G(DT_BF16, 64, 64, 2, 2);
   } else if (dt == DT_F16) {
     if (shape == 0) TTSP_G(DT_F16, 128, 32, 4, 1);
-    else if (shape == 1) TTSP_G(DT_F16, 128, 128, 2, 2);
-    else if (shape == 2) TTSP_G(DT_F16, 64, 128, 2, 2);
+    else if (shape == 1) TTSP_G(DT_F16, 128, 128, 4, 2);
+    else if (shape == 2) TTSP_G(DT_F16, 64, 128, 2, 4);
     else TTSP_G(DT_F16, 64, 64, 2, 2);
   } else {
     return (int)hipErrorInvalidValue;
