@@ -286,15 +286,18 @@ def bench_gemm(rows: int = 512, copies: int = 4, reps: int = 20):
         lins = [Linear(M, K, True, seed=500 + 10 * i + c, device=dev) for c in range(copies)]
         x = torch.randn(rows, K, device=dev).to(torch.bfloat16)
         y = torch.empty(rows, M, dtype=torch.bfloat16, device=dev)
+        # the K split nf4gemv.matmul uses for this shape (fp32 partials in a workspace)
+        splits = lib.ttsp_nf4_gemm_splits(M, K, rows)
+        work = torch.empty(splits * rows * M, dtype=torch.float32, device=dev)
 
         def body():
             st = torch.cuda.current_stream().cuda_stream
             for lin in lins:
-                rc = lib.ttsp_nf4_gemm(x.data_ptr(), _lib.DT_BF16, lin.w.data_ptr(), _lib.ptr(lin.a8),
-                                       lin.amax.data_ptr(), _lib.ptr(lin.code2), lin.offset, lut.data_ptr(),
-                                       y.data_ptr(), 0, 0, M, K, rows, 64, 256, st)
+                rc = lib.ttsp_nf4_gemm_split(x.data_ptr(), _lib.DT_BF16, lin.w.data_ptr(), _lib.ptr(lin.a8),
+                                             lin.amax.data_ptr(), _lib.ptr(lin.code2), lin.offset, lut.data_ptr(),
+                                             y.data_ptr(), 0, 0, M, K, rows, 64, 256, work.data_ptr(), splits, st)
                 if rc:
-                    raise RuntimeError(f"ttsp_nf4_gemm failed: {rc}")
+                    raise RuntimeError(f"ttsp_nf4_gemm_split failed: {rc}")
 
         body()
         torch.cuda.synchronize()
@@ -303,7 +306,7 @@ def bench_gemm(rows: int = 512, copies: int = 4, reps: int = 20):
         time_graph(graph, 2, stream)
         sec = time_graph(graph, reps, stream) / copies
         flop = 2 * rows * M * K
-        res.append({"name": name, "M": M, "K": K, "us": round(sec * 1e6, 2),
+        res.append({"name": name, "M": M, "K": K, "k_splits": splits, "us": round(sec * 1e6, 2),
                     "tflops": round(flop / sec / 1e12, 1)})
         total_s += sec
         total_flop += flop

@@ -45,6 +45,23 @@ int ttsp_nf4_gemm(const void* X, int x_dtype, const uint8_t* W, const uint8_t* A
                   const void* R, int epi, int M, int K, int N, int blocksize, int blocksize2,
                   void* stream);
 
+/* How many K splits ttsp_nf4_gemm_split uses for this shape (1: none, then no
+ * workspace is needed). The split is chosen so the output tiles times the
+ * splits give every CU a workgroup. Host-only. Replaces: the reference's
+ * slicing of the rows into MAX_N = 32 launches (app/engine/nf4gemv.py:460-477),
+ * which it does instead of splitting K. */
+int ttsp_nf4_gemm_splits(int M, int K, int N);
+
+/* ttsp_nf4_gemm with the K loop split `splits` ways (exactly
+ * ttsp_nf4_gemm_splits(M, K, N), N > 1): each split writes fp32 partial sums
+ * to `work` (splits * N * M floats, 16-byte aligned, the caller's), and a
+ * second kernel adds them in split order, rounds and applies the epilogue.
+ * splits == 1 is ttsp_nf4_gemm. Replaces: as ttsp_nf4_gemm. */
+int ttsp_nf4_gemm_split(const void* X, int x_dtype, const uint8_t* W, const uint8_t* A8,
+                        const float* AMAX, const float* CODE2, float offset, const float* LUT,
+                        void* Y, const void* R, int epi, int M, int K, int N, int blocksize,
+                        int blocksize2, float* work, int splits, void* stream);
+
 /* The batch-1 matmuls of a decode block in one launch each (K <= 10240):
  *   W3 == NULL: Y = epi(n(X) . dequant(W1)^T), epi as ttsp_nf4_gemm;
  *   W3 != NULL: Y = round(round(silu(round(n(X) . W1^T))) * round(n(X) . W3^T)),
@@ -175,7 +192,7 @@ int ttsp_prefill_attention(const void* Q, long long q_seq_stride, long long q_he
                            const void* K, long long k_seq_stride, long long k_head_stride,
                            const void* V, long long v_seq_stride, long long v_head_stride,
                            const void* mask, long long mask_row_stride, void* Y, int S, int nh,
-                           int nkv, int L, float scale, int dtype, hipStream_t stream);
+                           int nkv, int L, float scale, int dtype, void* stream);
 
 /* Largest query heads per kv head ttsp_prefill_attention takes (8). */
 int ttsp_prefill_max_groups(void);

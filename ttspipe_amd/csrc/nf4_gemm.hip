@@ -66,7 +66,7 @@ __global__ __launch_bounds__(64 * WM * WN) void nf4_gemm_kernel(
     const uint16_t* __restrict__ X, const uint8_t* __restrict__ W, const uint8_t* __restrict__ A8,
     const float* __restrict__ AMAX, const float* __restrict__ CODE2, float offset,
     const float* __restrict__ LUT, uint16_t* __restrict__ Y, const uint16_t* __restrict__ R,
-    int epi, int M, int K, int N, int bs_shift, int bs2_shift) {
+    int epi, int M, int K, int N, int bs_shift, int bs2_shift, float* __restrict__ YP) {
   constexpr int GEMM_THREADS = 64 * WM * WN;
   constexpr int TM = BM / WM / 32, TN = BN / WN / 32;  // MFMA blocks per wave
   constexpr int A_CH = BM * (KT / 16);                                  // 8-byte packed chunks (16 codes) per step
@@ -87,7 +87,9 @@ __global__ __launch_bounds__(64 * WM * WN) void nf4_gemm_kernel(
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave / WN, wn = wave % WN;
   const int m0 = blockIdx.x * BM, n0 = blockIdx.y * BN;
-  const int nsteps = K / KT;
+  // split-K (gridDim.z > 1): workgroup z takes K-steps [z S, z S + S) and
+  // writes its fp32 partial sums to YP[z][n][m]; a second kernel adds them
+  const int nsteps = K / KT / gridDim.z, kbase = blockIdx.z * nsteps * KT;
   const size_t rowbytes = (size_t)K / 2;
 
   if (tid < 16) lut_s[tid] = LUT[tid];
@@ -104,7 +106,7 @@ __global__ __launch_bounds__(64 * WM * WN) void nf4_gemm_kernel(
 
   // step clamped into range: the loads past the last step repeat it and go unused
   auto load_step = [&](Stage& sg, int step) {
-    const int k0 = min(step, nsteps - 1) * KT;
+    const int k0 = kbase + min(step, nsteps - 1) * KT;
 #pragma unroll
     for (int i = 0; i < A_PER_T; ++i) {
       const int c = min(tid + i * GEMM_THREADS, A_CH - 1);  // chunk: row c / 4, codes 16 (c % 4) ..
@@ -209,6 +211,27 @@ __global__ __launch_bounds__(64 * WM * WN) void nf4_gemm_kernel(
     }
   }
 
+  if (YP) {  // split-K partials: 4 consecutive rows m per 16-byte store
+    float* yp = YP + (size_t)blockIdx.z * N * M;
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j) {
+        const int n = n0 + wn * (BN / WN) + j * 32 + (lane & 31);
+        if (n >= N) continue;
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const int m = m0 + wm * (BM / WM) + i * 32 + 8 * g + 4 * (lane >> 5);
+          if (m + 4 <= M) {
+            *reinterpret_cast<float4*>(yp + (size_t)n * M + m) =
+                make_float4(acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2], acc[i][j][4 * g + 3]);
+          } else {
+            for (int c = 0; c < 4 && m + c < M; ++c) yp[(size_t)n * M + m + c] = acc[i][j][4 * g + c];
+          }
+        }
+      }
+    return;
+  }
   // epilogue: accumulator r of lane l is (row 8*(r/4) + 4*(l/32) + r%4, column
   // l%32); each value is rounded to the activation type and the tile goes
   // through LDS as Y rows (the operand buffers are free after the last
@@ -272,37 +295,122 @@ __global__ __launch_bounds__(64 * WM * WN) void nf4_gemm_kernel(
   }
 }
 
+// Y[n][m] = epilogue(round(sum over z of YP[z][n][m])), the sum in z order;
+// 8 consecutive m per thread (16-byte stores when vec).
+template <int DT>
+__global__ __launch_bounds__(256) void nf4_gemm_reduce_kernel(const float* __restrict__ YP, int splits,
+                                                              uint16_t* __restrict__ Y,
+                                                              const uint16_t* __restrict__ R, int epi, int M,
+                                                              int N) {
+  const int chunks = (M + 7) / 8;
+  const long long c = (long long)blockIdx.x * 256 + threadIdx.x;
+  if (c >= (long long)chunks * N) return;
+  const int n = (int)(c / chunks), m = (int)(c % chunks) * 8;
+  const bool vec = (epi & 4) != 0;
+  const int ep = epi & 3;
+  const size_t o = (size_t)n * M + m;
+  float acc[8];
+  if (vec && m + 8 <= M) {
+    const float4* p = reinterpret_cast<const float4*>(YP + o);
+    float4 a = p[0], b = p[1];
+    for (int z = 1; z < splits; ++z) {
+      const float4* q = reinterpret_cast<const float4*>(YP + (size_t)z * N * M + o);
+      const float4 u = q[0], v = q[1];
+      a.x += u.x, a.y += u.y, a.z += u.z, a.w += u.w;
+      b.x += v.x, b.y += v.y, b.z += v.z, b.w += v.w;
+    }
+    acc[0] = a.x, acc[1] = a.y, acc[2] = a.z, acc[3] = a.w, acc[4] = b.x, acc[5] = b.y, acc[6] = b.z, acc[7] = b.w;
+    uint32_t rw[4] = {0u, 0u, 0u, 0u};
+    if (ep) {
+      const uint4 rv = *reinterpret_cast<const uint4*>(R + o);
+      rw[0] = rv.x, rw[1] = rv.y, rw[2] = rv.z, rw[3] = rv.w;
+    }
+    uint32_t ow[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      uint32_t h2[2];
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        const float y = Elem<DT>::load(Elem<DT>::store(acc[2 * q + u]));
+        const float r = Elem<DT>::load(rw[q] >> (16 * u));
+        float v = y;
+        if (ep == 1) v = __fadd_rn(r, y);
+        else if (ep == 2) v = __fmul_rn(Elem<DT>::load(Elem<DT>::store(silu_rn(r))), y);
+        h2[u] = Elem<DT>::store(v);
+      }
+      ow[q] = h2[0] | (h2[1] << 16);
+    }
+    *reinterpret_cast<uint4*>(Y + o) = make_uint4(ow[0], ow[1], ow[2], ow[3]);
+  } else {
+    for (int u = 0; u < 8 && m + u < M; ++u) {
+      float a = YP[o + u];
+      for (int z = 1; z < splits; ++z) a += YP[(size_t)z * N * M + o + u];
+      const float y = Elem<DT>::load(Elem<DT>::store(a));
+      float v = y;
+      if (ep == 1) v = __fadd_rn(Elem<DT>::load(R[o + u]), y);
+      else if (ep == 2) v = __fmul_rn(Elem<DT>::load(Elem<DT>::store(silu_rn(Elem<DT>::load(R[o + u])))), y);
+      Y[o + u] = Elem<DT>::store(v);
+    }
+  }
+}
+
 template <int DT, int BM, int BN, int WM, int WN, int PF>
 static void launch_gemm(const void* X, const uint8_t* W, const uint8_t* A8, const float* AMAX,
                         const float* CODE2, float offset, const float* LUT, void* Y, const void* R,
-                        int epi, int M, int K, int N, int bs_shift, int bs2_shift, hipStream_t st) {
-  const dim3 grid((M + BM - 1) / BM, (N + BN - 1) / BN);
+                        int epi, int M, int K, int N, int bs_shift, int bs2_shift, float* YP, int splits,
+                        hipStream_t st) {
+  const dim3 grid((M + BM - 1) / BM, (N + BN - 1) / BN, splits);
   if (A8)
     hipLaunchKernelGGL((nf4_gemm_kernel<DT, BM, BN, WM, WN, true, PF>), grid, dim3(64 * WM * WN), 0, st,
                        (const uint16_t*)X, W, A8, AMAX, CODE2, offset, LUT, (uint16_t*)Y,
-                       (const uint16_t*)R, epi, M, K, N, bs_shift, bs2_shift);
+                       (const uint16_t*)R, epi, M, K, N, bs_shift, bs2_shift, YP);
   else
     hipLaunchKernelGGL((nf4_gemm_kernel<DT, BM, BN, WM, WN, false, PF>), grid, dim3(64 * WM * WN), 0, st,
                        (const uint16_t*)X, W, A8, AMAX, CODE2, offset, LUT, (uint16_t*)Y,
-                       (const uint16_t*)R, epi, M, K, N, bs_shift, bs2_shift);
+                       (const uint16_t*)R, epi, M, K, N, bs_shift, bs2_shift, YP);
+}
+
+// Tile shape and K-split of a launch: unsplit with the largest tile (128 x
+// 128, then 64 x 128) that gives every CU a workgroup; else the largest tile
+// that does with the fewest splits (2, 4, 8; each split at least 8 K-steps,
+// an even number); otherwise 64 x 64 tiles, unsplit. Rows <= 32 take the
+// 128 x 32 tile. (Measured on the 512-row layer: a split costs more than a
+// smaller tile while the smaller tile still fills the GPU.)
+struct GemmPlan {
+  int shape, splits;
+};
+static GemmPlan gemm_plan(int M, int K, int N) {
+  if (N <= 32) return {0, 1};
+  const int steps = K / KT;
+  const auto tiles = [&](int bm, int bn) { return (long long)((M + bm - 1) / bm) * ((N + bn - 1) / bn); };
+  const int shapes[2][3] = {{1, 128, 128}, {2, 64, 128}};
+  for (const auto& sh : shapes)
+    if (tiles(sh[1], sh[2]) >= 256) return {sh[0], 1};
+  for (const auto& sh : shapes)
+    for (int sp = 2; sp <= 8; sp *= 2) {
+      if (steps % (2 * sp) || steps / sp < 8) break;
+      if (tiles(sh[1], sh[2]) * sp >= 256) return {sh[0], sp};
+    }
+  return {3, 1};
 }
 
 int gemm_mfma(const void* X, int dt, const uint8_t* W, const uint8_t* A8, const float* AMAX,
               const float* CODE2, float offset, const float* LUT, void* Y, const void* R, int epi,
-              int M, int K, int N, int bs_shift, int bs2_shift, hipStream_t st) {
+              int M, int K, int N, int bs_shift, int bs2_shift, const GemmPlan& plan, float* YP,
+              hipStream_t st) {
   if (K % (2 * KT)) return (int)hipErrorInvalidValue;
-  const bool pf4 = (K / KT) % 4 == 0;
+  const int splits = plan.splits;
+  if (splits > 1 && (!YP || (K / KT) % (2 * splits))) return (int)hipErrorInvalidValue;
+  float* yp = splits > 1 ? YP : nullptr;
+  const bool pf4 = (K / KT / splits) % 4 == 0;
 #define TTSP_G(DTV, BMV, BNV, WMV, WNV)                                                                     \
   (pf4 ? launch_gemm<DTV, BMV, BNV, WMV, WNV, 4>(X, W, A8, AMAX, CODE2, offset, LUT, Y, R, epi, M, K, N,    \
-                                                 bs_shift, bs2_shift, st)                                   \
+                                                 bs_shift, bs2_shift, yp, splits, st)                       \
        : launch_gemm<DTV, BMV, BNV, WMV, WNV, 2>(X, W, A8, AMAX, CODE2, offset, LUT, Y, R, epi, M, K, N,    \
-                                                 bs_shift, bs2_shift, st))
-  // the largest tile that still gives every CU a workgroup (small M: more,
-  // smaller tiles, so the K loops of several workgroups overlap per CU);
+                                                 bs_shift, bs2_shift, yp, splits, st))
   // 8 waves for the 128 x 128 and 64 x 128 tiles (two a SIMD: one wave's
   // dequantisation runs while the other's matrix products do)
-  const auto tiles = [&](int bm, int bn) { return (long long)((M + bm - 1) / bm) * ((N + bn - 1) / bn); };
-  const int shape = N <= 32 ? 0 : tiles(128, 128) >= 256 ? 1 : tiles(64, 128) >= 256 ? 2 : 3;
+  const int shape = plan.shape;
   if (dt == DT_BF16) {
     if (shape == 0) TTSP_G(DT_BF16, 128, 32, 4, 1);
     else if (shape == 1) TTSP_G(DT_BF16, 128, 128, 4, 2);
@@ -317,6 +425,16 @@ int gemm_mfma(const void* X, int dt, const uint8_t* W, const uint8_t* A8, const 
     return (int)hipErrorInvalidValue;
   }
 #undef TTSP_G
+  if (splits > 1) {
+    const long long chunks = (long long)((M + 7) / 8) * N;
+    const dim3 rg((unsigned)((chunks + 255) / 256));
+    if (dt == DT_BF16)
+      hipLaunchKernelGGL(nf4_gemm_reduce_kernel<DT_BF16>, rg, dim3(256), 0, st, YP, splits, (uint16_t*)Y,
+                         (const uint16_t*)R, epi, M, N);
+    else
+      hipLaunchKernelGGL(nf4_gemm_reduce_kernel<DT_F16>, rg, dim3(256), 0, st, YP, splits, (uint16_t*)Y,
+                         (const uint16_t*)R, epi, M, N);
+  }
   TTSP_RETURN_LAUNCH();
 }
 
@@ -328,26 +446,64 @@ int gemv_n1(const void* X, int dt, const uint8_t* W, const uint8_t* A8, const fl
 
 using namespace ttsp;
 
+// Argument checks shared by the entry points; fills the scale shifts.
+static int gemm_args(const void* X, const uint8_t* W, const uint8_t* A8, const float* AMAX, const float* CODE2,
+                     const float* LUT, void* Y, const void* R, int epi, int M, int K, int N, int blocksize,
+                     int blocksize2, int* bs_shift, int* bs2_shift) {
+  if (N <= 0 || M <= 0 || K <= 0 || !X || !W || !AMAX || !LUT || !Y) return (int)hipErrorInvalidValue;
+  if (A8 && !CODE2) return (int)hipErrorInvalidValue;
+  *bs_shift = 0, *bs2_shift = 0;
+  while ((1 << *bs_shift) < blocksize) ++*bs_shift;
+  if (A8)
+    while ((1 << *bs2_shift) < blocksize2) ++*bs2_shift;
+  if ((1 << *bs_shift) != blocksize || *bs_shift < 6 || (A8 && (1 << *bs2_shift) != blocksize2))
+    return (int)hipErrorInvalidValue;
+  if (K % 128 || K % blocksize || epi < 0 || epi > 2 || (epi && !R)) return (int)hipErrorInvalidValue;
+  return 0;
+}
+
 // One entry for every row count: one row takes the bandwidth-bound GEMV,
-// more rows the MFMA kernel (weights read once per BN rows).
+// more rows the MFMA kernel (weights read once per BN rows), unsplit.
 extern "C" int ttsp_nf4_gemm(const void* X, int x_dtype, const uint8_t* W, const uint8_t* A8,
                              const float* AMAX, const float* CODE2, float offset, const float* LUT,
                              void* Y, const void* R, int epi, int M, int K, int N, int blocksize,
                              int blocksize2, hipStream_t stream) {
-  if (N <= 0 || M <= 0 || K <= 0 || !X || !W || !AMAX || !LUT || !Y) return (int)hipErrorInvalidValue;
-  if (A8 && !CODE2) return (int)hipErrorInvalidValue;
-  if (N == 1)
+  if (N == 1 && N > 0 && M > 0 && K > 0 && X && W && AMAX && LUT && Y && (!A8 || CODE2))
     return gemv_n1(X, x_dtype, W, A8, AMAX, CODE2, offset, LUT, Y, R, epi, M, K, blocksize,
                    blocksize2, stream);
-  int bs_shift = 0, bs2_shift = 0;
-  while ((1 << bs_shift) < blocksize) ++bs_shift;
-  if (A8)
-    while ((1 << bs2_shift) < blocksize2) ++bs2_shift;
-  if ((1 << bs_shift) != blocksize || bs_shift < 6 || (A8 && (1 << bs2_shift) != blocksize2))
-    return (int)hipErrorInvalidValue;
-  if (K % 128 || K % blocksize || epi < 0 || epi > 2 || (epi && !R)) return (int)hipErrorInvalidValue;
+  int bs_shift, bs2_shift;
+  if (int rc = gemm_args(X, W, A8, AMAX, CODE2, LUT, Y, R, epi, M, K, N, blocksize, blocksize2, &bs_shift,
+                         &bs2_shift))
+    return rc;
   // vectorised output rows: 8 elements per 16-byte store
   const bool vec = M % 8 == 0 && (uintptr_t)Y % 16 == 0 && (!epi || (uintptr_t)R % 16 == 0);
+  // unsplit: the largest tile that still gives every CU a workgroup
+  const auto tiles = [&](int bm, int bn) { return (long long)((M + bm - 1) / bm) * ((N + bn - 1) / bn); };
+  const GemmPlan plan{N <= 32 ? 0 : tiles(128, 128) >= 256 ? 1 : tiles(64, 128) >= 256 ? 2 : 3, 1};
   return gemm_mfma(X, x_dtype, W, A8, AMAX, CODE2, offset, LUT, Y, R, epi | (vec ? 4 : 0), M, K, N, bs_shift,
-                   bs2_shift, stream);
+                   bs2_shift, plan, nullptr, stream);
+}
+
+extern "C" int ttsp_nf4_gemm_splits(int M, int K, int N) {
+  if (M <= 0 || K <= 0 || N <= 1 || K % 128) return 1;
+  return gemm_plan(M, K, N).splits;
+}
+
+extern "C" int ttsp_nf4_gemm_split(const void* X, int x_dtype, const uint8_t* W, const uint8_t* A8,
+                                   const float* AMAX, const float* CODE2, float offset, const float* LUT,
+                                   void* Y, const void* R, int epi, int M, int K, int N, int blocksize,
+                                   int blocksize2, float* work, int splits, hipStream_t stream) {
+  if (N <= 1 || splits < 1 || splits != ttsp_nf4_gemm_splits(M, K, N))
+    return (int)hipErrorInvalidValue;
+  if (splits == 1)
+    return ttsp_nf4_gemm(X, x_dtype, W, A8, AMAX, CODE2, offset, LUT, Y, R, epi, M, K, N, blocksize,
+                         blocksize2, stream);
+  int bs_shift, bs2_shift;
+  if (int rc = gemm_args(X, W, A8, AMAX, CODE2, LUT, Y, R, epi, M, K, N, blocksize, blocksize2, &bs_shift,
+                         &bs2_shift))
+    return rc;
+  if (!work || (uintptr_t)work % 16) return (int)hipErrorInvalidValue;
+  const bool vec = M % 8 == 0 && (uintptr_t)Y % 16 == 0 && (!epi || (uintptr_t)R % 16 == 0);
+  return gemm_mfma(X, x_dtype, W, A8, AMAX, CODE2, offset, LUT, Y, R, epi | (vec ? 4 : 0), M, K, N, bs_shift,
+                   bs2_shift, gemm_plan(M, K, N), work, stream);
 }

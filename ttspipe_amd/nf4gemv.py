@@ -194,10 +194,21 @@ def matmul(module, x, *, epi: int = EPI_NONE, operand=None, out=None):
         out = torch.empty((rows, M), dtype=x.dtype, device=x.device)
     elif out.dtype != x.dtype or out.numel() != rows * M or not out.is_contiguous():
         return None
-    rc = _lib.lib().ttsp_nf4_gemm(
-        flat.data_ptr(), dt, fast["w"], fast["a8"], fast["amax"], fast["code2"], fast["offset"],
-        fast["lut"].data_ptr(), out.data_ptr(), _lib.ptr(operand) if epi else 0, epi, M, K, rows,
-        fast["bs"], fast["bs2"], _lib.stream())
+    lib = _lib.lib()
+    splits = lib.ttsp_nf4_gemm_splits(M, K, rows) if rows > 1 else 1
+    if splits > 1:
+        # K split over workgroups (too few output tiles to fill the GPU): fp32
+        # partials in a workspace, summed in split order by a second kernel
+        work = torch.empty(splits * rows * M, dtype=torch.float32, device=x.device)
+        rc = lib.ttsp_nf4_gemm_split(
+            flat.data_ptr(), dt, fast["w"], fast["a8"], fast["amax"], fast["code2"], fast["offset"],
+            fast["lut"].data_ptr(), out.data_ptr(), _lib.ptr(operand) if epi else 0, epi, M, K, rows,
+            fast["bs"], fast["bs2"], work.data_ptr(), splits, _lib.stream())
+    else:
+        rc = lib.ttsp_nf4_gemm(
+            flat.data_ptr(), dt, fast["w"], fast["a8"], fast["amax"], fast["code2"], fast["offset"],
+            fast["lut"].data_ptr(), out.data_ptr(), _lib.ptr(operand) if epi else 0, epi, M, K, rows,
+            fast["bs"], fast["bs2"], _lib.stream())
     if rc:
         raise RuntimeError(f"ttsp_nf4_gemm failed: hipError_t {rc}")
     _stats["fast"] += 1
