@@ -404,7 +404,8 @@ def main() -> int:
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--skip-cpu", action="store_true")
     ap.add_argument("--skip-decode", action="store_true")
-    ap.add_argument("--only", choices=["layer", "kernel", "c1", "copy", "decode", "gemm", "pattn"], default=None,
+    ap.add_argument("--only", choices=["layer", "kernel", "c1", "copy", "decode", "gemm", "pattn", "prefill"],
+                    default=None,
                     help="run one GPU measurement only (for profiling runs)")
     ap.add_argument("--decode-steps", type=int, default=256, help="greedy frames the decode benchmark times")
     ap.add_argument("--cpu-decode-frames", type=int, default=3, help="frames the CPU baseline's decode times")
@@ -433,6 +434,10 @@ def main() -> int:
         out["gemm"] = bench_gemm()
     if args.only in (None, "pattn"):
         out["pattn"] = bench_prefill_attention()
+    if args.only in (None, "prefill"):
+        from ttspipe_amd import dualar
+
+        out["prefill"] = dualar.prefill_benchmark(512)
     decode = None
     if args.only in (None, "decode") and not args.skip_decode:
         from ttspipe_amd import dualar
@@ -493,6 +498,7 @@ def main() -> int:
         "decode": decode,
         "prefill_gemm": out["gemm"],
         "prefill_attention": out["pattn"],
+        "prefill_512": out["prefill"],
         "cpu_baseline": cpu,
     }
     print(json.dumps(line))

@@ -68,6 +68,27 @@ class DualARConfig:
         return 1 + self.num_codebooks
 
 
+#: Padded span lengths a prompt is prefilled at; longer prompts go through in
+#: spans of the largest (the reference's buckets stop at 32 because its MMA
+#: kernel takes at most 32 rows, graphs.py:137; the GEMM here takes any).
+PREFILL_BUCKETS = (16, 32, 64, 128, 256, 512)
+
+def prefill_spans(n: int):
+    """(offset, real length, bucket) of each span an n-token prompt is
+    prefilled in: spans of the largest bucket, the rest padded to the
+    smallest bucket that holds it (reference: graphs.py:316-320)."""
+    if n <= 0:
+        return []
+    top = PREFILL_BUCKETS[-1]
+    full = (n - 1) // top
+    sizes = [top] * full + [n - top * full]
+    out, off = [], 0
+    for size in sizes:
+        out.append((off, size, next(b for b in PREFILL_BUCKETS if b >= size)))
+        off += size
+    return out
+
+
 SMALL = DualARConfig(dim=512, n_layer=3, n_head=4, n_local_heads=2, intermediate_size=1024,
                      vocab_size=512, fast_dim=256, fast_n_layer=2, fast_n_head=2, fast_n_local_heads=1,
                      fast_intermediate_size=512, num_codebooks=4, codebook_size=512, max_seq_len=320,
@@ -279,6 +300,10 @@ class SyntheticDualAR:
         self.fast_h = torch.empty(1, 1, cfg.fast_dim, dtype=bf, device=dev)
         self.fast_logits = torch.empty(1, cfg.codebook_size, dtype=bf, device=dev)
         self.graph = None
+        # prompt prefill: the fork's causal mask rows, one captured graph per bucket
+        self.causal = torch.tril(torch.ones(cfg.max_seq_len, cfg.max_seq_len, dtype=torch.bool, device=dev))
+        self.prefill_graphs = {}
+        self.prefill_token = torch.zeros(1, dtype=torch.int32, device=dev)
         self.reset()
 
     # ------------------------------------------------------------------ state
@@ -378,6 +403,82 @@ class SyntheticDualAR:
         self.step_index.add_(1)
         self.pos.add_(1)
 
+    # ---------------------------------------------------------------- prefill
+
+    def prefill_forward(self, inp, pos, last) -> None:
+        """The slow transformer over a prompt span: `inp` (n_tokens, n) int32
+        token rows at positions `pos` (n,) int64 write their KV entries; the
+        final norm and output head run on span index `last` (1,) int64, whose
+        greedy token lands in `prefill_token` and logits in `logits`
+        (reference: DecodeGraphs._prefill_body, graphs.py:219-231, through
+        BaseTransformer.forward_generate with the whole cache as the window)."""
+        import torch
+
+        cfg = self.cfg
+        n = inp.shape[1]
+        rows = torch.clamp(inp.long(), 0, cfg.vocab_size - 1)
+        rows = rows + (torch.arange(cfg.n_tokens, device=inp.device) * cfg.vocab_size).view(-1, 1)
+        emb = self.tensors["embeddings"].view(-1, cfg.dim).index_select(0, rows.reshape(-1))
+        x = emb.view(cfg.n_tokens, n, cfg.dim).float().sum(0).to(self.dtype).view(1, n, cfg.dim)
+        freqs = self.freqs.index_select(0, pos)
+        mask = self.causal.index_select(0, pos).view(1, 1, n, cfg.max_seq_len)
+        for blk in self.layers:
+            x = blk(x, freqs, mask, pos)
+        h = x.index_select(1, last)
+        self._fused(self.output, h, self.tensors["norm"], cfg.norm_eps, self.logits)
+        rc = self._lib.ttsp_argmax(self.logits.data_ptr(), cfg.vocab_size, _lib.DT_BF16, self.prefill_token.data_ptr(),
+                                   _lib.stream())
+        self._check(rc, "ttsp_argmax")
+
+    def capture_prefill(self, buckets=None) -> None:
+        """One graph per padded span length (after an eager warm-up of each)."""
+        import torch
+
+        for b in buckets or PREFILL_BUCKETS:
+            if b in self.prefill_graphs:
+                continue
+            inp = torch.zeros(self.cfg.n_tokens, b, dtype=torch.int32, device=self.device)
+            pos = torch.arange(b, dtype=torch.long, device=self.device)
+            last = torch.zeros(1, dtype=torch.long, device=self.device)
+            self.prefill_forward(inp, pos, last)
+            torch.cuda.synchronize()
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g):
+                self.prefill_forward(inp, pos, last)
+            self.prefill_graphs[b] = (g, inp, pos, last)
+
+    def prefill(self, tokens, start: int, graphed: bool = True) -> bool:
+        """KV entries for `tokens` (n_tokens, n) int32 at [start, start + n),
+        in spans of the largest bucket and a last span padded to a bucket (the
+        padding repeats the last real token; its KV entries land past the
+        prompt, where decoding overwrites them before reading them); the last
+        real position's token in `prefill_token`. False (nothing done) when
+        the padded span runs past the cache (reference: graphs.py:304-335)."""
+        import torch
+
+        n = tokens.shape[-1]
+        spans = prefill_spans(n)
+        if not spans or start + spans[-1][0] + spans[-1][2] > self.cfg.max_seq_len:
+            return False
+        for off, size, b in spans:
+            if graphed:
+                if b not in self.prefill_graphs:
+                    self.capture_prefill([b])
+                g, inp, pos, last = self.prefill_graphs[b]
+            else:
+                inp = torch.empty(self.cfg.n_tokens, b, dtype=torch.int32, device=self.device)
+                pos = torch.empty(b, dtype=torch.long, device=self.device)
+                last = torch.empty(1, dtype=torch.long, device=self.device)
+            inp[:, :size].copy_(tokens[:, off:off + size])
+            inp[:, size:].copy_(tokens[:, off + size - 1:off + size].expand(-1, b - size))
+            torch.arange(start + off, start + off + b, out=pos)
+            last.fill_(size - 1)
+            if graphed:
+                g.replay()
+            else:
+                self.prefill_forward(inp, pos, last)
+        return True
+
     def capture(self) -> None:
         """Record one step as a HIP graph (after a warm-up step outside capture)."""
         import torch
@@ -461,3 +562,30 @@ def benchmark(n_steps: int = 256, warmup: int = 8, cfg: DualARConfig = DualARCon
                       f"FFN {cfg.intermediate_size}), fast {cfg.fast_n_layer}x d{cfg.fast_dim} "
                       f"({cfg.fast_n_head}q/{cfg.fast_n_local_heads}kv, FFN {cfg.fast_intermediate_size}), "
                       f"{cfg.num_codebooks} codebooks of {cfg.codebook_size}, KV from {cfg.prefill_len}"}
+
+
+def prefill_benchmark(n_tokens: int = 512, reps: int = 5, cfg: DualARConfig = DualARConfig()) -> dict:
+    """ms to prefill an `n_tokens` prompt (one captured bucket graph per span)
+    through the slow transformer, from position 0, synthetic tokens."""
+    import torch
+
+    model = SyntheticDualAR(cfg)
+    g = torch.Generator(device=model.device).manual_seed(cfg.seed)
+    toks = torch.randint(0, cfg.codebook_size, (cfg.n_tokens, n_tokens), generator=g, device=model.device,
+                         dtype=torch.int32)
+    model.capture_prefill(sorted({b for _, _, b in prefill_spans(n_tokens)}))
+    assert model.prefill(toks, 0)
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record(stream)
+    for _ in range(reps):
+        model.prefill(toks, 0)
+    end.record(stream)
+    end.synchronize()
+    ms = start.elapsed_time(end) / reps
+    token = int(model.prefill_token.item())
+    del model
+    torch.cuda.empty_cache()
+    return {"tokens": n_tokens, "ms": round(ms, 3), "tokens_per_s": round(n_tokens / ms * 1e3, 1),
+            "first_token": token, "layers": cfg.n_layer}

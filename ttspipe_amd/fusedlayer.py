@@ -25,8 +25,15 @@ Rounding follows the fork: wherever it produces a 16-bit tensor, so does this
 (reference: fusedlayer.py:56-159, 212-269). Every reduction has a fixed order,
 so a step's output is a deterministic function of its inputs.
 
-Only a single position (B = S = 1) takes this path; anything else returns
-None and the block's own forward runs.
+Only a single position (B = S = 1) takes this path. Several positions (a
+prompt prefill) take `prefill_block`: the same block as NF4 GEMMs with the
+residual adds and the SwiGLU gate in their epilogues, the fork's norms and
+rotary as HIP kernels, and the whole causal attention in one launch
+(`fastpath.prefill_attention`) - seven GEMM launches, four norm/rotary
+launches and one attention launch around the fork's q/k head norms. The
+reference has no fused prefill block (it declines S > 1, fusedlayer.py:198)
+and runs the unpatched block; the results agree with that order up to the
+roundings the epilogues keep (tests compare the layer output).
 """
 
 from __future__ import annotations
@@ -41,7 +48,7 @@ HEAD_DIM = 128
 #: Cache positions per attention workgroup (the kernel's ACHUNK).
 CHUNK = 64
 
-_stats = {"fused": 0, "fallback": 0}
+_stats = {"fused": 0, "fallback": 0, "prefill": 0}
 _installed = False
 
 
@@ -210,6 +217,77 @@ def _block_classes():
     return classes
 
 
+def _prefill_eligible(block, x, mask, input_pos) -> bool:
+    import torch
+
+    from ttspipe_amd import nf4gemv
+
+    a, ff = block.attention, block.feed_forward
+    if x.dim() != 3 or x.shape[0] != 1 or x.shape[1] < 2:
+        return False
+    if x.dtype not in (torch.float16, torch.bfloat16) or x.device.type != "cuda" or not x.is_contiguous():
+        return False
+    if mask is None or input_pos is None or input_pos.numel() != x.shape[1] or a.kv_cache is None:
+        return False
+    if a.head_dim != HEAD_DIM or a.n_head % a.n_local_heads:
+        return False
+    for linear in (a.wqkv, a.wo, ff.w1, ff.w2, ff.w3):
+        if getattr(linear, "bias", None) is not None or not nf4gemv.prepare(linear):
+            return False
+    return True
+
+
+def prefill_block(block, x, freqs_cis, mask, input_pos):
+    """`TransformerBlock.forward` for several positions (B = 1, S > 1), or None.
+
+    The fork's block in its own order with the prefill kernels: RMSNorm,
+    wqkv GEMM, q/k head norms (the fork's modules), rotary, KV-cache write,
+    one-launch causal attention, wo GEMM with the residual add in its
+    epilogue, RMSNorm, w1 GEMM, w3 GEMM with the SwiGLU gate in its epilogue,
+    w2 GEMM with the residual add (reference: the unfused block the reference
+    runs for S > 1, fastpath.py:207-271 and fusedlayer.py:198).
+    """
+    from ttspipe_amd import fastpath, fusedops, nf4gemv
+    from ttspipe_amd.llama import apply_rotary_emb
+
+    if not _lib.gpu_present() or not _prefill_eligible(block, x, mask, input_pos):
+        return None
+    a, ff = block.attention, block.feed_forward
+    bsz, n, _ = x.shape
+    nh, nkv, hd = a.n_head, a.n_local_heads, a.head_dim
+    an, fn = block.attention_norm, block.ffn_norm
+    xn = fusedops.rms_norm(x, an.weight, an.eps)
+    qkv = None if xn is None else nf4gemv.matmul(a.wqkv, xn)
+    if qkv is None:
+        return None
+    q, k, v = qkv.split([nh * hd, nkv * hd, nkv * hd], dim=-1)
+    q, k, v = q.view(bsz, n, nh, hd), k.view(bsz, n, nkv, hd), v.view(bsz, n, nkv, hd)
+    if a.attention_qk_norm:
+        q, k = a.q_norm(q), a.k_norm(k)
+    fq = fusedops.rope(q, freqs_cis)
+    fk = fusedops.rope(k, freqs_cis) if fq is not None else None
+    if fk is None:
+        fusedops.note_rope_fallback()
+        fq, fk = apply_rotary_emb(q, freqs_cis), apply_rotary_emb(k, freqs_cis)
+    q, k, v = (t.transpose(1, 2) for t in (fq, fk, v))
+    k, v = a.kv_cache.update(input_pos, k, v)
+    if mask.shape[-1] < k.shape[2]:
+        k, v = k[:, :, : mask.shape[-1]], v[:, :, : mask.shape[-1]]
+    y = fastpath.prefill_attention(q, k, v, mask, nh, nkv, hd)
+    if y is None:
+        y = fastpath.decode_attention(q, k, v, mask, nh, nkv, hd)
+    y = y.transpose(1, 2).contiguous().view(bsz, n, nh * hd)
+    h = nf4gemv.matmul(a.wo, y, epi=nf4gemv.EPI_RESIDUAL, operand=x)
+    hn = None if h is None else fusedops.rms_norm(h, fn.weight, fn.eps)
+    g = None if hn is None else nf4gemv.matmul(ff.w1, hn)
+    u = None if g is None else nf4gemv.matmul(ff.w3, hn, epi=nf4gemv.EPI_SILU_GATE, operand=g)
+    out = None if u is None else nf4gemv.matmul(ff.w2, u, epi=nf4gemv.EPI_RESIDUAL, operand=h)
+    if out is None:
+        raise RuntimeError("prefill_block: a GEMM declined after the KV cache was written")
+    _stats["prefill"] += 1
+    return out
+
+
 def install() -> bool:
     """Route single-position `TransformerBlock.forward` calls through `decode_block`."""
     global _installed
@@ -223,6 +301,8 @@ def install() -> bool:
 
         def forward(self, x, freqs_cis, mask, input_pos=None, _original=original):
             out = decode_block(self, x, freqs_cis, mask, input_pos)
+            if out is None and x.dim() == 3 and x.shape[1] > 1:
+                out = prefill_block(self, x, freqs_cis, mask, input_pos)
             if out is not None:
                 return out
             if x.shape[1] == 1:
