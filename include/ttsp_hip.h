@@ -115,6 +115,17 @@ int ttsp_qk_rope_kv(const void* QKV, const void* QW, const void* KW, float eps, 
                     int ftype, const long long* POS, void* Q, void* KC, void* VC, int nh, int nkv,
                     int max_len, int dtype, void* stream);
 
+/* ttsp_qk_rope_kv for `rows` positions at once (a prompt prefill): row r
+ * reads QKV + r*qkv_row_stride (elements, >= (nh + 2*nkv)*128), its rotary
+ * row F + r*128 elements and POS[r], and writes Q + r*nh*128 and cache
+ * position POS[r]; rows <= 65535. Same arithmetic per row as the one-position
+ * entry. Replaces: the q/k head norms, apply_rotary_emb and KVCache.update of
+ * the block's forward for S > 1 (fastpath.py:216-234), which the reference
+ * runs as torch ops. */
+int ttsp_qk_rope_kv_rows(const void* QKV, long long qkv_row_stride, const void* QW, const void* KW,
+                         float eps, const void* F, int ftype, const long long* POS, void* Q, void* KC,
+                         void* VC, int nh, int nkv, int max_len, int rows, int dtype, void* stream);
+
 /* Grouped-query decode attention of Q [nh*128] over cache positions
  * [0, min(POS[0] + 1, max_len)), split into nchunk chunks of
  * ttsp_attn_chunk() positions, then merged: Y [nh*128]. Scratch (caller's):

@@ -30,11 +30,16 @@ __global__ __launch_bounds__(HD) void qk_rope_kv_kernel(
     const uint16_t* __restrict__ QKV, const uint16_t* __restrict__ QW,
     const uint16_t* __restrict__ KW, float eps, const void* __restrict__ F, int ftype,
     const long long* __restrict__ POS, uint16_t* __restrict__ Q, uint16_t* __restrict__ KC,
-    uint16_t* __restrict__ VC, int nh, int nkv, int max_len) {
+    uint16_t* __restrict__ VC, int nh, int nkv, int max_len, int qkv_rs) {
   __shared__ float sx[HD];
   __shared__ float part[HD / 64];
+  // row blockIdx.y of a run of positions: its QKV row, rotary row and Q row
+  const int row = blockIdx.y;
+  QKV += (size_t)row * qkv_rs;
+  Q += (size_t)row * nh * HD;
+  F = (const uint8_t*)F + (size_t)row * HD * (ftype == DT_F32 ? 4 : 2);
   const int head = blockIdx.x, d = threadIdx.x;
-  const long long pos = POS[0];
+  const long long pos = POS[row];
   if (pos < 0 || pos >= max_len) return;  // no cache slot to write: leave everything untouched
   if (head >= nh + nkv) {
     const int vh = head - nh - nkv;
@@ -354,11 +359,29 @@ extern "C" int ttsp_qk_rope_kv(const void* QKV, const void* QW, const void* KW, 
 #define TTSP_QK(DTV)                                                                            \
   hipLaunchKernelGGL(qk_rope_kv_kernel<DTV>, dim3(nh + 2 * nkv), dim3(HD), 0, stream,           \
                      (const uint16_t*)QKV, (const uint16_t*)QW, (const uint16_t*)KW, eps, F, ftype, \
-                     POS, (uint16_t*)Q, (uint16_t*)KC, (uint16_t*)VC, nh, nkv, max_len)
+                     POS, (uint16_t*)Q, (uint16_t*)KC, (uint16_t*)VC, nh, nkv, max_len, 0)
   if (dtype == DT_F16) TTSP_QK(DT_F16);
   else if (dtype == DT_BF16) TTSP_QK(DT_BF16);
   else return (int)hipErrorInvalidValue;
 #undef TTSP_QK
+  TTSP_RETURN_LAUNCH();
+}
+
+extern "C" int ttsp_qk_rope_kv_rows(const void* QKV, long long qkv_row_stride, const void* QW, const void* KW,
+                                    float eps, const void* F, int ftype, const long long* POS, void* Q, void* KC,
+                                    void* VC, int nh, int nkv, int max_len, int rows, int dtype,
+                                    hipStream_t stream) {
+  if (nh <= 0 || nkv <= 0 || max_len <= 0 || ftype < 0 || ftype > 2 || rows <= 0 || rows > 65535 ||
+      qkv_row_stride < (long long)(nh + 2 * nkv) * HD || qkv_row_stride > (1LL << 30))
+    return (int)hipErrorInvalidValue;
+#define TTSP_QKR(DTV)                                                                            \
+  hipLaunchKernelGGL(qk_rope_kv_kernel<DTV>, dim3(nh + 2 * nkv, rows), dim3(HD), 0, stream,     \
+                     (const uint16_t*)QKV, (const uint16_t*)QW, (const uint16_t*)KW, eps, F, ftype, \
+                     POS, (uint16_t*)Q, (uint16_t*)KC, (uint16_t*)VC, nh, nkv, max_len, (int)qkv_row_stride)
+  if (dtype == DT_F16) TTSP_QKR(DT_F16);
+  else if (dtype == DT_BF16) TTSP_QKR(DT_BF16);
+  else return (int)hipErrorInvalidValue;
+#undef TTSP_QKR
   TTSP_RETURN_LAUNCH();
 }
 

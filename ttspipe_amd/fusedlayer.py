@@ -241,12 +241,16 @@ def prefill_block(block, x, freqs_cis, mask, input_pos):
     """`TransformerBlock.forward` for several positions (B = 1, S > 1), or None.
 
     The fork's block in its own order with the prefill kernels: RMSNorm,
-    wqkv GEMM, q/k head norms (the fork's modules), rotary, KV-cache write,
-    one-launch causal attention, wo GEMM with the residual add in its
-    epilogue, RMSNorm, w1 GEMM, w3 GEMM with the SwiGLU gate in its epilogue,
-    w2 GEMM with the residual add (reference: the unfused block the reference
-    runs for S > 1, fastpath.py:207-271 and fusedlayer.py:198).
+    wqkv GEMM, q/k head norms + rotary + KV-cache write for every row in one
+    launch (the decode step's kernel over rows; the fork's modules when the
+    cache or tables do not fit it), one-launch causal attention, wo GEMM with
+    the residual add in its epilogue, RMSNorm, w1 GEMM, w3 GEMM with the
+    SwiGLU gate in its epilogue, w2 GEMM with the residual add (reference: the
+    unfused block the reference runs for S > 1, fastpath.py:207-271 and
+    fusedlayer.py:198).
     """
+    import torch
+
     from ttspipe_amd import fastpath, fusedops, nf4gemv
     from ttspipe_amd.llama import apply_rotary_emb
 
@@ -260,17 +264,36 @@ def prefill_block(block, x, freqs_cis, mask, input_pos):
     qkv = None if xn is None else nf4gemv.matmul(a.wqkv, xn)
     if qkv is None:
         return None
-    q, k, v = qkv.split([nh * hd, nkv * hd, nkv * hd], dim=-1)
-    q, k, v = q.view(bsz, n, nh, hd), k.view(bsz, n, nkv, hd), v.view(bsz, n, nkv, hd)
-    if a.attention_qk_norm:
-        q, k = a.q_norm(q), a.k_norm(k)
-    fq = fusedops.rope(q, freqs_cis)
-    fk = fusedops.rope(k, freqs_cis) if fq is not None else None
-    if fk is None:
-        fusedops.note_rope_fallback()
-        fq, fk = apply_rotary_emb(q, freqs_cis), apply_rotary_emb(k, freqs_cis)
-    q, k, v = (t.transpose(1, 2) for t in (fq, fk, v))
-    k, v = a.kv_cache.update(input_pos, k, v)
+    kc, vc = a.kv_cache.k_cache, a.kv_cache.v_cache
+    max_len = kc.shape[2]
+    ftype = _lib.dtype_code(freqs_cis.dtype)
+    rows_ok = (ftype is not None and freqs_cis.is_contiguous() and freqs_cis.numel() == n * hd
+               and input_pos.dtype == torch.long and input_pos.is_contiguous() and kc.is_contiguous()
+               and vc.is_contiguous() and kc.dtype == x.dtype and tuple(kc.shape) == (1, nkv, max_len, hd))
+    if rows_ok:
+        # head norms, rotary and the KV write for every row in one launch
+        q = torch.empty(bsz, n, nh, hd, dtype=x.dtype, device=x.device)
+        qn, kn = (a.q_norm, a.k_norm) if a.attention_qk_norm else (None, None)
+        eps = float(qn.eps) if qn is not None else 0.0
+        rc = _lib.lib().ttsp_qk_rope_kv_rows(
+            qkv.data_ptr(), qkv.shape[-1], _lib.ptr(None if qn is None else qn.weight),
+            _lib.ptr(None if kn is None else kn.weight), eps, freqs_cis.data_ptr(), ftype, input_pos.data_ptr(),
+            q.data_ptr(), kc.data_ptr(), vc.data_ptr(), nh, nkv, max_len, n, _lib.dtype_code(x.dtype),
+            _lib.stream())
+        _lib.check(rc, "ttsp_qk_rope_kv_rows")
+        q, k, v = q.transpose(1, 2), kc, vc
+    else:
+        q, k, v = qkv.split([nh * hd, nkv * hd, nkv * hd], dim=-1)
+        q, k, v = q.view(bsz, n, nh, hd), k.view(bsz, n, nkv, hd), v.view(bsz, n, nkv, hd)
+        if a.attention_qk_norm:
+            q, k = a.q_norm(q), a.k_norm(k)
+        fq = fusedops.rope(q, freqs_cis)
+        fk = fusedops.rope(k, freqs_cis) if fq is not None else None
+        if fk is None:
+            fusedops.note_rope_fallback()
+            fq, fk = apply_rotary_emb(q, freqs_cis), apply_rotary_emb(k, freqs_cis)
+        q, k, v = (t.transpose(1, 2) for t in (fq, fk, v))
+        k, v = a.kv_cache.update(input_pos, k, v)
     if mask.shape[-1] < k.shape[2]:
         k, v = k[:, :, : mask.shape[-1]], v[:, :, : mask.shape[-1]]
     y = fastpath.prefill_attention(q, k, v, mask, nh, nkv, hd)
