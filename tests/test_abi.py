@@ -74,6 +74,46 @@ def test_gemv_shape_covers_every_row_and_column(M, K):
     assert J * KS * 64 >= K // 8 and (J - 1) * KS * 64 < K // 8  # no wholly idle chunk slot
 
 
+@pytest.mark.parametrize("N", [2, 32, 33, 64, 70, 512, 2048])
+@pytest.mark.parametrize("M,K", [(4096, 2560), (1024, 2560), (2560, 4096), (9728, 2560), (2560, 9728),
+                                 (6144, 2560), (1536, 1024), (3072, 1024), (1024, 3072), (64, 128)])
+def test_gemm_split_plan(M, K, N):
+    """The K split a prefill GEMM takes (host-only query): none for N <= 32 or
+    when the output tiles already fill the GPU; otherwise each split covers an
+    even number of at least 8 K-steps of 64 codes, and the split workgroups
+    fill the GPU."""
+    from ttspipe_amd import _lib
+
+    lib = _lib.load()
+    sp = lib.ttsp_nf4_gemm_splits(M, K, N)
+    assert sp in (1, 2, 4, 8)
+    steps = K // 64
+    tiles = {(bm, bn): -(-M // bm) * -(-N // bn) for bm, bn in ((128, 128), (64, 128))}
+    if N <= 32 or max(tiles.values()) >= 256:
+        assert sp == 1
+    if sp > 1:
+        assert steps % (2 * sp) == 0 and steps // sp >= 8
+        assert max(tiles.values()) * sp >= 256
+    assert lib.ttsp_nf4_gemm_splits(M, K, 1) == 1
+
+
+def test_gemm_split_entry_rejects_a_mismatched_split():
+    from ttspipe_amd import _lib
+
+    lib = _lib.load()
+    sp = lib.ttsp_nf4_gemm_splits(2560, 9728, 512)
+    assert sp == 4
+    for bad in (1, 2, 8):  # anything but the plan's split, before any launch
+        assert lib.ttsp_nf4_gemm_split(8, 1, 8, None, 8, None, 0.0, 8, 8, None, 0, 2560, 9728, 512, 64, 256, 16,
+                                       bad, None) == 1
+    # the plan's split without a workspace
+    assert lib.ttsp_nf4_gemm_split(8, 1, 8, None, 8, None, 0.0, 8, 8, None, 0, 2560, 9728, 512, 64, 256, None,
+                                   sp, None) == 1
+    # rows-kernel arguments
+    assert lib.ttsp_qk_rope_kv_rows(8, 100, None, None, 1e-6, 8, 1, 8, 8, 8, 8, 4, 2, 64, 3, 1, None) == 1
+    assert lib.ttsp_qk_rope_kv_rows(8, 1024, None, None, 1e-6, 8, 1, 8, 8, 8, 8, 4, 2, 64, 0, 1, None) == 1
+
+
 def test_invalid_arguments_are_rejected_before_any_launch():
     from ttspipe_amd import _lib
 
