@@ -316,22 +316,27 @@ def bench_gemm(rows: int = 512, copies: int = 4, reps: int = 20):
             "pct_of_mfma_peak": round(100 * total_flop / total_s / 1e12 / MFMA_PEAK_TFLOPS, 2)}
 
 
-def bench_prefill_attention(rows: int = 512, prefixes=(0, 1536), n_head: int = 32, n_kv: int = 8, reps: int = 20):
+def bench_prefill_attention(cases=((512, 0), (512, 1536), (64, 2000)), n_head: int = 32, n_kv: int = 8,
+                            reps: int = 20):
     """Prefill attention of `rows` new positions (32 q / 8 kv heads of 128,
-    bf16) over a cached prefix, with the fork's causal mask, as one HIP
-    launch; torch's scaled_dot_product_attention with the same boolean mask
-    (the reference's path beyond 64 positions) timed beside it. FLOPs count
-    the allowed (query, key) pairs: 4 * 128 per pair and head."""
+    bf16) over a cached prefix, for each (rows, prefix) case, with the fork's
+    causal mask, as the HIP path runs it (one launch, or a key split and its
+    merge for a short run over a long cache); torch's
+    scaled_dot_product_attention with the same boolean mask (the reference's
+    path beyond 64 positions) timed beside it. FLOPs count the allowed
+    (query, key) pairs: 4 * 128 per pair and head."""
     import torch
     import torch.nn.functional as F
 
-    from ttspipe_amd import fastpath
+    from ttspipe_amd import _lib, fastpath
 
     dev = torch.device("cuda", 0)
     g = torch.Generator(device=dev).manual_seed(11)
     out = []
-    for prefix in prefixes:
+    for rows, prefix in cases:
         L = prefix + rows
+        splits = _lib.lib().ttsp_prefill_attention_splits(rows, n_kv, L)
+        work = torch.empty(max(fastpath.prefill_work_floats(rows, n_head, splits), 4), device=dev)
         max_len = ((L + 255) // 256) * 256
         q = torch.randn(1, rows, n_head, 128, device=dev, generator=g).to(torch.bfloat16).transpose(1, 2)
         kc = torch.randn(1, n_kv, max_len, 128, device=dev, generator=g).to(torch.bfloat16)
@@ -342,7 +347,7 @@ def bench_prefill_attention(rows: int = 512, prefixes=(0, 1536), n_head: int = 3
         y = torch.empty(1, rows, n_head * 128, dtype=torch.bfloat16, device=dev)
 
         def ours():
-            if fastpath.prefill_attention(q, k, v, mask, n_head, n_kv, 128, out=y) is None:
+            if fastpath.prefill_attention(q, k, v, mask, n_head, n_kv, 128, out=y, work=work) is None:
                 raise RuntimeError("prefill attention declined")
 
         def sdpa():
@@ -358,7 +363,7 @@ def bench_prefill_attention(rows: int = 512, prefixes=(0, 1536), n_head: int = 3
             times[name] = time_graph(graph, reps, stream) / 4
         pairs = rows * prefix + rows * (rows + 1) // 2
         flop = 4 * 128 * pairs * n_head
-        out.append({"rows": rows, "prefix": prefix, "us": round(times["hip"] * 1e6, 2),
+        out.append({"rows": rows, "prefix": prefix, "key_splits": splits, "us": round(times["hip"] * 1e6, 2),
                     "tflops": round(flop / times["hip"] / 1e12, 1),
                     "pct_of_mfma_peak": round(100 * flop / times["hip"] / 1e12 / MFMA_PEAK_TFLOPS, 2),
                     "torch_sdpa_us": round(times["sdpa"] * 1e6, 1)})

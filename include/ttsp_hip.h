@@ -208,6 +208,27 @@ int ttsp_prefill_attention(const void* Q, long long q_seq_stride, long long q_he
 /* Largest query heads per kv head ttsp_prefill_attention takes (8). */
 int ttsp_prefill_max_groups(void);
 
+/* Key splits for ttsp_prefill_attention_split at (S, nkv, L): 1 when the
+ * (kv head, 32-query) workgroups already fill the GPU or the keys are few
+ * (under 16 blocks of 32), else up to 16 so that a short run of positions
+ * over a long cached prefix still spreads over the CUs. Host only. Replaces: nothing (the reference's SDPA picks its own split,
+ * app/engine/fastpath.py:244-268). */
+int ttsp_prefill_attention_splits(int S, int nkv, int L);
+
+/* ttsp_prefill_attention with the keys split into `splits` (1..16) ranges of
+ * whole 32-key blocks over separate workgroups, each writing its unnormalised
+ * output, running max and sum to `work` (fp32, 16-byte aligned,
+ * splits * S * nh * 130 floats), then one merge launch writing Y. splits = 1
+ * is ttsp_prefill_attention (work unused). Same results to rounding: the
+ * splits merge in fp32 before the one division. Replaces: the same call as
+ * ttsp_prefill_attention. */
+int ttsp_prefill_attention_split(const void* Q, long long q_seq_stride, long long q_head_stride,
+                                 const void* K, long long k_seq_stride, long long k_head_stride,
+                                 const void* V, long long v_seq_stride, long long v_head_stride,
+                                 const void* mask, long long mask_row_stride, void* Y, int S, int nh,
+                                 int nkv, int L, float scale, int dtype, float* work, int splits,
+                                 void* stream);
+
 /* out[d] = round(sum_{c < ntok} E[(c*vocab + tok[c]) * D + d]) (tok int32 on the
  * device, clamped into [0, vocab)). Replaces: the codebook-embedding lookup of
  * a decode step (app/engine/graphs.py:124-131 via the fork's _fast_embed /

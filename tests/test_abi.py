@@ -114,6 +114,42 @@ def test_gemm_split_entry_rejects_a_mismatched_split():
     assert lib.ttsp_qk_rope_kv_rows(8, 1024, None, None, 1e-6, 8, 1, 8, 8, 8, 8, 4, 2, 64, 0, 1, None) == 1
 
 
+@pytest.mark.parametrize("S", [1, 7, 32, 64, 100, 512, 2048])
+@pytest.mark.parametrize("nkv", [1, 2, 8, 16])
+@pytest.mark.parametrize("L_extra", [0, 64, 500, 2000, 8000])
+def test_prefill_key_split_plan(S, nkv, L_extra):
+    """The key split of a prefill attention (host-only query): none once the
+    (kv head, 32-query) workgroups number 128 or below 16 key blocks of 32;
+    otherwise a power of two up to 16, each split holding at least 3 key
+    blocks, doubling only while the workgroups stay under 256."""
+    from ttspipe_amd import _lib
+
+    lib = _lib.load()
+    L = S + L_extra
+    sp = lib.ttsp_prefill_attention_splits(S, nkv, L)
+    wg = nkv * -(-S // 32)
+    blocks = -(-L // 32)
+    assert sp in (1, 2, 4, 8, 16)
+    if wg >= 128 or blocks < 16:
+        assert sp == 1
+    if sp > 1:
+        assert blocks // sp >= 3 and wg * sp // 2 < 256
+    if sp < 16 and wg < 128 and blocks >= 16:  # stopped because it filled the GPU or ran out of blocks
+        assert wg * sp >= 256 or blocks // (2 * sp) < 3
+
+
+def test_prefill_split_entry_rejects_bad_splits_before_any_launch():
+    from ttspipe_amd import _lib
+
+    lib = _lib.load()
+    p = 1 << 20  # aligned stand-in pointers: every call below is refused before a launch
+    args = (p, 1024, 128, p, 256, 4096, p, 256, 4096, p, 64, p, 4, 8, 2, 16, 0.088, 1)
+    assert lib.ttsp_prefill_attention_split(*args, p, 0, None) == 1
+    assert lib.ttsp_prefill_attention_split(*args, p, 17, None) == 1
+    assert lib.ttsp_prefill_attention_split(*args, None, 2, None) == 1  # no workspace
+    assert lib.ttsp_prefill_attention_split(*args, p + 4, 2, None) == 1  # workspace not 16-byte aligned
+
+
 def test_invalid_arguments_are_rejected_before_any_launch():
     from ttspipe_amd import _lib
 

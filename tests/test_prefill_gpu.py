@@ -5,8 +5,9 @@ fp64 attention on the CPU and against the reference's formula
 Bar: a floating-point kernel (scores on the matrix cores, probabilities
 rounded to the activation type before the second product), so within 5e-3
 of fp64 in the reference's measure, max |got - ref| / max |ref| (the bar of
-the decode attention, tests/test_nf4gemv.py:224-242); NaN exactly where the
-reference's softmax gives NaN (a row with no allowed key).
+the decode attention, tests/test_nf4gemv.py:224-242), and within twice that
+of the reference's own bf16/fp16 result; NaN exactly where the reference's
+softmax gives NaN (a row with no allowed key).
 """
 
 from __future__ import annotations
@@ -82,6 +83,8 @@ CASES = [  # (S, prefix, nh, nkv)
     (100, 0, 16, 16),     # one query head per kv head
     (65, 5, 8, 1),        # eight query heads per kv head
     (200, 2900, 8, 2),    # the fast transformer's head shape over a long cache
+    (64, 2000, 32, 8),    # a short run over a long cached prefix: keys split over workgroups
+    (16, 3000, 8, 2),     # the same with the fast transformer's heads (16 splits)
 ]
 
 
@@ -96,8 +99,11 @@ def test_prefill_attention_matches_fp64_and_the_reference_formula(S, prefix, nh,
     got = y[0].float().cpu().numpy()
     assert np.isfinite(got).all()
     assert relative_error(got, exact) < TOL
+    # the reference's formula rounds its own output to the activation type: two
+    # results each within TOL of fp64 lie within 2 TOL of each other
     theirs = decode_attention(q, k, v, mask, nh, nkv, D)[0].float().cpu().numpy()
-    assert relative_error(got, theirs) < TOL
+    assert relative_error(theirs, exact) < TOL
+    assert relative_error(got, theirs) < 2 * TOL
 
 
 def test_arbitrary_mask_and_rows_with_no_key():
@@ -117,6 +123,60 @@ def test_arbitrary_mask_and_rows_with_no_key():
     keep = [i for i in range(S) if i != 3]
     assert np.isfinite(y[:, keep]).all()
     assert relative_error(y[:, keep], exact[:, keep]) < TOL
+
+
+def _split_call(q, k, v, mask, nh, nkv, splits):
+    from ttspipe_amd import _lib
+    from ttspipe_amd.fastpath import prefill_work_floats
+
+    S, L = q.shape[2], k.shape[2]
+    out = torch.full((1, S, nh * D), 7.0, dtype=q.dtype, device="cuda")
+    work = torch.full((max(prefill_work_floats(S, nh, splits), 4),), float("nan"), device="cuda")
+    rc = _lib.load().ttsp_prefill_attention_split(
+        q.data_ptr(), q.stride(2), q.stride(1), k.data_ptr(), k.stride(2), k.stride(1), v.data_ptr(), v.stride(2),
+        v.stride(1), mask.data_ptr(), mask.stride(2), out.data_ptr(), S, nh, nkv, L, D**-0.5,
+        _lib.dtype_code(q.dtype), work.data_ptr(), splits, _lib.stream())
+    assert rc == 0
+    torch.cuda.synchronize()
+    return out.view(1, S, nh, D).transpose(1, 2)[0].float().cpu().numpy()
+
+
+@pytest.mark.parametrize("S,prefix,nh,nkv", [(64, 2000, 32, 8), (40, 0, 8, 2), (100, 900, 16, 2), (5, 300, 8, 8)])
+def test_any_key_split_gives_the_unsplit_result(S, prefix, nh, nkv):
+    """Splits 1, 2, 3, 7 and 16 of the keys: every split count (also ones
+    the plan never picks, and splits left with no allowed key by the causal
+    mask) within the bar of fp64. The probabilities are rounded relative to a
+    different running max in each split, so two split counts agree to twice
+    the bar."""
+    q, k, v, mask = _setup(S, prefix, nh, nkv, torch.bfloat16, seed=11 + S)
+    exact = _fp64(q, k, v, mask)
+    one = _split_call(q, k, v, mask, nh, nkv, 1)
+    assert relative_error(one, exact) < TOL
+    for sp in (2, 3, 7, 16):
+        got = _split_call(q, k, v, mask, nh, nkv, sp)
+        assert np.isfinite(got).all(), sp
+        assert relative_error(got, exact) < TOL, sp
+        assert relative_error(got, one) < 2 * TOL, sp  # each within TOL of fp64
+
+
+def test_key_split_rows_with_no_key_are_nan():
+    S, L, nh, nkv = 40, 600, 8, 2
+    q, k, v, _ = _setup(S, L - S, nh, nkv, torch.float16, seed=4)
+    g = torch.Generator().manual_seed(2)
+    store = torch.rand(S, 608, generator=g) < 0.05
+    store[7] = False
+    store[20, :] = False
+    store[20, 599] = True  # only the last key (the last split)
+    store[21, :] = False
+    store[21, 0] = True  # only the first key (the first split)
+    mask = store.cuda()[None, None, :, :L]
+    exact = _fp64(q, k, v, mask)
+    for sp in (4, 16):
+        y = _split_call(q, k, v, mask, nh, nkv, sp)
+        assert np.isnan(y[:, 7]).all()
+        keep = [i for i in range(S) if i != 7]
+        assert np.isfinite(y[:, keep]).all()
+        assert relative_error(y[:, keep], exact[:, keep]) < TOL
 
 
 def test_declines_what_it_does_not_take():
@@ -170,6 +230,27 @@ def test_captured_in_a_graph_replays_identically():
         graph.replay()
         torch.cuda.synchronize()
         assert torch.equal(out.view(1, 96, 8, D).transpose(1, 2), eager)
+
+
+def test_key_split_captured_in_a_graph_replays_identically():
+    from ttspipe_amd import _lib, fastpath
+
+    S, prefix, nh, nkv = 64, 2000, 32, 8
+    assert _lib.load().ttsp_prefill_attention_splits(S, nkv, S + prefix) > 1
+    q, k, v, mask = _setup(S, prefix, nh, nkv, torch.bfloat16, seed=6)
+    out = torch.empty(1, S, nh * D, dtype=torch.bfloat16, device="cuda")
+    work = torch.empty(fastpath.prefill_work_floats(S, nh, 16), device="cuda")
+    eager = fastpath.prefill_attention(q, k, v, mask, nh, nkv, D).clone()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        fastpath.prefill_attention(q, k, v, mask, nh, nkv, D, out=out, work=work)
+    for _ in range(3):
+        out.zero_()
+        work.zero_()
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out.view(1, S, nh, D).transpose(1, 2), eager)
 
 
 def test_attention_forward_takes_the_kernel_for_a_prefill():

@@ -51,6 +51,9 @@ SIGNATURES: dict[str, list] = {
     "ttsp_prefill_attention": [_vp, _ll, _ll, _vp, _ll, _ll, _vp, _ll, _ll, _vp, _ll, _vp, _i, _i, _i, _i, _f, _i,
                                _vp],
     "ttsp_prefill_max_groups": [],
+    "ttsp_prefill_attention_splits": [_i, _i, _i],
+    "ttsp_prefill_attention_split": [_vp, _ll, _ll, _vp, _ll, _ll, _vp, _ll, _ll, _vp, _ll, _vp, _i, _i, _i, _i, _f,
+                                     _i, _vp, _i, _vp],
     "ttsp_sample_topk": [_vp, _i, _i, _vp, _vp, _vp, _vp, _vp, _vp],
     "ttsp_sample_max_top_k": [],
     "ttsp_embed_sum": [_vp, _vp, _i, _i, _i, _vp, _i, _vp],

@@ -126,6 +126,8 @@ struct PrefillArgs {
   int k_ss, k_sh, v_ss, v_sh, m_ss;  // elements (bytes for the mask); the host bounds them
   int S, nh, nkv, L;
   float scale2;  // scale * log2(e): scores in log2 units
+  int bps;       // key blocks per split (gridDim.z splits)
+  float* WO;     // splits > 1: unnormalised O [z][i][head][128], then m, l [z][i][head]
 };
 
 // LDS of one staged key block: K rows, V rows, mask tile (bytes)
@@ -152,6 +154,7 @@ __global__ __launch_bounds__(64 * G * NS) void prefill_attn_kernel(const Prefill
   const int i = q0 + ql;  // this lane's query
   const int nq = min(PA_QB, a.S - q0);
   const int L = a.L;
+  const int z = blockIdx.z, kb0 = z * a.bps * PA_KB;  // key split: first key of this split
   const __amdgpu_buffer_rsrc_t kr = pa_rsrc(a.K + (size_t)kh * a.k_sh, (uint32_t)((L - 1) * a.k_ss + HD) * 2);
   const __amdgpu_buffer_rsrc_t vr = pa_rsrc(a.V + (size_t)kh * a.v_sh, (uint32_t)((L - 1) * a.v_ss + HD) * 2);
   // the mask buffer ends with the 16-byte piece holding the last row's byte
@@ -189,19 +192,19 @@ __global__ __launch_bounds__(64 * G * NS) void prefill_attn_kernel(const Prefill
 #pragma unroll
     for (int n = 0; n < KPT; ++n) {
       const int p = min(tid + n * NT, NKP - 1), blk = p / (PA_KB * (HD / 8)), q = p % (PA_KB * (HD / 8));
-      const int j = min(NS * t * PA_KB + blk * PA_KB + q / (HD / 8), L - 1), e = (q % (HD / 8)) * 8;
+      const int j = min(kb0 + NS * t * PA_KB + blk * PA_KB + q / (HD / 8), L - 1), e = (q % (HD / 8)) * 8;
       r.k[n] = pa_ld16(kr, (uint32_t)(j * a.k_ss + e) * 2);
     }
 #pragma unroll
     for (int n = 0; n < VPT; ++n) {
       const int p = min(tid + n * NT, NVP - 1), blk = p / (PA_KB * (HD / 8)), q = p % (PA_KB * (HD / 8));
-      const int j = min(NS * t * PA_KB + blk * PA_KB + q / (HD / 8), L - 1), e = (q % (HD / 8)) * 8;
+      const int j = min(kb0 + NS * t * PA_KB + blk * PA_KB + q / (HD / 8), L - 1), e = (q % (HD / 8)) * 8;
       r.v[n] = pa_ld16(vr, (uint32_t)(j * a.v_ss + e) * 2);
     }
 #pragma unroll
     for (int n = 0; n < MPT; ++n) {
       const int p = min(tid + n * NT, NMP - 1), blk = p / (PA_QB * 2), q = p % (PA_QB * 2);
-      const int c = min(NS * t * PA_KB + blk * PA_KB + 16 * (q & 1), 16 * (ncg - 1));
+      const int c = min(kb0 + NS * t * PA_KB + blk * PA_KB + 16 * (q & 1), 16 * (ncg - 1));
       r.m[n] = pa_ld16(mr, (uint32_t)(min(q >> 1, nq - 1) * a.m_ss + c));
     }
   };
@@ -227,7 +230,7 @@ __global__ __launch_bounds__(64 * G * NS) void prefill_attn_kernel(const Prefill
     for (int n = 0; n < MPT; ++n) {
       const int p = tid + n * NT, blk = p / (PA_QB * 2), q = p % (PA_QB * 2);
       if (NMP % NT == 0 || p < NMP) {
-        const u32x4 m = pa_mask_tail(r.m[n], NS * t * PA_KB + blk * PA_KB + 16 * (q & 1), L);
+        const u32x4 m = pa_mask_tail(r.m[n], kb0 + NS * t * PA_KB + blk * PA_KB + 16 * (q & 1), L);
         *reinterpret_cast<u32x4*>(lds + (size_t)(buf * NS + blk) * PA_BLK + PA_KT + PA_VT + (q >> 1) * PA_MROW +
                                   16 * (q & 1)) = m;
         if ((q >> 1) < nq && !pa_all_set(m)) full[t % 3] = 0;  // rows past nq are never used
@@ -262,7 +265,8 @@ __global__ __launch_bounds__(64 * G * NS) void prefill_attn_kernel(const Prefill
   int last = -1;
 #pragma unroll
   for (int w = 0; w < NW; ++w) last = max(last, wmax[w]);
-  const int nkb = (last + PA_KB) / PA_KB;  // blocks holding keys 0 .. last
+  // this workgroup's key blocks: split z of the blocks holding keys 0 .. last
+  const int nkb = max(0, min((last + PA_KB) / PA_KB, (z + 1) * a.bps) - z * a.bps);
   const int nit = (nkb + NS - 1) / NS;
   // wait for Q here: a wait inside the loop would also wait for the
   // prefetch loads issued after it
@@ -389,10 +393,27 @@ __global__ __launch_bounds__(64 * G * NS) void prefill_attn_kernel(const Prefill
     const float mref = mm == -__builtin_inff() ? 0.0f : mm;
     const float f1 = pa_exp2(mrun - mref), f2 = pa_exp2(m2 - mref);
     lrun = lrun * f1 + l2 * f2;
+    mrun = mm;  // o and lrun are now relative to the merged max (the key-split merge reads it)
 #pragma unroll
     for (int d = 0; d < HD / 32; ++d)
 #pragma unroll
       for (int r = 0; r < 16; ++r) o[d][r] = o[d][r] * f1 + mg[(16 * d + r) * 64] * f2;
+  }
+  if (a.WO) {  // key split: O unnormalised, max and sum of this split, for the merge kernel
+    if (i < a.S) {
+      float* wo = a.WO + (((size_t)z * a.S + i) * a.nh + head) * HD;
+#pragma unroll
+      for (int d = 0; d < HD / 32; ++d)
+#pragma unroll
+        for (int g = 0; g < 4; ++g)
+          *reinterpret_cast<float4*>(wo + 32 * d + 8 * g + 4 * h) =
+              make_float4(o[d][4 * g], o[d][4 * g + 1], o[d][4 * g + 2], o[d][4 * g + 3]);
+      if (h == 0) {
+        float* ml = a.WO + (size_t)gridDim.z * a.S * a.nh * HD + (((size_t)z * a.S + i) * a.nh + head) * 2;
+        *reinterpret_cast<float2*>(ml) = make_float2(mrun, lrun);
+      }
+    }
+    return;
   }
   // Y[i][head][dim] = O^T[dim][i] / l (a row with no allowed key: 0 / 0, as the reference's softmax)
   if (i < a.S) {
@@ -410,26 +431,86 @@ __global__ __launch_bounds__(64 * G * NS) void prefill_attn_kernel(const Prefill
   }
 }
 
+// Y[i][head][8 dims] from the splits' partials: weights 2^(m_z - max m),
+// sums in split order, O / l rounded once (a row with no allowed key in any
+// split: 0 / 0). Every split's loads are issued before the first is used
+// (SPM >= splits slots, indices clamped, weight 0 past the last split), so
+// the kernel costs one memory round trip whatever the split count.
+template <int DT, int SPM>
+__global__ __launch_bounds__(256) void prefill_merge_kernel(const float* __restrict__ WO, int splits, int S, int nh,
+                                                            uint16_t* __restrict__ Y) {
+  const long long t = (long long)blockIdx.x * 256 + threadIdx.x;
+  if (t >= (long long)S * nh * (HD / 8)) return;
+  const int d0 = (int)(t % (HD / 8)) * 8;
+  const long long ih = t / (HD / 8);  // i * nh + head
+  const size_t plane = (size_t)S * nh;  // (query, head) pairs per split
+  const float* ml = WO + (size_t)splits * plane * HD;
+  float2 mlz[SPM];
+  float4 u[SPM], v[SPM];
+#pragma unroll
+  for (int z = 0; z < SPM; ++z) {
+    const size_t zi = (size_t)min(z, splits - 1) * plane + ih;
+    mlz[z] = *reinterpret_cast<const float2*>(ml + zi * 2);
+    u[z] = *reinterpret_cast<const float4*>(WO + zi * HD + d0);
+    v[z] = *reinterpret_cast<const float4*>(WO + zi * HD + d0 + 4);
+  }
+  __builtin_amdgcn_sched_barrier(0);  // all loads in flight before the first use
+  float mx = -__builtin_inff();
+#pragma unroll
+  for (int z = 0; z < SPM; ++z) mx = fmaxf(mx, mlz[z].x);  // clamped slots repeat the last split
+  const float mref = mx == -__builtin_inff() ? 0.0f : mx;
+  float num[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f}, den = 0.0f;
+#pragma unroll
+  for (int z = 0; z < SPM; ++z) {
+    const float w = z < splits ? pa_exp2(mlz[z].x - mref) : 0.0f;
+    den = __builtin_fmaf(w, mlz[z].y, den);
+    num[0] = __builtin_fmaf(w, u[z].x, num[0]), num[1] = __builtin_fmaf(w, u[z].y, num[1]);
+    num[2] = __builtin_fmaf(w, u[z].z, num[2]), num[3] = __builtin_fmaf(w, u[z].w, num[3]);
+    num[4] = __builtin_fmaf(w, v[z].x, num[4]), num[5] = __builtin_fmaf(w, v[z].y, num[5]);
+    num[6] = __builtin_fmaf(w, v[z].z, num[6]), num[7] = __builtin_fmaf(w, v[z].w, num[7]);
+  }
+  const float inv = 1.0f / den;
+  uint4 out;
+  out.x = pa_pack<DT>(num[0] * inv, num[1] * inv);
+  out.y = pa_pack<DT>(num[2] * inv, num[3] * inv);
+  out.z = pa_pack<DT>(num[4] * inv, num[5] * inv);
+  out.w = pa_pack<DT>(num[6] * inv, num[7] * inv);
+  *reinterpret_cast<uint4*>(Y + (size_t)ih * HD + d0) = out;
+}
+
+// Key splits for a launch: none while the (kv head, 32-query) workgroups
+// already number 128, or for fewer than 16 key blocks (the merge launch costs
+// about what 4 pipeline steps save); otherwise doubled up to 16 while the
+// workgroups stay under 256 and each split keeps at least 3 key blocks.
+static int prefill_splits(int S, int nkv, int L) {
+  const long long wg = (long long)nkv * ((S + PA_QB - 1) / PA_QB);
+  const int blocks = (L + PA_KB - 1) / PA_KB;
+  if (wg >= 128 || blocks < 16) return 1;
+  int sp = 1;
+  while (wg * sp < 256 && sp < 16 && blocks / (2 * sp) >= 3) sp *= 2;
+  return sp;
+}
+
 }  // namespace ttsp
 
 using namespace ttsp;
 
 extern "C" int ttsp_prefill_max_groups() { return PA_MAX_GROUPS; }
 
-extern "C" int ttsp_prefill_attention(const void* Q, long long q_seq_stride, long long q_head_stride,
-                                      const void* K, long long k_seq_stride, long long k_head_stride,
-                                      const void* V, long long v_seq_stride, long long v_head_stride,
-                                      const void* mask, long long mask_row_stride, void* Y, int S, int nh,
-                                      int nkv, int L, float scale, int dtype, hipStream_t stream) {
+static int prefill_launch(const void* Q, long long q_seq_stride, long long q_head_stride, const void* K,
+                          long long k_seq_stride, long long k_head_stride, const void* V, long long v_seq_stride,
+                          long long v_head_stride, const void* mask, long long mask_row_stride, void* Y, int S,
+                          int nh, int nkv, int L, float scale, int dtype, float* work, int splits,
+                          hipStream_t stream) {
   if (!Q || !K || !V || !mask || !Y || S <= 0 || nh <= 0 || nkv <= 0 || nh % nkv || L <= 0 ||
-      nh / nkv > PA_MAX_GROUPS || S > (1 << 20) || mask_row_stride < L)
+      nh / nkv > PA_MAX_GROUPS || S > (1 << 20) || mask_row_stride < L || splits < 1 || splits > 16)
     return (int)hipErrorInvalidValue;
   // 16-byte pieces: every row start and the bases aligned
   const long long st[6] = {q_seq_stride, q_head_stride, k_seq_stride, k_head_stride, v_seq_stride, v_head_stride};
   for (long long s : st)
     if (s < 0 || s % 8) return (int)hipErrorInvalidValue;
   if (mask_row_stride % 16 || (uintptr_t)Q % 16 || (uintptr_t)K % 16 || (uintptr_t)V % 16 ||
-      (uintptr_t)mask % 16 || (uintptr_t)Y % 16)
+      (uintptr_t)mask % 16 || (uintptr_t)Y % 16 || (splits > 1 && (!work || (uintptr_t)work % 16)))
     return (int)hipErrorInvalidValue;
   // K, V (one kv head) and the mask rows of one workgroup are addressed with
   // 32-bit byte offsets
@@ -437,11 +518,13 @@ extern "C" int ttsp_prefill_attention(const void* Q, long long q_seq_stride, lon
   if (((L - 1) * k_seq_stride + 128) * 2 > lim || ((L - 1) * v_seq_stride + 128) * 2 > lim ||
       k_head_stride > lim || v_head_stride > lim || 31 * mask_row_stride + L > lim)
     return (int)hipErrorInvalidValue;
+  const int blocks = (L + PA_KB - 1) / PA_KB;
   PrefillArgs a{(const uint16_t*)Q, (const uint16_t*)K, (const uint16_t*)V, (const uint8_t*)mask, (uint16_t*)Y,
                 q_seq_stride, q_head_stride, (int)k_seq_stride, (int)k_head_stride, (int)v_seq_stride,
-                (int)v_head_stride, (int)mask_row_stride, S, nh, nkv, L, scale * PA_LOG2E};
+                (int)v_head_stride, (int)mask_row_stride, S, nh, nkv, L, scale * PA_LOG2E,
+                (blocks + splits - 1) / splits, splits > 1 ? work : nullptr};
   const int groups = nh / nkv;
-  const dim3 grid(nkv, (S + PA_QB - 1) / PA_QB);
+  const dim3 grid(nkv, (S + PA_QB - 1) / PA_QB, splits);
   // two key splits for 1, 2 and 4 heads per kv head (at most 8 waves, two a
   // SIMD at ~240 registers), one otherwise
 #define TTSP_PA_G(DTV, G)                                                                                   \
@@ -470,5 +553,51 @@ extern "C" int ttsp_prefill_attention(const void* Q, long long q_seq_stride, lon
   }
 #undef TTSP_PA
 #undef TTSP_PA_G
+  if (splits > 1) {
+    const long long n = (long long)S * nh * (HD / 8);
+    const dim3 mg((unsigned)((n + 255) / 256));
+#define TTSP_PM(DTV, SPM) \
+  hipLaunchKernelGGL((prefill_merge_kernel<DTV, SPM>), mg, dim3(256), 0, stream, work, splits, S, nh, (uint16_t*)Y)
+#define TTSP_PM_SP(DTV)          \
+  if (splits <= 2)               \
+    TTSP_PM(DTV, 2);             \
+  else if (splits <= 4)          \
+    TTSP_PM(DTV, 4);             \
+  else if (splits <= 8)          \
+    TTSP_PM(DTV, 8);             \
+  else                           \
+    TTSP_PM(DTV, 16);
+    if (dtype == DT_F16) {
+      TTSP_PM_SP(DT_F16)
+    } else {
+      TTSP_PM_SP(DT_BF16)
+    }
+#undef TTSP_PM_SP
+#undef TTSP_PM
+  }
   TTSP_RETURN_LAUNCH();
+}
+
+extern "C" int ttsp_prefill_attention(const void* Q, long long q_seq_stride, long long q_head_stride,
+                                      const void* K, long long k_seq_stride, long long k_head_stride,
+                                      const void* V, long long v_seq_stride, long long v_head_stride,
+                                      const void* mask, long long mask_row_stride, void* Y, int S, int nh,
+                                      int nkv, int L, float scale, int dtype, hipStream_t stream) {
+  return prefill_launch(Q, q_seq_stride, q_head_stride, K, k_seq_stride, k_head_stride, V, v_seq_stride,
+                        v_head_stride, mask, mask_row_stride, Y, S, nh, nkv, L, scale, dtype, nullptr, 1, stream);
+}
+
+extern "C" int ttsp_prefill_attention_splits(int S, int nkv, int L) {
+  if (S <= 0 || nkv <= 0 || L <= 0) return 1;
+  return prefill_splits(S, nkv, L);
+}
+
+extern "C" int ttsp_prefill_attention_split(const void* Q, long long q_seq_stride, long long q_head_stride,
+                                            const void* K, long long k_seq_stride, long long k_head_stride,
+                                            const void* V, long long v_seq_stride, long long v_head_stride,
+                                            const void* mask, long long mask_row_stride, void* Y, int S, int nh,
+                                            int nkv, int L, float scale, int dtype, float* work, int splits,
+                                            hipStream_t stream) {
+  return prefill_launch(Q, q_seq_stride, q_head_stride, K, k_seq_stride, k_head_stride, V, v_seq_stride,
+                        v_head_stride, mask, mask_row_stride, Y, S, nh, nkv, L, scale, dtype, work, splits, stream);
 }

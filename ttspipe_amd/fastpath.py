@@ -52,7 +52,7 @@ def _prefill_eligible(q, k, v, mask, n_head, n_local_heads, head_dim) -> bool:
     return mask.stride(3) == 1 and mask.stride(2) % 16 == 0 and mask.stride(2) >= L and mask.data_ptr() % 16 == 0
 
 
-def prefill_attention(q, k, v, mask, n_head, n_local_heads, head_dim, out=None):
+def prefill_attention(q, k, v, mask, n_head, n_local_heads, head_dim, out=None, work=None):
     """`decode_attention` in one launch: q (1, n_head, S, 128), k/v (1,
     n_local_heads, L, 128) with the last dim contiguous (any seq/head strides
     that keep rows 16-byte aligned, e.g. the KV cache sliced to L), mask bool
@@ -60,7 +60,10 @@ def prefill_attention(q, k, v, mask, n_head, n_local_heads, head_dim, out=None):
     transposed view of a contiguous (1, S, n_head * 128) tensor (`out=` may
     supply that tensor), so the caller's `transpose(1, 2).contiguous()` is free;
     None when declined. A query whose mask row allows no key gets NaN, as the
-    reference's softmax over all -inf scores."""
+    reference's softmax over all -inf scores. A short run over a long cache
+    splits its keys over several workgroups (`ttsp_prefill_attention_splits`)
+    through an fp32 workspace: `work=` may supply one of at least
+    `prefill_work_floats(...)` elements, else it is allocated per call."""
     import torch
 
     from ttspipe_amd import _lib
@@ -73,13 +76,28 @@ def prefill_attention(q, k, v, mask, n_head, n_local_heads, head_dim, out=None):
         out = torch.empty(1, seqlen, n_head * head_dim, dtype=q.dtype, device=q.device)
     elif out.shape != (1, seqlen, n_head * head_dim) or out.dtype != q.dtype or not out.is_contiguous():
         raise ValueError("out must be a contiguous (1, S, n_head * head_dim) tensor of q's dtype")
-    rc = _lib.lib().ttsp_prefill_attention(
+    lib = _lib.lib()
+    splits = lib.ttsp_prefill_attention_splits(seqlen, n_local_heads, L)
+    need = prefill_work_floats(seqlen, n_head, splits)
+    if splits > 1 and work is None:
+        work = torch.empty(need, dtype=torch.float32, device=q.device)
+    elif splits > 1 and (work.dtype != torch.float32 or work.numel() < need or not work.is_contiguous()
+                         or work.data_ptr() % 16):
+        raise ValueError(f"work must be a contiguous 16-byte aligned fp32 tensor of at least {need} elements")
+    rc = lib.ttsp_prefill_attention_split(
         q.data_ptr(), q.stride(2), q.stride(1), k.data_ptr(), k.stride(2), k.stride(1), v.data_ptr(), v.stride(2),
         v.stride(1), mask.data_ptr(), mask.stride(2), out.data_ptr(), seqlen, n_head, n_local_heads, L,
-        float(head_dim**-0.5), _lib.dtype_code(q.dtype), _lib.stream())
-    _lib.check(rc, "ttsp_prefill_attention")
+        float(head_dim**-0.5), _lib.dtype_code(q.dtype), work.data_ptr() if splits > 1 else None, splits,
+        _lib.stream())
+    _lib.check(rc, "ttsp_prefill_attention_split")
     _stats["prefill_attn"] += 1
     return out.view(1, seqlen, n_head, head_dim).transpose(1, 2)
+
+
+def prefill_work_floats(seqlen: int, n_head: int, splits: int) -> int:
+    """fp32 elements of the key-split workspace: per split, position and head
+    the unnormalised output (128) and the running max and sum (2); 0 unsplit."""
+    return 0 if splits <= 1 else splits * seqlen * n_head * (HEAD_DIM + 2)
 
 
 def decode_attention(q, k, v, mask, n_head, n_local_heads, head_dim):
