@@ -210,8 +210,9 @@ int ttsp_prefill_max_groups(void);
 
 /* Key splits for ttsp_prefill_attention_split at (S, nkv, L): 1 when the
  * (kv head, 32-query) workgroups already fill the GPU or the keys are few
- * (under 16 blocks of 32), else up to 16 so that a short run of positions
- * over a long cached prefix still spreads over the CUs. Host only. Replaces: nothing (the reference's SDPA picks its own split,
+ * (under 16 blocks of 32), 2 for half a GPU of workgroups over a cached
+ * prefix of 1024+ keys, else up to 16 so that a short run of positions over
+ * a long cached prefix still spreads over the CUs. Host only. Replaces: nothing (the reference's SDPA picks its own split,
  * app/engine/fastpath.py:244-268). */
 int ttsp_prefill_attention_splits(int S, int nkv, int L);
 

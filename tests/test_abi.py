@@ -118,10 +118,11 @@ def test_gemm_split_entry_rejects_a_mismatched_split():
 @pytest.mark.parametrize("nkv", [1, 2, 8, 16])
 @pytest.mark.parametrize("L_extra", [0, 64, 500, 2000, 8000])
 def test_prefill_key_split_plan(S, nkv, L_extra):
-    """The key split of a prefill attention (host-only query): none once the
-    (kv head, 32-query) workgroups number 128 or below 16 key blocks of 32;
-    otherwise a power of two up to 16, each split holding at least 3 key
-    blocks, doubling only while the workgroups stay under 256."""
+    """The key split of a prefill attention (host-only query): none below 16
+    key blocks of 32 or from 256 (kv head, 32-query) workgroups; two for
+    128-255 workgroups over a cached prefix of 1024 keys or more, else none;
+    below 128 workgroups a power of two up to 16, each split holding at least
+    3 key blocks, doubling only while the workgroups stay under 256."""
     from ttspipe_amd import _lib
 
     lib = _lib.load()
@@ -130,8 +131,11 @@ def test_prefill_key_split_plan(S, nkv, L_extra):
     wg = nkv * -(-S // 32)
     blocks = -(-L // 32)
     assert sp in (1, 2, 4, 8, 16)
-    if wg >= 128 or blocks < 16:
+    if wg >= 256 or blocks < 16:
         assert sp == 1
+    elif wg >= 128:
+        assert sp == (2 if L_extra >= 1024 else 1)
+        return
     if sp > 1:
         assert blocks // sp >= 3 and wg * sp // 2 < 256
     if sp < 16 and wg < 128 and blocks >= 16:  # stopped because it filled the GPU or ran out of blocks

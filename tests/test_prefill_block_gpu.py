@@ -45,10 +45,13 @@ def test_prefill_spans_follow_the_buckets():
 @pytest.mark.parametrize("qk_norm", [True, False])
 def test_prefill_block_matches_the_unpatched_block(qk_norm):
     from tests.test_fused_gpu import _block
-    from ttspipe_amd import fusedlayer
+    from ttspipe_amd import fusedlayer, fusedops, nf4gemv
     from ttspipe_amd.llama import TransformerBlock, precompute_freqs_cis
 
-    assert fusedlayer.install()
+    # the worker's installs (app/engine/worker.py:565-586): the unpatched
+    # block's norms and linears then run the same kernels as the prefill
+    # block's, whatever ran before this test
+    assert nf4gemv.install() and fusedops.install() and fusedlayer.install()
     block, _ = _block(torch.bfloat16, qk_norm, max_len=128, seed=3)
     kc, vc = block.attention.kv_cache.k_cache, block.attention.kv_cache.v_cache
     kc.normal_()

@@ -478,14 +478,18 @@ __global__ __launch_bounds__(256) void prefill_merge_kernel(const float* __restr
   *reinterpret_cast<uint4*>(Y + (size_t)ih * HD + d0) = out;
 }
 
-// Key splits for a launch: none while the (kv head, 32-query) workgroups
-// already number 128, or for fewer than 16 key blocks (the merge launch costs
-// about what 4 pipeline steps save); otherwise doubled up to 16 while the
-// workgroups stay under 256 and each split keeps at least 3 key blocks.
+// Key splits for a launch: none for fewer than 16 key blocks (the merge
+// launch costs about what 4 pipeline steps save) or once the (kv head,
+// 32-query) workgroups number 256; two for 128-255 workgroups over a cached
+// prefix of at least 1024 keys (the keys before the run, which every query
+// sees: without them a causal run's diagonal work is too uneven to gain);
+// otherwise doubled up to 16 while the workgroups stay under 256 and each
+// split keeps at least 3 key blocks.
 static int prefill_splits(int S, int nkv, int L) {
   const long long wg = (long long)nkv * ((S + PA_QB - 1) / PA_QB);
   const int blocks = (L + PA_KB - 1) / PA_KB;
-  if (wg >= 128 || blocks < 16) return 1;
+  if (blocks < 16 || wg >= 256) return 1;
+  if (wg >= 128) return L - S >= 1024 ? 2 : 1;
   int sp = 1;
   while (wg * sp < 256 && sp < 16 && blocks / (2 * sp) >= 3) sp *= 2;
   return sp;
