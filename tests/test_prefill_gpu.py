@@ -159,6 +159,27 @@ def test_any_key_split_gives_the_unsplit_result(S, prefix, nh, nkv):
         assert relative_error(got, one) < 2 * TOL, sp  # each within TOL of fp64
 
 
+@pytest.mark.parametrize("S,prefix", [(64, 1500), (512, 0), (200, 700)])
+def test_key_split_over_the_whole_cache_splits_the_live_keys(S, prefix):
+    """K/V and the mask over the whole cache (4096 positions), as a captured
+    prefill passes them, the mask cutting the keys to the live prefix: the
+    splits divide the keys the mask allows, and the result keeps the bar."""
+    from ttspipe_amd import _lib
+
+    nh, nkv, max_len = 32, 8, 4096
+    q, k, v, _ = _setup(S, prefix, nh, nkv, torch.bfloat16, max_len=max_len, seed=S + 1)
+    kc, vc = k.new_zeros(1, nkv, max_len, D), v.new_zeros(1, nkv, max_len, D)
+    kc[:, :, : prefix + S], vc[:, :, : prefix + S] = k, v
+    kc[:, :, prefix + S :] = 1e4  # keys past the live length carry huge values: the mask must cut them
+    causal = torch.tril(torch.ones(max_len, max_len, dtype=torch.bool, device="cuda"))
+    mask = causal[None, None, torch.arange(prefix, prefix + S, device="cuda")]
+    assert _lib.load().ttsp_prefill_attention_splits(S, nkv, max_len) > 1
+    y = _run(q, kc, vc, mask, nh, nkv)[0].float().cpu().numpy()
+    exact = _fp64(q, k, v, mask[..., : prefix + S])
+    assert np.isfinite(y).all()
+    assert relative_error(y, exact) < TOL
+
+
 def test_key_split_rows_with_no_key_are_nan():
     S, L, nh, nkv = 40, 600, 8, 2
     q, k, v, _ = _setup(S, L - S, nh, nkv, torch.float16, seed=4)

@@ -126,8 +126,7 @@ struct PrefillArgs {
   int k_ss, k_sh, v_ss, v_sh, m_ss;  // elements (bytes for the mask); the host bounds them
   int S, nh, nkv, L;
   float scale2;  // scale * log2(e): scores in log2 units
-  int bps;       // key blocks per split (gridDim.z splits)
-  float* WO;     // splits > 1: unnormalised O [z][i][head][128], then m, l [z][i][head]
+  float* WO;     // SPLIT: unnormalised O [z][i][head][128], then m, l [z][i][head]
 };
 
 // LDS of one staged key block: K rows, V rows, mask tile (bytes)
@@ -136,7 +135,11 @@ constexpr int PA_VT = PA_KB * PA_VROW * 2;
 constexpr int PA_MT = PA_QB * PA_MROW;
 constexpr int PA_BLK = PA_KT + PA_VT + PA_MT;
 
-template <int DT, int G, int NS>
+// SPLIT: gridDim.z workgroups share each (kv head, query block), split z
+// taking the z-th of gridDim.z equal runs of the key blocks that hold keys
+// 0 .. last (the mask scan's result, the same in every split), and writing
+// partials to WO; its first staging loads then wait for the scan.
+template <int DT, int G, int NS, bool SPLIT>
 __global__ __launch_bounds__(64 * G * NS) void prefill_attn_kernel(const PrefillArgs a) {
   constexpr int NT = 64 * G * NS, NW = NT / 64;
   constexpr int NKP = NS * PA_KB * (HD / 8), NVP = NKP, NMP = NS * PA_QB * 2;
@@ -154,7 +157,8 @@ __global__ __launch_bounds__(64 * G * NS) void prefill_attn_kernel(const Prefill
   const int i = q0 + ql;  // this lane's query
   const int nq = min(PA_QB, a.S - q0);
   const int L = a.L;
-  const int z = blockIdx.z, kb0 = z * a.bps * PA_KB;  // key split: first key of this split
+  const int z = blockIdx.z;
+  int kb0 = 0;  // first key of this workgroup's run (SPLIT: set after the mask scan)
   const __amdgpu_buffer_rsrc_t kr = pa_rsrc(a.K + (size_t)kh * a.k_sh, (uint32_t)((L - 1) * a.k_ss + HD) * 2);
   const __amdgpu_buffer_rsrc_t vr = pa_rsrc(a.V + (size_t)kh * a.v_sh, (uint32_t)((L - 1) * a.v_ss + HD) * 2);
   // the mask buffer ends with the 16-byte piece holding the last row's byte
@@ -237,10 +241,12 @@ __global__ __launch_bounds__(64 * G * NS) void prefill_attn_kernel(const Prefill
       }
     }
   };
-  load(rs[0], 0);
-  __builtin_amdgcn_sched_barrier(0);
-  load(rs[1], 1);
-  __builtin_amdgcn_sched_barrier(0);
+  if constexpr (!SPLIT) {
+    load(rs[0], 0);
+    __builtin_amdgcn_sched_barrier(0);
+    load(rs[1], 1);
+    __builtin_amdgcn_sched_barrier(0);
+  }
 
   // the last key any of the workgroup's queries may see: the first step's
   // piece, then (only where it holds no allowed key) the rest of the row
@@ -265,8 +271,19 @@ __global__ __launch_bounds__(64 * G * NS) void prefill_attn_kernel(const Prefill
   int last = -1;
 #pragma unroll
   for (int w = 0; w < NW; ++w) last = max(last, wmax[w]);
-  // this workgroup's key blocks: split z of the blocks holding keys 0 .. last
-  const int nkb = max(0, min((last + PA_KB) / PA_KB, (z + 1) * a.bps) - z * a.bps);
+  // this workgroup's key blocks: all blocks holding keys 0 .. last, or split
+  // z's run of them
+  const int live = (last + PA_KB) / PA_KB;
+  int nkb = live;
+  if constexpr (SPLIT) {
+    const int bps = (live + (int)gridDim.z - 1) / (int)gridDim.z;
+    kb0 = z * bps * PA_KB;
+    nkb = max(0, min(live, (z + 1) * bps) - z * bps);
+    load(rs[0], 0);
+    __builtin_amdgcn_sched_barrier(0);
+    load(rs[1], 1);
+    __builtin_amdgcn_sched_barrier(0);
+  }
   const int nit = (nkb + NS - 1) / NS;
   // wait for Q here: a wait inside the loop would also wait for the
   // prefetch loads issued after it
@@ -399,7 +416,7 @@ __global__ __launch_bounds__(64 * G * NS) void prefill_attn_kernel(const Prefill
 #pragma unroll
       for (int r = 0; r < 16; ++r) o[d][r] = o[d][r] * f1 + mg[(16 * d + r) * 64] * f2;
   }
-  if (a.WO) {  // key split: O unnormalised, max and sum of this split, for the merge kernel
+  if constexpr (SPLIT) {  // O unnormalised, max and sum of this split, for the merge kernel
     if (i < a.S) {
       float* wo = a.WO + (((size_t)z * a.S + i) * a.nh + head) * HD;
 #pragma unroll
@@ -522,19 +539,22 @@ static int prefill_launch(const void* Q, long long q_seq_stride, long long q_hea
   if (((L - 1) * k_seq_stride + 128) * 2 > lim || ((L - 1) * v_seq_stride + 128) * 2 > lim ||
       k_head_stride > lim || v_head_stride > lim || 31 * mask_row_stride + L > lim)
     return (int)hipErrorInvalidValue;
-  const int blocks = (L + PA_KB - 1) / PA_KB;
   PrefillArgs a{(const uint16_t*)Q, (const uint16_t*)K, (const uint16_t*)V, (const uint8_t*)mask, (uint16_t*)Y,
                 q_seq_stride, q_head_stride, (int)k_seq_stride, (int)k_head_stride, (int)v_seq_stride,
                 (int)v_head_stride, (int)mask_row_stride, S, nh, nkv, L, scale * PA_LOG2E,
-                (blocks + splits - 1) / splits, splits > 1 ? work : nullptr};
+                splits > 1 ? work : nullptr};
   const int groups = nh / nkv;
   const dim3 grid(nkv, (S + PA_QB - 1) / PA_QB, splits);
   // two key splits for 1, 2 and 4 heads per kv head (at most 8 waves, two a
   // SIMD at ~240 registers), one otherwise
 #define TTSP_PA_G(DTV, G)                                                                                   \
   case G:                                                                                                   \
-    hipLaunchKernelGGL((prefill_attn_kernel<DTV, G, PA_SPLITS(G)>), grid, dim3(64 * G * PA_SPLITS(G)), 0, \
-                       stream, a);                                                                          \
+    if (splits > 1)                                                                                         \
+      hipLaunchKernelGGL((prefill_attn_kernel<DTV, G, PA_SPLITS(G), true>), grid, dim3(64 * G * PA_SPLITS(G)), \
+                         0, stream, a);                                                                     \
+    else                                                                                                    \
+      hipLaunchKernelGGL((prefill_attn_kernel<DTV, G, PA_SPLITS(G), false>), grid, dim3(64 * G * PA_SPLITS(G)), \
+                         0, stream, a);                                                                     \
     break;
 #define TTSP_PA(DTV)                           \
   switch (groups) {                            \
