@@ -73,6 +73,7 @@ __global__ __launch_bounds__(64 * WM * WN) void nf4_gemm_kernel(
   constexpr int A_PER_T = (A_CH + GEMM_THREADS - 1) / GEMM_THREADS;     // per thread (the last partly idle)
   constexpr int B_PER_T = BN * (KT / 8) / GEMM_THREADS;                 // 16-byte activation chunks per thread
   static_assert(B_PER_T >= 1 && BN * (KT / 8) % GEMM_THREADS == 0, "tile too small for the workgroup");
+  static_assert(GEMM_THREADS >= 256, "the code tables are filled one entry per thread");
 
   // the operand tiles (two buffers each); after the K loop the same memory
   // holds the output tile, BN rows of BM + 8 elements
@@ -81,7 +82,7 @@ __global__ __launch_bounds__(64 * WM * WN) void nf4_gemm_kernel(
   __shared__ __align__(16) uint16_t smem[OPS > YS ? OPS : YS];
   uint16_t (*As)[BM * LROW] = reinterpret_cast<uint16_t (*)[BM * LROW]>(smem);
   uint16_t (*Bs)[BN * LROW] = reinterpret_cast<uint16_t (*)[BN * LROW]>(smem + 2 * BM * LROW);
-  __shared__ float lut_s[16];
+  __shared__ float2 lut2_s[256];  // byte -> (code of its high nibble, code of its low nibble)
   __shared__ float code2_s[NESTED ? 256 : 1];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -92,7 +93,7 @@ __global__ __launch_bounds__(64 * WM * WN) void nf4_gemm_kernel(
   const int nsteps = K / KT / gridDim.z, kbase = blockIdx.z * nsteps * KT;
   const size_t rowbytes = (size_t)K / 2;
 
-  if (tid < 16) lut_s[tid] = LUT[tid];
+  if (tid < 256) lut2_s[tid] = make_float2(LUT[tid >> 4], LUT[tid & 15]);
   if constexpr (NESTED)
     if (tid < 256) code2_s[tid] = CODE2[tid];
 
@@ -139,16 +140,16 @@ __global__ __launch_bounds__(64 * WM * WN) void nf4_gemm_kernel(
       float s = sg.s[i];
       if constexpr (NESTED) s = __fadd_rn(__fmul_rn(code2_s[sg.a8[i]], s), offset);
       const uint32_t wv[2] = {sg.w[i].x, sg.w[i].y};
-      // all 16 code lookups in flight before the first is used (one LDS
-      // round trip per step instead of one per byte)
+      // one lookup per byte (both codes), all 8 in flight before the first
+      // is used (one LDS round trip per step instead of one per byte)
       float cv[16];
 #pragma unroll
       for (int q = 0; q < 2; ++q)
 #pragma unroll
         for (int bb = 0; bb < 4; ++bb) {
-          const uint32_t byte = (wv[q] >> (8 * bb)) & 0xffu;
-          cv[2 * (q * 4 + bb)] = lut_s[byte >> 4];
-          cv[2 * (q * 4 + bb) + 1] = lut_s[byte & 15u];
+          const float2 pc = lut2_s[(wv[q] >> (8 * bb)) & 0xffu];
+          cv[2 * (q * 4 + bb)] = pc.x;
+          cv[2 * (q * 4 + bb) + 1] = pc.y;
         }
       uint32_t o[8];
 #pragma unroll
@@ -176,7 +177,7 @@ __global__ __launch_bounds__(64 * WM * WN) void nf4_gemm_kernel(
 
 #pragma unroll
   for (int i = 0; i < PF; ++i) load_step(stg[i], i);
-  __syncthreads();  // lut_s / code2_s
+  __syncthreads();  // lut2_s / code2_s
   store_step(stg[0], 0);
   __syncthreads();
   load_step(stg[0], PF);
