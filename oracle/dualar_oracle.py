@@ -84,9 +84,35 @@ class OracleDualAR:
 
     # -------------------------------------------------------------- frame
 
-    def step(self, tokens, pos):
-        """One frame: the token column at slow position pos -> the next column."""
+    def fast_prime(self, fx):
+        """Fast position 0 (reference graphs.py:76-89): every fast layer but the
+        last in full; the last only for its KV entries (its output feeds
+        nothing)."""
         cfg = self.cfg
+        fmax = cfg.fast_max_len
+        for i in range(cfg.fast_n_layer - 1):
+            fx = self.block(f"fast_layers.{i}", fx, self.fast_freqs[0], 0, cfg.fast_n_head, cfg.fast_n_local_heads,
+                            fmax, fmax)
+        self._qkv_rope_kv(f"fast_layers.{cfg.fast_n_layer - 1}", fx, self.fast_freqs[0], 0, cfg.fast_n_head,
+                          cfg.fast_n_local_heads, fmax)
+
+    def fast_step(self, token, i):
+        """Codebook step i >= 1 at fast position i: the embedding of the token
+        just chosen through every fast layer, the fast norm and head -> logits."""
+        cfg = self.cfg
+        fmax = cfg.fast_max_len
+        h = o.embed_sum(self.t["fast_embeddings"], np.asarray([token], np.int32), cfg.codebook_size, cfg.fast_dim, BF)
+        for j in range(cfg.fast_n_layer):
+            h = self.block(f"fast_layers.{j}", h, self.fast_freqs[i], i, cfg.fast_n_head, cfg.fast_n_local_heads,
+                           fmax, fmax)
+        return self.gemv("fast_output", self.norm(h, "fast_norm"))
+
+    def step(self, tokens, pos):
+        """One frame: the token column at slow position pos -> the next column.
+        When `self.logits_log` is a list, each head's logits (bf16 bits) are
+        appended to it: the slow head's, then one per codebook step."""
+        cfg = self.cfg
+        log = getattr(self, "logits_log", None)
         tok = np.asarray(tokens, np.int32)
         x = o.embed_sum(self.t["embeddings"], tok, cfg.vocab_size, cfg.dim, BF)
         for i in range(cfg.n_layer):
@@ -94,22 +120,17 @@ class OracleDualAR:
                            cfg.max_seq_len, cfg.max_seq_len)
         hn = self.norm(x, "norm")
         logits = self.gemv("output", hn)
+        if log is not None:
+            log.append(logits)
         out = np.zeros(cfg.n_tokens, np.int32)
         out[0] = o.argmax(logits, BF)
-        fmax = cfg.fast_max_len
-        fx = self.gemv("fast_project_in", hn)
-        for i in range(cfg.fast_n_layer - 1):
-            fx = self.block(f"fast_layers.{i}", fx, self.fast_freqs[0], 0, cfg.fast_n_head, cfg.fast_n_local_heads,
-                            fmax, fmax)
-        self._qkv_rope_kv(f"fast_layers.{cfg.fast_n_layer - 1}", fx, self.fast_freqs[0], 0, cfg.fast_n_head,
-                          cfg.fast_n_local_heads, fmax)
+        self.fast_prime(self.gemv("fast_project_in", hn))
+        # codebook 0 is the semantic token, clamped into the codebook
         out[1] = min(max(int(out[0]), 0), cfg.codebook_size - 1)
         for i in range(1, cfg.num_codebooks):
-            h = o.embed_sum(self.t["fast_embeddings"], out[i:i + 1], cfg.codebook_size, cfg.fast_dim, BF)
-            for j in range(cfg.fast_n_layer):
-                h = self.block(f"fast_layers.{j}", h, self.fast_freqs[i], i, cfg.fast_n_head,
-                               cfg.fast_n_local_heads, fmax, fmax)
-            fl = self.gemv("fast_output", self.norm(h, "fast_norm"))
+            fl = self.fast_step(int(out[i]), i)
+            if log is not None:
+                log.append(fl)
             out[i + 1] = o.argmax(fl, BF)
         return out
 

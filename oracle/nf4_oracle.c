@@ -207,10 +207,11 @@ static inline float epilogue(float acc, int epi, float r, int dt) {
 
 /* The GPU GEMV's arithmetic, in its order (ttspipe_amd/csrc/nf4_gemv.hip):
  * lane l of K-slice ks owns dwords d = l + 64*(j*KS + ks); per dword the 8
- * codes (rounded to fp16; bf16 activations first scaled by 2^-e, e from the
- * largest |x| of the vector, and converted to fp16) are chained
- * q = fma(c_k, x_k, q) from q = +0 in code order, then acc = fma(q, s_block, acc); lanes are summed by the xor butterfly,
- * slices left to right; then the epilogue. */
+ * codes (the code points rounded to fp16, multiplied by the activations as
+ * fp32 - fp16 and bf16 values are both exact in fp32, so every product is
+ * exact) are chained q = fma(c_k, x_k, q) from q = +0 in code order, then
+ * acc = fma(q, s_block, acc); lanes are summed by the xor butterfly, slices
+ * left to right; then the epilogue. */
 void orc_gemv_emul(const void* X, int dt, const uint8_t* W, const uint8_t* A8, const float* AMAX,
                    const float* CODE2, float offset, const float* LUT, uint16_t* Y, const void* R,
                    int epi, int M, int K, int bs, int bs2, int KS, int J) {

@@ -234,19 +234,57 @@ def test_prefill_gemm_512_rows(nf4, orc, name, shape):
 
 
 @pytest.mark.parametrize("epi", [1, 2])
-def test_gemm_epilogues(nf4, orc, epi):
-    M, K, rows, dtype = 2560, 9728, 24, torch.float16
+@pytest.mark.parametrize("rows", [24, 512])
+def test_gemm_epilogues(nf4, orc, epi, rows):
+    """Residual and SwiGLU-gate epilogues of the GEMM (24 rows: unsplit; 512
+    rows at 2560 x 9728: the K-split plan, where the reduce kernel applies
+    them) against the closed forms round(R + round(y)) and
+    round(round(silu(R)) * round(y)) evaluated on the oracle's fp64 product,
+    within the 2e-3 bar beyond the output's own rounding. An epilogue with its
+    operands swapped misses that bar by an order of magnitude."""
+    from ttspipe_amd import _lib
+
+    M, K, dtype = 2560, 9728, torch.float16
+    if rows == 512:
+        assert _lib.load().ttsp_nf4_gemm_splits(M, K, rows) > 1
     layer = random_layer(M, K, True, seed=31)
     lin = to_linear(layer, dtype)
     xb = randn_bits(rows * K, dtype, seed=32, scale=0.5)
     rb = randn_bits(rows * M, dtype, seed=33)
     assert nf4.prepare(lin)
     y = nf4.matmul(lin, from_bits(xb, dtype).view(rows, K), epi=epi, operand=from_bits(rb, dtype).view(rows, M))
-    plain = nf4.matmul(lin, from_bits(xb, dtype).view(rows, K))
-    r = o.to_f32(rb, 0).astype(np.float64)
-    p = o.to_f32(bits(plain), 0).astype(np.float64)
-    expect = r + p if epi == 1 else (r / (1 + np.exp(-r))) * p
-    assert relative_error(o.to_f32(bits(y), 0), expect) < 5e-3
+    sample = np.arange(0, rows, 7)
+    ref = orc.nf4_gemm_ref(xb.reshape(rows, K)[sample], o.DT_F16, **oracle_args(layer), M=M, K=K,
+                           N=sample.size, bs=64, bs2=256).astype(np.float64)
+    yr = o.to_f32(o.from_f32(ref.astype(np.float32), o.DT_F16), o.DT_F16).astype(np.float64)
+    r = o.to_f32(rb, o.DT_F16).astype(np.float64).reshape(rows, M)[sample]
+    silu = o.to_f32(o.from_f32((r / (1 + np.exp(-r))).astype(np.float32), o.DT_F16), o.DT_F16).astype(np.float64)
+    expect = r + yr if epi == 1 else silu * yr
+    got = o.to_f32(bits(y), o.DT_F16).reshape(rows, M)[sample]
+    assert beyond_rounding_error(got, expect, o.DT_F16) < 2e-3
+    if epi == 2:
+        swapped = (yr / (1 + np.exp(-yr))) * r
+        assert beyond_rounding_error(got, swapped, o.DT_F16) > 2e-2
+
+
+@pytest.mark.parametrize("rows", [512, 300])
+def test_split_gemm_with_rows_not_a_multiple_of_four(nf4, orc, rows):
+    """1540 output features (M % 4 == 2) at K = 2560: 512 rows take a K split,
+    whose fp32 partial sums are then stored without 16-byte vectors."""
+    from ttspipe_amd import _lib
+
+    M, K, dtype = 1540, 2560, torch.bfloat16
+    splits = _lib.load().ttsp_nf4_gemm_splits(M, K, rows)
+    assert splits > 1
+    layer = random_layer(M, K, True, seed=1540)
+    lin = to_linear(layer, dtype)
+    xb = randn_bits(rows * K, dtype, seed=41)
+    y = lin(from_bits(xb, dtype).view(rows, K))
+    sample = np.arange(0, rows, 13)
+    ref = orc.nf4_gemm_ref(xb.reshape(rows, K)[sample], o.DT_BF16, **oracle_args(layer), M=M, K=K,
+                           N=sample.size, bs=64, bs2=256)
+    got = o.to_f32(bits(y), o.DT_BF16).reshape(rows, M)[sample]
+    assert beyond_rounding_error(got, ref, o.DT_BF16) < 2e-3
 
 
 # ------------------------------------------------------------ fused forms (one launch)

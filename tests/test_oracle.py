@@ -316,6 +316,63 @@ def test_qk_rope_kv_matches_unfused_ops(orc):
     assert not KC[:, :pos].any() and not KC[:, pos + 1 :].any()
 
 
+@pytest.mark.parametrize("dt", [o.DT_BF16, o.DT_F16])
+def test_qk_head_norm_rounds_once_bitwise(orc, dt):
+    """The head norm is y = round((x * r) * w) with a single rounding to the
+    16-bit type, r = 1 / sqrt(ss / 128 + eps) in fp32 (reference
+    fusedlayer.py:75-83), followed by the no-fma rotary; restated here in
+    numpy float32 and compared bit for bit. x are multiples of 1/16 below 4,
+    so every square and every partial sum of squares is exact in fp32 and the
+    sum does not depend on its order. A double-rounding mutant,
+    round(round(x * r) * w), differs on a visible fraction of elements."""
+    from ttspipe_amd.llama import precompute_freqs_cis
+
+    nh, nkv, max_len, pos, eps = 6, 2, 32, 21, 1e-6
+    rng = np.random.default_rng(40 + dt)
+    xf = (rng.integers(-63, 64, (nh + 2 * nkv, 128)) / 16.0).astype(np.float32)
+    wf = o.to_f32(o.from_f32((rng.random((2, 128)) + 0.5).astype(np.float32), dt), dt)
+    qkv = o.from_f32(xf.reshape(-1), dt)
+    assert np.array_equal(o.to_f32(qkv, dt).reshape(xf.shape), xf)  # exact in the 16-bit type
+    freqs = precompute_freqs_cis(max_len, 128, 1e6)[pos]
+    fb = freqs.contiguous().view(torch.int16).numpy().view(np.uint16).reshape(-1)
+    Q = np.zeros(nh * 128, np.uint16)
+    KC = np.zeros(nkv * max_len * 128, np.uint16)
+    VC = np.zeros(nkv * max_len * 128, np.uint16)
+    orc.qk_rope_kv(qkv, o.from_f32(wf[0], dt), o.from_f32(wf[1], dt), eps, fb, o.DT_BF16, pos, Q, KC, VC,
+                   nh, nkv, max_len, dt)
+    f = o.to_f32(fb, o.DT_BF16).reshape(64, 2)
+    c, s = f[:, 0], f[:, 1]
+
+    def expect(x, w, double):
+        ss = np.float32((x.astype(np.float64) ** 2).sum())  # exact, so any order
+        r = np.float32(1.0) / np.sqrt(ss / np.float32(128.0) + np.float32(eps))
+        xr = x * r
+        if double:
+            xr = o.to_f32(o.from_f32(xr, dt), dt)
+        y = o.to_f32(o.from_f32(xr * w, dt), dt)
+        x0, x1 = y[0::2], y[1::2]
+        out = np.empty(128, np.float32)
+        out[0::2] = x0 * c - x1 * s
+        out[1::2] = x1 * c + x0 * s
+        return o.from_f32(out, dt)
+
+    got_q = Q.reshape(nh, 128)
+    got_k = KC.reshape(nkv, max_len, 128)[:, pos]
+    differ = 0
+    for h in range(nh + nkv):
+        got = got_q[h] if h < nh else got_k[h - nh]
+        w = wf[0] if h < nh else wf[1]
+        assert np.array_equal(got, expect(xf[h], w, False)), f"head {h}: {first_diff(got, expect(xf[h], w, False))}"
+        differ += int((got != expect(xf[h], w, True)).sum())
+    assert differ > 0.02 * (nh + nkv) * 128, f"the double-rounding mutant differs on only {differ} elements"
+    assert np.array_equal(VC.reshape(nkv, max_len, 128)[:, pos], qkv.reshape(-1, 128)[nh + nkv:])
+
+
+def first_diff(a, b):
+    i = np.flatnonzero(a != b)
+    return "identical" if i.size == 0 else f"{i.size} differ, first at {i[0]}: {a[i[0]]:#06x} vs {b[i[0]]:#06x}"
+
+
 def test_exp_is_within_a_few_ulp(orc):
     x = np.linspace(-86.9, 88.5, 20001, dtype=np.float32)
     got = orc.exp_cw(x).astype(np.float64)

@@ -180,3 +180,69 @@ def test_prefill_refuses_a_span_padded_past_the_cache(fresh):
     assert not m.prefill(_tokens(m, 300, 3), 0)  # 300 pads to 512 > 320
     assert not m.prefill(_tokens(m, 20, 4), 300)  # 20 pads to 32: 332 > 320
     assert torch.equal(before, m.layers[0].attention.kv_cache.k_cache)
+
+
+@pytest.fixture(scope="module")
+def roomy():
+    """The reduced model with a cache long enough for two prompt spans."""
+    import dataclasses
+
+    from ttspipe_amd.dualar import SMALL, SyntheticDualAR
+
+    return SyntheticDualAR(dataclasses.replace(SMALL, max_seq_len=1280))
+
+
+def _kv_state(m, upto):
+    return [(b.attention.kv_cache.k_cache[:, :, :upto].clone(), b.attention.kv_cache.v_cache[:, :, :upto].clone())
+            for b in m.layers]
+
+
+def _set_kv(m, state):
+    for b, (k, v) in zip(m.layers, state):
+        b.attention.kv_cache.k_cache[:, :, :k.shape[2]].copy_(k)
+        b.attention.kv_cache.v_cache[:, :, :v.shape[2]].copy_(v)
+
+
+def _assert_same_prefill(m, eager, upto):
+    for i, ((k0, v0), (k1, v1)) in enumerate(zip(eager["kv"], _kv_state(m, upto))):
+        assert torch.equal(k0, k1) and torch.equal(v0, v1), f"layer {i} KV rows differ from the eager prefill"
+    assert torch.equal(m.logits, eager["logits"]) and int(m.prefill_token.item()) == eager["token"]
+
+
+@pytest.mark.gpu
+def test_graphed_prefill_captures_buckets_without_touching_live_kv(roomy):
+    """A 600-token prompt with no bucket captured beforehand: the second span's
+    bucket (128) is captured after the first span's KV rows are written, and
+    its warm-up runs at positions 0..127; the result must equal the eager
+    prefill, KV rows and logits bit for bit."""
+    m = roomy
+    m.prefill_graphs.clear()
+    initial = _kv_state(m, m.cfg.max_seq_len)
+    toks = _tokens(m, 600, 5)
+    assert m.prefill(toks, 0, graphed=False)
+    torch.cuda.synchronize()
+    eager = {"kv": _kv_state(m, 600), "logits": m.logits.clone(), "token": int(m.prefill_token.item())}
+    _set_kv(m, initial)
+    assert m.prefill(toks, 0, graphed=True)
+    torch.cuda.synchronize()
+    assert sorted(m.prefill_graphs) == [128, 512]
+    _assert_same_prefill(m, eager, 600)
+
+
+@pytest.mark.gpu
+def test_graphed_prefill_after_an_eager_one_keeps_its_context(roomy):
+    """An eager 64-token prompt at position 0, then 100 more tokens graphed at
+    position 64 whose bucket is captured on the spot: the first prompt's KV
+    rows survive the capture and the continuation equals the all-eager run."""
+    m = roomy
+    m.prefill_graphs.clear()
+    initial = _kv_state(m, m.cfg.max_seq_len)
+    head, tail = _tokens(m, 64, 6), _tokens(m, 100, 7)
+    assert m.prefill(head, 0, graphed=False) and m.prefill(tail, 64, graphed=False)
+    torch.cuda.synchronize()
+    eager = {"kv": _kv_state(m, 164), "logits": m.logits.clone(), "token": int(m.prefill_token.item())}
+    _set_kv(m, initial)
+    assert m.prefill(head, 0, graphed=False) and m.prefill(tail, 64, graphed=True)
+    torch.cuda.synchronize()
+    assert 128 in m.prefill_graphs
+    _assert_same_prefill(m, eager, 164)

@@ -213,7 +213,9 @@ __global__ __launch_bounds__(64 * WM * WN) void nf4_gemm_kernel(
   }
 
   if (YP) {  // split-K partials: 4 consecutive rows m per 16-byte store
+    // (n * M + m is a multiple of 4 only when M is: m always is)
     float* yp = YP + (size_t)blockIdx.z * N * M;
+    const bool v4 = (M & 3) == 0;
 #pragma unroll
     for (int i = 0; i < TM; ++i)
 #pragma unroll
@@ -223,7 +225,7 @@ __global__ __launch_bounds__(64 * WM * WN) void nf4_gemm_kernel(
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
           const int m = m0 + wm * (BM / WM) + i * 32 + 8 * g + 4 * (lane >> 5);
-          if (m + 4 <= M) {
+          if (v4 && m + 4 <= M) {
             *reinterpret_cast<float4*>(yp + (size_t)n * M + m) =
                 make_float4(acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2], acc[i][j][4 * g + 3]);
           } else {

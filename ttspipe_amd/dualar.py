@@ -431,20 +431,32 @@ class SyntheticDualAR:
         self._check(rc, "ttsp_argmax")
 
     def capture_prefill(self, buckets=None) -> None:
-        """One graph per padded span length (after an eager warm-up of each)."""
+        """One graph per padded span length (after an eager warm-up of each).
+
+        The warm-up runs the span at positions 0..b-1, which writes those KV
+        rows of every slow layer; they are saved first and put back after, so
+        a bucket can be captured while a prompt is live in the cache (the
+        logits and `prefill_token` the warm-up leaves are overwritten by the
+        next span anyway)."""
         import torch
 
         for b in buckets or PREFILL_BUCKETS:
-            if b in self.prefill_graphs:
+            if b in self.prefill_graphs or b > self.cfg.max_seq_len:
                 continue
             inp = torch.zeros(self.cfg.n_tokens, b, dtype=torch.int32, device=self.device)
             pos = torch.arange(b, dtype=torch.long, device=self.device)
             last = torch.zeros(1, dtype=torch.long, device=self.device)
+            saved = [(blk.attention.kv_cache.k_cache[:, :, :b].clone(), blk.attention.kv_cache.v_cache[:, :, :b].clone())
+                     for blk in self.layers]
             self.prefill_forward(inp, pos, last)
             torch.cuda.synchronize()
             g = torch.cuda.CUDAGraph()
             with torch.cuda.graph(g):
                 self.prefill_forward(inp, pos, last)
+            for blk, (kc, vc) in zip(self.layers, saved):
+                blk.attention.kv_cache.k_cache[:, :, :b].copy_(kc)
+                blk.attention.kv_cache.v_cache[:, :, :b].copy_(vc)
+            del saved
             self.prefill_graphs[b] = (g, inp, pos, last)
 
     def prefill(self, tokens, start: int, graphed: bool = True) -> bool:
