@@ -168,19 +168,26 @@ int ttsp_attn_nf4_gemv(const void* QKV, const void* QW, const void* KW, float ep
                        const float* CODE2, float offset, const float* LUT, void* Y, const void* R, int epi,
                        int M, int blocksize, int blocksize2, int dtype, void* stream);
 
-/* Top-k / top-p sampling of one row L [V] (fp16 or bf16 as dtype): the
- * largest top_k = TOPK[0] entries (1..ttsp_sample_max_top_k(), ties by lowest
- * index), sorted; the first and every one whose inclusive cumulative
- * probability under softmax(L) is <= TOPP[0] are kept; OUT[0] = the kept index
- * maximising L[i] / max(TEMP[0], 1e-5) - log(-log(U[i])) (U: one uniform
- * float per index), ties to the lowest index. TEMP and TOPP have L's dtype.
- * One workgroup. Replaces: sample_topk, app/engine/fusedsample.py:28-223. */
+/* Top-k / top-p sampling of one row L [V] (fp16 or bf16 as dtype, V up to
+ * ttsp_sample_max_vocab()): the largest top_k = TOPK[0] entries
+ * (1..ttsp_sample_max_top_k(), ties by lowest index), sorted; the first and
+ * every one whose inclusive cumulative probability under softmax(L) is <=
+ * TOPP[0] are kept; OUT[0] = the kept index maximising
+ * L[i] / max(TEMP[0], 1e-5) - log(-log(U[i])) (U: one uniform float per
+ * index), ties to the lowest index. TEMP and TOPP have L's dtype. One
+ * workgroup. Replaces: sample_topk, app/engine/fusedsample.py:28-223. */
 int ttsp_sample_topk(const void* L, int V, int dtype, const void* TEMP, const void* TOPP,
                      const long long* TOPK, const float* U, int* OUT, void* stream);
 
 /* The largest top_k ttsp_sample_topk serves (64). Replaces: MAX_TOP_K,
  * app/engine/fusedsample.py:26. */
 int ttsp_sample_max_top_k(void);
+
+/* The longest row ttsp_sample_topk serves (32768: the row is held in LDS).
+ * The reference's kernel streams rows of any length; a longer row here is
+ * declined and the caller's sampler runs (app/engine/fusedsample.py:226-238
+ * is that fallback for top_k above MAX_TOP_K). */
+int ttsp_sample_max_vocab(void);
 
 /* Cache positions per attention chunk (64). Replaces: CHUNK,
  * app/engine/fusedlayer.py:40. */

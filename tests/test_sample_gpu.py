@@ -100,3 +100,32 @@ def test_sampler_is_deterministic_and_greedy_limits():
     top = set(torch.topk(row.float(), 30).indices.tolist())
     for _ in range(50):
         assert int(fusedsample.sample(row, t, torch.tensor([1.0], device="cuda"), k).item()) in top
+
+
+@pytest.mark.parametrize("V", [1, 7, 63, 64, 65, 257, 4095, 32768])
+def test_sampler_row_lengths(V):
+    """Rows shorter than k, rows that do not fill the workgroup's stride and
+    the longest row served, against the oracle."""
+    dtype = torch.bfloat16
+    dt = dt_code(dtype)
+    rng = np.random.default_rng(V)
+    checked = 0
+    for trial in range(6):
+        lb = o.from_f32((rng.standard_normal(V) * 2.0).astype(np.float32), dt)
+        u = rng.random(V).astype(np.float32)
+        l = o.to_f32(lb, dt).astype(np.float64)
+        tq = float(o.to_f32(o.from_f32(np.float32([0.8]), dt), dt)[0])
+        pq = float(o.to_f32(o.from_f32(np.float32([0.9]), dt), dt)[0])
+        if _ambiguous(l, tq, pq, 64, u):
+            continue
+        assert _draw(lb, dtype, 0.8, 0.9, 64, u) == o.sample_topk_ref(l, tq, pq, 64, u)[0], f"trial {trial}"
+        checked += 1
+    assert checked >= 4
+
+
+def test_sampler_declines_rows_longer_than_it_holds():
+    from ttspipe_amd import fusedsample
+
+    row = torch.zeros(fusedsample.MAX_VOCAB + 1, device="cuda", dtype=torch.float16)
+    t, p = torch.tensor([1.0], device="cuda"), torch.tensor([1.0], device="cuda")
+    assert fusedsample.sample(row, t, p, torch.tensor([5], device="cuda")) is None

@@ -56,6 +56,7 @@ SIGNATURES: dict[str, list] = {
                                      _i, _vp, _i, _vp],
     "ttsp_sample_topk": [_vp, _i, _i, _vp, _vp, _vp, _vp, _vp, _vp],
     "ttsp_sample_max_top_k": [],
+    "ttsp_sample_max_vocab": [],
     "ttsp_embed_sum": [_vp, _vp, _i, _i, _i, _vp, _i, _vp],
     "ttsp_argmax": [_vp, _i, _i, _vp, _vp],
     "ttsp_synth_fill": [_vp, _ll, ctypes.c_ulonglong, _i, _f, _f, _vp],

@@ -119,8 +119,8 @@ __device__ __forceinline__ RopeF load_rope(const void* __restrict__ F, int ftype
 }
 
 // Head norm and rotary of one 128-wide head held by a wave (lane l: elements
-// l and l + 64), the arithmetic of qk_rope_kv_kernel: the norm's sum is the
-// two 64-element halves (rising DPP sums) added, one rounding after x * r * w;
+// l and l + 64), used by every kernel that writes q/k heads: the norm's sum is
+// the two 64-element halves (rising DPP sums) added, one rounding after x * r * w;
 // rotary pairs (2i, 2i+1) with the partner in lane l ^ 1, separately rounded
 // products and sum. Returns the rotated values, not yet rounded. nwl, nwh
 // are the norm weights of elements l and l + 64 (unused when norm is false).

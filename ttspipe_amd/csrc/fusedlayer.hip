@@ -25,46 +25,44 @@
 
 namespace ttsp {
 
+// Head norms, rotary and the KV-cache write of one or more positions: one
+// wave per head (QKV_WAVES heads a workgroup, any mix of q, k and v heads),
+// lane l holding elements l and l + 64 - the decode attention's own head
+// arithmetic (head_norm_rope), so both paths give the same bits. A q head goes
+// to Q, a k head to KC[kv][pos], a v head is copied to VC[kv][pos]. Row
+// blockIdx.y reads its own QKV row, rotary row and position; the rotary table
+// is read a dword at a time (4-byte aligned).
+constexpr int QKV_WAVES = 4;
+
 template <int DT>
-__global__ __launch_bounds__(HD) void qk_rope_kv_kernel(
+__global__ __launch_bounds__(64 * QKV_WAVES) void qk_rope_kv_kernel(
     const uint16_t* __restrict__ QKV, const uint16_t* __restrict__ QW,
     const uint16_t* __restrict__ KW, float eps, const void* __restrict__ F, int ftype,
     const long long* __restrict__ POS, uint16_t* __restrict__ Q, uint16_t* __restrict__ KC,
     uint16_t* __restrict__ VC, int nh, int nkv, int max_len, int qkv_rs) {
-  __shared__ float sx[HD];
-  __shared__ float part[HD / 64];
-  // row blockIdx.y of a run of positions: its QKV row, rotary row and Q row
+  const int lane = threadIdx.x & 63;
+  const int head = blockIdx.x * QKV_WAVES + (threadIdx.x >> 6);
   const int row = blockIdx.y;
-  QKV += (size_t)row * qkv_rs;
-  Q += (size_t)row * nh * HD;
-  F = (const uint8_t*)F + (size_t)row * HD * (ftype == DT_F32 ? 4 : 2);
-  const int head = blockIdx.x, d = threadIdx.x;
+  if (head >= nh + 2 * nkv) return;
   const long long pos = POS[row];
   if (pos < 0 || pos >= max_len) return;  // no cache slot to write: leave everything untouched
+  const uint16_t* src = QKV + (size_t)row * qkv_rs + (size_t)head * HD;
   if (head >= nh + nkv) {
-    const int vh = head - nh - nkv;
-    VC[((long long)vh * max_len + pos) * HD + d] = QKV[(size_t)(nh + nkv + vh) * HD + d];
+    uint16_t* v = VC + ((long long)(head - nh - nkv) * max_len + pos) * HD;
+    v[lane] = src[lane];
+    v[lane + 64] = src[lane + 64];
     return;
   }
   const bool is_q = head < nh;
-  float x = Elem<DT>::load(QKV[(size_t)head * HD + d]);
   const uint16_t* w = is_q ? QW : KW;
-  if (w != nullptr) {
-    const float v = wave_sum_dpp(__fmul_rn(x, x));
-    if ((d & 63) == 0) part[d >> 6] = v;
-    __syncthreads();
-    const float ss = __fadd_rn(part[0], part[1]);
-    const float r = rsqrt_rn(__fadd_rn(__fdiv_rn(ss, (float)HD), eps));
-    x = Elem<DT>::load(Elem<DT>::store(__fmul_rn(__fmul_rn(x, r), Elem<DT>::load(w[d]))));
-  }
-  sx[d] = x;
-  __syncthreads();
-  const float x0 = sx[d & ~1], x1 = sx[d | 1];
-  const float fr = load_elem(F, d & ~1, ftype), fi = load_elem(F, d | 1, ftype);
-  const float y = (d & 1) ? __fadd_rn(__fmul_rn(x1, fr), __fmul_rn(x0, fi))
-                          : __fsub_rn(__fmul_rn(x0, fr), __fmul_rn(x1, fi));
-  if (is_q) Q[(size_t)head * HD + d] = Elem<DT>::store(y);
-  else KC[((long long)(head - nh) * max_len + pos) * HD + d] = Elem<DT>::store(y);
+  const RopeF f = load_rope((const uint8_t*)F + (size_t)row * HD * (ftype == DT_F32 ? 4 : 2), ftype, lane);
+  float lo = Elem<DT>::load(src[lane]), hi = Elem<DT>::load(src[lane + 64]);
+  const uint16_t nwl = w ? w[lane] : 0, nwh = w ? w[lane + 64] : 0;
+  head_norm_rope<DT>(lo, hi, w != nullptr, nwl, nwh, eps, f, lane);
+  uint16_t* dst = is_q ? Q + (size_t)row * nh * HD + (size_t)head * HD
+                       : KC + ((long long)(head - nh) * max_len + pos) * HD;
+  dst[lane] = Elem<DT>::store(lo);
+  dst[lane + 64] = Elem<DT>::store(hi);
 }
 
 template <int DT>
@@ -355,9 +353,11 @@ extern "C" int ttsp_qk_rope_kv(const void* QKV, const void* QW, const void* KW, 
                                const void* F, int ftype, const long long* POS, void* Q, void* KC,
                                void* VC, int nh, int nkv, int max_len, int dtype,
                                hipStream_t stream) {
-  if (nh <= 0 || nkv <= 0 || max_len <= 0 || ftype < 0 || ftype > 2) return (int)hipErrorInvalidValue;
+  if (nh <= 0 || nkv <= 0 || max_len <= 0 || ftype < 0 || ftype > 2 || (uintptr_t)F % 4)
+    return (int)hipErrorInvalidValue;
 #define TTSP_QK(DTV)                                                                            \
-  hipLaunchKernelGGL(qk_rope_kv_kernel<DTV>, dim3(nh + 2 * nkv), dim3(HD), 0, stream,           \
+  hipLaunchKernelGGL(qk_rope_kv_kernel<DTV>, dim3((nh + 2 * nkv + QKV_WAVES - 1) / QKV_WAVES), dim3(64 * QKV_WAVES), \
+                     0, stream,                                                                 \
                      (const uint16_t*)QKV, (const uint16_t*)QW, (const uint16_t*)KW, eps, F, ftype, \
                      POS, (uint16_t*)Q, (uint16_t*)KC, (uint16_t*)VC, nh, nkv, max_len, 0)
   if (dtype == DT_F16) TTSP_QK(DT_F16);
@@ -372,10 +372,11 @@ extern "C" int ttsp_qk_rope_kv_rows(const void* QKV, long long qkv_row_stride, c
                                     void* VC, int nh, int nkv, int max_len, int rows, int dtype,
                                     hipStream_t stream) {
   if (nh <= 0 || nkv <= 0 || max_len <= 0 || ftype < 0 || ftype > 2 || rows <= 0 || rows > 65535 ||
-      qkv_row_stride < (long long)(nh + 2 * nkv) * HD || qkv_row_stride > (1LL << 30))
+      qkv_row_stride < (long long)(nh + 2 * nkv) * HD || qkv_row_stride > (1LL << 30) || (uintptr_t)F % 4)
     return (int)hipErrorInvalidValue;
 #define TTSP_QKR(DTV)                                                                            \
-  hipLaunchKernelGGL(qk_rope_kv_kernel<DTV>, dim3(nh + 2 * nkv, rows), dim3(HD), 0, stream,     \
+  hipLaunchKernelGGL(qk_rope_kv_kernel<DTV>, dim3((nh + 2 * nkv + QKV_WAVES - 1) / QKV_WAVES, rows),          \
+                     dim3(64 * QKV_WAVES), 0, stream,                                           \
                      (const uint16_t*)QKV, (const uint16_t*)QW, (const uint16_t*)KW, eps, F, ftype, \
                      POS, (uint16_t*)Q, (uint16_t*)KC, (uint16_t*)VC, nh, nkv, max_len, (int)qkv_row_stride)
   if (dtype == DT_F16) TTSP_QKR(DT_F16);

@@ -312,7 +312,9 @@ def prefill_block(block, x, freqs_cis, mask, input_pos):
 
 
 def install() -> bool:
-    """Route single-position `TransformerBlock.forward` calls through `decode_block`."""
+    """Patch `TransformerBlock.forward`: one-position calls go to `decode_block`,
+    multi-position calls to `prefill_block`, anything either declines to the
+    block's own forward."""
     global _installed
     if not _lib.gpu_present():
         return False

@@ -43,7 +43,9 @@ def _built():
 
 
 def rms_norm(x, weight, eps: float, out=None):
-    """`x * rsqrt(mean(x*x) + eps) * weight` over the last axis, or None."""
+    """The fork's RMSNorm of x over its last axis on the GPU kernel (two
+    roundings: after the normalisation and after the weight), or None when
+    the kernel cannot take these tensors."""
     lib = _built()
     if lib is None or not enabled:
         return None

@@ -1,17 +1,18 @@
-"""The NF4 matmul for decode and prefill, reading bitsandbytes-layout weights in place.
+"""NF4 linear layers on MI355X: one kernel library serves single-token decode and prompt prefill.
 
 Drop-in for the reference's `app/engine/nf4gemv.py` (same public names and
 behaviour: `MAX_N`, `NF4_CODE`, `EPI_*`, `available`, `prepare`, `matmul`,
 `install`, `stats`, `module._nf4_fast`, class attributes `_nf4_patched` /
-`_nf4_original_forward`). The arithmetic runs in `libttsp_hip.so`:
+`_nf4_original_forward`). The packed codes and their scales stay where
+bitsandbytes put them; `libttsp_hip.so` reads them directly:
 
-* one activation row -> the HBM-bound GEMV (`csrc/nf4_gemv.hip`): the packed
-  weight is streamed once with coalesced 256-byte wave loads, codes resolve
-  through an LDS pair table into `v_dot2_f32_{f16,bf16}`, deterministic wave
-  reductions;
-* several rows -> the MFMA GEMM (`csrc/nf4_gemm.hip`): NF4 tiles dequantised
-  into LDS feed `v_mfma_f32_32x32x16`, so a prompt reads each weight once per
-  tile of rows rather than once per row.
+* a single activation row goes to the GEMV (`csrc/nf4_gemv.hip`), a pure
+  stream of the packed weight: 256-byte wave loads, both codes of a byte
+  looked up at once in an LDS table, fp32 fma chains and DPP lane sums in a
+  fixed order (so results are reproducible bit for bit);
+* two or more rows go to the GEMM (`csrc/nf4_gemm.hip`), where each K-step's
+  weight tile is dequantised into LDS and multiplied by
+  `v_mfma_f32_32x32x16`: one dequantisation serves a whole tile of rows.
 
 Unlike the reference (fp16 only, nf4gemv.py:439) both fp16 and bf16
 activations are served; anything else is declined (`None`), exactly where the
@@ -43,7 +44,8 @@ _stats = {"fast": 0, "fallback": 0, "layers": 0}
 
 
 def stats() -> dict:
-    """Calls served by the kernel, calls handed back to the layer's own forward, layers covered."""
+    """Counters: `fast` (matmuls the kernels ran), `fallback` (calls the layer's
+    own forward took), `layers` (modules prepared for the kernels)."""
     return dict(_stats)
 
 
@@ -78,13 +80,15 @@ def _lut(device):
 
 
 def prepare(module) -> bool:
-    """Attach what the kernel needs to one NF4 layer, or record that it cannot serve it.
+    """Check one 4-bit layer once and cache the verdict on it as `_nf4_fast`.
 
-    Idempotent and cached on the module (`_nf4_fast`): a dict, or None for a
-    declined layer. Eligibility is the reference's (nf4gemv.py:333-376):
-    nf4, on the GPU, blocksize a power of two >= 64, in_features a multiple of
-    128 and of the blocksize, 16-byte aligned packed weight, uint8/fp32 nested
-    scales (or fp32 plain ones) forming a rectangle over the rows.
+    The cached value is the launch description (a dict) or None when the
+    kernels cannot read this layer; later calls return the cached verdict.
+    The conditions match the reference's (nf4gemv.py:333-376): NF4 codes on
+    the GPU; a power-of-two blocksize of at least 64; in_features divisible by
+    128 and by the blocksize; a 16-byte aligned packed weight; scales that are
+    either fp32 per block or the uint8 + fp32 double-quantised pair, one row of
+    blocks per output feature.
     """
     import torch
 
@@ -94,26 +98,26 @@ def prepare(module) -> bool:
 
     def reject(why: str) -> bool:
         module._nf4_fast = None
-        logger.debug("nf4 kernel declines %s: %s", type(module).__name__, why)
+        logger.debug("%s stays on its own forward (%s)", type(module).__name__, why)
         return False
 
     weight = getattr(module, "weight", None)
     quant_state = getattr(weight, "quant_state", None)
     if quant_state is None:
-        return reject("weight is not quantised yet")
+        return reject("no quant_state: the weight has not been packed")
     if getattr(quant_state, "quant_type", None) != "nf4":
-        return reject(f"quant_type={getattr(quant_state, 'quant_type', None)}")
+        return reject(f"codes are {getattr(quant_state, 'quant_type', None)!r}, the kernels read only 'nf4'")
     if weight.device.type != "cuda":
-        return reject("weight is not on a GPU")
+        return reject(f"packed weight lives on {weight.device.type}")
 
     out_features, in_features = tuple(quant_state.shape)
     blocksize = int(quant_state.blocksize)
     if blocksize < 64 or blocksize & (blocksize - 1):
-        return reject(f"blocksize {blocksize} is not a power of two >= 64")
+        return reject(f"scale block of {blocksize} codes (needs 64, 128, 256, ...)")
     if in_features % blocksize or in_features % 128:
-        return reject(f"in_features {in_features} is not a multiple of 128 and {blocksize}")
+        return reject(f"{in_features} input features do not split into 128-code steps and {blocksize}-code blocks")
     if weight.data_ptr() % 16:
-        return reject("packed weight is not 16-byte aligned")
+        return reject("packed weight starts off a 16-byte boundary")
 
     nblk = in_features // blocksize
     nested = bool(getattr(quant_state, "nested", False))
@@ -121,24 +125,25 @@ def prepare(module) -> bool:
         state2 = quant_state.state2
         bs2 = int(state2.blocksize)
         if bs2 <= 0 or bs2 & (bs2 - 1):
-            return reject(f"second-level blocksize {bs2} is not a power of two")
+            return reject(f"double-quant group of {bs2} blocks is not a power of two")
         if quant_state.absmax.dtype != torch.uint8 or state2.absmax.dtype != torch.float32:
-            return reject("second-level scales are not the uint8/fp32 pair the kernel reads")
+            return reject(f"double-quant scales are {quant_state.absmax.dtype}/{state2.absmax.dtype}, "
+                          "the kernels read uint8 indices and fp32 group maxima")
         if state2.code.dtype != torch.float32 or state2.code.numel() != 256:
-            return reject("second-level code is not a 256-entry fp32 table")
+            return reject("double-quant code table is not 256 fp32 values")
         scales = (quant_state.absmax, state2.absmax, state2.code)
         offset = float(quant_state.offset)
     else:
         if quant_state.absmax.dtype != torch.float32:
-            return reject(f"scales are {quant_state.absmax.dtype}, not float32")
+            return reject(f"per-block scales are {quant_state.absmax.dtype}; the kernels read fp32")
         scales = (None, quant_state.absmax, None)
         offset = 0.0
         bs2 = 0
     if quant_state.absmax.numel() != out_features * nblk:
-        return reject("scales do not form a rectangle over the weight rows")
+        return reject(f"{quant_state.absmax.numel()} scales for {out_features} rows of {nblk} blocks")
     for t in scales:
         if t is not None and (t.device != weight.device or not t.is_contiguous()):
-            return reject("scales are not contiguous on the weight's device")
+            return reject("a scale tensor is strided or on another device than the weight")
 
     module._nf4_fast = {
         "nested": nested,
@@ -159,12 +164,14 @@ def prepare(module) -> bool:
 
 
 def matmul(module, x, *, epi: int = EPI_NONE, operand=None, out=None):
-    """`x @ module.weight.T` for any number of input rows, or None if not applicable.
+    """Return x times the layer's weight transposed (fp16 or bf16 rows, any
+    count), or None when the kernels cannot take this call.
 
-    `epi` fuses what the fork does right after: `operand + xW` (residual add)
-    or `silu(operand) * xW` (the SwiGLU gate), rounded as the unfused ops
-    round. `operand` has the output's shape and x's dtype, contiguous, on the
-    same device. `out` (optional) receives the result in place.
+    `epi` folds the operation that follows in the fork into the store:
+    EPI_RESIDUAL gives `operand + y`, EPI_SILU_GATE `silu(operand) * y`, each
+    rounded exactly where the separate torch ops would round. `operand` must
+    match the output in shape, dtype and device and be contiguous; `out`, if
+    given, is written in place.
     """
     import torch
 
@@ -291,10 +298,11 @@ def _classes():
 
 
 def install(model=None) -> bool:
-    """Route fp16/bf16 NF4 `Linear4bit` calls through the kernels.
-
-    Patches the class, so it covers every instance including later ones.
-    Returns whether the fast path is live.
+    """Patch `Linear4bit.forward` (ours, and bitsandbytes' when importable) so
+    that fp16/bf16 calls on NF4 layers run on the kernels; layers or calls the
+    kernels cannot take keep the original forward. Class-level, so instances
+    created later are covered too. Returns False when the kernels are not
+    usable here (no GPU); with `model`, every layer is prepared immediately.
     """
     if not available():
         return False
@@ -322,7 +330,8 @@ def install(model=None) -> bool:
 
 
 def _prepare_all(model) -> None:
-    """Prepare every NF4 layer now, so no decode step pays for it."""
+    """Run `prepare` on every 4-bit layer of `model` up front (the checks and
+    pointer gathering then never happen inside a decode step or a capture)."""
     classes = tuple(_classes())
     served = declined = 0
     for module in model.modules():
@@ -331,4 +340,4 @@ def _prepare_all(model) -> None:
                 served += 1
             else:
                 declined += 1
-    logger.info("nf4 kernel ready for %d of %d 4-bit layers", served, served + declined)
+    logger.info("NF4 kernels serve %d 4-bit layers; %d keep their own forward", served, declined)
