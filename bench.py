@@ -41,6 +41,9 @@ MALL_BYTES = 256 * 2**20
 #: per dispatch (bench.py --only kernel --direct), each scaled by the same counter on a plain
 #: 64 MiB copy (FETCH_SIZE x 1.9992, WRITE_SIZE x 1.0). Re-measure when the kernel changes.
 GEMV_TRAFFIC_BYTES = 13_211_842
+#: Mean dispatch duration of the same kernel in `rocprofv3 --kernel-trace --stats -- python3 bench.py
+#: --only kernel` (the summary is committed with the profiles). Re-measure when the kernel changes.
+GEMV_ROCPROF_AVG_US = 6.361
 
 # (name, out_features, in_features) of one decoder layer's linears
 LAYER = [("q", 4096, 2560), ("k", 1024, 2560), ("v", 1024, 2560), ("o", 2560, 4096),
@@ -139,6 +142,41 @@ def capture(fn):
     return graph
 
 
+def time_exact_steps(body, ncopy: int, steps: int, warmup: int, sustained_replays: int = 100):
+    """Run exactly `warmup` untimed steps, then time exactly `steps` steps; a
+    step is one pass over one weight copy, and consecutive steps walk the
+    copies in order. `body(n)` launches the first n copies' steps. Steps go
+    as replays of a graph over all ncopy copies plus one graph over the first
+    steps % ncopy of them (copy 0 follows the last copy, so every step still
+    reads weights the cache no longer holds). The timed region is bracketed by
+    device synchronisation and timed with HIP events on the launch stream.
+    Also returns a sustained figure over `sustained_replays` full replays."""
+    import torch
+
+    stream = torch.cuda.current_stream()
+    graphs = {ncopy: capture(lambda: body(ncopy))}
+    for n in {steps % ncopy, warmup % ncopy} - {0}:
+        graphs[n] = capture(lambda n=n: body(n))
+
+    def run(n_steps):
+        for _ in range(n_steps // ncopy):
+            graphs[ncopy].replay()
+        if n_steps % ncopy:
+            graphs[n_steps % ncopy].replay()
+
+    run(warmup)
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record(stream)
+    run(steps)
+    end.record(stream)
+    end.synchronize()
+    torch.cuda.synchronize()
+    sec = start.elapsed_time(end) / 1e3 / steps
+    sustained = time_graph(graphs[ncopy], sustained_replays, stream) / ncopy
+    return sec, sustained
+
+
 def bench_layer(steps: int, warmup: int):
     """C2: the seven linears of one layer, nested absmax, bf16 x."""
     import torch
@@ -157,22 +195,17 @@ def bench_layer(steps: int, warmup: int):
     xs = {K: torch.randn(K, device=dev).to(torch.bfloat16) for K in {K for _, _, K in LAYER}}
     ys = {name: torch.empty(M, dtype=torch.bfloat16, device=dev) for name, M, _ in LAYER}
 
-    def body():
+    def body(n):
         st = torch.cuda.current_stream().cuda_stream
-        for layer in copies:
+        for layer in copies[:n]:
             for (name, M, K), lin in zip(LAYER, layer):
                 launch(lib, lut, lin, xs[K], ys[name], _lib.DT_BF16, st)
 
-    body()
+    body(ncopy)
     torch.cuda.synchronize()
-    graph = capture(body)
-    stream = torch.cuda.current_stream()
-    reps_w = max(1, warmup // ncopy)
-    time_graph(graph, reps_w, stream)
-    reps = max(1, steps // ncopy)
-    sec = time_graph(graph, reps, stream) / ncopy
-    return {"step_bytes": step_bytes, "sec_per_step": sec, "steps": reps * ncopy, "copies": ncopy,
-            "warmup": reps_w * ncopy}
+    sec, sustained = time_exact_steps(body, ncopy, steps, warmup)
+    return {"step_bytes": step_bytes, "sec_per_step": sec, "steps": steps, "copies": ncopy, "warmup": warmup,
+            "sustained_sec_per_step": sustained}
 
 
 def bench_fused_layer(steps: int, warmup: int):
@@ -199,25 +232,20 @@ def bench_fused_layer(steps: int, warmup: int):
     xs = {K: torch.randn(K, device=dev).to(torch.bfloat16) for K in {K for _, _, K in FUSED_LAYER}}
     ys = {name: torch.empty(M, dtype=torch.bfloat16, device=dev) for name, M, _ in FUSED_LAYER}
 
-    def body():
+    def body(n):
         st = torch.cuda.current_stream().cuda_stream
-        for layer in copies:
+        for layer in copies[:n]:
             for name, M, K in FUSED_LAYER:
                 if name == "gate_up":
                     launch_swiglu(lib, lut, layer[name], layer["up"], xs[K], ys[name], st)
                 else:
                     launch(lib, lut, layer[name], xs[K], ys[name], _lib.DT_BF16, st)
 
-    body()
+    body(ncopy)
     torch.cuda.synchronize()
-    graph = capture(body)
-    stream = torch.cuda.current_stream()
-    reps_w = max(1, warmup // ncopy)
-    time_graph(graph, reps_w, stream)
-    reps = max(1, steps // ncopy)
-    sec = time_graph(graph, reps, stream) / ncopy
-    return {"step_bytes": step_bytes, "sec_per_step": sec, "steps": reps * ncopy, "copies": ncopy,
-            "warmup": reps_w * ncopy}
+    sec, sustained = time_exact_steps(body, ncopy, steps, warmup)
+    return {"step_bytes": step_bytes, "sec_per_step": sec, "steps": steps, "copies": ncopy, "warmup": warmup,
+            "sustained_sec_per_step": sustained}
 
 
 def bench_kernel(M, K, nested, dtype_name, launches_per_copy=1, min_bytes=2 * MALL_BYTES, direct=False):
@@ -316,6 +344,116 @@ def bench_gemm(rows: int = 512, copies: int = 4, reps: int = 20):
             "pct_of_mfma_peak": round(100 * total_flop / total_s / 1e12 / MFMA_PEAK_TFLOPS, 2)}
 
 
+def bench_small_n(ns=(1, 2, 4, 8, 16, 32), min_bytes: int = 2 * MALL_BYTES, replays: int = 20):
+    """The reference's small-N table (nf4gemv.py:20-28: a frame of matmuls at
+    N = 1, 8, 16, 32 input rows): the seven projections of one layer at N
+    bf16 rows each (N = 1 through the GEMV, N > 1 through the MFMA GEMM),
+    graph-replayed over > 512 MB of distinct weight copies. Reports us per
+    layer and the effective rate (the layer's algorithmic bytes at N rows per
+    second), the reference's "effective" column."""
+    import torch
+
+    from ttspipe_amd import _lib
+    from ttspipe_amd.quant import NF4_CODE
+
+    lib = _lib.load()
+    dev = torch.device("cuda", 0)
+    lut = torch.tensor(NF4_CODE, dtype=torch.float32, device=dev)
+    weight_bytes = sum(M * K // 2 for _, M, K in LAYER)
+    ncopy = max(2, math.ceil(min_bytes / weight_bytes))
+    copies = [[Linear(M, K, True, seed=9000 + 10 * c + i, device=dev) for i, (_, M, K) in enumerate(LAYER)]
+              for c in range(ncopy)]
+    out = []
+    for n in ns:
+        xs = {K: torch.randn(n, K, device=dev).to(torch.bfloat16) for K in {K for _, _, K in LAYER}}
+        ys = {name: torch.empty(n, M, dtype=torch.bfloat16, device=dev) for name, M, _ in LAYER}
+
+        def body():
+            st = torch.cuda.current_stream().cuda_stream
+            for layer in copies:
+                for (name, M, K), lin in zip(LAYER, layer):
+                    rc = lib.ttsp_nf4_gemm(xs[K].data_ptr(), _lib.DT_BF16, lin.w.data_ptr(), _lib.ptr(lin.a8),
+                                           lin.amax.data_ptr(), _lib.ptr(lin.code2), lin.offset, lut.data_ptr(),
+                                           ys[name].data_ptr(), 0, 0, M, K, n, 64, 256, st)
+                    if rc:
+                        raise RuntimeError(f"ttsp_nf4_gemm failed: {rc}")
+
+        body()
+        torch.cuda.synchronize()
+        graph = capture(body)
+        stream = torch.cuda.current_stream()
+        time_graph(graph, 2, stream)
+        sec = time_graph(graph, replays, stream) / ncopy
+        nbytes = sum(nf4_bytes(M, K, True, 2) + 2 * (n - 1) * (M + K) for _, M, K in LAYER)
+        out.append({"rows": n, "layer_us": round(sec * 1e6, 2), "effective_gbs": round(nbytes / sec / 1e9, 1),
+                    "rel_to_n1": None})
+    for r in out:
+        r["rel_to_n1"] = round(r["layer_us"] / out[0]["layer_us"], 2)
+    return {"layer": "q, k, v, o, gate, up, down (7 launches), NF4 nested, bf16", "copies": ncopy, "points": out}
+
+
+def bench_norm_rope(min_bytes: int = 2 * MALL_BYTES, replays: int = 20):
+    """RMSNorm of hidden [S, 2560] and rotary of q [S, 32, 128] and k
+    [S, 8, 128] (bf16, theta 1e6 table, random positions in [0, 4096)) at
+    decode (S = 1) and prefill (S = 512), each op over distinct input copies
+    (> 512 MB for the prefill shapes) so the inputs stream from HBM.
+    Algorithmic bytes: norm 2*S*D*2 + 2*D; rotary per tensor 2*S*H*128*2 plus
+    its S rows of the table (read once per tensor: q and k are two launches)."""
+    import torch
+
+    from ttspipe_amd import _lib
+    from ttspipe_amd.llama import precompute_freqs_cis
+
+    lib = _lib.load()
+    dev = torch.device("cuda", 0)
+    D, nh, nkv, hd, eps = 2560, 32, 8, 128, 1e-6
+    g = torch.Generator(device=dev).manual_seed(31)
+    table = precompute_freqs_cis(4096, hd, 1e6).to(dev)
+    out = {}
+    for S in (1, 512):
+        per = 2 * S * D * 2 + 2 * (S * (nh + nkv) * hd * 2)
+        ncopy = max(4, min(400, math.ceil(min_bytes / per)))
+        xs = [torch.randn(S, D, device=dev, generator=g).to(torch.bfloat16) for _ in range(ncopy)]
+        w = (1.0 + 0.1 * torch.randn(D, device=dev, generator=g)).to(torch.bfloat16)
+        q = [torch.randn(1, S, nh, hd, device=dev, generator=g).to(torch.bfloat16) for _ in range(ncopy)]
+        k = [torch.randn(1, S, nkv, hd, device=dev, generator=g).to(torch.bfloat16) for _ in range(ncopy)]
+        pos = torch.randint(0, 4096, (S,), device=dev, generator=g)
+        f = table.index_select(0, pos).contiguous()
+        yn = torch.empty(S, D, dtype=torch.bfloat16, device=dev)
+        yq, yk = torch.empty_like(q[0]), torch.empty_like(k[0])
+
+        def norm_body():
+            st = torch.cuda.current_stream().cuda_stream
+            for x in xs:
+                _lib.check(lib.ttsp_rms_norm(x.data_ptr(), w.data_ptr(), yn.data_ptr(), S, D, eps, _lib.DT_BF16, st),
+                           "ttsp_rms_norm")
+
+        def rope_body():
+            st = torch.cuda.current_stream().cuda_stream
+            for a, b in zip(q, k):
+                for t, y, h in ((a, yq, nh), (b, yk, nkv)):
+                    _lib.check(lib.ttsp_rope(t.data_ptr(), f.data_ptr(), _lib.DT_BF16, y.data_ptr(), t.numel() // 2,
+                                             hd // 2, h, S, _lib.DT_BF16, st), "ttsp_rope")
+
+        res = {}
+        for name, body, launches, nbytes in (
+                ("rms_norm", norm_body, 1, 2 * S * D * 2 + 2 * D),
+                ("rope_qk", rope_body, 2, 2 * S * (nh + nkv) * hd * 2 + 2 * S * (hd // 2) * 2 * 2)):
+            body()
+            torch.cuda.synchronize()
+            graph = capture(body)
+            stream = torch.cuda.current_stream()
+            time_graph(graph, 2, stream)
+            sec = time_graph(graph, replays, stream) / ncopy
+            res[name] = {"us": round(sec * 1e6, 3), "launches": launches, "bytes": nbytes,
+                         "gbs": round(nbytes / sec / 1e9, 1),
+                         "pct_of_hbm_peak": round(100 * nbytes / sec / 1e9 / HBM_PEAK_GBS, 2)}
+        res["copies"] = ncopy
+        out["decode_1" if S == 1 else f"prefill_{S}"] = res
+        del xs, q, k
+    return out
+
+
 def bench_prefill_attention(cases=((512, 0), (512, 1536), (64, 2000)), n_head: int = 32, n_kv: int = 8,
                             reps: int = 20):
     """Prefill attention of `rows` new positions (32 q / 8 kv heads of 128,
@@ -409,7 +547,8 @@ def main() -> int:
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--skip-cpu", action="store_true")
     ap.add_argument("--skip-decode", action="store_true")
-    ap.add_argument("--only", choices=["layer", "kernel", "c1", "copy", "decode", "gemm", "pattn", "prefill"],
+    ap.add_argument("--only", choices=["layer", "kernel", "c1", "copy", "decode", "gemm", "pattn", "prefill",
+                                       "smalln", "normrope"],
                     default=None,
                     help="run one GPU measurement only (for profiling runs)")
     ap.add_argument("--decode-steps", type=int, default=256, help="greedy frames the decode benchmark times")
@@ -439,6 +578,10 @@ def main() -> int:
         out["gemm"] = bench_gemm()
     if args.only in (None, "pattn"):
         out["pattn"] = bench_prefill_attention()
+    if args.only in (None, "smalln"):
+        out["smalln"] = bench_small_n()
+    if args.only in (None, "normrope"):
+        out["normrope"] = bench_norm_rope()
     if args.only in (None, "prefill"):
         from ttspipe_amd import dualar
 
@@ -479,6 +622,10 @@ def main() -> int:
             "bytes_per_step": fused["step_bytes"],
             "weight_copies_rotated": fused["copies"],
             "pct_of_hbm_peak": round(100 * value / HBM_PEAK_GBS, 1),
+            "sustained_over_100_replays": {
+                "steps": 100 * fused["copies"],
+                "gbs": round(fused["step_bytes"] / fused["sustained_sec_per_step"] / 1e9, 1),
+                "ms_per_step": round(fused["sustained_sec_per_step"] * 1e3, 5)},
             "seven_separate_launches": {"gbs": round(separate, 1), "ms_per_step": round(layer["sec_per_step"] * 1e3, 5),
                                         "bytes_per_step": layer["step_bytes"]},
         },
@@ -491,7 +638,12 @@ def main() -> int:
             "frac": round(kern["gbs"] / HBM_PEAK_GBS, 4),
             "traffic": GEMV_TRAFFIC_BYTES,
             "avg_launch_us": round(kern["sec"] * 1e6, 3),
+            "avg_launch_us_is": "launch-to-launch interval of back-to-back graph-replayed launches (HIP events)",
             "bytes_per_launch": kern["bytes"],
+            "rocprof_avg_us": GEMV_ROCPROF_AVG_US,
+            "rocprof_avg_us_is": "mean begin-to-end dispatch duration in the kernel trace of `bench.py --only "
+                                 "kernel` (the tracer's completion signals keep launches from overlapping)",
+            "frac_rocprof": round(kern["bytes"] / (GEMV_ROCPROF_AVG_US * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
         },
         "gemv_fp16_plain": {
             "shape": "9728x2560 fp16 x, fp32 absmax bs64",
@@ -502,6 +654,8 @@ def main() -> int:
         },
         "decode": decode,
         "prefill_gemm": out["gemm"],
+        "small_n_gemm": out["smalln"],
+        "norm_rope": out["normrope"],
         "prefill_attention": out["pattn"],
         "prefill_512": out["prefill"],
         "cpu_baseline": cpu,

@@ -50,6 +50,29 @@ def _cpu_model() -> str:
     return platform.processor() or "unknown"
 
 
+def host() -> dict:
+    """This host as the baseline ran on it: CPU model, the logical CPUs this
+    process may run on (the threads used), the physical cores those CPUs
+    belong to (distinct (package, core) pairs in sysfs), and the machine's
+    logical CPU count."""
+    cpus = sorted(os.sched_getaffinity(0))
+    cores = set()
+    for c in cpus:
+        base = Path(f"/sys/devices/system/cpu/cpu{c}/topology")
+        try:
+            cores.add((int((base / "physical_package_id").read_text()), int((base / "core_id").read_text())))
+        except (OSError, ValueError):
+            cores.add((0, c))
+    return {"model": _cpu_model(), "logical_cpus_used": len(cpus), "physical_cores_used": len(cores),
+            "logical_cpus_on_host": os.cpu_count()}
+
+
+def _host_text() -> str:
+    h = host()
+    return (f"{h['model']}; {h['logical_cpus_used']} logical CPUs on {h['physical_cores_used']} physical cores "
+            f"available to this process (host has {h['logical_cpus_on_host']} logical CPUs)")
+
+
 def gemv(x_bf16: np.ndarray, packed: np.ndarray, absmax_bf16: np.ndarray, code_bf16: np.ndarray, n_out: int,
          threads: int | None = None, force_scalar: bool = False) -> np.ndarray:
     lib = _lib()
@@ -109,7 +132,8 @@ def run(layer_shapes, seconds: float = 10.0, threads: int | None = None) -> dict
         "sample": f"{steps} steps of the same 7-linear layer (bf16 x, dense bf16 absmax as the reference's CPU "
                   f"path stores it), {ncopy} weight copies rotated, {el:.1f} s; "
                   f"{'AVX512-BF16 kernel' if avx else 'scalar fallback (no AVX512-BF16 on this host)'}; "
-                  f"{_cpu_model()}, {os.cpu_count()} logical CPUs",
+                  f"{_host_text()}",
+        "host": host(),
     }
 
 
