@@ -200,7 +200,7 @@ def test_fp32_activations_are_declined(nf4):
 
 # ------------------------------------------------------------------ GEMM (N > 1)
 
-@pytest.mark.parametrize("rows", [2, 5, 8, 9, 16, 19, 32, 33, 70])
+@pytest.mark.parametrize("rows", [2, 5, 8, 9, 16, 17, 19, 32, 33, 48, 64, 65, 70])
 @pytest.mark.parametrize("shape", [(6144, 2560), (2560, 9728), (1544, 2560)])
 @pytest.mark.parametrize("dtype", DTYPES)
 def test_several_positions_within_bar(nf4, orc, shape, rows, dtype):
@@ -214,6 +214,19 @@ def test_several_positions_within_bar(nf4, orc, shape, rows, dtype):
     dt = dt_code(dtype)
     ref = orc.nf4_gemm_ref(xb, dt, **oracle_args(layer), M=M, K=K, N=rows, bs=64, bs2=256)
     assert beyond_rounding_error(o.to_f32(bits(y), dt), ref.reshape(-1), dt) < 2e-3
+
+
+@pytest.mark.parametrize("rows", [3, 16, 17, 40])
+def test_few_rows_over_a_long_row(nf4, orc, rows):
+    """K = 16384: up to 16 rows the few-row kernel splits K over 16 waves; more
+    rows than its limit for that K go to the tiled GEMM. Both within the bar."""
+    M, K, dtype = 272, 16384, torch.bfloat16
+    layer = random_layer(M, K, True, seed=rows + 7)
+    lin = to_linear(layer, dtype)
+    xb = randn_bits(rows * K, dtype, seed=rows + 8, scale=0.5)
+    y = lin(from_bits(xb, dtype).view(rows, K))
+    ref = orc.nf4_gemm_ref(xb, o.DT_BF16, **oracle_args(layer), M=M, K=K, N=rows, bs=64, bs2=256)
+    assert beyond_rounding_error(o.to_f32(bits(y), o.DT_BF16), ref.reshape(-1), o.DT_BF16) < 2e-3
 
 
 @pytest.mark.parametrize("name,shape", [("q", (4096, 2560)), ("k", (1024, 2560)), ("o", (2560, 4096)),

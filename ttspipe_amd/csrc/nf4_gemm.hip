@@ -376,14 +376,19 @@ static void launch_gemm(const void* X, const uint8_t* W, const uint8_t* A8, cons
 // Tile shape and K-split of a launch: unsplit with the largest tile (128 x
 // 128, then 64 x 128) that gives every CU a workgroup; else the largest tile
 // that does with the fewest splits (2, 4, 8; each split at least 8 K-steps,
-// an even number); otherwise 64 x 64 tiles, unsplit. Rows <= 32 take the
-// 128 x 32 tile. (Measured on the 512-row layer: a split costs more than a
-// smaller tile while the smaller tile still fills the GPU.)
+// an even number); otherwise 64 x 64 tiles, unsplit. Up to SKINNY_MAX_N rows
+// take the skinny kernel (nf4_skinny.hip), shape 0, never split. (Measured on
+// the 512-row layer: a split costs more than a smaller tile while the smaller
+// tile still fills the GPU.)
 struct GemmPlan {
   int shape, splits;
 };
+constexpr int SKINNY_MAX_N = 64;
+int skinny_max_k(int N);
+static bool skinny(int K, int N) { return N <= SKINNY_MAX_N && K <= skinny_max_k(N); }
+
 static GemmPlan gemm_plan(int M, int K, int N) {
-  if (N <= 32) return {0, 1};
+  if (skinny(K, N)) return {0, 1};
   const int steps = K / KT;
   const auto tiles = [&](int bm, int bn) { return (long long)((M + bm - 1) / bm) * ((N + bn - 1) / bn); };
   const int shapes[2][3] = {{1, 128, 128}, {2, 64, 128}};
@@ -415,13 +420,11 @@ int gemm_mfma(const void* X, int dt, const uint8_t* W, const uint8_t* A8, const 
   // dequantisation runs while the other's matrix products do)
   const int shape = plan.shape;
   if (dt == DT_BF16) {
-    if (shape == 0) TTSP_G(DT_BF16, 128, 32, 4, 1);
-    else if (shape == 1) TTSP_G(DT_BF16, 128, 128, 4, 2);
+    if (shape == 1) TTSP_G(DT_BF16, 128, 128, 4, 2);
     else if (shape == 2) TTSP_G(DT_BF16, 64, 128, 2, 4);
     else TTSP_G(DT_BF16, 64, 64, 2, 2);
   } else if (dt == DT_F16) {
-    if (shape == 0) TTSP_G(DT_F16, 128, 32, 4, 1);
-    else if (shape == 1) TTSP_G(DT_F16, 128, 128, 4, 2);
+    if (shape == 1) TTSP_G(DT_F16, 128, 128, 4, 2);
     else if (shape == 2) TTSP_G(DT_F16, 64, 128, 2, 4);
     else TTSP_G(DT_F16, 64, 64, 2, 2);
   } else {
@@ -444,6 +447,9 @@ int gemm_mfma(const void* X, int dt, const uint8_t* W, const uint8_t* A8, const 
 int gemv_n1(const void* X, int dt, const uint8_t* W, const uint8_t* A8, const float* AMAX,
             const float* CODE2, float offset, const float* LUT, void* Y, const void* R, int epi,
             int M, int K, int blocksize, int blocksize2, hipStream_t st);
+int gemm_skinny(const void* X, int dt, const uint8_t* W, const uint8_t* A8, const float* AMAX, const float* CODE2,
+                float offset, const float* LUT, void* Y, const void* RES, int epi, int M, int K, int N, int bs_shift,
+                int bs2_shift, hipStream_t st);
 
 }  // namespace ttsp
 
@@ -465,8 +471,9 @@ static int gemm_args(const void* X, const uint8_t* W, const uint8_t* A8, const f
   return 0;
 }
 
-// One entry for every row count: one row takes the bandwidth-bound GEMV,
-// more rows the MFMA kernel (weights read once per BN rows), unsplit.
+// One entry for every row count: one row takes the bandwidth-bound GEMV, up
+// to 64 rows the skinny MFMA kernel (weights streamed once), more rows the
+// tiled MFMA kernel (weights read once per BN rows), unsplit.
 extern "C" int ttsp_nf4_gemm(const void* X, int x_dtype, const uint8_t* W, const uint8_t* A8,
                              const float* AMAX, const float* CODE2, float offset, const float* LUT,
                              void* Y, const void* R, int epi, int M, int K, int N, int blocksize,
@@ -478,11 +485,13 @@ extern "C" int ttsp_nf4_gemm(const void* X, int x_dtype, const uint8_t* W, const
   if (int rc = gemm_args(X, W, A8, AMAX, CODE2, LUT, Y, R, epi, M, K, N, blocksize, blocksize2, &bs_shift,
                          &bs2_shift))
     return rc;
+  if (skinny(K, N))
+    return gemm_skinny(X, x_dtype, W, A8, AMAX, CODE2, offset, LUT, Y, R, epi, M, K, N, bs_shift, bs2_shift, stream);
   // vectorised output rows: 8 elements per 16-byte store
   const bool vec = M % 8 == 0 && (uintptr_t)Y % 16 == 0 && (!epi || (uintptr_t)R % 16 == 0);
   // unsplit: the largest tile that still gives every CU a workgroup
   const auto tiles = [&](int bm, int bn) { return (long long)((M + bm - 1) / bm) * ((N + bn - 1) / bn); };
-  const GemmPlan plan{N <= 32 ? 0 : tiles(128, 128) >= 256 ? 1 : tiles(64, 128) >= 256 ? 2 : 3, 1};
+  const GemmPlan plan{tiles(128, 128) >= 256 ? 1 : tiles(64, 128) >= 256 ? 2 : 3, 1};
   return gemm_mfma(X, x_dtype, W, A8, AMAX, CODE2, offset, LUT, Y, R, epi | (vec ? 4 : 0), M, K, N, bs_shift,
                    bs2_shift, plan, nullptr, stream);
 }
