@@ -11,6 +11,10 @@ records:
   kernel's summation order and therefore the bits the oracle reproduces (a
   GPU test asserts the library still reports these, so a kernel whose order
   changed fails loudly instead of comparing against stale ids);
+* per frame, sha256 digests of the slow head's logits and of the last
+  codebook step's logits (bf16 bit patterns): the decode of this random model
+  falls into a few recurring token columns, so the logits carry most of what
+  distinguishes one frame from the next;
 * sha256 digests of the K and V cache rows written at frames 0, 128 and 255
   in slow layers 0, 17 and 35, and of the rotary tables the frame used.
 
@@ -86,10 +90,14 @@ def make(frames: int, cfg=None) -> dict:
                        code2=create_dynamic_map().numpy(), freqs_bits=fb, fast_freqs_bits=ffb)
     t0 = time.time()
     hist = np.zeros((frames, cfg.n_tokens), np.int32)
+    slow_logits, fast_logits = [], []
     tok = np.asarray(first_tokens(cfg), np.int32)
     for f in range(frames):
+        orc.logits_log = []
         tok = orc.step(tok, cfg.prefill_len + f)
         hist[f] = tok
+        slow_logits.append(digest(orc.logits_log[0]))
+        fast_logits.append(digest(orc.logits_log[-1]))
         print(f"frame {f}: {tok.tolist()} ({time.time() - t0:.0f} s)", flush=True)
     kv = {}
     for layer in KV_LAYERS:
@@ -111,6 +119,8 @@ def make(frames: int, cfg=None) -> dict:
         "fast_freqs_sha256": digest(ffb),
         "kv_rows_sha256": kv,
         "tokens": hist.tolist(),
+        "slow_logits_sha256": slow_logits,
+        "last_fast_logits_sha256": fast_logits,
         "cpu_seconds": round(time.time() - t0, 1),
     }
 
