@@ -151,6 +151,25 @@ int ttsp_attn_decode_qkv(const void* QKV, const void* QW, const void* KW, float 
                          float* PACC, void* Y, int nh, int nkv, int max_len, int nchunk, float scale,
                          int dtype, void* stream);
 
+/* ttsp_attn_decode_qkv without scratch arguments, for callers that cannot
+ * allocate (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc); it has no counterpart in the reference. The split-K
+ * partials live in a device array inside the library, one per GPU, allocated
+ * with the library and held until the process ends: nh * nchunk <=
+ * ttsp_attn_decode_qkv_noalloc_max_slots() (4096, about 2.1 MB), larger
+ * requests return hipErrorInvalidValue. Nothing is allocated and nothing needs
+ * clearing (every slot the merge reads is written by the same call). All calls
+ * on one GPU share that array: calls that overlap on one GPU (two streams)
+ * race. The first call on a device looks the array up and must not be the
+ * first thing captured into a graph on a device that has never run it.
+ * Results equal ttsp_attn_decode_qkv bit for bit. */
+int ttsp_attn_decode_qkv_noalloc(const void* QKV, const void* QW, const void* KW, float eps, const void* F,
+                                 int ftype, const long long* POS, void* KC, void* VC, void* Y, int nh, int nkv,
+                                 int max_len, int nchunk, float scale, int dtype, void* stream);
+
+/* The largest nh * nchunk ttsp_attn_decode_qkv_noalloc serves (4096). */
+int ttsp_attn_decode_qkv_noalloc_max_slots(void);
+
 /* ttsp_attn_decode_qkv for a cache of at most one chunk, and the attention
  * output projection, in one launch: every workgroup of the NF4 GEMV that
  * computes Y = epi(attention . W^T) first computes the whole attention (all

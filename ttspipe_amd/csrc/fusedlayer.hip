@@ -23,6 +23,8 @@
 // All of these are deterministic: no atomics, fixed orders.
 #include "attn_common.h"
 
+#include <mutex>
+
 namespace ttsp {
 
 // Head norms, rotary and the KV-cache write of one or more positions: one
@@ -436,3 +438,57 @@ extern "C" int ttsp_attn_decode_qkv(const void* QKV, const void* QW, const void*
 #undef TTSP_AQ
   TTSP_RETURN_LAUNCH();
 }
+
+// ---------------------------------------------------------------------------
+// The allocation-free form of ttsp_attn_decode_qkv: the split-K partials live
+// in a file-scope device array (one copy per GPU, held until the process
+// ends) instead of caller buffers. Host code never passes the array's name to
+// a kernel: its device address is looked up once per device with that device
+// current (hipGetSymbolAddress) and kept in attn_scratch_ptr.
+constexpr int NOALLOC_SLOTS = 4096;  // nh * nchunk: e.g. 32 heads over a 8192-position cache
+constexpr int NOALLOC_FLOATS = NOALLOC_SLOTS * (2 + HD);  // PM, PL, then PACC [slots][128]
+static __device__ __align__(256) float scratch[NOALLOC_FLOATS];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex attn_scratch_mu;
+float* attn_scratch_ptr[kMaxDevices];
+
+// The scratch array's address on the device `stream` runs on (the current
+// device for the null stream); set up on the first call for that device.
+int attn_scratch(hipStream_t stream, float** out) {
+  int dev = 0;
+  hipError_t rc = stream ? hipStreamGetDevice(stream, &dev) : hipGetDevice(&dev);
+  if (rc != hipSuccess) return (int)rc;
+  if (dev < 0 || dev >= kMaxDevices) return (int)hipErrorInvalidDevice;
+  std::lock_guard<std::mutex> lock(attn_scratch_mu);
+  if (!attn_scratch_ptr[dev]) {
+    int cur = 0;
+    if ((rc = hipGetDevice(&cur)) != hipSuccess) return (int)rc;
+    if (cur != dev && (rc = hipSetDevice(dev)) != hipSuccess) return (int)rc;
+    void* p = nullptr;
+    rc = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (cur != dev) {
+      const hipError_t back = hipSetDevice(cur);
+      if (rc == hipSuccess) rc = back;
+    }
+    if (rc != hipSuccess) return (int)rc;
+    attn_scratch_ptr[dev] = static_cast<float*>(p);
+  }
+  *out = attn_scratch_ptr[dev];
+  return 0;
+}
+}  // namespace
+
+extern "C" int ttsp_attn_decode_qkv_noalloc(const void* QKV, const void* QW, const void* KW, float eps,
+                                            const void* F, int ftype, const long long* POS, void* KC, void* VC,
+                                            void* Y, int nh, int nkv, int max_len, int nchunk, float scale,
+                                            int dtype, hipStream_t stream) {
+  if (nh <= 0 || nchunk <= 0 || (long long)nh * nchunk > NOALLOC_SLOTS) return (int)hipErrorInvalidValue;
+  float* s = nullptr;
+  if (int rc = attn_scratch(stream, &s)) return rc;
+  return ttsp_attn_decode_qkv(QKV, QW, KW, eps, F, ftype, POS, KC, VC, s, s + NOALLOC_SLOTS, s + 2 * NOALLOC_SLOTS, Y,
+                              nh, nkv, max_len, nchunk, scale, dtype, stream);
+}
+
+extern "C" int ttsp_attn_decode_qkv_noalloc_max_slots(void) { return NOALLOC_SLOTS; }
