@@ -275,14 +275,6 @@ int ttsp_argmax(const void* X, int n, int dtype, int* out, void* stream);
 int ttsp_synth_fill(void* out, long long n, unsigned long long seed, int kind, float scale,
                     float offset, void* stream);
 
-/* Numerics self-tests (no counterpart in the reference; for the test suite):
- * op 0 exp, 1 correctly rounded sqrt, 2 1/sqrt, 3 silu, each as the kernels
- * compute them; fma16: fma(a.hi, b.hi, fma(a.lo, b.lo, c)) on packed fp16
- * pairs, the GEMV's inner step. */
-int ttsp_selftest_math(const float* in, int n, int op, float* out, void* stream);
-int ttsp_selftest_fma16(const uint32_t* a, const uint32_t* b, const float* c, int n, float* out,
-                        void* stream);
-
 #ifdef __cplusplus
 }
 #endif

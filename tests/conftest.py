@@ -48,6 +48,23 @@ def hip():
 
 
 @pytest.fixture(scope="session")
+def selftest():
+    """The numerics self-test library (tests/csrc/selftest.hip), loaded."""
+    import ctypes
+
+    from tests import build_selftest
+
+    if not build_selftest.LIB.exists():
+        raise RuntimeError(f"{build_selftest.LIB} is not built; run `python -m tests.build_selftest`")
+    lib = ctypes.CDLL(str(build_selftest.LIB))
+    vp, i = ctypes.c_void_p, ctypes.c_int
+    lib.ttsp_selftest_math.argtypes = [vp, i, i, vp, vp]
+    lib.ttsp_selftest_fma16.argtypes = [vp, vp, vp, i, vp, vp]
+    lib.ttsp_selftest_math.restype = lib.ttsp_selftest_fma16.restype = i
+    return lib
+
+
+@pytest.fixture(scope="session")
 def orc():
     from oracle import oracle
 

@@ -1,7 +1,8 @@
-// Numerics self-test entry points: evaluate the device primitives every
-// kernel relies on (exp_cw, sqrt_rn, silu_rn, the fp16-operand fma) over
-// caller arrays, so a test can compare them bit for bit against IEEE CPU
-// arithmetic. No counterpart in the reference; used by the test suite.
+// Numerics self-test entry points - TEST INFRASTRUCTURE, built into
+// tests/libttsp_selftest.so, not the product library: evaluate the device
+// primitives every kernel relies on (exp_cw, sqrt_rn, silu_rn, the
+// fp16-operand fma, from ttspipe_amd/csrc/ttsp_common.h) over caller arrays,
+// so a test can compare them bit for bit against IEEE CPU arithmetic.
 #include "ttsp_common.h"
 
 namespace ttsp {

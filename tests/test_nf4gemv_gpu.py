@@ -34,7 +34,7 @@ def nf4():
 
 # ------------------------------------------------------------ numerics primitives
 
-def test_fp16_fma_chain_is_ieee(hip, orc):
+def test_fp16_fma_chain_is_ieee(selftest, orc):
     """The GEMV's inner step, fma(a.hi, b.hi, fma(a.lo, b.lo, c)) on fp16 halves
     (v_fma_mix_f32), equals IEEE fmaf bit for bit - over random, tiny, huge and
     exactly cancelling operands."""
@@ -54,14 +54,14 @@ def test_fp16_fma_chain_is_ieee(hip, orc):
     bt = torch.from_numpy(b.view(np.int32)).cuda()
     ct = torch.from_numpy(c).cuda()
     out = torch.empty(n, dtype=torch.float32, device="cuda")
-    assert hip.ttsp_selftest_fma16(at.data_ptr(), bt.data_ptr(), ct.data_ptr(), n, out.data_ptr(), _lib.stream()) == 0
+    assert selftest.ttsp_selftest_fma16(at.data_ptr(), bt.data_ptr(), ct.data_ptr(), n, out.data_ptr(), _lib.stream()) == 0
     got = out.cpu().numpy()
     expect = o.fma16_chain(a, b, c)
     assert np.array_equal(got.view(np.uint32), expect.view(np.uint32)), first_mismatch(got, expect)
 
 
 @pytest.mark.parametrize("op", [0, 1, 2, 3])
-def test_device_math_matches_the_oracle_bit_for_bit(hip, orc, op):
+def test_device_math_matches_the_oracle_bit_for_bit(selftest, orc, op):
     from ttspipe_amd import _lib
 
     rng = np.random.default_rng(op)
@@ -73,7 +73,7 @@ def test_device_math_matches_the_oracle_bit_for_bit(hip, orc, op):
         x = rng.uniform(-30, 30, 40000).astype(np.float32)
     xt = torch.from_numpy(x).cuda()
     out = torch.empty_like(xt)
-    assert hip.ttsp_selftest_math(xt.data_ptr(), x.size, op, out.data_ptr(), _lib.stream()) == 0
+    assert selftest.ttsp_selftest_math(xt.data_ptr(), x.size, op, out.data_ptr(), _lib.stream()) == 0
     got = out.cpu().numpy()
     if op == 0:
         expect = orc.exp_cw(x)

@@ -62,8 +62,6 @@ SIGNATURES: dict[str, list] = {
     "ttsp_embed_sum": [_vp, _vp, _i, _i, _i, _vp, _i, _vp],
     "ttsp_argmax": [_vp, _i, _i, _vp, _vp],
     "ttsp_synth_fill": [_vp, _ll, ctypes.c_ulonglong, _i, _f, _f, _vp],
-    "ttsp_selftest_math": [_vp, _i, _i, _vp, _vp],
-    "ttsp_selftest_fma16": [_vp, _vp, _vp, _i, _vp, _vp],
 }
 
 
