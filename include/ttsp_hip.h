@@ -94,14 +94,16 @@ int ttsp_nf4_dequant(const uint8_t* W, const uint8_t* A8, const float* AMAX, con
 int ttsp_gemv_shape(int M, int K, int* J, int* KS, int* RPW);
 
 /* Fork RMSNorm over the last axis: Y = round(round(X * r) * Wt),
- * r = 1 / sqrt(sum(X^2) / D + eps); rows x D, D % 8 == 0, dtype F16/BF16.
+ * r = 1 / sqrt(sum(X^2) / D + eps); rows x D, D % 8 == 0, dtype F16/BF16,
+ * X, Wt and Y 16-byte aligned.
  * Replaces: rms_norm kernel + launch, app/engine/fusedops.py:61-94, 169-196. */
 int ttsp_rms_norm(const void* X, const void* Wt, void* Y, int rows, int D, float eps, int dtype,
                   void* stream);
 
 /* Interleaved-pair rotary of X [B, S, heads, 2*half_dim] against
  * F [S, half_dim, 2] (cos, sin) of type ftype: y0 = x0*c - x1*s, y1 = x1*c + x0*s,
- * no fma, one rounding. pairs = X elements / 2.
+ * no fma, one rounding. pairs = X elements / 2; X and Y 4-byte aligned
+ * (16-byte aligned with half_dim % 4 == 0 takes the four-pairs-a-thread form).
  * Replaces: rope kernel + launch, app/engine/fusedops.py:103-133, 199-236. */
 int ttsp_rope(const void* X, const void* F, int ftype, void* Y, long long pairs, int half_dim,
               int heads, int seq, int dtype, void* stream);

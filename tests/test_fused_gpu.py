@@ -34,8 +34,10 @@ def fused():
 
 # ------------------------------------------------------------------ RMSNorm
 
+# rows up to 4096 wide are held in registers, wider ones streamed twice;
+# 520 and 4104 leave the last 64-chunk step partly filled
 @pytest.mark.parametrize("rows,width", [(1, 2560), (32, 128), (8, 128), (1, 9728), (3, 2560), (1, 40),
-                                        (512, 2560), (1, 1024)])
+                                        (512, 2560), (1, 1024), (5, 520), (2, 4096), (2, 4104)])
 @pytest.mark.parametrize("dtype", DTYPES)
 def test_rms_norm_bit_exact_and_matches_the_fork(fused, orc, rows, width, dtype):
     from ttspipe_amd.llama import RMSNorm
@@ -82,8 +84,9 @@ def test_patched_norm_falls_back_without_changing_the_answer(fused):
 
 # ------------------------------------------------------------------ rotary
 
+# head dims that are multiples of 8 take four pairs a thread; 6 and 10 one
 @pytest.mark.parametrize("shape", [(1, 1, 32, 128), (1, 1, 8, 128), (1, 4, 32, 128), (2, 3, 8, 64),
-                                   (1, 512, 32, 128)])
+                                   (1, 512, 32, 128), (1, 3, 4, 6), (2, 5, 3, 10)])
 @pytest.mark.parametrize("fdt", [torch.bfloat16, torch.float32, torch.float16])
 @pytest.mark.parametrize("dtype", DTYPES)
 def test_rope_is_bit_exact(fused, orc, shape, fdt, dtype):
@@ -99,6 +102,22 @@ def test_rope_is_bit_exact(fused, orc, shape, fdt, dtype):
     assert torch.equal(y.cpu(), theirs)
     ours = orc.rope(bits(x), bits(f), dt_code(fdt), d // 2, h, s, dt_code(dtype))
     assert np.array_equal(bits(y), ours)
+
+
+@pytest.mark.parametrize("offset", [0, 2, 8])
+def test_rope_on_a_buffer_not_16_byte_aligned(fused, offset):
+    """A contiguous tensor starting 4 or 16 bytes into its buffer gives the same bits."""
+    from ttspipe_amd.llama import apply_rotary_emb
+
+    shape = (1, 6, 8, 128)
+    n = int(np.prod(shape))
+    g = torch.Generator().manual_seed(offset + 5)
+    buf = torch.randn(n + 8, generator=g).to(torch.bfloat16)
+    x = buf.cuda()[offset : offset + n].view(shape)
+    f = torch.randn(6, 64, 2, generator=g).to(torch.float32).cuda()
+    y = fused.rope(x, f)
+    assert y is not None
+    assert torch.equal(y.cpu(), apply_rotary_emb(x.cpu(), f.cpu()))
 
 
 def test_rope_uses_the_frequencies_of_its_own_position(fused):

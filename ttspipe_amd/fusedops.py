@@ -57,7 +57,7 @@ def rms_norm(x, weight, eps: float, out=None):
     width = x.shape[-1]
     if width != weight.numel() or width == 0 or width % 8:
         return None
-    if x.data_ptr() % 16 or weight.data_ptr() % 16:
+    if x.data_ptr() % 16 or weight.data_ptr() % 16 or (out is not None and out.data_ptr() % 16):
         return None
     if out is None:
         import torch
@@ -86,6 +86,8 @@ def rope(x, freqs_cis, out=None):
     bsz, seq, heads, head_dim = x.shape
     half_dim = head_dim // 2
     if head_dim % 2 or freqs_cis.numel() != seq * half_dim * 2 or x.numel() == 0:
+        return None
+    if x.data_ptr() % 4 or (out is not None and out.data_ptr() % 4):  # a pair is one 32-bit word
         return None
     if out is None:
         import torch
