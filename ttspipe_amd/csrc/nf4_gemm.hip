@@ -373,13 +373,14 @@ static void launch_gemm(const void* X, const uint8_t* W, const uint8_t* A8, cons
                        (const uint16_t*)R, epi, M, K, N, bs_shift, bs2_shift, YP);
 }
 
-// Tile shape and K-split of a launch: unsplit with the largest tile (128 x
-// 128, then 64 x 128) that gives every CU a workgroup; else the largest tile
-// that does with the fewest splits (2, 4, 8; each split at least 8 K-steps,
-// an even number); otherwise 64 x 64 tiles, unsplit. Up to SKINNY_MAX_N rows
-// take the skinny kernel (nf4_skinny.hip), shape 0, never split. (Measured on
-// the 512-row layer: a split costs more than a smaller tile while the smaller
-// tile still fills the GPU.)
+// Tile shape and K-split of a launch: 64 x 128 tiles (8 waves), unsplit when
+// they give every CU a workgroup; else the smallest split (2, 4, 8; each split
+// an even number of at least 8 K-steps) that gives every CU two workgroups, or
+// the largest that gives it one; otherwise unsplit, 64 x 128 tiles down to 128
+// of them, 64 x 64 below. Up to SKINNY_MAX_N rows take the skinny kernel
+// (nf4_skinny.hip), shape 0, never split. (Measured at 512 rows: 64 x 128
+// beats 128 x 128 on every layer shape, by 8-10 % at 9728 x 2560 and
+// 2560 x 9728; unsplit tile shapes give identical bits.)
 struct GemmPlan {
   int shape, splits;
 };
@@ -387,19 +388,26 @@ constexpr int SKINNY_MAX_N = 64;
 int skinny_max_k(int N);
 static bool skinny(int K, int N) { return N <= SKINNY_MAX_N && K <= skinny_max_k(N); }
 
+static long long gemm_tiles(int M, int N, int bm, int bn) {
+  return (long long)((M + bm - 1) / bm) * ((N + bn - 1) / bn);
+}
+
+static int unsplit_shape(int M, int N) { return gemm_tiles(M, N, 64, 128) >= 128 ? 2 : 3; }
+
 static GemmPlan gemm_plan(int M, int K, int N) {
   if (skinny(K, N)) return {0, 1};
   const int steps = K / KT;
-  const auto tiles = [&](int bm, int bn) { return (long long)((M + bm - 1) / bm) * ((N + bn - 1) / bn); };
-  const int shapes[2][3] = {{1, 128, 128}, {2, 64, 128}};
-  for (const auto& sh : shapes)
-    if (tiles(sh[1], sh[2]) >= 256) return {sh[0], 1};
-  for (const auto& sh : shapes)
-    for (int sp = 2; sp <= 8; sp *= 2) {
-      if (steps % (2 * sp) || steps / sp < 8) break;
-      if (tiles(sh[1], sh[2]) * sp >= 256) return {sh[0], sp};
+  const long long t = gemm_tiles(M, N, 64, 128);
+  if (t >= 256) return {2, 1};
+  int splits = 1;
+  for (int sp = 2; sp <= 8; sp *= 2) {
+    if (steps % (2 * sp) || steps / sp < 8) break;
+    if (t * sp >= 256) {
+      splits = sp;
+      if (t * sp >= 512) break;
     }
-  return {3, 1};
+  }
+  return splits > 1 ? GemmPlan{2, splits} : GemmPlan{unsplit_shape(M, N), 1};
 }
 
 int gemm_mfma(const void* X, int dt, const uint8_t* W, const uint8_t* A8, const float* AMAX,
@@ -416,16 +424,14 @@ int gemm_mfma(const void* X, int dt, const uint8_t* W, const uint8_t* A8, const 
                                                  bs_shift, bs2_shift, yp, splits, st)                       \
        : launch_gemm<DTV, BMV, BNV, WMV, WNV, 2>(X, W, A8, AMAX, CODE2, offset, LUT, Y, R, epi, M, K, N,    \
                                                  bs_shift, bs2_shift, yp, splits, st))
-  // 8 waves for the 128 x 128 and 64 x 128 tiles (two a SIMD: one wave's
-  // dequantisation runs while the other's matrix products do)
+  // 8 waves for the 64 x 128 tiles (two a SIMD: one wave's dequantisation
+  // runs while the other's matrix products do), 4 for 64 x 64
   const int shape = plan.shape;
   if (dt == DT_BF16) {
-    if (shape == 1) TTSP_G(DT_BF16, 128, 128, 4, 2);
-    else if (shape == 2) TTSP_G(DT_BF16, 64, 128, 2, 4);
+    if (shape == 2) TTSP_G(DT_BF16, 64, 128, 2, 4);
     else TTSP_G(DT_BF16, 64, 64, 2, 2);
   } else if (dt == DT_F16) {
-    if (shape == 1) TTSP_G(DT_F16, 128, 128, 4, 2);
-    else if (shape == 2) TTSP_G(DT_F16, 64, 128, 2, 4);
+    if (shape == 2) TTSP_G(DT_F16, 64, 128, 2, 4);
     else TTSP_G(DT_F16, 64, 64, 2, 2);
   } else {
     return (int)hipErrorInvalidValue;
@@ -489,9 +495,8 @@ extern "C" int ttsp_nf4_gemm(const void* X, int x_dtype, const uint8_t* W, const
     return gemm_skinny(X, x_dtype, W, A8, AMAX, CODE2, offset, LUT, Y, R, epi, M, K, N, bs_shift, bs2_shift, stream);
   // vectorised output rows: 8 elements per 16-byte store
   const bool vec = M % 8 == 0 && (uintptr_t)Y % 16 == 0 && (!epi || (uintptr_t)R % 16 == 0);
-  // unsplit: the largest tile that still gives every CU a workgroup
-  const auto tiles = [&](int bm, int bn) { return (long long)((M + bm - 1) / bm) * ((N + bn - 1) / bn); };
-  const GemmPlan plan{tiles(128, 128) >= 256 ? 1 : tiles(64, 128) >= 256 ? 2 : 3, 1};
+  // unsplit: 64 x 128 tiles, or 64 x 64 when fewer than 128 of those
+  const GemmPlan plan{unsplit_shape(M, N), 1};
   return gemm_mfma(X, x_dtype, W, A8, AMAX, CODE2, offset, LUT, Y, R, epi | (vec ? 4 : 0), M, K, N, bs_shift,
                    bs2_shift, plan, nullptr, stream);
 }
