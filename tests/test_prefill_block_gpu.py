@@ -1,11 +1,14 @@
 """The multi-position (prompt prefill) block and the Dual-AR prompt prefill
 with its bucket graphs (GPU), plus the span arithmetic (CPU).
 
-Bar: the fused prefill block against the block's own unpatched forward
-(the same GEMMs, the epilogues keep the unfused roundings; the head norms
-run in the decode step's kernel instead of the fork's torch modules), at the
-reference's block bar rel-norm < 2e-2 (tests/test_nf4cpu.py:175-191), V rows
-identical; the many-row head-norm/rotary/KV kernel bit for bit against the
+Bar: the fused prefill block against a float64 restatement of the block
+with the fork's roundings that no kernel of this repository feeds
+(tests/refblock.py; weights from the numpy dequantisation), rel-norm < 3e-3,
+a bar each planted mistake of the restatement misses by more than twice
+(CPU test); against the block's own unpatched forward (the same GEMMs, the
+epilogues keep the unfused roundings; the head norms run in the decode
+step's kernel instead of the fork's torch modules), at the reference's block
+bar rel-norm < 2e-2 (tests/test_nf4cpu.py:175-191), V rows identical; the many-row head-norm/rotary/KV kernel bit for bit against the
 one-position kernel; the model's prompt prefill against the same
 positions decoded one at a time through the decode kernels (different GEMM
 and attention kernels, so the reference's 2e-2 block bar on the KV rows and
@@ -71,6 +74,112 @@ def test_prefill_block_matches_the_unpatched_block(qk_norm):
     assert _rel(ours, theirs) < 2e-2
     assert _rel(ours_k, kc[:, :, 24:64]) < 2e-2
     assert torch.equal(ours_v, vc[:, :, 24:64])  # V rows are copied as they are
+
+
+# ------------------------------------------------ against an fp64 block
+
+REF_BAR = 3e-3  # rel-norm of the block output against the fp64 block with the fork's roundings
+REF_START, REF_ROWS, REF_LEN = 24, 40, 128
+
+
+def _ref_inputs(dtype, qk_norm, seed=3):
+    """The fp64 reference's inputs for `_block(dtype, qk_norm, max_len=128,
+    seed)`: its dequantised weights (numpy closed form) and norm weights (the
+    same seeded generator), seeded x rows and cache, the positions'
+    frequencies."""
+    from oracle import oracle as o
+    from tests.nf4data import dequant_numpy, random_layer
+    from ttspipe_amd.llama import precompute_freqs_cis
+
+    dt = o.DT_BF16 if dtype == torch.bfloat16 else o.DT_F16
+    nh, nkv, D, inter = 4, 2, 512, 1024
+    W = {}
+    for i, (name, M, K) in enumerate([("wqkv", (nh + 2 * nkv) * 128, D), ("wo", D, nh * 128), ("w1", inter, D),
+                                      ("w3", inter, D), ("w2", D, inter)]):
+        W[name] = o.to_f32(dequant_numpy(random_layer(M, K, True, seed=seed * 10 + i), dt), dt).astype(
+            np.float64).reshape(M, K)
+    g = torch.Generator().manual_seed(seed)
+    names = ["attention_norm", "ffn_norm"] + (["q_norm", "k_norm"] if qk_norm else [])
+    norms = {n: (torch.rand(D if "attention" in n or "ffn" in n else 128, generator=g) + 0.5).to(dtype)
+             .double().numpy() for n in names}
+    rng = np.random.default_rng(seed + 100)
+    q16 = lambda a: o.from_f32(a.astype(np.float32), dt)  # noqa: E731
+    xb = q16(rng.standard_normal((REF_ROWS, D)))
+    kcb, vcb = q16(rng.standard_normal((nkv, REF_LEN, 128))), q16(rng.standard_normal((nkv, REF_LEN, 128)))
+    pos = list(range(REF_START, REF_START + REF_ROWS))
+    freqs = precompute_freqs_cis(REF_LEN, 128, 1e6)[pos]
+    f64 = lambda b: o.to_f32(b, dt).astype(np.float64)  # noqa: E731
+    rnd = lambda t: f64(q16(np.asarray(t)))  # noqa: E731
+    return dict(W=W, norms=norms, xb=xb, kcb=kcb, vcb=vcb, pos=pos, freqs=freqs, dt=dt, f64=f64, rnd=rnd,
+                nh=nh, nkv=nkv)
+
+
+def _ref(c, qk_norm, mutant=None):
+    from tests.refblock import block_fp64
+
+    f64 = c["f64"]
+    return block_fp64(c["W"], c["norms"], f64(c["xb"]), c["freqs"].double().numpy(), f64(c["kcb"]), f64(c["vcb"]),
+                      c["pos"], c["nh"], c["nkv"], qk_norm, rnd=c["rnd"], mutant=mutant)
+
+
+@pytest.mark.parametrize("qk_norm", [True, False])
+def test_fp64_block_reference_catches_planted_mistakes(qk_norm):
+    """Each planted mistake of the reference block (no rotary, no q/k norm,
+    query heads mapped to KV heads modulo, a mask one position too wide)
+    moves its output more than twice the bar the fused block is held to."""
+    from tests.refblock import MUTANTS, rel_norm
+
+    c = _ref_inputs(torch.bfloat16, qk_norm)
+    ref = _ref(c, qk_norm)[0]
+    for m in MUTANTS:
+        if m == "no_qk_norm" and not qk_norm:
+            continue
+        assert rel_norm(_ref(c, qk_norm, m)[0], ref) > 2 * REF_BAR, m
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("qk_norm", [True, False])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_prefill_block_matches_an_fp64_block(qk_norm, dtype):
+    """The fused prefill block (40 rows at positions 24..63 over a 128-row
+    cache) against the block restated in float64 with the fork's roundings
+    (tests/refblock.py; no kernel of this repository feeds it): the output
+    within REF_BAR (rel-norm), the new K and V rows within one 16-bit ulp of
+    each head row's largest element (the products' own roundings)."""
+    from tests.refblock import rel_norm
+    from tests.test_fused_gpu import _block
+    from ttspipe_amd import fusedlayer, fusedops, nf4gemv
+
+    assert nf4gemv.install() and fusedops.install() and fusedlayer.install()
+    block, _ = _block(dtype, qk_norm, max_len=REF_LEN, seed=3)
+    c = _ref_inputs(dtype, qk_norm)
+    for n, w in c["norms"].items():
+        mod = getattr(block, n, None) or getattr(block.attention, n)
+        assert np.array_equal(mod.weight.double().cpu().numpy(), w)
+    dev = lambda b, shape: torch.from_numpy(b.view(np.int16).copy()).view(dtype).cuda().view(shape)  # noqa: E731
+    kv = block.attention.kv_cache
+    kv.k_cache.copy_(dev(c["kcb"], kv.k_cache.shape))
+    kv.v_cache.copy_(dev(c["vcb"], kv.v_cache.shape))
+    pos = torch.tensor(c["pos"], device="cuda")
+    mask = torch.tril(torch.ones(REF_LEN, REF_LEN, dtype=torch.bool, device="cuda"))[None, None, pos]
+    before = fusedlayer.stats()["prefill"]
+    with torch.inference_mode():
+        ours = block(dev(c["xb"], (1, REF_ROWS, 512)), c["freqs"].cuda(), mask, pos)
+    assert fusedlayer.stats()["prefill"] == before + 1
+    ref, k_ref, v_ref = _ref(c, qk_norm)
+    got = ours.double().cpu().numpy().reshape(REF_ROWS, 512)
+    rel = rel_norm(got, ref)
+    k_got = kv.k_cache[0, :, REF_START : REF_START + REF_ROWS].double().cpu().numpy().transpose(1, 0, 2)
+    v_got = kv.v_cache[0, :, REF_START : REF_START + REF_ROWS].double().cpu().numpy().transpose(1, 0, 2)
+    # in ulps of each head row's largest element (rotation may cancel two
+    # rounded inputs into a value far smaller than either)
+    mant = 7 if dtype == torch.bfloat16 else 10
+    row_ulp = lambda t: 2.0 ** (np.floor(np.log2(np.abs(t).max(-1, keepdims=True))) - mant)  # noqa: E731
+    k_ulps = float(np.max(np.abs(k_got - k_ref) / row_ulp(k_ref)))
+    v_ulps = float(np.max(np.abs(v_got - v_ref) / row_ulp(v_ref)))
+    print(f"prefill block vs fp64 block: rel {rel:.2e}, K rows {k_ulps:.1f} ulp, V rows {v_ulps:.1f} ulp")
+    assert rel < REF_BAR
+    assert k_ulps <= 1.0 and v_ulps <= 1.0
 
 
 @pytest.mark.gpu
