@@ -49,6 +49,64 @@ def test_conversions_match_numpy_and_torch(orc, dt):
     assert np.array_equal(back, torch.from_numpy(x).to(tdt).float().numpy(), equal_nan=True)
 
 
+def _round_f32(x) -> float:
+    """Exact rational -> nearest fp32, ties to even (subnormals included)."""
+    from fractions import Fraction
+
+    if x == 0:
+        return 0.0
+    sign, a = (-1 if x < 0 else 1), abs(Fraction(x))
+    e = a.numerator.bit_length() - a.denominator.bit_length()
+    if Fraction(2) ** e > a:
+        e -= 1
+    q = max(e - 23, -149)  # the ulp's exponent
+    m = a / Fraction(2) ** q
+    n, rem = divmod(m.numerator, m.denominator)
+    if 2 * rem > m.denominator or (2 * rem == m.denominator and n % 2):
+        n += 1
+    return sign * float(Fraction(n) * Fraction(2) ** q)
+
+
+def test_fma16_chain_is_two_exactly_rounded_fmas(orc):
+    """orc_fma16_chain (the GEMV's v_fma_mix chain: fma(a.hi, b.hi,
+    fma(a.lo, b.lo, c)), fp16 operands, fp32 accumulator) against exact
+    rational arithmetic with one fp32 rounding per fma, over random operands
+    and the edge cases (zeros, signs, subnormal and large fp16, tiny and huge
+    c). (A product of two fp16 values is exact in fp32, so an fma and a
+    multiply-then-add agree; what the chain fixes is the rounding after each
+    add and the order.) The chain rounded once at the end, or the pair taken
+    in the other order, disagrees on a visible share of the same inputs."""
+    from fractions import Fraction
+
+    rng = np.random.default_rng(16)
+    n = 4000
+    h = rng.integers(0, 1 << 16, size=(2, n), dtype=np.uint32)
+    h[:, :200] = rng.choice(np.array([0x0000, 0x8000, 0x0001, 0x03ff, 0x7bff, 0xfbff, 0x3c00, 0xbc00], np.uint32),
+                            size=(2, 200))
+    h2 = rng.integers(0, 1 << 16, size=(2, n), dtype=np.uint32)
+    finite = lambda u: (u & 0x7c00) != 0x7c00  # noqa: E731
+    keep = finite(h[0]) & finite(h[1]) & finite(h2[0]) & finite(h2[1])
+    a = (h[0] | (h2[0] << 16))[keep].astype(np.uint32)
+    b = (h[1] | (h2[1] << 16))[keep].astype(np.uint32)
+    c = (rng.standard_normal(a.size) * np.exp2(rng.integers(-30, 30, a.size))).astype(np.float32)
+    c[:50] = 0.0
+    got = orc.fma16_chain(a, b, c)
+    f16 = lambda u: float(np.uint16(u).view(np.float16))  # noqa: E731
+    diff_once = diff_order = 0
+    for i in range(a.size):
+        alo, ahi, blo, bhi = f16(a[i] & 0xFFFF), f16(a[i] >> 16), f16(b[i] & 0xFFFF), f16(b[i] >> 16)
+        t = _round_f32(Fraction(alo) * Fraction(blo) + Fraction(float(c[i])))
+        want = _round_f32(Fraction(ahi) * Fraction(bhi) + Fraction(t))
+        if math.isinf(want) or abs(want) > 3.4e38:
+            continue
+        assert got[i] == np.float32(want), (i, hex(a[i]), hex(b[i]), c[i], got[i], want)
+        once = _round_f32(Fraction(alo) * Fraction(blo) + Fraction(float(c[i])) + Fraction(ahi) * Fraction(bhi))
+        diff_once += np.float32(once) != np.float32(want)
+        t2 = _round_f32(Fraction(ahi) * Fraction(bhi) + Fraction(float(c[i])))
+        diff_order += np.float32(_round_f32(Fraction(alo) * Fraction(blo) + Fraction(t2))) != np.float32(want)
+    assert diff_once > a.size // 50 and diff_order > a.size // 50, (diff_once, diff_order)
+
+
 def test_packing_layout_is_high_nibble_first():
     """The product quantiser's bytes decode, through the oracle's unpacking,
     to the nearest-code indices computed independently (the reference's
