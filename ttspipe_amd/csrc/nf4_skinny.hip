@@ -267,9 +267,13 @@ static void launch_skinny(const void* X, const uint8_t* W, const uint8_t* A8, co
 // Launch shape. NW: the fewest waves (4, 8, 16) whose K runs fit SK_MAXS
 // steps; with fewer than 256 row tiles, at least 8 (more waves per row tile).
 // MS: the step budget, 5 when the runs fit it (fewer repeated loads), else
-// SK_MAXS. R: 32 rows per workgroup when that still gives every CU one (the
-// X slices are then read half as often), else 16. Returns false when no
-// shape fits (see skinny_max_k).
+// SK_MAXS. R: with 512 or more row tiles, several tiles a workgroup (each X
+// fragment then serves R of them: the activation traffic, which binds from 16
+// rows up, drops by R) - 4 for 17-32 rows and 2 otherwise with 4 waves, 2 for
+// up to 32 rows with 8 - else 1. (Measured at 9728 x 2560: 32 rows 16.8 us
+// with R = 4 against 18.3 with 2, 64 rows 32.7 with R = 2 against 38.7 with 1;
+// at 256 row tiles R = 1 stays the fastest.) Returns false when no shape fits
+// (see skinny_max_k).
 template <int DT, int NT>
 static bool skinny_shape(const void* X, const uint8_t* W, const uint8_t* A8, const float* AMAX, const float* CODE2,
                          float offset, const float* LUT, void* Y, const void* RES, int epi, int M, int K, int N,
@@ -289,6 +293,13 @@ static bool skinny_shape(const void* X, const uint8_t* W, const uint8_t* A8, con
     if (ms5) TTSP_L(RV, NWV, 5); \
     else TTSP_L(RV, NWV, SK_MAXS); \
   } while (0)
+  const bool many = tiles >= 2 * 256;
+  if constexpr (NT == 2) {
+    if (many && nw == 4 && ms5) { TTSP_L(4, 4, 5); return true; }
+  }
+  if constexpr (NT == 4) {
+    if (many && nw == 4 && ms5) { TTSP_L(2, 4, 5); return true; }
+  }
   if constexpr (NT <= 2) {
     if (r2 && nw == 4) { TTSP_MS(2, 4); return true; }
     if (r2) { TTSP_MS(2, 8); return true; }
