@@ -269,6 +269,24 @@ int ttsp_embed_sum(const void* E, const int* tok, int ntok, int vocab, int D, vo
  * the sampler (app/engine/graphs.py:57-73, fusedsample.py). */
 int ttsp_argmax(const void* X, int n, int dtype, int* out, void* stream);
 
+/* ttsp_argmax and a one-row ttsp_embed_sum in one launch, the same bits:
+ * tok[0] = argmax(X[0..n)), t = that clamped into [0, vocab), tok2[0] = t
+ * unless tok2 is NULL, out[0..D) = row t of E [vocab][D]. Replaces: a frame's
+ * greedy token and its codebook embedding, app/engine/graphs.py:121-131
+ * (_sample, the clamp into the codebook, _fast_embed). */
+int ttsp_argmax_embed(const void* X, int n, int dtype, int* tok, int* tok2, const void* E, int vocab, int D,
+                      void* out, void* stream);
+
+/* A decode frame's bookkeeping in one launch: history[step[0]] = tokens
+ * (int32 [rows][ntok]; skipped when step[0] is outside [0, rows)), step[0] += 1,
+ * pos[0] += 1, and the next frame's rotary row frow = F[pos[0]] (row_elems
+ * 16-bit values per row of F [npos]; pos clamped into [0, npos)). step and pos
+ * are int64. Replaces: the frame advance of app/engine/graphs.py:197-217
+ * (codes into the history, pos.add_(1)) and the rotary-row lookup at the
+ * next frame's start. */
+int ttsp_frame_advance(const int* tokens, int ntok, int* history, int rows, long long* step, long long* pos,
+                       const void* F, int npos, int row_elems, void* frow, void* stream);
+
 /* Deterministic synthetic data: element i of a tensor seeded `seed` is a
  * function of splitmix64(splitmix64(seed) ^ i). kind 0: uint8 (top byte);
  * 1/2/3: u*scale + offset as bf16/f16/f32 with u uniform in [-1, 1).

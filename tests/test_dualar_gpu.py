@@ -123,3 +123,83 @@ def test_benchmark_model_256_frames_match_the_oracle_fixture():
     assert np.array_equal(again, got)
     del model
     torch.cuda.empty_cache()
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("n,vocab,D", [(4096, 4096, 1024), (4096, 1024, 1024), (700, 4096, 1000), (1, 8, 64),
+                                       (40000, 4096, 2560)])
+def test_argmax_embed_equals_argmax_then_embed(dtype, n, vocab, D):
+    """ttsp_argmax_embed == ttsp_argmax then a one-row ttsp_embed_sum, bit for
+    bit: ties (the lowest index), the winner past the table (clamped), -0.0
+    entries of the table (0 + -0 rounds to +0, as embed_sum), every row
+    element."""
+    from ttspipe_amd import _lib
+
+    lib, st = _lib.lib(), _lib.stream()
+    dt = _lib.dtype_code(dtype)
+    g = torch.Generator(device="cuda").manual_seed(n + vocab)
+    for case in range(4):
+        x = torch.randn(n, device="cuda", generator=g).to(dtype)
+        if case == 1:  # a tie of the maximum at two indices
+            top = x.max()
+            x[n // 3] = top
+            x[n // 2] = top
+        if case == 2:  # the winner past the table
+            x[n - 1] = 100.0
+        E = torch.randn(vocab, D, device="cuda", generator=g).to(dtype)
+        E[:, ::7] = -0.0
+        tok = torch.full((2,), -5, dtype=torch.int32, device="cuda")
+        ref_tok = torch.full((2,), -5, dtype=torch.int32, device="cuda")
+        out = torch.empty(D, dtype=dtype, device="cuda")
+        ref = torch.empty(D, dtype=dtype, device="cuda")
+        _lib.check(lib.ttsp_argmax_embed(x.data_ptr(), n, dt, tok.data_ptr(), tok[1:].data_ptr(), E.data_ptr(), vocab,
+                                         D, out.data_ptr(), st), "argmax_embed")
+        _lib.check(lib.ttsp_argmax(x.data_ptr(), n, dt, ref_tok.data_ptr(), st), "argmax")
+        torch.clamp(ref_tok[:1], 0, vocab - 1, out=ref_tok[1:2])
+        _lib.check(lib.ttsp_embed_sum(E.data_ptr(), ref_tok[1:].data_ptr(), 1, vocab, D, ref.data_ptr(), dt, st),
+                   "embed_sum")
+        assert torch.equal(tok, ref_tok), (case, tok.tolist(), ref_tok.tolist())
+        assert torch.equal(out.view(torch.int16), ref.view(torch.int16)), case
+        top = x.float().max()
+        assert int(tok[0]) == int((x.float() == top).nonzero()[0])  # the lowest index holding the maximum
+
+
+def test_frame_advance_equals_the_torch_bookkeeping():
+    """ttsp_frame_advance == history.index_copy_(0, step, tokens),
+    step.add_(1), pos.add_(1), index_select(freqs, 0, pos): three frames in a
+    row, the last one past the history's rows (its row is not written) and
+    with pos at the table's end (the row clamps)."""
+    from ttspipe_amd import _lib
+    from ttspipe_amd.llama import precompute_freqs_cis
+
+    lib, st = _lib.lib(), _lib.stream()
+    freqs = precompute_freqs_cis(300, 128, 1e6).cuda()
+    ntok, rows = 11, 2
+    hist = torch.zeros(rows, ntok, dtype=torch.int32, device="cuda")
+    step = torch.zeros(1, dtype=torch.long, device="cuda")
+    pos = torch.full((1,), 297, dtype=torch.long, device="cuda")
+    frow = torch.empty(1, 64, 2, dtype=freqs.dtype, device="cuda")
+    hist_ref = hist.clone()
+    for f in range(3):
+        tokens = torch.arange(ntok, dtype=torch.int32, device="cuda") * (f + 3)
+        _lib.check(lib.ttsp_frame_advance(tokens.data_ptr(), ntok, hist.data_ptr(), rows, step.data_ptr(),
+                                          pos.data_ptr(), freqs.data_ptr(), freqs.shape[0], 128, frow.data_ptr(), st),
+                   "frame_advance")
+        if f < rows:
+            hist_ref[f] = tokens
+        assert torch.equal(hist, hist_ref)
+        assert int(step) == f + 1 and int(pos) == 298 + f
+        assert torch.equal(frow[0].view(torch.int16), freqs[min(298 + f, 299)].view(torch.int16))
+
+
+def test_reset_to_a_longer_history_drops_the_captured_frame(small):
+    """A captured frame writes into the history it was captured with: a reset
+    that has to allocate a longer history drops the graph (it is captured
+    again on the next graphed decode) instead of leaving it pointing at freed
+    memory."""
+    small.capture()
+    assert small.graph is not None
+    small.reset(small.history.shape[0] + 8)
+    assert small.graph is None
+    small.decode(4)
+    assert small.graph is not None

@@ -61,6 +61,8 @@ SIGNATURES: dict[str, list] = {
     "ttsp_sample_max_vocab": [],
     "ttsp_embed_sum": [_vp, _vp, _i, _i, _i, _vp, _i, _vp],
     "ttsp_argmax": [_vp, _i, _i, _vp, _vp],
+    "ttsp_argmax_embed": [_vp, _i, _i, _vp, _vp, _vp, _i, _i, _vp, _vp],
+    "ttsp_frame_advance": [_vp, _i, _vp, _i, _vp, _vp, _vp, _i, _i, _vp, _vp],
     "ttsp_synth_fill": [_vp, _ll, ctypes.c_ulonglong, _i, _f, _f, _vp],
 }
 

@@ -1,6 +1,7 @@
 // Small kernels a greedy Dual-AR decode step needs between the transformer
 // blocks (the synthetic frame of app/engine/graphs.py:76-132 with argmax in
-// place of sampling): summed codebook-embedding gather, greedy argmax, and a
+// place of sampling): summed codebook-embedding gather, greedy argmax (alone,
+// or with the embedding row it selects), the frame's bookkeeping, and a
 // counter-based fill that materialises seeded synthetic weights on the device.
 #include "ttsp_common.h"
 
@@ -23,10 +24,10 @@ __global__ __launch_bounds__(256) void embed_sum_kernel(const uint16_t* __restri
   out[d] = Elem<DT>::store(acc);
 }
 
-// Index of the largest logit, the lowest index on ties (NaN never wins).
+// Index of the largest of X[0..n), the lowest index on ties (NaN never wins;
+// 0 when nothing beats -inf), valid in thread 0 after the call. One workgroup.
 template <int DT>
-__global__ __launch_bounds__(1024) void argmax_kernel(const uint16_t* __restrict__ X, int n,
-                                                     int* __restrict__ out) {
+__device__ __forceinline__ int block_argmax(const uint16_t* __restrict__ X, int n) {
   __shared__ float bv[16];
   __shared__ int bi[16];
   const int tid = threadIdx.x;
@@ -47,7 +48,58 @@ __global__ __launch_bounds__(1024) void argmax_kernel(const uint16_t* __restrict
     const int nw = (blockDim.x + 63) >> 6;
     for (int w = 1; w < nw; ++w)
       if (bv[w] > best || (bv[w] == best && bi[w] < idx)) { best = bv[w]; idx = bi[w]; }
-    out[0] = idx == 0x7fffffff ? 0 : idx;
+  }
+  return idx == 0x7fffffff ? 0 : idx;
+}
+
+template <int DT>
+__global__ __launch_bounds__(1024) void argmax_kernel(const uint16_t* __restrict__ X, int n,
+                                                     int* __restrict__ out) {
+  const int idx = block_argmax<DT>(X, n);
+  if (threadIdx.x == 0) out[0] = idx;
+}
+
+// The greedy token and the embedding row it selects, in one launch (argmax
+// then a one-row embed_sum): tok[0] = argmax(X[0..n)), t = that clamped into
+// [0, vocab), tok2[0] = t when tok2 is given, out[d] = round(0 + E[t D + d])
+// (embed_sum's arithmetic for one row).
+template <int DT>
+__global__ __launch_bounds__(1024) void argmax_embed_kernel(const uint16_t* __restrict__ X, int n,
+                                                           int* __restrict__ tok, int* __restrict__ tok2,
+                                                           const uint16_t* __restrict__ E, int vocab, int D,
+                                                           uint16_t* __restrict__ out) {
+  __shared__ int t_s;
+  const int idx = block_argmax<DT>(X, n);
+  if (threadIdx.x == 0) {
+    const int t = idx < 0 ? 0 : (idx >= vocab ? vocab - 1 : idx);
+    tok[0] = idx;
+    if (tok2) tok2[0] = t;
+    t_s = t;
+  }
+  __syncthreads();
+  const uint16_t* row = E + (size_t)t_s * D;
+  for (int d = threadIdx.x; d < D; d += blockDim.x) out[d] = Elem<DT>::store(__fadd_rn(0.0f, Elem<DT>::load(row[d])));
+}
+
+// A decode frame's bookkeeping in one launch: history[step] = tokens (ntok
+// entries; nothing once step is outside [0, rows)), step += 1, pos += 1, and
+// the next frame's rotary row frow = F[pos] (row_elems 16-bit values; pos
+// clamped into [0, npos)). Every thread reads step and pos before thread 0
+// writes them.
+__global__ __launch_bounds__(256) void frame_advance_kernel(const int* __restrict__ tokens, int ntok,
+                                                            int* __restrict__ history, int rows,
+                                                            long long* __restrict__ step, long long* __restrict__ pos,
+                                                            const uint16_t* __restrict__ F, int npos, int row_elems,
+                                                            uint16_t* __restrict__ frow) {
+  const long long s = step[0], p = pos[0] + 1;
+  const long long pr = p < 0 ? 0 : (p >= npos ? npos - 1 : p);
+  for (int i = threadIdx.x; i < ntok; i += blockDim.x)
+    if (s >= 0 && s < rows) history[s * ntok + i] = tokens[i];
+  for (int i = threadIdx.x; i < row_elems; i += blockDim.x) frow[i] = F[pr * row_elems + i];
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    step[0] = s + 1;
+    pos[0] = p;
   }
 }
 
@@ -99,6 +151,30 @@ extern "C" int ttsp_embed_sum(const void* E, const int* tok, int ntok, int vocab
                        ntok, vocab, D, (uint16_t*)out);
   else
     return (int)hipErrorInvalidValue;
+  TTSP_RETURN_LAUNCH();
+}
+
+extern "C" int ttsp_argmax_embed(const void* X, int n, int dtype, int* tok, int* tok2, const void* E, int vocab,
+                                 int D, void* out, hipStream_t stream) {
+  if (n <= 0 || vocab <= 0 || D <= 0 || !X || !tok || !E || !out) return (int)hipErrorInvalidValue;
+  if (dtype == DT_F16)
+    hipLaunchKernelGGL(argmax_embed_kernel<DT_F16>, dim3(1), dim3(1024), 0, stream, (const uint16_t*)X, n, tok, tok2,
+                       (const uint16_t*)E, vocab, D, (uint16_t*)out);
+  else if (dtype == DT_BF16)
+    hipLaunchKernelGGL(argmax_embed_kernel<DT_BF16>, dim3(1), dim3(1024), 0, stream, (const uint16_t*)X, n, tok, tok2,
+                       (const uint16_t*)E, vocab, D, (uint16_t*)out);
+  else
+    return (int)hipErrorInvalidValue;
+  TTSP_RETURN_LAUNCH();
+}
+
+extern "C" int ttsp_frame_advance(const int* tokens, int ntok, int* history, int rows, long long* step,
+                                  long long* pos, const void* F, int npos, int row_elems, void* frow,
+                                  hipStream_t stream) {
+  if (ntok <= 0 || rows <= 0 || npos <= 0 || row_elems <= 0 || !tokens || !history || !step || !pos || !F || !frow)
+    return (int)hipErrorInvalidValue;
+  hipLaunchKernelGGL(frame_advance_kernel, dim3(1), dim3(256), 0, stream, tokens, ntok, history, rows, step, pos,
+                     (const uint16_t*)F, npos, row_elems, (uint16_t*)frow);
   TTSP_RETURN_LAUNCH();
 }
 

@@ -313,10 +313,13 @@ class SyntheticDualAR:
         import torch
 
         self.pos.fill_(self.cfg.prefill_len)
+        # the first frame's rotary row; each frame's last launch writes the next one's
+        torch.index_select(self.freqs, 0, self.pos, out=self.freq_row)
         self.tokens.copy_(torch.tensor(first_tokens(self.cfg), dtype=torch.int32))
         self.step_index.zero_()
         if self.history is None or self.history.shape[0] < n_steps:
             self.history = torch.zeros(n_steps, self.cfg.n_tokens, dtype=torch.int32, device=self.device)
+            self.graph = None  # a captured frame holds the old history's address: capture again
         else:
             self.history.zero_()
 
@@ -366,42 +369,46 @@ class SyntheticDualAR:
 
     def step(self) -> None:
         """One frame: tokens (device) at position pos -> next frame's tokens; pos += 1."""
-        import torch
-
         cfg, lib, st = self.cfg, self._lib, _lib.stream()
         # slow transformer
         rc = lib.ttsp_embed_sum(self.tensors["embeddings"].data_ptr(), self.tokens.data_ptr(), cfg.n_tokens,
                                 cfg.vocab_size, cfg.dim, self.x.data_ptr(), _lib.DT_BF16, st)
         self._check(rc, "ttsp_embed_sum")
-        torch.index_select(self.freqs, 0, self.pos, out=self.freq_row)
+        # (freq_row holds the rotary row of pos: reset() or the last frame wrote it)
         h = self._run_blocks(self.layers, self.ws, self.x, self.freq_row, self.mask, self.pos).view(1, 1, -1)
         # the final norm runs inside both consumers (head and fast projection)
         norm, eps = self.tensors["norm"], cfg.norm_eps
         self._fused(self.output, h, norm, eps, self.logits)
-        rc = lib.ttsp_argmax(self.logits.data_ptr(), cfg.vocab_size, _lib.DT_BF16, self.tokens.data_ptr(), st)
-        self._check(rc, "ttsp_argmax")
         # fast transformer: prime at fast position 0 with the projected hidden state
         fx = self._fused(self.fast_project_in, h, norm, eps, self.fast_h)
         p0 = self.fast_pos[0]
         x = self._run_blocks(self.fast_layers[:-1], self.fws, fx, self.fast_freqs[0], self.fast_mask, p0)
         self._fast_kv_only(self.fast_layers[-1], x, self.fast_freqs[0], p0)
-        # codebook 0 is the semantic token (clamped into the codebook); its
-        # embedding starts the fast steps
-        torch.clamp(self.tokens[:1], 0, cfg.codebook_size - 1, out=self.tokens[1:2])
+        # codebook 0 is the semantic token, clamped into the codebook; its
+        # embedding starts the fast steps (one launch: argmax, clamp, row)
+        emb = self.tensors["fast_embeddings"].data_ptr()
+        rc = lib.ttsp_argmax_embed(self.logits.data_ptr(), cfg.vocab_size, _lib.DT_BF16, self.tokens.data_ptr(),
+                                   self.tokens[1:].data_ptr(), emb, cfg.codebook_size, cfg.fast_dim,
+                                   self.fast_h.data_ptr(), st)
+        self._check(rc, "ttsp_argmax_embed")
         for i in range(1, cfg.num_codebooks):
-            rc = lib.ttsp_embed_sum(self.tensors["fast_embeddings"].data_ptr(), self.tokens[i:].data_ptr(), 1,
-                                    cfg.codebook_size, cfg.fast_dim, self.fast_h.data_ptr(), _lib.DT_BF16, st)
-            self._check(rc, "ttsp_embed_sum")
             x = self._run_blocks(self.fast_layers, self.fws, self.fast_h, self.fast_freqs[i], self.fast_mask,
                                  self.fast_pos[i])
             self._fused(self.fast_output, x.view(1, 1, -1), self.tensors["fast_norm"], cfg.norm_eps, self.fast_logits)
-            rc = lib.ttsp_argmax(self.fast_logits.data_ptr(), cfg.codebook_size, _lib.DT_BF16,
-                                 self.tokens[i + 1:].data_ptr(), st)
-            self._check(rc, "ttsp_argmax")
-        # bookkeeping on the device
-        self.history.index_copy_(0, self.step_index, self.tokens.view(1, -1))
-        self.step_index.add_(1)
-        self.pos.add_(1)
+            tok = self.tokens[i + 1:].data_ptr()
+            if i + 1 < cfg.num_codebooks:  # the token and the next codebook step's embedding
+                rc = lib.ttsp_argmax_embed(self.fast_logits.data_ptr(), cfg.codebook_size, _lib.DT_BF16, tok, None,
+                                           emb, cfg.codebook_size, cfg.fast_dim, self.fast_h.data_ptr(), st)
+                self._check(rc, "ttsp_argmax_embed")
+            else:
+                rc = lib.ttsp_argmax(self.fast_logits.data_ptr(), cfg.codebook_size, _lib.DT_BF16, tok, st)
+                self._check(rc, "ttsp_argmax")
+        # bookkeeping on the device: history row, step and position, the next rotary row
+        rc = lib.ttsp_frame_advance(self.tokens.data_ptr(), cfg.n_tokens, self.history.data_ptr(),
+                                    self.history.shape[0], self.step_index.data_ptr(), self.pos.data_ptr(),
+                                    self.freqs.data_ptr(), self.freqs.shape[0], self.freqs[0].numel(),
+                                    self.freq_row.data_ptr(), st)
+        self._check(rc, "ttsp_frame_advance")
 
     # ---------------------------------------------------------------- prefill
 
