@@ -168,6 +168,14 @@ def test_invalid_arguments_are_rejected_before_any_launch():
     assert lib.ttsp_nf4_dequant(8, None, 8, None, 0.0, 8, 8, 1, -1, 64, 256, None) == 1
     assert lib.ttsp_attn_decode(8, 8, 8, 8, 8, 8, 8, 8, 32, 7, 64, 1, 0.1, 1, None) == 1  # nh % nkv
     assert lib.ttsp_attn_chunk() == 64
+    # the frame's glue: empty rows, tables or histories, missing pointers, an unknown dtype
+    assert lib.ttsp_argmax_embed(8, 0, 1, 8, None, 8, 16, 8, 8, None) == 1
+    assert lib.ttsp_argmax_embed(8, 16, 1, 8, None, 8, 0, 8, 8, None) == 1
+    assert lib.ttsp_argmax_embed(8, 16, 1, None, None, 8, 16, 8, 8, None) == 1
+    assert lib.ttsp_argmax_embed(8, 16, 7, 8, None, 8, 16, 8, 8, None) == 1
+    assert lib.ttsp_frame_advance(8, 11, 8, 0, 8, 8, 8, 300, 128, 8, None) == 1
+    assert lib.ttsp_frame_advance(8, 11, 8, 4, 8, None, 8, 300, 128, 8, None) == 1
+    assert lib.ttsp_frame_advance(8, 0, 8, 4, 8, 8, 8, 300, 128, 8, None) == 1
 
 
 def test_drop_ins_decline_without_a_gpu():
