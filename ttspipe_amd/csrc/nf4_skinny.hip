@@ -265,15 +265,18 @@ static void launch_skinny(const void* X, const uint8_t* W, const uint8_t* A8, co
 }
 
 // Launch shape. NW: the fewest waves (4, 8, 16) whose K runs fit SK_MAXS
-// steps; with fewer than 256 row tiles, at least 8 (more waves per row tile).
-// MS: the step budget, 5 when the runs fit it (fewer repeated loads), else
-// SK_MAXS. R: with 512 or more row tiles, several tiles a workgroup (each X
-// fragment then serves R of them: the activation traffic, which binds from 16
-// rows up, drops by R) - 4 for 17-32 rows and 2 otherwise with 4 waves, 2 for
-// up to 32 rows with 8 - else 1. (Measured at 9728 x 2560: 32 rows 16.8 us
-// with R = 4 against 18.3 with 2, 64 rows 32.7 with R = 2 against 38.7 with 1;
-// at 256 row tiles R = 1 stays the fastest.) Returns false when no shape fits
-// (see skinny_max_k).
+// steps; with fewer than 256 row tiles and runs of more than 5 steps at 4
+// waves, at least 8 (more waves per row tile). MS: the step budget, 5 when
+// the runs fit it (fewer repeated loads), else SK_MAXS. R: with 512 or more
+// row tiles, several tiles a workgroup (each X fragment then serves R of them:
+// the activation traffic, which binds from 16 rows up, drops by R) - 4 for
+// 17-32 rows and 2 otherwise with 4 waves, 2 from 9 rows with 8 - else 1.
+// (Measured: at 9728 x 2560 two tiles cost 0.4-0.9 us more than one up to 8
+// rows and save 0.7 at 16; 32 rows 16.8 us with R = 4 against 18.3 with 2,
+// 64 rows 32.7 with R = 2 against 38.7 with 1; at 1024 x 2560 four waves take
+// 5.7 / 6.4 / 9.3 us for 4 / 16 / 32 rows against 6.9 / 9.1 / 14.2 with
+// eight, at 2560 x 4096 and 1024 x 3072 eight are faster.) Returns false when
+// no shape fits (see skinny_max_k).
 template <int DT, int NT>
 static bool skinny_shape(const void* X, const uint8_t* W, const uint8_t* A8, const float* AMAX, const float* CODE2,
                          float offset, const float* LUT, void* Y, const void* RES, int epi, int M, int K, int N,
@@ -282,10 +285,10 @@ static bool skinny_shape(const void* X, const uint8_t* W, const uint8_t* A8, con
   int nw = (steps + SK_MAXS - 1) / SK_MAXS;
   if (nw > 16) return false;
   nw = nw <= 4 ? 4 : nw <= 8 ? 8 : 16;
-  if (tiles < 256 && nw < 8) nw = 8;
+  if (tiles < 256 && nw < 8 && steps > 4 * 5) nw = 8;
   const int run = (steps + nw - 1) / nw;
   const bool ms5 = run <= 5;
-  const bool r2 = NT <= 2 && nw <= 8 && tiles >= 2 * 256;
+  const bool r2 = NT <= 2 && nw <= 8 && tiles >= 2 * 256 && N > 8;
 #define TTSP_L(RV, NWV, MSV) \
   launch_skinny<DT, RV, NT, NWV, MSV>(X, W, A8, AMAX, CODE2, offset, LUT, Y, RES, epi, M, K, N, bs_shift, bs2_shift, st)
 #define TTSP_MS(RV, NWV) \
