@@ -79,21 +79,28 @@ def test_gemv_shape_covers_every_row_and_column(M, K):
                                  (6144, 2560), (1536, 1024), (3072, 1024), (1024, 3072), (64, 128)])
 def test_gemm_split_plan(M, K, N):
     """The K split a prefill GEMM takes (host-only query): none for N <= 32 or
-    when the output tiles already fill the GPU; otherwise each split covers an
-    even number of at least 8 K-steps of 64 codes, and the split workgroups
-    fill the GPU."""
+    when the 64 x 128 output tiles already fill the GPU; otherwise each split
+    covers an even number of at least 8 K-steps of 64 codes. Up to 128 tiles
+    it is the largest such split whose workgroups fit one to a CU; between
+    128 and 256 tiles, 4 splits when each keeps more than 16 K-steps."""
     from ttspipe_amd import _lib
 
     lib = _lib.load()
     sp = lib.ttsp_nf4_gemm_splits(M, K, N)
     assert sp in (1, 2, 4, 8)
     steps = K // 64
-    tiles = {(bm, bn): -(-M // bm) * -(-N // bn) for bm, bn in ((128, 128), (64, 128))}
-    if N <= 32 or max(tiles.values()) >= 256:
+    t = -(-M // 64) * -(-N // 128)
+    if N <= 32 or t >= 256:
         assert sp == 1
     if sp > 1:
         assert steps % (2 * sp) == 0 and steps // sp >= 8
-        assert max(tiles.values()) * sp >= 256
+    if N > 64 and t > 128:
+        assert sp == (4 if t < 256 and steps % 8 == 0 and steps > 64 else 1)
+    elif N > 64:
+        # the split fits one pass, and twice it would not (or is not allowed)
+        assert t * sp <= 256
+        nxt = 2 * sp
+        assert nxt > 8 or steps % (2 * nxt) or steps // nxt < 8 or t * nxt > 256
     assert lib.ttsp_nf4_gemm_splits(M, K, 1) == 1
 
 

@@ -374,13 +374,19 @@ static void launch_gemm(const void* X, const uint8_t* W, const uint8_t* A8, cons
 }
 
 // Tile shape and K-split of a launch: 64 x 128 tiles (8 waves), unsplit when
-// they give every CU a workgroup; else the smallest split (2, 4, 8; each split
-// an even number of at least 8 K-steps) that gives every CU two workgroups, or
-// the largest that gives it one; otherwise unsplit, 64 x 128 tiles down to 128
-// of them, 64 x 64 below. Up to SKINNY_MAX_N rows take the skinny kernel
-// (nf4_skinny.hip), shape 0, never split. (Measured at 512 rows: 64 x 128
-// beats 128 x 128 on every layer shape, by 8-10 % at 9728 x 2560 and
-// 2560 x 9728; unsplit tile shapes give identical bits.)
+// they give every CU a workgroup. Up to 128 tiles, the largest split (2, 4,
+// 8; each split an even number of at least 8 K-steps) whose workgroups still
+// fit one to a CU: a split's fp32 partial sums cost a write and a read of
+// splits x N x M floats, so a second pass of workgroups only pays where each
+// split keeps a long K run. Between 128 and 256 tiles no split fits one pass,
+// and 4 splits pay only past 16 K-steps each. Unsplit launches take 64 x 128
+// tiles down to 128 of them, 64 x 64 below. Up to SKINNY_MAX_N rows take the
+// skinny kernel (nf4_skinny.hip), shape 0, never split. Measured on the five
+// projections of a 2560-wide layer (wqkv 6144 x 2560, wo 2560 x 4096, w1 and
+// w3 9728 x 2560, w2 2560 x 9728): 187 -> 125 us at 128 rows against a rule
+// that sought two workgroups a CU, 200 -> 184 us at 256 rows, equal at 512
+// rows (where 64 x 128 beats 128 x 128 by 8-10 % at 9728 x 2560 and
+// 2560 x 9728; unsplit tile shapes give identical bits).
 struct GemmPlan {
   int shape, splits;
 };
@@ -400,11 +406,12 @@ static GemmPlan gemm_plan(int M, int K, int N) {
   const long long t = gemm_tiles(M, N, 64, 128);
   if (t >= 256) return {2, 1};
   int splits = 1;
-  for (int sp = 2; sp <= 8; sp *= 2) {
-    if (steps % (2 * sp) || steps / sp < 8) break;
-    if (t * sp >= 256) {
+  if (t > 128) {
+    if (steps % 8 == 0 && steps / 4 > 16) splits = 4;
+  } else {
+    for (int sp = 2; sp <= 8; sp *= 2) {
+      if (steps % (2 * sp) || steps / sp < 8 || t * sp > 256) break;
       splits = sp;
-      if (t * sp >= 512) break;
     }
   }
   return splits > 1 ? GemmPlan{2, splits} : GemmPlan{unsplit_shape(M, N), 1};
