@@ -229,12 +229,16 @@ def test_few_rows_over_a_long_row(nf4, orc, rows):
     assert beyond_rounding_error(o.to_f32(bits(y), o.DT_BF16), ref.reshape(-1), o.DT_BF16) < 2e-3
 
 
+@pytest.mark.parametrize("rows", [128, 256, 512])
 @pytest.mark.parametrize("name,shape", [("q", (4096, 2560)), ("k", (1024, 2560)), ("o", (2560, 4096)),
-                                        ("gate", (9728, 2560)), ("down", (2560, 9728))])
-def test_prefill_gemm_512_rows(nf4, orc, name, shape):
-    """The prefill workload: 512 bf16 rows through each projection shape."""
+                                        ("gate", (9728, 2560)), ("down", (2560, 9728)), ("qkv", (6144, 2560)),
+                                        ("narrow", (1024, 4096))])
+def test_prefill_gemm_bucket_rows(nf4, orc, name, shape, rows):
+    """The prefill workload: 128, 256 and 512 bf16 rows (prompt buckets)
+    through each projection shape; between them the launch plan takes every
+    K split it has (none, 2, 4 and 8 ways: 8 for the narrow shape at 128)."""
     M, K = shape
-    rows, dtype = 512, torch.bfloat16
+    dtype = torch.bfloat16
     layer = random_layer(M, K, True, seed=len(name))
     lin = to_linear(layer, dtype)
     xb = randn_bits(rows * K, dtype, seed=99)
