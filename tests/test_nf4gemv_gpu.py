@@ -143,6 +143,37 @@ def test_gemv_bit_exact_and_within_bar(nf4, orc, shape, nested, dtype):
     assert beyond_rounding_error(o.to_f32(got, dt), ref.reshape(-1), dt) < 2e-3
 
 
+@pytest.mark.parametrize("shape", [(4961, 384), (16000, 256), (4100, 128), (9000, 512)])
+@pytest.mark.parametrize("pair", [False, True])
+def test_one_chunk_rows_with_three_or_more_rows_a_wave(nf4, orc, shape, pair):
+    """K <= 512 (one 64-dword chunk per lane) with more than 4096 rows (3 to 8
+    rows a wave): the code lookups run ahead of the arithmetic, and must not
+    reach a weight row before its load is issued. They once did, and every
+    wave's third row came out wrong. Plain one-weight form and the SwiGLU
+    pair, against the oracle bit for bit."""
+    M, K = shape
+    dtype = torch.bfloat16
+    dt = dt_code(dtype)
+    J, KS, RPW = gemv_shape(M, K)
+    assert J == 1 and RPW >= 3
+    l1 = random_layer(M, K, False, seed=M + K)
+    w1 = to_linear(l1, dtype)
+    assert nf4.prepare(w1)
+    xb = randn_bits(K, dtype, seed=K + 3)
+    x = from_bits(xb, dtype).view(1, 1, K)
+    g1 = orc.gemv_emul(xb, dt, **oracle_args(l1), M=M, K=K, bs=64, KS=KS, J=J)
+    if pair:
+        l3 = random_layer(M, K, False, seed=M + K + 1)
+        w3 = to_linear(l3, dtype)
+        assert nf4.prepare(w3)
+        y = nf4.matmul_fused(w1, x, module3=w3)
+        expect = orc.gemv_emul(xb, dt, **oracle_args(l3), M=M, K=K, bs=64, KS=KS, J=J, R=g1, epi=2)
+    else:
+        y = nf4.matmul(w1, x)
+        expect = g1
+    assert np.array_equal(bits(y), expect), f"M={M} K={K} RPW={RPW}: {first_mismatch(bits(y), expect)}"
+
+
 @pytest.mark.parametrize("epi", [1, 2])
 @pytest.mark.parametrize("dtype", DTYPES)
 def test_gemv_epilogues_bit_exact(nf4, orc, epi, dtype):

@@ -484,9 +484,13 @@ __global__ __launch_bounds__(GEMV_THREADS) void nf4_gemv_kernel(
   for (int j = 0; j < J; ++j) sblk4[j] = 4 * (wave * SW + 8 * j + (lane >> sh));
   // The (row, chunk) items in order, the code lookups LA items ahead of the
   // arithmetic (sched_barrier keeps the compiler from pulling them back), the
-  // next weight row requested at each row's start.
+  // next weight row requested at each row's start. A lookup may only reach
+  // rows already requested: row r + PF is requested when row r starts, so the
+  // lookahead stays within PF rows of items (with one chunk per lane and three
+  // or more rows a wave, three items ahead would read a row before its load).
   constexpr int T = NM * RPW * J;
-  constexpr int LA = GEMV_LOOKAHEAD < T ? GEMV_LOOKAHEAD : T;
+  constexpr int LA0 = GEMV_LOOKAHEAD < T ? GEMV_LOOKAHEAD : T;
+  constexpr int LA = LA0 < PF * J ? LA0 : PF * J;
   float sc[T];
   uint32_t cp[T][4];
   auto lookup = [&](int t) {
