@@ -101,6 +101,24 @@ def test_matmul_random_shapes_within_bar(nf4, orc, case):
     assert splits  # (recorded for the failure message of a future plan change)
 
 
+@pytest.mark.parametrize("case", range(6))
+def test_few_rows_random_shapes_within_bar(nf4, orc, case):
+    """2 to 64 rows (the few-row kernel wherever K allows it) at random layer
+    shapes, every row checked."""
+    rng = np.random.default_rng(2500 + case)
+    for i, (M, K, bs, nested, dtype, _) in enumerate(_shapes(8, 2500 + case, 2)):
+        rows = int(rng.integers(2, 65))
+        layer = random_layer(M, K, nested, seed=case * 100 + i + 90, bs=bs)
+        lin = to_linear(layer, dtype)
+        xb = randn_bits(rows * K, dtype, seed=rows + i + 5)
+        y = lin(from_bits(xb, dtype).view(rows, K))
+        dt = dt_code(dtype)
+        ref = orc.nf4_gemm_ref(xb, dt, **oracle_args(layer), M=M, K=K, N=rows, bs=bs, bs2=layer["bs2"] or 256)
+        got = o.to_f32(bits(y), dt).reshape(rows, M)
+        where = f"M={M} K={K} rows={rows} bs={bs} nested={nested} {dtype}"
+        assert beyond_rounding_error(got, ref, dt) < 2e-3, where
+
+
 FORMS = ("norm", "norm+swiglu", "swiglu", "norm+residual")
 
 
