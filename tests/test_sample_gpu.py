@@ -129,3 +129,32 @@ def test_sampler_declines_rows_longer_than_it_holds():
     row = torch.zeros(fusedsample.MAX_VOCAB + 1, device="cuda", dtype=torch.float16)
     t, p = torch.tensor([1.0], device="cuda"), torch.tensor([1.0], device="cuda")
     assert fusedsample.sample(row, t, p, torch.tensor([5], device="cuda")) is None
+
+
+@pytest.mark.parametrize("case", range(4))
+def test_sampler_random_settings(case):
+    """Random row lengths (1 to 32768), k (1 to 100), top-p, temperatures and
+    logit spreads (down to bf16/fp16 spacing, where ties abound): the drawn
+    index equals the oracle's wherever the decision is not within rounding of
+    a boundary."""
+    rng = np.random.default_rng(9000 + case)
+    checked = 0
+    for trial in range(40):
+        dtype = DTYPES[int(rng.integers(0, 2))]
+        dt = dt_code(dtype)
+        V = int(rng.integers(1, 32769))
+        topk, topp = int(rng.integers(1, 101)), float(rng.choice([0.0, 0.3, 0.8, 0.95, 1.0]))
+        temp = float(rng.choice([0.05, 0.5, 1.0, 1.7]))
+        spread = float(rng.choice([0.02, 1.0, 4.0]))
+        lb = o.from_f32((rng.standard_normal(V) * spread).astype(np.float32), dt)
+        u = rng.random(V).astype(np.float32)
+        tq = float(o.to_f32(o.from_f32(np.float32([temp]), dt), dt)[0])
+        pq = float(o.to_f32(o.from_f32(np.float32([topp]), dt), dt)[0])
+        l = o.to_f32(lb, dt).astype(np.float64)
+        if _ambiguous(l, tq, pq, topk, u):
+            continue
+        expect = o.sample_topk_ref(l, tq, pq, topk, u)[0]
+        where = f"trial {trial}: V={V} k={topk} p={topp} T={temp} spread={spread} {dtype}"
+        assert _draw(lb, dtype, temp, topp, topk, u) == expect, where
+        checked += 1
+    assert checked >= 25
