@@ -203,3 +203,42 @@ def test_reset_to_a_longer_history_drops_the_captured_frame(small):
     assert small.graph is None
     small.decode(4)
     assert small.graph is not None
+
+
+def _random_config(rng, seed):
+    """A small Dual-AR model of random shape (widths multiples of 128, any
+    GQA grouping the kernels take, 1-3 layers each side, 2-6 codebooks)."""
+    from ttspipe_amd.dualar import DualARConfig
+
+    nkv = int(rng.choice([1, 2, 4]))
+    fnkv = int(rng.choice([1, 2]))
+    ncb = int(rng.integers(2, 7))
+    prefill_len = int(rng.integers(1, 200))
+    return DualARConfig(
+        dim=128 * int(rng.integers(2, 9)), n_layer=int(rng.integers(1, 4)), n_head=nkv * int(rng.choice([1, 2, 4])),
+        n_local_heads=nkv, intermediate_size=128 * int(rng.integers(2, 13)),
+        vocab_size=int(rng.choice([256, 512, 640])), fast_dim=128 * int(rng.integers(1, 5)),
+        fast_n_layer=int(rng.integers(1, 4)), fast_n_head=fnkv * int(rng.choice([1, 2, 4])),
+        fast_n_local_heads=fnkv, fast_intermediate_size=128 * int(rng.integers(1, 9)), num_codebooks=ncb,
+        codebook_size=int(rng.choice([128, 256, 512])), max_seq_len=prefill_len + 8 + int(rng.integers(1, 100)),
+        prefill_len=prefill_len, qk_norm=bool(rng.integers(0, 2)), seed=seed,
+        fast_max_len=int(rng.choice([ncb, 16])))
+
+
+@pytest.mark.parametrize("case", range(8))
+def test_random_model_shapes_match_the_oracle(case):
+    """Eight greedy frames of a randomly shaped model, graph-replayed and
+    eager, against the oracle: the frame's launch plans (GEMV splits, fused
+    or two-launch attention + wo, chunk counts of the slow cache) at shapes
+    the two fixed models do not have."""
+    from ttspipe_amd.dualar import SyntheticDualAR, first_tokens
+
+    cfg = _random_config(np.random.default_rng(700 + case), seed=31 + case)
+    model = SyntheticDualAR(cfg)
+    got = model.decode(8, graphed=True)
+    ref = _oracle(model).decode(first_tokens(cfg), cfg.prefill_len, 8)
+    diff = np.flatnonzero((got != ref).any(axis=1))
+    assert diff.size == 0, f"{cfg}: first differing frame {diff[0]}: gpu {got[diff[0]]} oracle {ref[diff[0]]}"
+    assert np.array_equal(model.decode(8, graphed=False), got)
+    del model
+    torch.cuda.empty_cache()
