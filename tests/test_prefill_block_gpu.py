@@ -82,17 +82,18 @@ REF_BAR = 3e-3  # rel-norm of the block output against the fp64 block with the f
 REF_START, REF_ROWS, REF_LEN = 24, 40, 128
 
 
-def _ref_inputs(dtype, qk_norm, seed=3):
-    """The fp64 reference's inputs for `_block(dtype, qk_norm, max_len=128,
-    seed)`: its dequantised weights (numpy closed form) and norm weights (the
-    same seeded generator), seeded x rows and cache, the positions'
+def _ref_inputs(dtype, qk_norm, seed=3, nh=4, nkv=2, D=512, inter=1024, start=REF_START, rows=REF_ROWS,
+                length=REF_LEN):
+    """The fp64 reference's inputs for `_block(dtype, qk_norm, D, nh, nkv,
+    inter, max_len=length, seed)`: its dequantised weights (numpy closed
+    form) and norm weights (the same seeded generator), seeded x rows at
+    positions start.. start + rows - 1 and cache, the positions'
     frequencies."""
     from oracle import oracle as o
     from tests.nf4data import dequant_numpy, random_layer
     from ttspipe_amd.llama import precompute_freqs_cis
 
     dt = o.DT_BF16 if dtype == torch.bfloat16 else o.DT_F16
-    nh, nkv, D, inter = 4, 2, 512, 1024
     W = {}
     for i, (name, M, K) in enumerate([("wqkv", (nh + 2 * nkv) * 128, D), ("wo", D, nh * 128), ("w1", inter, D),
                                       ("w3", inter, D), ("w2", D, inter)]):
@@ -104,14 +105,14 @@ def _ref_inputs(dtype, qk_norm, seed=3):
              .double().numpy() for n in names}
     rng = np.random.default_rng(seed + 100)
     q16 = lambda a: o.from_f32(a.astype(np.float32), dt)  # noqa: E731
-    xb = q16(rng.standard_normal((REF_ROWS, D)))
-    kcb, vcb = q16(rng.standard_normal((nkv, REF_LEN, 128))), q16(rng.standard_normal((nkv, REF_LEN, 128)))
-    pos = list(range(REF_START, REF_START + REF_ROWS))
-    freqs = precompute_freqs_cis(REF_LEN, 128, 1e6)[pos]
+    xb = q16(rng.standard_normal((rows, D)))
+    kcb, vcb = q16(rng.standard_normal((nkv, length, 128))), q16(rng.standard_normal((nkv, length, 128)))
+    pos = list(range(start, start + rows))
+    freqs = precompute_freqs_cis(length, 128, 1e6)[pos]
     f64 = lambda b: o.to_f32(b, dt).astype(np.float64)  # noqa: E731
     rnd = lambda t: f64(q16(np.asarray(t)))  # noqa: E731
     return dict(W=W, norms=norms, xb=xb, kcb=kcb, vcb=vcb, pos=pos, freqs=freqs, dt=dt, f64=f64, rnd=rnd,
-                nh=nh, nkv=nkv)
+                nh=nh, nkv=nkv, D=D, inter=inter, start=start, rows=rows, length=length, seed=seed)
 
 
 def _ref(c, qk_norm, mutant=None):
@@ -137,6 +138,46 @@ def test_fp64_block_reference_catches_planted_mistakes(qk_norm):
         assert rel_norm(_ref(c, qk_norm, m)[0], ref) > 2 * REF_BAR, m
 
 
+def _block_against_fp64(dtype, qk_norm, **shape):
+    """The fused prefill block of `_ref_inputs(dtype, qk_norm, **shape)`'s
+    shape on the GPU against the fp64 block: (rel-norm of the output, K-row
+    and V-row error in ulps of each head row's largest element)."""
+    from tests.refblock import rel_norm
+    from tests.test_fused_gpu import _block
+    from ttspipe_amd import fusedlayer, fusedops, nf4gemv
+
+    assert nf4gemv.install() and fusedops.install() and fusedlayer.install()
+    c = _ref_inputs(dtype, qk_norm, **shape)
+    D, rows, start, length = c["D"], c["rows"], c["start"], c["length"]
+    block, _ = _block(dtype, qk_norm, dim=D, n_head=c["nh"], n_local_heads=c["nkv"], inter=c["inter"],
+                      max_len=length, seed=c["seed"])
+    for n, w in c["norms"].items():
+        mod = getattr(block, n, None) or getattr(block.attention, n)
+        assert np.array_equal(mod.weight.double().cpu().numpy(), w)
+    dev = lambda b, shape: torch.from_numpy(b.view(np.int16).copy()).view(dtype).cuda().view(shape)  # noqa: E731
+    kv = block.attention.kv_cache
+    kv.k_cache.copy_(dev(c["kcb"], kv.k_cache.shape))
+    kv.v_cache.copy_(dev(c["vcb"], kv.v_cache.shape))
+    pos = torch.tensor(c["pos"], device="cuda")
+    mask = torch.tril(torch.ones(length, length, dtype=torch.bool, device="cuda"))[None, None, pos]
+    before = fusedlayer.stats()["prefill"]
+    with torch.inference_mode():
+        ours = block(dev(c["xb"], (1, rows, D)), c["freqs"].cuda(), mask, pos)
+    assert fusedlayer.stats()["prefill"] == before + 1
+    ref, k_ref, v_ref = _ref(c, qk_norm)
+    got = ours.double().cpu().numpy().reshape(rows, D)
+    rel = rel_norm(got, ref)
+    k_got = kv.k_cache[0, :, start : start + rows].double().cpu().numpy().transpose(1, 0, 2)
+    v_got = kv.v_cache[0, :, start : start + rows].double().cpu().numpy().transpose(1, 0, 2)
+    # in ulps of each head row's largest element (rotation may cancel two
+    # rounded inputs into a value far smaller than either)
+    mant = 7 if dtype == torch.bfloat16 else 10
+    row_ulp = lambda t: 2.0 ** (np.floor(np.log2(np.abs(t).max(-1, keepdims=True))) - mant)  # noqa: E731
+    k_ulps = float(np.max(np.abs(k_got - k_ref) / row_ulp(k_ref)))
+    v_ulps = float(np.max(np.abs(v_got - v_ref) / row_ulp(v_ref)))
+    return rel, k_ulps, v_ulps
+
+
 @pytest.mark.gpu
 @pytest.mark.parametrize("qk_norm", [True, False])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
@@ -146,40 +187,31 @@ def test_prefill_block_matches_an_fp64_block(qk_norm, dtype):
     (tests/refblock.py; no kernel of this repository feeds it): the output
     within REF_BAR (rel-norm), the new K and V rows within one 16-bit ulp of
     each head row's largest element (the products' own roundings)."""
-    from tests.refblock import rel_norm
-    from tests.test_fused_gpu import _block
-    from ttspipe_amd import fusedlayer, fusedops, nf4gemv
-
-    assert nf4gemv.install() and fusedops.install() and fusedlayer.install()
-    block, _ = _block(dtype, qk_norm, max_len=REF_LEN, seed=3)
-    c = _ref_inputs(dtype, qk_norm)
-    for n, w in c["norms"].items():
-        mod = getattr(block, n, None) or getattr(block.attention, n)
-        assert np.array_equal(mod.weight.double().cpu().numpy(), w)
-    dev = lambda b, shape: torch.from_numpy(b.view(np.int16).copy()).view(dtype).cuda().view(shape)  # noqa: E731
-    kv = block.attention.kv_cache
-    kv.k_cache.copy_(dev(c["kcb"], kv.k_cache.shape))
-    kv.v_cache.copy_(dev(c["vcb"], kv.v_cache.shape))
-    pos = torch.tensor(c["pos"], device="cuda")
-    mask = torch.tril(torch.ones(REF_LEN, REF_LEN, dtype=torch.bool, device="cuda"))[None, None, pos]
-    before = fusedlayer.stats()["prefill"]
-    with torch.inference_mode():
-        ours = block(dev(c["xb"], (1, REF_ROWS, 512)), c["freqs"].cuda(), mask, pos)
-    assert fusedlayer.stats()["prefill"] == before + 1
-    ref, k_ref, v_ref = _ref(c, qk_norm)
-    got = ours.double().cpu().numpy().reshape(REF_ROWS, 512)
-    rel = rel_norm(got, ref)
-    k_got = kv.k_cache[0, :, REF_START : REF_START + REF_ROWS].double().cpu().numpy().transpose(1, 0, 2)
-    v_got = kv.v_cache[0, :, REF_START : REF_START + REF_ROWS].double().cpu().numpy().transpose(1, 0, 2)
-    # in ulps of each head row's largest element (rotation may cancel two
-    # rounded inputs into a value far smaller than either)
-    mant = 7 if dtype == torch.bfloat16 else 10
-    row_ulp = lambda t: 2.0 ** (np.floor(np.log2(np.abs(t).max(-1, keepdims=True))) - mant)  # noqa: E731
-    k_ulps = float(np.max(np.abs(k_got - k_ref) / row_ulp(k_ref)))
-    v_ulps = float(np.max(np.abs(v_got - v_ref) / row_ulp(v_ref)))
+    rel, k_ulps, v_ulps = _block_against_fp64(dtype, qk_norm)
     print(f"prefill block vs fp64 block: rel {rel:.2e}, K rows {k_ulps:.1f} ulp, V rows {v_ulps:.1f} ulp")
     assert rel < REF_BAR
     assert k_ulps <= 1.0 and v_ulps <= 1.0
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("case", range(6))
+def test_random_block_shapes_match_an_fp64_block(case):
+    """The same bars at randomly drawn block shapes: width 256-1024, 1-8 kv
+    heads with 1-4 query heads each, FFN 256-2048, 2-200 new rows after a
+    0-300 position prefix (so the GEMMs take the few-row kernel and every
+    split, and the attention one or several key blocks)."""
+    rng = np.random.default_rng(900 + case)
+    nkv = int(rng.choice([1, 2, 4, 8]))
+    shape = dict(nkv=nkv, nh=nkv * int(rng.choice([1, 2, 4])), D=128 * int(rng.integers(2, 9)),
+                 inter=128 * int(rng.integers(2, 17)), start=int(rng.integers(0, 301)), rows=int(rng.integers(2, 201)),
+                 seed=40 + case)
+    shape["length"] = shape["start"] + shape["rows"] + int(rng.integers(0, 64))
+    dtype = [torch.bfloat16, torch.float16][int(rng.integers(0, 2))]
+    qk_norm = bool(rng.integers(0, 2))
+    rel, k_ulps, v_ulps = _block_against_fp64(dtype, qk_norm, **shape)
+    where = f"{shape} {dtype} qk_norm={qk_norm}: rel {rel:.2e}, K {k_ulps:.1f} ulp, V {v_ulps:.1f} ulp"
+    assert rel < REF_BAR, where
+    assert k_ulps <= 1.0 and v_ulps <= 1.0, where
 
 
 @pytest.mark.gpu
