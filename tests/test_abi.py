@@ -80,9 +80,10 @@ def test_gemv_shape_covers_every_row_and_column(M, K):
 def test_gemm_split_plan(M, K, N):
     """The K split a prefill GEMM takes (host-only query): none for N <= 32 or
     when the 64 x 128 output tiles already fill the GPU; otherwise each split
-    covers an even number of at least 8 K-steps of 64 codes. Up to 128 tiles
-    it is the largest such split whose workgroups fit one to a CU; between
-    128 and 256 tiles, 4 splits when each keeps more than 16 K-steps."""
+    covers an even number of at least 8 K-steps of 64 codes. 33 to 64 rows:
+    4 splits where that allows, else 2. More rows: up to 128 tiles the
+    largest such split whose workgroups fit one to a CU; between 128 and 256
+    tiles, 4 splits when each keeps more than 16 K-steps."""
     from ttspipe_amd import _lib
 
     lib = _lib.load()
@@ -94,7 +95,10 @@ def test_gemm_split_plan(M, K, N):
         assert sp == 1
     if sp > 1:
         assert steps % (2 * sp) == 0 and steps // sp >= 8
-    if N > 64 and t > 128:
+    if 32 < N <= 64:  # 64 x 64 tiles, the K split 4 ways where each keeps 8 K-steps, else 2
+        expect = 4 if steps % 8 == 0 and steps // 4 >= 8 else 2 if steps % 4 == 0 and steps // 2 >= 8 else 1
+        assert sp == expect
+    elif N > 64 and t > 128:
         assert sp == (4 if t < 256 and steps % 8 == 0 and steps > 64 else 1)
     elif N > 64:
         # the split fits one pass, and twice it would not (or is not allowed)

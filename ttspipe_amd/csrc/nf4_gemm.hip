@@ -380,8 +380,9 @@ static void launch_gemm(const void* X, const uint8_t* W, const uint8_t* A8, cons
 // splits x N x M floats, so a second pass of workgroups only pays where each
 // split keeps a long K run. Between 128 and 256 tiles no split fits one pass,
 // and 4 splits pay only past 16 K-steps each. Unsplit launches take 64 x 128
-// tiles down to 128 of them, 64 x 64 below. Up to SKINNY_MAX_N rows take the
-// skinny kernel (nf4_skinny.hip), shape 0, never split. Measured on the five
+// tiles down to 128 of them, 64 x 64 below. 33 to 64 rows take 64 x 64 tiles
+// with a K split (below); up to SKINNY_MAX_N rows otherwise the skinny kernel
+// (nf4_skinny.hip), shape 0, never split. Measured on the five
 // projections of a 2560-wide layer (wqkv 6144 x 2560, wo 2560 x 4096, w1 and
 // w3 9728 x 2560, w2 2560 x 9728): 187 -> 125 us at 128 rows against a rule
 // that sought two workgroups a CU, 200 -> 184 us at 256 rows, equal at 512
@@ -400,9 +401,24 @@ static long long gemm_tiles(int M, int N, int bm, int bn) {
 
 static int unsplit_shape(int M, int N) { return gemm_tiles(M, N, 64, 128) >= 128 ? 2 : 3; }
 
+// From 33 rows (where the skinny kernel's tiles double) a K split of 64 x 64
+// tiles - one row tile covers every input row - beats the skinny kernel:
+// 4 ways where each split keeps 8 or more K-steps, else 2. Measured at 33-64
+// rows: 20-45 % faster on the five layer shapes (9728 x 2560 at 33 rows
+// 20.4 against 26.0 us, 2560 x 9728 at 64 rows 25.9 against 45.6) and on
+// the 1024-wide fast-transformer shapes (1024 x 3072 at 64 rows 13.1 against
+// 25.2); at 28-32 rows the two tie over a layer, below that the skinny kernel
+// wins (8 rows: 12.1 against 17.4 at 9728 x 2560). The unsplit entry has no
+// workspace, and unsplit tiles lose to the skinny kernel there, so it keeps
+// the skinny kernel up to SKINNY_MAX_N rows.
+constexpr int SPLIT_SMALL_N = 32;
+
 static GemmPlan gemm_plan(int M, int K, int N) {
-  if (skinny(K, N)) return {0, 1};
   const int steps = K / KT;
+  if (N > SPLIT_SMALL_N && N <= 64)
+    for (int sp = 4; sp >= 2; sp /= 2)
+      if (steps % (2 * sp) == 0 && steps / sp >= 8) return {3, sp};
+  if (skinny(K, N)) return {0, 1};
   const long long t = gemm_tiles(M, N, 64, 128);
   if (t >= 256) return {2, 1};
   int splits = 1;

@@ -1,4 +1,5 @@
-// NF4 matmul for a few activation rows (2 <= N <= 64): Y[N][M] = X[N][K] . W^T,
+// NF4 matmul for a few activation rows (2 <= N <= 64; the split plan takes
+// 64 x 64 GEMM tiles from 33 rows, see nf4_gemm.hip): Y[N][M] = X[N][K] . W^T,
 // W in the bitsandbytes layout (nf4_gemv.hip describes it).
 //
 // With few rows the weights are still the traffic - every weight byte is used
