@@ -74,16 +74,33 @@ def test_gemv_shape_covers_every_row_and_column(M, K):
     assert J * KS * 64 >= K // 8 and (J - 1) * KS * 64 < K // 8  # no wholly idle chunk slot
 
 
-@pytest.mark.parametrize("N", [2, 32, 33, 64, 70, 512, 2048])
+def _dl_split(M, K, N):
+    """The direct-to-LDS kernel's split for 256 to 512 rows, or None: 4 where K
+    has 64 or more steps and there are at least 75 64 x 128 tiles; with fewer
+    steps none from 512 tiles and 2 from 300."""
+    steps, t = K // 64, -(-M // 64) * -(-N // 128)
+    if not 256 <= N <= 512:
+        return None
+    if steps >= 64:
+        return 4 if t >= 75 and steps % 8 == 0 and steps // 4 <= 64 else None
+    if t >= 512:
+        return 1
+    if t >= 300 and steps % 4 == 0:
+        return 2
+    return None
+
+
+@pytest.mark.parametrize("N", [2, 32, 33, 64, 70, 256, 512, 2048])
 @pytest.mark.parametrize("M,K", [(4096, 2560), (1024, 2560), (2560, 4096), (9728, 2560), (2560, 9728),
                                  (6144, 2560), (1536, 1024), (3072, 1024), (1024, 3072), (64, 128)])
 def test_gemm_split_plan(M, K, N):
     """The K split a prefill GEMM takes (host-only query): none for N <= 32 or
     when the 64 x 128 output tiles already fill the GPU; otherwise each split
     covers an even number of at least 8 K-steps of 64 codes. 33 to 64 rows:
-    4 splits where that allows, else 2. More rows: up to 128 tiles the
-    largest such split whose workgroups fit one to a CU; between 128 and 256
-    tiles, 4 splits when each keeps more than 16 K-steps."""
+    4 splits where that allows, else 2. 256 to 512 rows where the
+    direct-to-LDS kernel takes the launch: its split. More rows otherwise: up
+    to 128 tiles the largest such split whose workgroups fit one to a CU;
+    between 128 and 256 tiles, 4 splits when each keeps more than 16 K-steps."""
     from ttspipe_amd import _lib
 
     lib = _lib.load()
@@ -91,10 +108,14 @@ def test_gemm_split_plan(M, K, N):
     assert sp in (1, 2, 4, 8)
     steps = K // 64
     t = -(-M // 64) * -(-N // 128)
-    if N <= 32 or t >= 256:
-        assert sp == 1
     if sp > 1:
         assert steps % (2 * sp) == 0 and steps // sp >= 8
+    dl = _dl_split(M, K, N) if N > 64 else None
+    if dl is not None:
+        assert sp == dl
+        return
+    if N <= 32 or t >= 256:
+        assert sp == 1
     if 32 < N <= 64:  # 64 x 64 tiles, the K split 4 ways where each keeps 8 K-steps, else 2
         expect = 4 if steps % 8 == 0 and steps // 4 >= 8 else 2 if steps % 4 == 0 and steps // 2 >= 8 else 1
         assert sp == expect

@@ -282,19 +282,20 @@ def test_prefill_gemm_bucket_rows(nf4, orc, name, shape, rows):
 
 
 @pytest.mark.parametrize("epi", [1, 2])
-@pytest.mark.parametrize("rows", [24, 512])
-def test_gemm_epilogues(nf4, orc, epi, rows):
+@pytest.mark.parametrize("rows,shape", [(24, (2560, 9728)), (512, (2560, 9728)), (512, (9728, 2560))])
+def test_gemm_epilogues(nf4, orc, epi, rows, shape):
     """Residual and SwiGLU-gate epilogues of the GEMM (24 rows: unsplit; 512
     rows at 2560 x 9728: the K-split plan, where the reduce kernel applies
-    them) against the closed forms round(R + round(y)) and
+    them; 512 rows at 9728 x 2560: the unsplit direct-to-LDS kernel, which
+    applies them itself) against the closed forms round(R + round(y)) and
     round(round(silu(R)) * round(y)) evaluated on the oracle's fp64 product,
     within the 2e-3 bar beyond the output's own rounding. An epilogue with its
     operands swapped misses that bar by an order of magnitude."""
     from ttspipe_amd import _lib
 
-    M, K, dtype = 2560, 9728, torch.float16
+    (M, K), dtype = shape, torch.float16
     if rows == 512:
-        assert _lib.load().ttsp_nf4_gemm_splits(M, K, rows) > 1
+        assert _lib.load().ttsp_nf4_gemm_splits(M, K, rows) == (4 if M == 2560 else 1)
     layer = random_layer(M, K, True, seed=31)
     lin = to_linear(layer, dtype)
     xb = randn_bits(rows * K, dtype, seed=32, scale=0.5)
@@ -333,6 +334,32 @@ def test_split_gemm_with_rows_not_a_multiple_of_four(nf4, orc, rows):
                            N=sample.size, bs=64, bs2=256)
     got = o.to_f32(bits(y), o.DT_BF16).reshape(rows, M)[sample]
     assert beyond_rounding_error(got, ref, o.DT_BF16) < 2e-3
+
+
+@pytest.mark.parametrize("nested", [True, False])
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("shape,rows,splits", [((9728, 2560), 512, 1), ((6144, 2560), 512, 2),
+                                               ((2560, 4096), 256, 4), ((9730, 2560), 500, 1),
+                                               ((9730, 2560), 300, 2)])
+def test_direct_lds_gemm_launches(nf4, orc, shape, rows, splits, nested, dtype):
+    """Every launch the plan gives the direct-to-LDS kernel (unsplit, 2 and 4
+    K-splits) with bf16 and fp16 activations and nested and plain scales,
+    including ragged tiles (9730 weight rows: M % 4 == 2, a partial 64-row
+    tile; 500 and 300 activation rows: a partial 128-row tile), against the
+    oracle's fp64 product within the bar."""
+    from ttspipe_amd import _lib
+
+    M, K = shape
+    assert _lib.load().ttsp_nf4_gemm_splits(M, K, rows) == splits
+    layer = random_layer(M, K, nested, seed=M + rows)
+    lin = to_linear(layer, dtype)
+    xb = randn_bits(rows * K, dtype, seed=rows + 3)
+    y = lin(from_bits(xb, dtype).view(rows, K))
+    dt = dt_code(dtype)
+    sample = np.concatenate([np.arange(0, rows, 41), [rows - 1]])  # the last row sits in the partial tile
+    ref = orc.nf4_gemm_ref(xb.reshape(rows, K)[sample], dt, **oracle_args(layer), M=M, K=K, N=sample.size, bs=64)
+    got = o.to_f32(bits(y), dt).reshape(rows, M)[sample]
+    assert beyond_rounding_error(got, ref, dt) < 2e-3
 
 
 # ------------------------------------------------------------ fused forms (one launch)

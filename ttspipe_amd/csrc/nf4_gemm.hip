@@ -413,12 +413,41 @@ static int unsplit_shape(int M, int N) { return gemm_tiles(M, N, 64, 128) >= 128
 // the skinny kernel up to SKINNY_MAX_N rows.
 constexpr int SPLIT_SMALL_N = 32;
 
+bool gemm_dl_fits(int M, int K, int N, int splits);
+int gemm_dl(const void* X, int dt, const uint8_t* W, const uint8_t* A8, const float* AMAX, const float* CODE2,
+            float offset, const float* LUT, void* Y, const void* R, int epi, int M, int K, int N, int bs_shift,
+            int bs2_shift, int waves, int splits, float* YP, hipStream_t st);
+
+// 256 to 512 rows: the direct-to-LDS kernel (nf4_gemm_dl.hip, shape 4, 64 x
+// 128 tiles of 2 waves) with 4 K-splits where K has 64 or more steps and
+// there are at least 75 tiles; with fewer steps unsplit from 512 tiles and
+// with 2 splits from 300. Measured at 512 rows (bf16, nested scales): w1 /
+// w3 9728 x 2560 70.7 -> 52.0 us, w2 2560 x 9728 79.5 -> 58.2, wo 2560 x 4096
+// 40.3 -> 31.8, wqkv 6144 x 2560 45.7 -> 41.0; at 256 rows w1 43.8 -> 37.7,
+// w2 49.9 -> 45.7. The 64 x 128 kernel stays ahead at 128 rows, at
+// 4096 x 2560 and on the 1024-wide shapes (by 3-15 %).
+constexpr int DL_MIN_N = 256, DL_MAX_N = 512;
+static bool dl_plan(int M, int K, int N, GemmPlan* p) {
+  if (N < DL_MIN_N || N > DL_MAX_N) return false;
+  const int steps = K / KT;
+  const long long t = gemm_tiles(M, N, 64, 128);
+  if (steps >= 64) {
+    if (t >= 75 && steps % 8 == 0 && gemm_dl_fits(M, K, N, 4)) return *p = GemmPlan{4, 4}, true;
+    return false;
+  }
+  if (t >= 512 && gemm_dl_fits(M, K, N, 1)) return *p = GemmPlan{4, 1}, true;
+  if (t >= 300 && steps % 4 == 0 && gemm_dl_fits(M, K, N, 2)) return *p = GemmPlan{4, 2}, true;
+  return false;
+}
+
 static GemmPlan gemm_plan(int M, int K, int N) {
   const int steps = K / KT;
   if (N > SPLIT_SMALL_N && N <= 64)
     for (int sp = 4; sp >= 2; sp /= 2)
       if (steps % (2 * sp) == 0 && steps / sp >= 8) return {3, sp};
   if (skinny(K, N)) return {0, 1};
+  GemmPlan dl;
+  if (dl_plan(M, K, N, &dl)) return dl;
   const long long t = gemm_tiles(M, N, 64, 128);
   if (t >= 256) return {2, 1};
   int splits = 1;
@@ -450,7 +479,11 @@ int gemm_mfma(const void* X, int dt, const uint8_t* W, const uint8_t* A8, const 
   // 8 waves for the 64 x 128 tiles (two a SIMD: one wave's dequantisation
   // runs while the other's matrix products do), 4 for 64 x 64
   const int shape = plan.shape;
-  if (dt == DT_BF16) {
+  if (shape == 4) {
+    if (int rc = gemm_dl(X, dt, W, A8, AMAX, CODE2, offset, LUT, Y, R, epi, M, K, N, bs_shift, bs2_shift, 2,
+                         splits, yp, st))
+      return rc;
+  } else if (dt == DT_BF16) {
     if (shape == 2) TTSP_G(DT_BF16, 64, 128, 2, 4);
     else TTSP_G(DT_BF16, 64, 64, 2, 2);
   } else if (dt == DT_F16) {
@@ -518,8 +551,10 @@ extern "C" int ttsp_nf4_gemm(const void* X, int x_dtype, const uint8_t* W, const
     return gemm_skinny(X, x_dtype, W, A8, AMAX, CODE2, offset, LUT, Y, R, epi, M, K, N, bs_shift, bs2_shift, stream);
   // vectorised output rows: 8 elements per 16-byte store
   const bool vec = M % 8 == 0 && (uintptr_t)Y % 16 == 0 && (!epi || (uintptr_t)R % 16 == 0);
-  // unsplit: 64 x 128 tiles, or 64 x 64 when fewer than 128 of those
-  const GemmPlan plan{unsplit_shape(M, N), 1};
+  // unsplit: the direct-to-LDS kernel where the plan takes it unsplit, else
+  // 64 x 128 tiles, or 64 x 64 when fewer than 128 of those
+  GemmPlan plan{unsplit_shape(M, N), 1}, dl;
+  if (dl_plan(M, K, N, &dl) && dl.splits == 1) plan = dl;
   return gemm_mfma(X, x_dtype, W, A8, AMAX, CODE2, offset, LUT, Y, R, epi | (vec ? 4 : 0), M, K, N, bs_shift,
                    bs2_shift, plan, nullptr, stream);
 }

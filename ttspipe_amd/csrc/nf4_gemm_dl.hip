@@ -1,0 +1,341 @@
+// NF4 GEMM with direct global->LDS operand streams (prompt prefill, 128-row
+// activation tiles): Y[N][M] = X[N][K] . W^T, the weight in the bitsandbytes
+// NF4 layout (nf4_gemv.hip gives it), each dequantised weight the exact
+// round(code * scale) of bitsandbytes' dequantize_4bit.
+//
+// A workgroup of W waves owns 32 W weight rows x 128 activation rows; each
+// wave owns 32 weight rows x all 128 activation rows (four 32x32 MFMA blocks,
+// v_mfma_f32_32x32x16). Per K-step of 64 codes:
+//   * the activations (128 rows x 128 bytes) and each wave's packed weight
+//     codes (32 rows x 32 bytes) arrive in a two-stage LDS ring by
+//     buffer_load ... lds: no VGPR staging, no VALU, issued one step ahead;
+//   * an activation load moves 8 whole 128-byte rows (coalesced); inside a
+//     row's LDS copy the 16-byte segment s of row t sits at slot
+//     s ^ ((t >> 1) & 7), so the MFMA B-fragment reads (16 consecutive rows,
+//     one segment each) hit 16 distinct slots of the 256-byte bank width;
+//   * each wave dequantises its own rows straight into the MFMA A operand
+//     (both codes of a byte from one lookup in a 256-entry table of code
+//     pairs, fp32 products, one pack-convert per pair).
+// Inside a step lane half h carries codes 32h .. 32h + 31 and k-slice kk the
+// MFMA's 8 of them; A and B agree, so each output sums the same products.
+// The scales of the workgroup's K range are staged once: nested a8 bytes per
+// (row, step) and per lane its row's amax pair, or plain fp32 absmax per
+// (row, step). A workgroup takes at most DL_MAX_STEPS K-steps.
+//
+// The barrier of a step is a bare s_barrier: __syncthreads' release fence
+// would also wait for the ring loads still in flight. Each wave waits for its
+// own loads of the step (vmcnt) before it; its LDS reads of the stage the
+// next loads refill fed its MFMAs, so they are complete. The step body takes
+// its LDS stages as restrict pointers of one inlined call: the compiler then
+// sees that the refill cannot change the stage being read and inserts no
+// wait for it.
+#include "ttsp_common.h"
+
+namespace ttsp {
+
+namespace {
+
+typedef __bf16 bf16x8_v __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8_v __attribute__((ext_vector_type(8)));
+typedef float f32x16_v __attribute__((ext_vector_type(16)));
+typedef __bf16 bf16x2_v __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2_v __attribute__((ext_vector_type(2)));
+typedef float f32x2_v __attribute__((ext_vector_type(2)));
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
+
+constexpr int KT = 64;             // codes per K-step
+constexpr int CH = 1024;           // bytes of one wave-wide 16-byte-per-lane load
+constexpr int BN = 128;            // activation rows per workgroup
+constexpr int BSTAGE = BN * 128;   // activation bytes per step
+constexpr int DL_MAX_STEPS = 64;   // K-steps a workgroup may take
+
+// s_waitcnt bounding vmcnt only (gfx9 encoding)
+#define TTSP_VMWAIT(n) __builtin_amdgcn_s_waitcnt(((n) & 15) | (((n) >> 4) << 14) | (7 << 4) | (15 << 8))
+
+template <int DT>
+__device__ __forceinline__ f32x16_v mfma32(u32x4 a, u32x4 b, f32x16_v c) {
+  if constexpr (DT == DT_BF16)
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_v, a), __builtin_bit_cast(bf16x8_v, b),
+                                                   c, 0, 0, 0);
+  else
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8_v, a), __builtin_bit_cast(f16x8_v, b), c,
+                                                  0, 0, 0);
+}
+
+// two fp32 products to the activation type, one hardware pack-convert
+template <int DT>
+__device__ __forceinline__ uint32_t pack2(float lo, float hi) {
+  const f32x2_v v = {opaque(lo), opaque(hi)};
+  if constexpr (DT == DT_BF16)
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2_v));
+  else
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, f16x2_v));
+}
+
+// One K-step: load a later step into stage dst (CPW activation loads, then
+// this wave's codes), then multiply the step in stage rd with scale sc.
+template <int DT, int CPW, typename RS>
+__device__ __forceinline__ void dl_step(const uint8_t* __restrict__ rd, uint8_t* __restrict__ dst,
+                                        const float2* __restrict__ lut, RS xr, RS wr, const uint32_t (&xoff)[CPW],
+                                        uint32_t woff, int xsoff, int wsoff, int wave, int lane, float sc,
+                                        f32x16_v (&acc)[4]) {
+#pragma unroll
+  for (int j = 0; j < CPW; ++j)
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(xr, (lds_ptr_t)(dst + (wave * CPW + j) * CH), 16, xoff[j], xsoff, 0, 0);
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(wr, (lds_ptr_t)(dst + BSTAGE + wave * CH), 16, woff, wsoff, 0, 0);
+  const u32x4 codes = *reinterpret_cast<const u32x4*>(rd + BSTAGE + wave * CH + lane * 16);
+#pragma unroll
+  for (int kk = 0; kk < 4; ++kk) {
+    u32x4 bf[4];
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+      const int t = 32 * b + (lane & 31), sg = 4 * (lane >> 5) + kk;
+      bf[b] = *reinterpret_cast<const u32x4*>(rd + t * 128 + ((sg ^ ((t >> 1) & 7)) << 4));
+    }
+    const uint32_t wv = codes[kk];
+    float cv[8];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float2 pc = lut[(wv >> (8 * j)) & 0xffu];  // (high nibble's code, low nibble's)
+      cv[2 * j] = pc.x;
+      cv[2 * j + 1] = pc.y;
+    }
+    u32x4 af;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) af[e] = pack2<DT>(__fmul_rn(cv[2 * e], sc), __fmul_rn(cv[2 * e + 1], sc));
+#pragma unroll
+    for (int b = 0; b < 4; ++b) acc[b] = mfma32<DT>(af, bf[b], acc[b]);
+  }
+}
+
+// epilogue of one value (y already rounded): ep 1 adds R, ep 2 multiplies by
+// round(silu(R)); the result rounded
+template <int DT>
+__device__ __forceinline__ uint16_t dl_epi(float y, uint16_t r, int ep) {
+  float v = y;
+  if (ep == 1) v = __fadd_rn(Elem<DT>::load(r), y);
+  else if (ep == 2) v = __fmul_rn(Elem<DT>::load(Elem<DT>::store(silu_rn(Elem<DT>::load(r)))), y);
+  return Elem<DT>::store(v);
+}
+
+template <int DT, bool NESTED, int W>
+__global__ __launch_bounds__(64 * W) void nf4_gemm_dl_kernel(
+    const uint16_t* __restrict__ X, const uint8_t* __restrict__ Wt, const uint8_t* __restrict__ A8,
+    const float* __restrict__ AMAX, const float* __restrict__ CODE2, float offset, const float* __restrict__ LUT,
+    uint16_t* __restrict__ Y, const uint16_t* __restrict__ R, int epi, int M, int K, int N, int bs_shift,
+    int bs2_shift, float* __restrict__ YP) {
+  // the buffer-resource type exists in device code only
+#if defined(__HIP_DEVICE_COMPILE__)
+  constexpr int BM = 32 * W;
+  constexpr int STAGE = BSTAGE + W * CH;
+  static_assert(16 % W == 0, "activation loads split evenly over the waves");
+  constexpr int CPW = 16 / W;
+  // one LDS object per ring stage, indexed at compile time (the step body
+  // reads one and refills the other)
+  __shared__ __align__(16) uint8_t ring0[STAGE];
+  __shared__ __align__(16) uint8_t ring1[STAGE];
+  __shared__ float2 lut2_s[256];
+  __shared__ float code2_s[NESTED ? 256 : 1];
+  __shared__ uint8_t a8_s[NESTED ? BM * DL_MAX_STEPS : 1];
+  __shared__ float am_s[NESTED ? 1 : BM * DL_MAX_STEPS];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int m0 = blockIdx.x * BM, n0 = blockIdx.y * BN;
+  // split-K (gridDim.z > 1): workgroup z takes K-steps [z S, z S + S) and
+  // writes fp32 partial sums to YP[z][n][m]
+  const int nsteps = K / KT / gridDim.z, kbase = blockIdx.z * nsteps * KT;
+
+  for (int i = tid; i < 256; i += 64 * W) {
+    lut2_s[i] = make_float2(LUT[i >> 4], LUT[i & 15]);
+    if constexpr (NESTED) code2_s[i] = CODE2[i];
+  }
+  // the workgroup's scale bytes (nested) or scales (plain), row r at r * DL_MAX_STEPS
+  for (int i = tid; i < BM * nsteps; i += 64 * W) {
+    const int r = i / nsteps, j = i - r * nsteps;
+    const int row = min(m0 + r, M - 1);
+    const long long b = ((long long)row * K + kbase + j * KT) >> bs_shift;
+    if constexpr (NESTED) a8_s[r * DL_MAX_STEPS + j] = A8[b];
+    else am_s[r * DL_MAX_STEPS + j] = AMAX[b];
+  }
+  // this lane's weight row; nested: its second-level scale for the steps
+  // before jsw and from jsw on (a workgroup's K range crosses at most one
+  // second-level group: 64 steps of 64 codes < one group of >= 256 blocks)
+  const int rl = 32 * wave + (lane & 31);
+  const int arow = min(m0 + rl, M - 1);
+  float amax_lo = 0.0f, amax_hi = 0.0f;
+  int jsw = nsteps;
+  if constexpr (NESTED) {
+    const long long e0 = (long long)arow * K + kbase;
+    const long long g0 = (e0 >> bs_shift) >> bs2_shift;
+    amax_lo = AMAX[g0];
+    const long long enext = ((g0 + 1) << bs2_shift) << bs_shift;  // first element of the next group
+    jsw = (int)min((long long)nsteps, (enext - e0 + KT - 1) / KT);
+    amax_hi = jsw < nsteps ? AMAX[g0 + 1] : amax_lo;
+  }
+
+  const __amdgpu_buffer_rsrc_t xr =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(X), (short)0, (int)((size_t)N * K * 2), 0x00020000);
+  const __amdgpu_buffer_rsrc_t wr =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(Wt), (short)0, (int)((size_t)M * K / 2), 0x00020000);
+  // activation load j of this wave: rows 8 q .. 8 q + 7 (q = wave CPW + j),
+  // lane l row 8 q + l / 8 and LDS slot l % 8, i.e. segment (l % 8) ^ ((t >> 1) & 7)
+  uint32_t xoff[CPW];
+#pragma unroll
+  for (int j = 0; j < CPW; ++j) {
+    const int t = 8 * (wave * CPW + j) + (lane >> 3);
+    const int sg = (lane & 7) ^ ((t >> 1) & 7);
+    xoff[j] = (uint32_t)min(n0 + t, N - 1) * (uint32_t)K * 2u + (uint32_t)sg * 16u;
+  }
+  // this wave's code load: lane l row l % 32, bytes 16 (l / 32) .. of the step's 32
+  const uint32_t woff = (uint32_t)arow * (uint32_t)(K / 2) + 16u * (lane >> 5);
+
+  f32x16_v acc[4];
+#pragma unroll
+  for (int b = 0; b < 4; ++b)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[b][r] = 0.0f;
+
+  __syncthreads();  // tables
+  {
+    const int k0 = kbase;
+#pragma unroll
+    for (int j = 0; j < CPW; ++j)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(xr, (lds_ptr_t)(ring0 + (wave * CPW + j) * CH), 16, xoff[j], k0 * 2, 0,
+                                               0);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(wr, (lds_ptr_t)(ring0 + BSTAGE + wave * CH), 16, woff, k0 / 2, 0, 0);
+  }
+  // step s (stage s % 2): its loads were issued one step before
+  auto one = [&](int s, uint8_t* rd, uint8_t* dst) {
+    TTSP_VMWAIT(0);
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    const int k0n = kbase + min(s + 1, nsteps - 1) * KT;  // the last step reloads itself, unread
+    float sc;
+    if constexpr (NESTED) {
+      const float am = s < jsw ? amax_lo : amax_hi;
+      sc = __fadd_rn(__fmul_rn(code2_s[a8_s[rl * DL_MAX_STEPS + s]], am), offset);
+    } else {
+      sc = am_s[rl * DL_MAX_STEPS + s];
+    }
+    dl_step<DT, CPW>(rd, dst, lut2_s, xr, wr, xoff, woff, k0n * 2, k0n / 2, wave, lane, sc, acc);
+  };
+  int s0 = 0;
+  for (; s0 + 2 <= nsteps; s0 += 2) {  // no branch inside: the compiler's own wait counts stay exact
+    one(s0, ring0, ring1);
+    one(s0 + 1, ring1, ring0);
+  }
+  if (s0 < nsteps) one(s0, ring0, ring1);
+  TTSP_VMWAIT(0);
+
+  // accumulator r of lane l is (row 8 (r / 4) + 4 (l / 32) + r % 4, column
+  // l % 32): 4 consecutive weight rows m of one activation row n per lane
+  const bool v4 = (M & 3) == 0;
+  if (YP) {
+    float* yp = YP + (size_t)blockIdx.z * N * M;
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+      const int n = n0 + 32 * b + (lane & 31);
+      if (n >= N) continue;
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int m = m0 + 32 * wave + 8 * g + 4 * (lane >> 5);
+        if (v4 && m + 4 <= M) {
+          *reinterpret_cast<float4*>(yp + (size_t)n * M + m) =
+              make_float4(acc[b][4 * g], acc[b][4 * g + 1], acc[b][4 * g + 2], acc[b][4 * g + 3]);
+        } else {
+          for (int c = 0; c < 4 && m + c < M; ++c) yp[(size_t)n * M + m + c] = acc[b][4 * g + c];
+        }
+      }
+    }
+    return;
+  }
+  const int ep = epi & 3;
+  const bool vec = v4 && (epi & 8);  // Y (and R) 8-byte aligned (host)
+#pragma unroll
+  for (int b = 0; b < 4; ++b) {
+    const int n = n0 + 32 * b + (lane & 31);
+    if (n >= N) continue;
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const int m = m0 + 32 * wave + 8 * g + 4 * (lane >> 5);
+      const size_t o = (size_t)n * M + m;
+      if (vec && m + 4 <= M) {
+        uint32_t rw[2] = {0u, 0u};
+        if (ep) {
+          const uint2 rv = *reinterpret_cast<const uint2*>(R + o);
+          rw[0] = rv.x, rw[1] = rv.y;
+        }
+        uint32_t ow[2];
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+          const uint16_t lo = dl_epi<DT>(Elem<DT>::load(Elem<DT>::store(acc[b][4 * g + 2 * q])), (uint16_t)rw[q], ep);
+          const uint16_t hi =
+              dl_epi<DT>(Elem<DT>::load(Elem<DT>::store(acc[b][4 * g + 2 * q + 1])), (uint16_t)(rw[q] >> 16), ep);
+          ow[q] = (uint32_t)lo | ((uint32_t)hi << 16);
+        }
+        *reinterpret_cast<uint2*>(Y + o) = make_uint2(ow[0], ow[1]);
+      } else {
+        for (int c = 0; c < 4 && m + c < M; ++c)
+          Y[o + c] = dl_epi<DT>(Elem<DT>::load(Elem<DT>::store(acc[b][4 * g + c])), ep ? R[o + c] : (uint16_t)0, ep);
+      }
+    }
+  }
+#endif
+}
+
+template <int DT, int W>
+int launch_dl(const void* X, const uint8_t* Wt, const uint8_t* A8, const float* AMAX, const float* CODE2,
+              float offset, const float* LUT, void* Y, const void* R, int epi, int M, int K, int N, int bs_shift,
+              int bs2_shift, int splits, float* YP, hipStream_t st) {
+  constexpr int BM = 32 * W;
+  const dim3 grid((M + BM - 1) / BM, (N + BN - 1) / BN, splits);
+  if (A8)
+    hipLaunchKernelGGL((nf4_gemm_dl_kernel<DT, true, W>), grid, dim3(64 * W), 0, st, (const uint16_t*)X, Wt, A8,
+                       AMAX, CODE2, offset, LUT, (uint16_t*)Y, (const uint16_t*)R, epi, M, K, N, bs_shift,
+                       bs2_shift, YP);
+  else
+    hipLaunchKernelGGL((nf4_gemm_dl_kernel<DT, false, W>), grid, dim3(64 * W), 0, st, (const uint16_t*)X, Wt, A8,
+                       AMAX, CODE2, offset, LUT, (uint16_t*)Y, (const uint16_t*)R, epi, M, K, N, bs_shift,
+                       bs2_shift, YP);
+  TTSP_RETURN_LAUNCH();
+}
+
+}  // namespace
+
+// Whether the kernel takes this launch: whole K-steps per split, at most
+// DL_MAX_STEPS of them, byte offsets of X and W below 2^31.
+bool gemm_dl_fits(int M, int K, int N, int splits) {
+  if (splits < 1 || K % KT || (K / KT) % splits || K / KT / splits > DL_MAX_STEPS) return false;
+  return (long long)N * K * 2 < (1ll << 31) && (long long)M * K / 2 < (1ll << 31);
+}
+
+// waves: 2 (64 weight rows a workgroup) or 4 (128). splits > 1 writes fp32
+// partials to YP (the caller reduces them and applies the epilogue); else
+// epi as nf4_gemm_kernel's (bit 2: vectorised output; 8-byte alignment of Y
+// and R is checked here).
+int gemm_dl(const void* X, int dt, const uint8_t* W, const uint8_t* A8, const float* AMAX, const float* CODE2,
+            float offset, const float* LUT, void* Y, const void* R, int epi, int M, int K, int N, int bs_shift,
+            int bs2_shift, int waves, int splits, float* YP, hipStream_t st) {
+  if (!gemm_dl_fits(M, K, N, splits) || (splits > 1 && !YP)) return (int)hipErrorInvalidValue;
+  const bool al8 = (uintptr_t)Y % 8 == 0 && (!(epi & 3) || (uintptr_t)R % 8 == 0);
+  const int e = (epi & 3) | (al8 ? 8 : 0);
+  float* yp = splits > 1 ? YP : nullptr;
+  if (dt == DT_BF16) {
+    if (waves == 2)
+      return launch_dl<DT_BF16, 2>(X, W, A8, AMAX, CODE2, offset, LUT, Y, R, e, M, K, N, bs_shift, bs2_shift, splits,
+                                   yp, st);
+    return launch_dl<DT_BF16, 4>(X, W, A8, AMAX, CODE2, offset, LUT, Y, R, e, M, K, N, bs_shift, bs2_shift, splits,
+                                 yp, st);
+  }
+  if (dt == DT_F16) {
+    if (waves == 2)
+      return launch_dl<DT_F16, 2>(X, W, A8, AMAX, CODE2, offset, LUT, Y, R, e, M, K, N, bs_shift, bs2_shift, splits,
+                                  yp, st);
+    return launch_dl<DT_F16, 4>(X, W, A8, AMAX, CODE2, offset, LUT, Y, R, e, M, K, N, bs_shift, bs2_shift, splits,
+                                yp, st);
+  }
+  return (int)hipErrorInvalidValue;
+}
+
+}  // namespace ttsp
