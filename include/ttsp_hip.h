@@ -34,7 +34,8 @@ enum { TTSP_F16 = 0, TTSP_BF16 = 1, TTSP_F32 = 2 };
 enum { TTSP_EPI_NONE = 0, TTSP_EPI_RESIDUAL = 1, TTSP_EPI_SILU_GATE = 2 };
 
 /* Y[N][M] = epi(X[N][K] . dequant(W)^T). N == 1 runs the HBM-bound GEMV, N > 1
- * the LDS-staged MFMA GEMM. epi 1: Y = round(R + round(XW)); epi 2:
+ * the MFMA GEMM (LDS-staged dequantisation; from 256 to 512 rows on large
+ * shapes, direct-to-LDS operand streams). epi 1: Y = round(R + round(XW)); epi 2:
  * Y = round(round(silu(R)) * round(XW)); R has Y's shape. Requires K % 128 == 0,
  * K % blocksize == 0, blocksize a power of two >= 64, blocksize2 a power of two
  * (nested only), 16-byte aligned X and W. A8 == NULL selects plain scales.
@@ -47,7 +48,9 @@ int ttsp_nf4_gemm(const void* X, int x_dtype, const uint8_t* W, const uint8_t* A
 
 /* How many K splits ttsp_nf4_gemm_split uses for this shape (1: none, then no
  * workspace is needed). The split is chosen so the output tiles times the
- * splits give every CU a workgroup. Host-only. Replaces: the reference's
+ * splits give every CU a workgroup; from 256 to 512 rows on large or long-K
+ * shapes it is the direct-to-LDS kernel's (1, 2 or 4, at most 64 K-steps of
+ * 64 codes per split). Host-only. Replaces: the reference's
  * slicing of the rows into MAX_N = 32 launches (app/engine/nf4gemv.py:460-477),
  * which it does instead of splitting K. */
 int ttsp_nf4_gemm_splits(int M, int K, int N);
