@@ -101,6 +101,62 @@ def test_matmul_random_shapes_within_bar(nf4, orc, case):
     assert splits  # (recorded for the failure message of a future plan change)
 
 
+def _dl_shapes(n: int, seed: int, splits: int):
+    """(M, K, bs, nested, dtype, rows) the launch plan gives the direct-to-LDS
+    kernel with `splits` K splits: 4 where K has 64 or more 64-code steps and
+    there are at least 75 64 x 128 tiles; with fewer steps unsplit from 512
+    tiles and 2 splits from 300."""
+    rng = np.random.default_rng(seed)
+    out = []
+    for _ in range(n):
+        rows = int(rng.integers(256, 513))
+        nt = -(-rows // 128)
+        if splits == 4:
+            K = 512 * int(rng.integers(8, 33))  # 64 to 256 steps, a multiple of 8
+            M = int(rng.integers(64 * (-(-75 // nt)), 9001))
+        elif splits == 1:
+            K = 128 * int(rng.integers(1, 32))  # fewer than 64 steps
+            M = int(rng.integers(64 * (-(-512 // nt)), 64 * (-(-512 // nt)) + 4001))
+        else:
+            K = 256 * int(rng.integers(1, 16))  # steps a multiple of 4, fewer than 64
+            lo, hi = 64 * (-(-300 // nt)), 64 * (512 // nt) - 1
+            if lo > hi:  # 256 rows: 2 row tiles need 150-255 weight tiles
+                rows, nt = 512, 4
+                lo, hi = 64 * 75, 64 * 128 - 1
+            M = int(rng.integers(lo, hi + 1))
+        bs = int(rng.choice([64, 128, 256]))
+        if K % bs:
+            bs = 64
+        out.append((M, K, bs, bool(rng.integers(0, 2)), DTYPES[int(rng.integers(0, 2))], rows))
+    return out
+
+
+@pytest.mark.parametrize("splits", [1, 2, 4])
+def test_direct_lds_gemm_random_shapes_within_bar(nf4, orc, splits):
+    """Six random shapes per launch form of the direct-to-LDS kernel
+    (unsplit, 2 and 4 K-splits): ragged weight and activation rows, block
+    sizes 64 to 256, plain and nested scales (whose second-level group may
+    change inside a workgroup's K range), bf16 and fp16; a sample of rows
+    against the oracle's fp64 product within the bar."""
+    from ttspipe_amd import _lib
+    from tests.test_abi import _dl_split
+
+    for i, (M, K, bs, nested, dtype, rows) in enumerate(_dl_shapes(6, 2700 + splits, splits)):
+        where = f"M={M} K={K} rows={rows} bs={bs} nested={nested} {dtype}"
+        assert _dl_split(M, K, rows) == splits, where
+        assert _lib.load().ttsp_nf4_gemm_splits(M, K, rows) == splits, where
+        layer = random_layer(M, K, nested, seed=splits * 100 + i + 7, bs=bs)
+        lin = to_linear(layer, dtype)
+        xb = randn_bits(rows * K, dtype, seed=rows + i + 11)
+        y = lin(from_bits(xb, dtype).view(rows, K))
+        dt = dt_code(dtype)
+        sample = np.unique(np.concatenate([np.linspace(0, rows - 1, 5).astype(int), [rows - 1]]))
+        ref = orc.nf4_gemm_ref(xb.reshape(rows, K)[sample], dt, **oracle_args(layer), M=M, K=K, N=sample.size,
+                               bs=bs, bs2=layer["bs2"] or 256)
+        got = o.to_f32(bits(y), dt).reshape(rows, M)[sample]
+        assert beyond_rounding_error(got, ref, dt) < 2e-3, where
+
+
 @pytest.mark.parametrize("case", range(6))
 def test_few_rows_random_shapes_within_bar(nf4, orc, case):
     """2 to 64 rows (the few-row kernel wherever K allows it) at random layer
