@@ -557,7 +557,8 @@ def main() -> int:
                     help="with --only kernel/c1: one launch per weight copy, no graph (counter runs)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
-        print("bench.py measures one GPU: this path has no multi-GPU mode (see DESIGN.md on sharding)",
+        print("bench.py measures one GPU: this path has no multi-GPU mode (the value is one GPU's "
+              "throughput; sharded, each GPU would stream its own share of every weight's rows)",
               file=sys.stderr)
         return 2
 
