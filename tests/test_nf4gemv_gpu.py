@@ -362,6 +362,29 @@ def test_direct_lds_gemm_launches(nf4, orc, shape, rows, splits, nested, dtype):
     assert beyond_rounding_error(got, ref, dt) < 2e-3
 
 
+@pytest.mark.parametrize("shape,rows,bs2", [((9728, 2560), 512, 16), ((2560, 4096), 256, 16),
+                                            ((6144, 2560), 512, 32)])
+def test_direct_lds_gemm_small_second_level_groups(nf4, orc, shape, rows, bs2):
+    """Nested scales with second-level groups of 16 or 32 blocks (1,024 or
+    2,048 codes) at launches the plan gives the direct-to-LDS kernel: where a
+    workgroup's K range (2,560 codes unsplit) could cross two group
+    boundaries the launch falls back to the 64 x 128 kernel; where it spans
+    at most one (1,024 codes a split for 16-block groups, 1,280 for 32) the
+    kernel switches the group's absmax mid-range. Against the oracle."""
+    M, K = shape
+    dtype = torch.bfloat16
+    layer = random_layer(M, K, True, seed=M + bs2, bs2=bs2)
+    lin = to_linear(layer, dtype)
+    xb = randn_bits(rows * K, dtype, seed=rows + bs2)
+    y = lin(from_bits(xb, dtype).view(rows, K))
+    dt = dt_code(dtype)
+    sample = np.concatenate([np.arange(0, rows, 37), [rows - 1]])
+    ref = orc.nf4_gemm_ref(xb.reshape(rows, K)[sample], dt, **oracle_args(layer), M=M, K=K, N=sample.size, bs=64,
+                           bs2=bs2)
+    got = o.to_f32(bits(y), dt).reshape(rows, M)[sample]
+    assert beyond_rounding_error(got, ref, dt) < 2e-3
+
+
 # ------------------------------------------------------------ fused forms (one launch)
 
 FUSED_SHAPES = [(6144, 2560), (9728, 2560), (2560, 9728), (1536, 1024), (3072, 1024), (1544, 2560), (64, 128)]

@@ -478,7 +478,12 @@ int gemm_mfma(const void* X, int dt, const uint8_t* W, const uint8_t* A8, const 
                                                  bs_shift, bs2_shift, yp, splits, st))
   // 8 waves for the 64 x 128 tiles (two a SIMD: one wave's dequantisation
   // runs while the other's matrix products do), 4 for 64 x 64
-  const int shape = plan.shape;
+  // The direct-to-LDS kernel resolves nested scales with at most one
+  // second-level group boundary inside a workgroup's K range (true for
+  // bitsandbytes' blocksize2 of 256); smaller groups take the 64 x 128
+  // kernel with the same split.
+  int shape = plan.shape;
+  if (shape == 4 && A8 && (long long)(K / splits) > (1LL << (bs_shift + bs2_shift))) shape = 2;
   if (shape == 4) {
     if (int rc = gemm_dl(X, dt, W, A8, AMAX, CODE2, offset, LUT, Y, R, epi, M, K, N, bs_shift, bs2_shift, 2,
                          splits, yp, st))
