@@ -18,9 +18,9 @@
 //     pairs, fp32 products, one pack-convert per pair).
 // Inside a step lane half h carries codes 32h .. 32h + 31 and k-slice kk the
 // MFMA's 8 of them; A and B agree, so each output sums the same products.
-// The scales of the workgroup's K range are staged once: nested a8 bytes per
-// (row, step) and per lane its row's amax pair, or plain fp32 absmax per
-// (row, step). A workgroup takes at most DL_MAX_STEPS K-steps.
+// Nested scales of the workgroup's K range are staged once (a8 bytes per
+// (row, step), per lane its row's amax pair); plain fp32 absmax arrives with
+// each step's loads. A workgroup takes at most DL_MAX_STEPS K-steps.
 //
 // The barrier of a step is a bare s_barrier: __syncthreads' release fence
 // would also wait for the ring loads still in flight. Each wave waits for its
@@ -72,17 +72,24 @@ __device__ __forceinline__ uint32_t pack2(float lo, float hi) {
     return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, f16x2_v));
 }
 
-// One K-step: load a later step into stage dst (CPW activation loads, then
-// this wave's codes), then multiply the step in stage rd with scale sc.
-template <int DT, int CPW, typename RS>
+// One K-step: load a later step into stage dst (CPW activation loads, this
+// wave's codes, and with plain scales its rows' absmax: one dword a
+// lane, lane l row l % 32), then multiply the step in stage rd with scale sc
+// (plain: read from the stage).
+template <int DT, int W, int CPW, bool PLAIN, typename RS>
 __device__ __forceinline__ void dl_step(const uint8_t* __restrict__ rd, uint8_t* __restrict__ dst,
-                                        const float2* __restrict__ lut, RS xr, RS wr, const uint32_t (&xoff)[CPW],
-                                        uint32_t woff, int xsoff, int wsoff, int wave, int lane, float sc,
-                                        f32x16_v (&acc)[4]) {
+                                        const float2* __restrict__ lut, RS xr, RS wr, RS ar,
+                                        const uint32_t (&xoff)[CPW], uint32_t woff, uint32_t aoff, int xsoff,
+                                        int wsoff, int asoff, int wave, int lane, float sc, f32x16_v (&acc)[4]) {
+  constexpr int SOFF = BSTAGE + W * CH;  // the plain scales' 256 bytes a wave
 #pragma unroll
   for (int j = 0; j < CPW; ++j)
     __builtin_amdgcn_raw_ptr_buffer_load_lds(xr, (lds_ptr_t)(dst + (wave * CPW + j) * CH), 16, xoff[j], xsoff, 0, 0);
   __builtin_amdgcn_raw_ptr_buffer_load_lds(wr, (lds_ptr_t)(dst + BSTAGE + wave * CH), 16, woff, wsoff, 0, 0);
+  if constexpr (PLAIN) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(ar, (lds_ptr_t)(dst + SOFF + wave * 256), 4, aoff, asoff, 0, 0);
+    sc = *reinterpret_cast<const float*>(rd + SOFF + wave * 256 + 4 * (lane & 31));
+  }
   const u32x4 codes = *reinterpret_cast<const u32x4*>(rd + BSTAGE + wave * CH + lane * 16);
 #pragma unroll
   for (int kk = 0; kk < 4; ++kk) {
@@ -127,7 +134,7 @@ __global__ __launch_bounds__(64 * W) void nf4_gemm_dl_kernel(
   // the buffer-resource type exists in device code only
 #if defined(__HIP_DEVICE_COMPILE__)
   constexpr int BM = 32 * W;
-  constexpr int STAGE = BSTAGE + W * CH;
+  constexpr int STAGE = BSTAGE + W * CH + (NESTED ? 0 : W * 256);
   static_assert(16 % W == 0, "activation loads split evenly over the waves");
   constexpr int CPW = 16 / W;
   // one LDS object per ring stage, indexed at compile time (the step body
@@ -137,7 +144,6 @@ __global__ __launch_bounds__(64 * W) void nf4_gemm_dl_kernel(
   __shared__ float2 lut2_s[256];
   __shared__ float code2_s[NESTED ? 256 : 1];
   __shared__ uint8_t a8_s[NESTED ? BM * DL_MAX_STEPS : 1];
-  __shared__ float am_s[NESTED ? 1 : BM * DL_MAX_STEPS];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int m0 = blockIdx.x * BM, n0 = blockIdx.y * BN;
@@ -149,13 +155,23 @@ __global__ __launch_bounds__(64 * W) void nf4_gemm_dl_kernel(
     lut2_s[i] = make_float2(LUT[i >> 4], LUT[i & 15]);
     if constexpr (NESTED) code2_s[i] = CODE2[i];
   }
-  // the workgroup's scale bytes (nested) or scales (plain), row r at r * DL_MAX_STEPS
-  for (int i = tid; i < BM * nsteps; i += 64 * W) {
-    const int r = i / nsteps, j = i - r * nsteps;
-    const int row = min(m0 + r, M - 1);
-    const long long b = ((long long)row * K + kbase + j * KT) >> bs_shift;
-    if constexpr (NESTED) a8_s[r * DL_MAX_STEPS + j] = A8[b];
-    else am_s[r * DL_MAX_STEPS + j] = AMAX[b];
+  // nested: the workgroup's scale bytes, entry r * DL_MAX_STEPS + j for row
+  // r, step j; lane l takes step l (steps past the range repeat the last,
+  // unread) of rows wave, wave + W, ...; all its loads are issued before the
+  // first is stored (a loop that stored each before loading the next paid a
+  // memory round trip per entry). Plain scales travel with each step's loads.
+  if constexpr (NESTED) {
+    static_assert(DL_MAX_STEPS == 64, "one step per lane");
+    constexpr int PER = BM / W;  // rows per wave
+    const int j = min(lane, nsteps - 1);
+    uint32_t v[PER];
+#pragma unroll
+    for (int u = 0; u < PER; ++u) {
+      const int row = min(m0 + wave + u * W, M - 1);
+      v[u] = A8[((long long)row * K + kbase + j * KT) >> bs_shift];
+    }
+#pragma unroll
+    for (int u = 0; u < PER; ++u) a8_s[(wave + u * W) * DL_MAX_STEPS + lane] = (uint8_t)v[u];
   }
   // this lane's weight row; nested: its second-level scale for the steps
   // before jsw and from jsw on (a workgroup's K range crosses at most one
@@ -188,6 +204,11 @@ __global__ __launch_bounds__(64 * W) void nf4_gemm_dl_kernel(
   }
   // this wave's code load: lane l row l % 32, bytes 16 (l / 32) .. of the step's 32
   const uint32_t woff = (uint32_t)arow * (uint32_t)(K / 2) + 16u * (lane >> 5);
+  // plain: lane l's absmax of row l % 32 (block (row K + k) >> bs_shift: the
+  // row's part per lane, the step's part uniform, both whole blocks)
+  const __amdgpu_buffer_rsrc_t ar = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<float*>(AMAX), (short)0, NESTED ? 0 : (int)(((size_t)M * K >> bs_shift) * 4), 0x00020000);
+  const uint32_t aoff = (uint32_t)(((long long)arow * K) >> bs_shift) * 4u;
 
   f32x16_v acc[4];
 #pragma unroll
@@ -203,6 +224,9 @@ __global__ __launch_bounds__(64 * W) void nf4_gemm_dl_kernel(
       __builtin_amdgcn_raw_ptr_buffer_load_lds(xr, (lds_ptr_t)(ring0 + (wave * CPW + j) * CH), 16, xoff[j], k0 * 2, 0,
                                                0);
     __builtin_amdgcn_raw_ptr_buffer_load_lds(wr, (lds_ptr_t)(ring0 + BSTAGE + wave * CH), 16, woff, k0 / 2, 0, 0);
+    if constexpr (!NESTED)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(ar, (lds_ptr_t)(ring0 + BSTAGE + W * CH + wave * 256), 4, aoff,
+                                               (k0 >> bs_shift) * 4, 0, 0);
   }
   // step s (stage s % 2): its loads were issued one step before
   auto one = [&](int s, uint8_t* rd, uint8_t* dst) {
@@ -211,14 +235,13 @@ __global__ __launch_bounds__(64 * W) void nf4_gemm_dl_kernel(
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
     const int k0n = kbase + min(s + 1, nsteps - 1) * KT;  // the last step reloads itself, unread
-    float sc;
+    float sc = 0.0f;  // plain: read inside the step
     if constexpr (NESTED) {
       const float am = s < jsw ? amax_lo : amax_hi;
       sc = __fadd_rn(__fmul_rn(code2_s[a8_s[rl * DL_MAX_STEPS + s]], am), offset);
-    } else {
-      sc = am_s[rl * DL_MAX_STEPS + s];
     }
-    dl_step<DT, CPW>(rd, dst, lut2_s, xr, wr, xoff, woff, k0n * 2, k0n / 2, wave, lane, sc, acc);
+    dl_step<DT, W, CPW, !NESTED>(rd, dst, lut2_s, xr, wr, ar, xoff, woff, aoff, k0n * 2, k0n / 2,
+                                 (k0n >> bs_shift) * 4, wave, lane, sc, acc);
   };
   int s0 = 0;
   for (; s0 + 2 <= nsteps; s0 += 2) {  // no branch inside: the compiler's own wait counts stay exact
