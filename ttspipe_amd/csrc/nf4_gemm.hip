@@ -421,11 +421,12 @@ int gemm_dl(const void* X, int dt, const uint8_t* W, const uint8_t* A8, const fl
 // 256 to 512 rows: the direct-to-LDS kernel (nf4_gemm_dl.hip, shape 4, 64 x
 // 128 tiles of 2 waves) with 4 K-splits where K has 64 or more steps and
 // there are at least 75 tiles; with fewer steps unsplit from 512 tiles and
-// with 2 splits from 300. Measured at 512 rows (bf16, nested scales): w1 /
-// w3 9728 x 2560 70.7 -> 52.0 us, w2 2560 x 9728 79.5 -> 58.2, wo 2560 x 4096
-// 40.3 -> 31.8, wqkv 6144 x 2560 45.7 -> 41.0; at 256 rows w1 43.8 -> 37.7,
-// w2 49.9 -> 45.7. The 64 x 128 kernel stays ahead at 128 rows, at
-// 4096 x 2560 and on the 1024-wide shapes (by 3-15 %).
+// with 2 splits from 300. Measured against the 64 x 128 kernel at its best
+// split, 512 rows (bf16, nested scales): w1 / w3 9728 x 2560 71.5 -> 48.4 us,
+// w2 2560 x 9728 70.1 -> 48.5, wo 2560 x 4096 40.7 -> 30.1, wqkv 6144 x 2560
+// 46.6 -> 36.5; at 256 rows w1 45.8 -> 34.0, w2 48.0 -> 39.8. The 64 x 128
+// kernel stays ahead or ties at 128 rows, at 4096 x 2560 and on the
+// 1024-wide shapes.
 constexpr int DL_MIN_N = 256, DL_MAX_N = 512;
 static bool dl_plan(int M, int K, int N, GemmPlan* p) {
   if (N < DL_MIN_N || N > DL_MAX_N) return false;
