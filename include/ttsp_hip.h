@@ -33,9 +33,10 @@ extern "C" {
 enum { TTSP_F16 = 0, TTSP_BF16 = 1, TTSP_F32 = 2 };
 enum { TTSP_EPI_NONE = 0, TTSP_EPI_RESIDUAL = 1, TTSP_EPI_SILU_GATE = 2 };
 
-/* Y[N][M] = epi(X[N][K] . dequant(W)^T). N == 1 runs the HBM-bound GEMV, N > 1
- * the MFMA GEMM (LDS-staged dequantisation; from 256 to 512 rows on large
- * shapes, direct-to-LDS operand streams). epi 1: Y = round(R + round(XW)); epi 2:
+/* Y[N][M] = epi(X[N][K] . dequant(W)^T). N == 1 runs the HBM-bound GEMV (rows
+ * of up to 32768 codes; a longer row takes the tiled kernel), N > 1 the MFMA
+ * GEMM (LDS-staged dequantisation; from 256 to 512 rows on large shapes,
+ * direct-to-LDS operand streams). epi 1: Y = round(R + round(XW)); epi 2:
  * Y = round(round(silu(R)) * round(XW)); R has Y's shape. Requires K % 128 == 0,
  * K % blocksize == 0, blocksize a power of two >= 64, blocksize2 a power of two
  * (nested only), 16-byte aligned X and W. A8 == NULL selects plain scales.
@@ -65,7 +66,8 @@ int ttsp_nf4_gemm_split(const void* X, int x_dtype, const uint8_t* W, const uint
                         void* Y, const void* R, int epi, int M, int K, int N, int blocksize,
                         int blocksize2, float* work, int splits, void* stream);
 
-/* The batch-1 matmuls of a decode block in one launch each (K <= 10240):
+/* The batch-1 matmuls of a decode block in one launch each (K <= 32768,
+ * K <= 4096 with NORM_W; ttsp_gemv_shape says whether a shape fits):
  *   W3 == NULL: Y = epi(n(X) . dequant(W1)^T), epi as ttsp_nf4_gemm;
  *   W3 != NULL: Y = round(round(silu(round(n(X) . W1^T))) * round(n(X) . W3^T)),
  *               W1 and W3 of one shape [M, K] (the SwiGLU gate, epi must be 0);
@@ -92,7 +94,8 @@ int ttsp_nf4_dequant(const uint8_t* W, const uint8_t* A8, const float* AMAX, con
 
 /* Launch shape the N == 1 GEMV uses for [M, K]: J 64-dword chunks per lane,
  * K split over KS waves, RPW rows per wave. The arithmetic order depends on KS
- * only. Host-only query; no GPU needed. Replaces: _config (app/engine/
+ * only. Returns nonzero (and zeros) when the GEMV cannot hold the rows
+ * (K > 32768). Host-only query; no GPU needed. Replaces: _config (app/engine/
  * nf4gemv.py:234-246). */
 int ttsp_gemv_shape(int M, int K, int* J, int* KS, int* RPW);
 

@@ -256,6 +256,23 @@ def test_dualar_specs_and_byte_account():
     assert b1 - b0 == cfg.n_layer * cfg.n_local_heads * cfg.head_dim * 2 * 2  # one more K and V row
 
 
+def test_decode_longer_than_the_cache_is_refused_on_the_host():
+    """Frame i writes slow position prefill_len + i: the benchmark model holds
+    2304 - 2048 = 256 frames, and one more is a ValueError before any launch
+    (the kernels would clamp the position instead of failing)."""
+    from ttspipe_amd import dualar
+
+    cfg = dualar.DualARConfig()
+    assert dualar.max_frames(cfg) == 256
+    dualar.check_frames(cfg, 256)
+    dualar.check_frames(cfg, 1)
+    for bad in (257, 512, 0, -1):
+        with pytest.raises(ValueError):
+            dualar.check_frames(cfg, bad)
+    small = dualar.SMALL
+    assert dualar.max_frames(small) == small.max_seq_len - small.prefill_len == 256
+
+
 def test_dualar_oracle_decode_is_deterministic_and_in_range(orc):
     """The reduced model through the CPU restatement: same frames twice, ids in range."""
     from oracle.dualar_oracle import OracleDualAR

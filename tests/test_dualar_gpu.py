@@ -192,17 +192,50 @@ def test_frame_advance_equals_the_torch_bookkeeping():
         assert torch.equal(frow[0].view(torch.int16), freqs[min(298 + f, 299)].view(torch.int16))
 
 
-def test_reset_to_a_longer_history_drops_the_captured_frame(small):
+@pytest.fixture(scope="module")
+def roomy():
+    """The reduced model with a cache that holds more frames than the
+    256-row history the model starts with."""
+    import dataclasses
+
+    from ttspipe_amd.dualar import SMALL, SyntheticDualAR
+
+    model = SyntheticDualAR(dataclasses.replace(SMALL, max_seq_len=SMALL.prefill_len + 300))
+    yield model
+    del model
+    torch.cuda.empty_cache()
+
+
+def test_reset_to_a_longer_history_drops_the_captured_frame(roomy):
     """A captured frame writes into the history it was captured with: a reset
     that has to allocate a longer history drops the graph (it is captured
     again on the next graphed decode) instead of leaving it pointing at freed
     memory."""
-    small.capture()
-    assert small.graph is not None
-    small.reset(small.history.shape[0] + 8)
-    assert small.graph is None
-    small.decode(4)
-    assert small.graph is not None
+    roomy.reset(4)
+    roomy.capture()
+    assert roomy.graph is not None
+    roomy.reset(roomy.history.shape[0] + 8)
+    assert roomy.graph is None
+    roomy.decode(4)
+    assert roomy.graph is not None
+
+
+def test_graphed_decode_longer_than_the_history_equals_eager(roomy):
+    """decode(n) with n above the history's rows, after a frame was captured
+    for the shorter history: the history grows, the frame is captured again,
+    and every frame equals the eager decode's."""
+    from ttspipe_amd.dualar import max_frames
+
+    roomy.decode(4)  # a captured frame for the current history
+    n = roomy.history.shape[0] + 8
+    assert n <= max_frames(roomy.cfg)
+    graphed = roomy.decode(n, graphed=True)
+    eager = roomy.decode(n, graphed=False)
+    assert graphed.shape == (n, roomy.cfg.n_tokens)
+    diff = np.flatnonzero((graphed != eager).any(axis=1))
+    assert diff.size == 0, f"first differing frame {diff[0]}: graphed {graphed[diff[0]]} eager {eager[diff[0]]}"
+    with pytest.raises(ValueError):
+        roomy.decode(max_frames(roomy.cfg) + 1)
 
 
 def _random_config(rng, seed):

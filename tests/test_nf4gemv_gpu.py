@@ -260,6 +260,59 @@ def test_few_rows_over_a_long_row(nf4, orc, rows):
     assert beyond_rounding_error(o.to_f32(bits(y), o.DT_BF16), ref.reshape(-1), o.DT_BF16) < 2e-3
 
 
+@pytest.mark.parametrize("K", [12416, 16384, 32768])
+@pytest.mark.parametrize("nested", [True, False])
+def test_one_row_over_a_long_row(nf4, orc, K, nested):
+    """One activation row past 12288 codes (the reference serves any K with
+    K % 128 == 0, nf4gemv.py:346-347): the GEMV stages the rest of x after
+    requesting its weight rows, bit for bit against the oracle - the plain
+    form, the residual epilogue and the SwiGLU pair."""
+    M, dtype = 200, torch.bfloat16
+    dt = dt_code(dtype)
+    assert nf4.gemv_fits(M, K)
+    J, KS, _ = gemv_shape(M, K)
+    l1 = random_layer(M, K, nested, seed=K + nested)
+    l3 = random_layer(M, K, nested, seed=K + nested + 2)
+    w1, w3 = to_linear(l1, dtype), to_linear(l3, dtype)
+    assert nf4.prepare(w1) and nf4.prepare(w3)
+    xb = randn_bits(K, dtype, seed=K + 5, scale=0.5)
+    rb = randn_bits(M, dtype, seed=K + 6)
+    x = from_bits(xb, dtype).view(1, 1, K)
+    kw = dict(M=M, K=K, bs=64, KS=KS, J=J, bs2=l1["bs2"] or 256)
+    g1 = orc.gemv_emul(xb, dt, **oracle_args(l1), **kw)
+    y = nf4.matmul(w1, x)
+    assert np.array_equal(bits(y), g1), f"K={K} KS={KS} J={J}: {first_mismatch(bits(y), g1)}"
+    ref = orc.nf4_gemm_ref(xb, dt, **oracle_args(l1), M=M, K=K, N=1, bs=64, bs2=l1["bs2"] or 256)
+    assert beyond_rounding_error(o.to_f32(bits(y), dt), ref.reshape(-1), dt) < 2e-3
+    y = nf4.matmul(w1, x, epi=nf4.EPI_RESIDUAL, operand=from_bits(rb, dtype).view(1, 1, M))
+    expect = orc.gemv_emul(xb, dt, **oracle_args(l1), **kw, R=rb, epi=1)
+    assert np.array_equal(bits(y), expect), first_mismatch(bits(y), expect)
+    y = nf4.matmul_fused(w1, x, module3=w3)
+    expect = orc.gemv_emul(xb, dt, **oracle_args(l3), **kw, R=g1, epi=2)
+    assert np.array_equal(bits(y), expect), first_mismatch(bits(y), expect)
+
+
+@pytest.mark.parametrize("nested", [True, False])
+def test_one_row_longer_than_the_gemv_holds(nf4, orc, nested):
+    """K = 65536 (beyond the GEMV's 32768): `matmul` serves the row through the
+    tiled kernel within the bar; the fused single-row forms decline (None),
+    never raise."""
+    M, K, dtype = 96, 65536, torch.bfloat16
+    assert not nf4.gemv_fits(M, K)
+    layer = random_layer(M, K, nested, seed=31 + nested)
+    lin = to_linear(layer, dtype)
+    assert nf4.prepare(lin)
+    xb = randn_bits(K, dtype, seed=33, scale=0.5)
+    x = from_bits(xb, dtype).view(1, 1, K)
+    before = nf4.stats()["fast"]
+    y = lin(x)
+    assert nf4.stats()["fast"] == before + 1 and y.shape == (1, 1, M)
+    ref = orc.nf4_gemm_ref(xb, o.DT_BF16, **oracle_args(layer), M=M, K=K, N=1, bs=64, bs2=layer["bs2"] or 256)
+    assert beyond_rounding_error(o.to_f32(bits(y), o.DT_BF16), ref.reshape(-1), o.DT_BF16) < 2e-3
+    assert nf4.matmul_fused(lin, x) is None
+    assert nf4.matmul_fused(lin, x, module3=lin) is None
+
+
 @pytest.mark.parametrize("rows", [128, 256, 512])
 @pytest.mark.parametrize("name,shape", [("q", (4096, 2560)), ("k", (1024, 2560)), ("o", (2560, 4096)),
                                         ("gate", (9728, 2560)), ("down", (2560, 9728)), ("qkv", (6144, 2560)),

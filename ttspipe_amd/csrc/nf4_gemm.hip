@@ -512,6 +512,7 @@ int gemm_mfma(const void* X, int dt, const uint8_t* W, const uint8_t* A8, const 
   TTSP_RETURN_LAUNCH();
 }
 
+bool gemv_fits(int M, int K, int blocksize);
 int gemv_n1(const void* X, int dt, const uint8_t* W, const uint8_t* A8, const float* AMAX,
             const float* CODE2, float offset, const float* LUT, void* Y, const void* R, int epi,
             int M, int K, int blocksize, int blocksize2, hipStream_t st);
@@ -539,21 +540,23 @@ static int gemm_args(const void* X, const uint8_t* W, const uint8_t* A8, const f
   return 0;
 }
 
-// One entry for every row count: one row takes the bandwidth-bound GEMV, up
-// to 64 rows the skinny MFMA kernel (weights streamed once), more rows the
-// tiled MFMA kernel (weights read once per BN rows), unsplit.
+// One entry for every row count: one row takes the bandwidth-bound GEMV (or,
+// past the 32768-code rows it holds, the tiled kernel), up to 64 rows the
+// skinny MFMA kernel (weights streamed once), more rows the tiled MFMA kernel
+// (weights read once per BN rows), unsplit.
 extern "C" int ttsp_nf4_gemm(const void* X, int x_dtype, const uint8_t* W, const uint8_t* A8,
                              const float* AMAX, const float* CODE2, float offset, const float* LUT,
                              void* Y, const void* R, int epi, int M, int K, int N, int blocksize,
                              int blocksize2, hipStream_t stream) {
-  if (N == 1 && N > 0 && M > 0 && K > 0 && X && W && AMAX && LUT && Y && (!A8 || CODE2))
+  if (N == 1 && M > 0 && K > 0 && X && W && AMAX && LUT && Y && (!A8 || CODE2) && gemv_fits(M, K, blocksize))
     return gemv_n1(X, x_dtype, W, A8, AMAX, CODE2, offset, LUT, Y, R, epi, M, K, blocksize,
                    blocksize2, stream);
   int bs_shift, bs2_shift;
   if (int rc = gemm_args(X, W, A8, AMAX, CODE2, LUT, Y, R, epi, M, K, N, blocksize, blocksize2, &bs_shift,
                          &bs2_shift))
     return rc;
-  if (skinny(K, N))
+  // (one row whose K the GEMV cannot hold, K > 32768, takes the tiled kernel below)
+  if (N >= 2 && skinny(K, N))
     return gemm_skinny(X, x_dtype, W, A8, AMAX, CODE2, offset, LUT, Y, R, epi, M, K, N, bs_shift, bs2_shift, stream);
   // vectorised output rows: 8 elements per 16-byte store
   const bool vec = M % 8 == 0 && (uintptr_t)Y % 16 == 0 && (!epi || (uintptr_t)R % 16 == 0);

@@ -57,7 +57,7 @@ constexpr int LUT_REP = 64;                    // table copies, one per lane
 constexpr int LUT_BYTES = 256 * LUT_REP * 4;   // 64 KiB
 constexpr int GEMV_WAVES = 8;                  // waves per workgroup
 constexpr int GEMV_THREADS = GEMV_WAVES * 64;
-constexpr int XC_MAX = 3;                      // x chunks per thread: K <= 3 * 512 * 8
+constexpr int XC_MAX = 3;                      // x chunks per thread held in registers (K <= 3 * 512 * 8)
 #ifndef GEMV_LOOKAHEAD
 #define GEMV_LOOKAHEAD 3                       // (row, chunk) items whose code lookups run ahead
 #endif
@@ -438,6 +438,13 @@ __global__ __launch_bounds__(GEMV_THREADS) void nf4_gemv_kernel(
       const int c = tid + i * nthr;
       if (i < XN && c < KD) xs[c] = xc[i];
     }
+    // rows longer than XC_MAX chunks a thread (K > 12288): the rest of x is
+    // loaded here, after the weight rows were requested, so this wait also
+    // waits for them - only those long rows pay it
+    for (int i = XC_MAX; i < XN; ++i) {
+      const int c = tid + i * nthr;
+      if (c < KD) xs[c] = *reinterpret_cast<const uint4*>(X + 8 * (size_t)c);
+    }
   } else {
     float sq = 0.0f;
     if (tid < KD) sq = dt == DT_BF16 ? sumsq8<DT_BF16>(xc[0], 0.0f) : sumsq8<DT_F16>(xc[0], 0.0f);
@@ -691,7 +698,6 @@ static int gemv_launch(const void* X, int dt, const void* G, float eps, const Nf
   const GemvShape g = gemv_shape(M, K, nm, bs_shift);
   if (!g.J) return (int)hipErrorInvalidValue;
   if (G && K / 8 > GEMV_THREADS) return (int)hipErrorInvalidValue;  // the norm: one chunk per thread
-  if (K / 8 > XC_MAX * GEMV_THREADS) return (int)hipErrorInvalidValue;
   const size_t att_bytes = att ? att_lds((int)((att->hcfg >> 8) & 255u), att->max_len) : 0;
   if (LUT_BYTES + gemv_dyn_lds(g, nm, K, bs_shift) + att_bytes > kLdsPerCU) return (int)hipErrorInvalidValue;
   if (att && (G || mat3)) return (int)hipErrorInvalidValue;
@@ -726,6 +732,16 @@ static int gemv_launch(const void* X, int dt, const void* G, float eps, const Nf
   const int rc = att ? dispatch_att(g, p, st, att_bytes) : nm == 1 ? dispatch_j<1>(g, p, st) : dispatch_j<2>(g, p, st);
   if (rc) return rc;
   TTSP_RETURN_LAUNCH();
+}
+
+// Whether the GEMV takes a one-weight launch of this shape (no norm): rows of
+// at most 64 chunks a lane-set (K <= 32768) whose LDS fits a CU. Larger rows
+// go to the tiled kernel.
+bool gemv_fits(int M, int K, int blocksize) {
+  const int bs_shift = log2_exact(blocksize);
+  if (bs_shift < 6 || bs_shift > 15 || M <= 0 || K <= 0 || K % 128 || K % blocksize || M >= (1 << 20)) return false;
+  const GemvShape g = gemv_shape(M, K, 1, bs_shift);
+  return g.J && LUT_BYTES + gemv_dyn_lds(g, 1, K, bs_shift) <= kLdsPerCU;
 }
 
 int gemv_n1(const void* X, int dt, const uint8_t* W, const uint8_t* A8, const float* AMAX,

@@ -177,6 +177,19 @@ def weight_specs(cfg: DualARConfig):
     return linears, vectors, caches
 
 
+def max_frames(cfg: DualARConfig) -> int:
+    """Frames a decode from position `prefill_len` can run before the slow
+    cache is full (frame i writes position prefill_len + i)."""
+    return cfg.max_seq_len - cfg.prefill_len
+
+
+def check_frames(cfg: DualARConfig, n_steps: int) -> None:
+    """Raise ValueError unless 1 <= `n_steps` and the frames fit the slow cache."""
+    if n_steps < 1 or n_steps > max_frames(cfg):
+        raise ValueError(f"{n_steps} frames from position {cfg.prefill_len} run past the "
+                         f"{cfg.max_seq_len}-position cache (at most {max_frames(cfg)} fit)")
+
+
 def first_tokens(cfg: DualARConfig):
     """The frame fed at position `prefill_len` (a fixed, in-range token column)."""
     return [(97 * (c + 1)) % (cfg.vocab_size if c == 0 else cfg.codebook_size) for c in range(cfg.n_tokens)]
@@ -308,10 +321,16 @@ class SyntheticDualAR:
 
     # ------------------------------------------------------------------ state
 
-    def reset(self, n_steps: int = 256) -> None:
-        """Position `prefill_len`, the first frame's tokens, an empty history."""
+    def reset(self, n_steps: int | None = None) -> None:
+        """Position `prefill_len`, the first frame's tokens, an empty history
+        of `n_steps` rows (default: 256, or as many frames as the cache holds
+        if fewer). Raises ValueError when `n_steps` frames would run past the
+        cache (the kernels would clamp the position, not fail)."""
         import torch
 
+        if n_steps is None:
+            n_steps = min(256, max_frames(self.cfg))
+        check_frames(self.cfg, n_steps)
         self.pos.fill_(self.cfg.prefill_len)
         # the first frame's rotary row; each frame's last launch writes the next one's
         torch.index_select(self.freqs, 0, self.pos, out=self.freq_row)
@@ -513,9 +532,13 @@ class SyntheticDualAR:
         """Reset, then n_steps frames; returns the [n_steps, n_tokens] token history (host)."""
         import torch
 
+        # reset first: a reset that grows the history drops a captured frame
+        # (it writes into the old history), so capture after it; capture()
+        # runs one eager frame, so reset again
+        self.reset(n_steps)
         if graphed and self.graph is None:
             self.capture()
-        self.reset(n_steps)
+            self.reset(n_steps)
         for _ in range(n_steps):
             if graphed:
                 self.graph.replay()
@@ -556,6 +579,7 @@ def benchmark(n_steps: int = 256, warmup: int = 8, cfg: DualARConfig = DualARCon
     import torch
 
     model = SyntheticDualAR(cfg)
+    model.reset(max(n_steps, warmup))  # the history the graph writes: grown before capture
     model.capture()
     model.reset(max(n_steps, warmup))
     for _ in range(warmup):

@@ -227,6 +227,13 @@ def matmul(module, x, *, epi: int = EPI_NONE, operand=None, out=None):
 NORM_MAX_K = 4096
 
 
+def gemv_fits(M: int, K: int) -> bool:
+    """Whether the single-row kernel takes an [M, K] weight (rows of at most
+    32768 codes). `matmul` serves longer rows through the tiled kernel; the
+    fused single-row forms decline them."""
+    return _lib.lib().ttsp_gemv_shape(M, K, None, None, None) == 0
+
+
 def matmul_fused(module, x, *, norm_weight=None, eps: float = 1e-6, module3=None, epi: int = EPI_NONE,
                  operand=None, out=None):
     """One input row through `module` in a single launch, or None if not applicable.
@@ -246,6 +253,8 @@ def matmul_fused(module, x, *, norm_weight=None, eps: float = 1e-6, module3=None
         return None
     K, M = fast["K"], fast["M"]
     if x.shape[-1] != K or x.numel() != K or not x.is_contiguous() or x.data_ptr() % 16:
+        return None
+    if not gemv_fits(M, K):
         return None
     fast3 = None
     if module3 is not None:
