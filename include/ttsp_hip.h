@@ -99,6 +99,16 @@ int ttsp_nf4_dequant(const uint8_t* W, const uint8_t* A8, const float* AMAX, con
  * nf4gemv.py:234-246). */
 int ttsp_gemv_shape(int M, int K, int* J, int* KS, int* RPW);
 
+/* Launch shape ttsp_nf4_gemm uses for N = 1 or 2 activation rows through the
+ * GEMV (each weight byte's codes looked up once, one fp32 chain per row; row
+ * n's result equals a one-row launch, bit for bit). Returns nonzero (and
+ * zeros) when those rows take the MFMA kernels instead (N > 2, or rows longer
+ * than the GEMV holds).
+ * Host-only query. Replaces: _config for small N (app/engine/nf4gemv.py:
+ * 234-246), whose N <= 8 launches are the reference's near-N=1 design point
+ * (nf4gemv.py:20-28). */
+int ttsp_gemv_rows_shape(int M, int K, int N, int* J, int* KS, int* RPW);
+
 /* Fork RMSNorm over the last axis: Y = round(round(X * r) * Wt),
  * r = 1 / sqrt(sum(X^2) / D + eps); rows x D, D % 8 == 0, dtype F16/BF16,
  * X, Wt and Y 16-byte aligned.

@@ -43,6 +43,16 @@ def gemv_shape(M: int, K: int):
     return J.value, KS.value, RPW.value
 
 
+def gemv_rows_shape(M: int, K: int, N: int):
+    """(J, KS, RPW) of N activation rows through the GEMV, or None when those
+    rows take the MFMA kernels."""
+    from ttspipe_amd import _lib
+
+    J, KS, RPW = ctypes.c_int(), ctypes.c_int(), ctypes.c_int()
+    rc = _lib.load().ttsp_gemv_rows_shape(M, K, N, ctypes.byref(J), ctypes.byref(KS), ctypes.byref(RPW))
+    return (J.value, KS.value, RPW.value) if rc == 0 else None
+
+
 def first_mismatch(a: np.ndarray, b: np.ndarray) -> str:
     idx = np.flatnonzero(a != b)
     if idx.size == 0:

@@ -16,7 +16,7 @@ import torch
 
 from oracle import oracle as o
 from tests.conftest import beyond_rounding_error, relative_error
-from tests.gpuutil import bits, dt_code, first_mismatch, from_bits, gemv_shape, randn_bits
+from tests.gpuutil import bits, dt_code, first_mismatch, from_bits, gemv_rows_shape, gemv_shape, randn_bits
 from tests.nf4data import dequant_numpy, oracle_args, random_layer, to_linear
 
 pytestmark = pytest.mark.gpu
@@ -141,6 +141,59 @@ def test_gemv_bit_exact_and_within_bar(nf4, orc, shape, nested, dtype):
     assert np.array_equal(got, expect), f"M={M} K={K} KS={KS} J={J}: {first_mismatch(got, expect)}"
     ref = orc.nf4_gemm_ref(xb, dt, **oracle_args(layer), M=M, K=K, N=1, bs=64, bs2=layer["bs2"] or 256)
     assert beyond_rounding_error(o.to_f32(got, dt), ref.reshape(-1), dt) < 2e-3
+
+
+@pytest.mark.parametrize("shape", GEMV_SHAPES)
+@pytest.mark.parametrize("nested", [True, False])
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_two_rows_through_the_gemv(nf4, orc, shape, nested, dtype):
+    """Two activation rows take the GEMV (one code lookup per weight byte, one
+    fp32 chain per row) with the one-row launch's K split: row n equals the
+    oracle's one-row emulation of x[n] bit for bit (so two rows give exactly
+    what two one-row calls give), and each is within the bar. Three rows take
+    the MFMA kernels."""
+    M, K = shape
+    rows = 2
+    sh = gemv_rows_shape(M, K, rows)
+    assert sh is not None, f"{rows} rows of {M}x{K} should take the GEMV"
+    assert sh == gemv_shape(M, K), "two rows keep the one-row launch shape"
+    assert gemv_rows_shape(M, K, 3) is None
+    J, KS, _ = sh
+    layer = random_layer(M, K, nested, seed=M * 3 + K + rows)
+    lin = to_linear(layer, dtype)
+    dt = dt_code(dtype)
+    xb = randn_bits(rows * K, dtype, seed=K + rows)
+    before = nf4.stats()["fast"]
+    y = lin(from_bits(xb, dtype).view(1, rows, K))
+    assert nf4.stats()["fast"] == before + 1 and y.shape == (1, rows, M)
+    got = bits(y).reshape(rows, M)
+    bs2 = layer["bs2"] or 256
+    for n in range(rows):
+        expect = orc.gemv_emul(xb[n * K:(n + 1) * K], dt, **oracle_args(layer), M=M, K=K, bs=64, KS=KS, J=J, bs2=bs2)
+        assert np.array_equal(got[n], expect), f"row {n} of {rows}, {M}x{K}: {first_mismatch(got[n], expect)}"
+    ref = orc.nf4_gemm_ref(xb, dt, **oracle_args(layer), M=M, K=K, N=rows, bs=64, bs2=bs2)
+    assert beyond_rounding_error(o.to_f32(got, dt).reshape(-1), ref.reshape(-1), dt) < 2e-3
+
+
+@pytest.mark.parametrize("rows", [2])
+@pytest.mark.parametrize("epi", [1, 2])
+def test_rows_through_the_gemv_with_epilogues(nf4, orc, rows, epi):
+    """The residual and gate epilogues of the two-row form read each row's own
+    operand row."""
+    M, K, dtype = 2560, 9728, torch.bfloat16
+    dt = dt_code(dtype)
+    J, KS, _ = gemv_rows_shape(M, K, rows)
+    layer = random_layer(M, K, True, seed=rows * 10 + epi)
+    lin = to_linear(layer, dtype)
+    assert nf4.prepare(lin)
+    xb = randn_bits(rows * K, dtype, seed=rows + 40, scale=0.5)
+    rb = randn_bits(rows * M, dtype, seed=rows + 50)
+    y = nf4.matmul(lin, from_bits(xb, dtype).view(rows, K), epi=epi, operand=from_bits(rb, dtype).view(rows, M))
+    got = bits(y).reshape(rows, M)
+    for n in range(rows):
+        expect = orc.gemv_emul(xb[n * K:(n + 1) * K], dt, **oracle_args(layer), M=M, K=K, bs=64, KS=KS, J=J,
+                               R=rb[n * M:(n + 1) * M], epi=epi)
+        assert np.array_equal(got[n], expect), f"row {n}: {first_mismatch(got[n], expect)}"
 
 
 @pytest.mark.parametrize("shape", [(4961, 384), (16000, 256), (4100, 128), (9000, 512)])

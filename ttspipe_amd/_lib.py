@@ -38,6 +38,7 @@ SIGNATURES: dict[str, list] = {
                             _i, _i, _i, _i, _i, _vp],
     "ttsp_nf4_dequant": [_vp, _vp, _vp, _vp, _f, _vp, _vp, _i, _ll, _i, _i, _vp],
     "ttsp_gemv_shape": [_i, _i, ctypes.POINTER(_i), ctypes.POINTER(_i), ctypes.POINTER(_i)],
+    "ttsp_gemv_rows_shape": [_i, _i, _i, ctypes.POINTER(_i), ctypes.POINTER(_i), ctypes.POINTER(_i)],
     "ttsp_rms_norm": [_vp, _vp, _vp, _i, _i, _f, _i, _vp],
     "ttsp_rope": [_vp, _vp, _i, _vp, _ll, _i, _i, _i, _i, _vp],
     "ttsp_qk_rope_kv": [_vp, _vp, _vp, _f, _vp, _i, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp],

@@ -512,10 +512,14 @@ int gemm_mfma(const void* X, int dt, const uint8_t* W, const uint8_t* A8, const 
   TTSP_RETURN_LAUNCH();
 }
 
-bool gemv_fits(int M, int K, int blocksize);
-int gemv_n1(const void* X, int dt, const uint8_t* W, const uint8_t* A8, const float* AMAX,
-            const float* CODE2, float offset, const float* LUT, void* Y, const void* R, int epi,
-            int M, int K, int blocksize, int blocksize2, hipStream_t st);
+bool gemv_fits(int M, int K, int blocksize, int N);
+int gemv_rows(const void* X, int dt, const uint8_t* W, const uint8_t* A8, const float* AMAX,
+              const float* CODE2, float offset, const float* LUT, void* Y, const void* R, int epi,
+              int M, int K, int N, int blocksize, int blocksize2, hipStream_t st);
+// Up to this many activation rows take the GEMV (each weight byte looked up
+// once, one fp32 chain per row) rather than the few-row MFMA kernel: two rows
+// cost 1.0-1.3x one row that way (gate 9728 x 2560: 7.5 against 9.4 us).
+constexpr int GEMV_ROWS_N = 2;
 int gemm_skinny(const void* X, int dt, const uint8_t* W, const uint8_t* A8, const float* AMAX, const float* CODE2,
                 float offset, const float* LUT, void* Y, const void* RES, int epi, int M, int K, int N, int bs_shift,
                 int bs2_shift, hipStream_t st);
@@ -540,17 +544,18 @@ static int gemm_args(const void* X, const uint8_t* W, const uint8_t* A8, const f
   return 0;
 }
 
-// One entry for every row count: one row takes the bandwidth-bound GEMV (or,
-// past the 32768-code rows it holds, the tiled kernel), up to 64 rows the
-// skinny MFMA kernel (weights streamed once), more rows the tiled MFMA kernel
-// (weights read once per BN rows), unsplit.
+// One entry for every row count: up to GEMV_ROWS_N rows take the
+// bandwidth-bound GEMV (or, past the rows it holds, the kernels below), up
+// to 64 rows the skinny MFMA kernel (weights streamed once), more rows the
+// tiled MFMA kernel (weights read once per BN rows), unsplit.
 extern "C" int ttsp_nf4_gemm(const void* X, int x_dtype, const uint8_t* W, const uint8_t* A8,
                              const float* AMAX, const float* CODE2, float offset, const float* LUT,
                              void* Y, const void* R, int epi, int M, int K, int N, int blocksize,
                              int blocksize2, hipStream_t stream) {
-  if (N == 1 && M > 0 && K > 0 && X && W && AMAX && LUT && Y && (!A8 || CODE2) && gemv_fits(M, K, blocksize))
-    return gemv_n1(X, x_dtype, W, A8, AMAX, CODE2, offset, LUT, Y, R, epi, M, K, blocksize,
-                   blocksize2, stream);
+  if (N >= 1 && N <= GEMV_ROWS_N && M > 0 && K > 0 && X && W && AMAX && LUT && Y && (!A8 || CODE2) &&
+      gemv_fits(M, K, blocksize, N))
+    return gemv_rows(X, x_dtype, W, A8, AMAX, CODE2, offset, LUT, Y, R, epi, M, K, N, blocksize, blocksize2,
+                     stream);
   int bs_shift, bs2_shift;
   if (int rc = gemm_args(X, W, A8, AMAX, CODE2, LUT, Y, R, epi, M, K, N, blocksize, blocksize2, &bs_shift,
                          &bs2_shift))

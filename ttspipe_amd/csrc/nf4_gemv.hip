@@ -93,12 +93,12 @@ struct AttnSrc {
 struct GemvParams {
   Nf4Mat mat[2];          // mat[1]: the SwiGLU form's second weight (w3)
   const float* LUT;       // the 16 NF4 code points
-  const uint16_t* X;      // [K]
+  const uint16_t* X;      // [N][K]
   const uint16_t* G;      // RMSNorm weight [K], or readable dummy
-  const uint16_t* R;      // epilogue operand [M], or readable dummy
-  uint16_t* Y;            // [M]
+  const uint16_t* R;      // epilogue operand [N][M], or readable dummy
+  uint16_t* Y;            // [N][M]
   float eps;
-  int M, K, KS, bs_shift, bs2_shift;
+  int M, K, N, KS, bs_shift, bs2_shift;  // N: activation rows (1, or up to NR of the rows form)
   int dt;                 // DT_F16 / DT_BF16
   int nested, norm, epi;  // flags; epi: 0 none, 1 residual, 2 silu gate
   AttnSrc att;            // the attention-prologue form only
@@ -186,15 +186,15 @@ __device__ __forceinline__ F8 to_f32(uint4 c) {
 }
 
 // Dynamic LDS after the static table: code2 [NM][256], norm partials [8],
-// K-slice partials [8][NM*RPW], the resolved scales [8 waves][NM][RPW][8 J]
-// (16-byte aligned), then x as staged [K/8].
+// K-slice partials [8][NM*NR*RPW], the resolved scales [8 waves][NM][RPW][8 J]
+// (16-byte aligned), then x as staged [NR][K/8].
 // The leading scalar arguments are what the first loads need (weight 0's
 // stream and scales, x, the code tables, the sizes): the command processor
 // preloads them into SGPRs, so those loads issue at wave start; the rest of
 // GemvParams is fetched once they are in flight. mk = M | (K / 128) << 20,
 // cfg = KS | bs_shift << 4 | bs2_shift << 8 | dt << 12 | nested << 14 |
 // norm << 15.
-template <int J, int RPW, int NM, bool ATT = false>
+template <int J, int RPW, int NM, bool ATT = false, int NR = 1>
 __global__ __launch_bounds__(GEMV_THREADS) void nf4_gemv_kernel(
     const uint32_t* __restrict__ W0, const uint16_t* __restrict__ X, const float* __restrict__ LUT,
     const uint8_t* __restrict__ A80, const float* __restrict__ AM0, const float* __restrict__ C20, uint32_t mk,
@@ -211,8 +211,8 @@ __global__ __launch_bounds__(GEMV_THREADS) void nf4_gemv_kernel(
   extern __shared__ __align__(16) unsigned char lds_dyn[];
   float* code2_s = reinterpret_cast<float*>(lds_dyn);  // [NM][256]
   float* wpart = code2_s + NM * 256;                   // [NW] norm partial sums
-  float* red = wpart + NW;                             // [NW][NM*RPW]
-  float* srow = red + NW * NM * RPW;                   // [NW][NM][RPW][8 J] scale slots
+  float* red = wpart + NW;                             // [NW][NM*NR*RPW]
+  float* srow = red + NW * NM * NR * RPW;              // [NW][NM][RPW][8 J] scale slots
 
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = uniform(tid >> 6);
@@ -264,16 +264,23 @@ __global__ __launch_bounds__(GEMV_THREADS) void nf4_gemv_kernel(
     sv[i] = (m ? AM1 : AM0)[nested ? gb >> bs2_shift : gb];
   }
   // x (and the norm weight): staged once per workgroup, chunk c = tid + 512 i
-  // by thread tid (one chunk per thread unless K > 4096, where there is no norm)
+  // of each activation row by thread tid (one chunk per thread unless
+  // K > 4096, where there is no norm); rows past N repeat row N - 1 (the rows
+  // form: NR > 1, one weight, no norm)
   const int XN = uniform((KD + nthr - 1) / nthr);
-  uint4 xc[XC_MAX];
+  uint4 xc[XC_MAX][NR];
   // (chunks past XN stay unset and unread: a zero-initialised chunk would make
   // the branch's join wait for the load)
   if constexpr (!ATT) {
-    xc[0] = *reinterpret_cast<const uint4*>(X + 8 * (size_t)min(tid, KD - 1));
 #pragma unroll
-    for (int i = 1; i < XC_MAX; ++i)
-      if (i < XN) xc[i] = *reinterpret_cast<const uint4*>(X + 8 * (size_t)min(tid + i * nthr, KD - 1));
+    for (int n = 0; n < NR; ++n) {
+      // (row 0 needs no argument beyond the preloaded ones: its loads issue at wave start)
+      const uint16_t* xrow = n == 0 ? X : X + (size_t)min(n, p.N - 1) * K;
+      xc[0][n] = *reinterpret_cast<const uint4*>(xrow + 8 * (size_t)min(tid, KD - 1));
+#pragma unroll
+      for (int i = 1; i < XC_MAX; ++i)
+        if (i < XN) xc[i][n] = *reinterpret_cast<const uint4*>(xrow + 8 * (size_t)min(tid + i * nthr, KD - 1));
+    }
   }
 
   // 2. the first PF rows of the weight stream; the rest is requested row by
@@ -296,7 +303,10 @@ __global__ __launch_bounds__(GEMV_THREADS) void nf4_gemv_kernel(
   for (int r = 0; r < PF; ++r) load_row(r);
   // the remaining arguments, in one round trip while those loads fly
   asm volatile("" ::"s"(p.G), "s"(p.R), "s"(p.Y), "s"(p.mat[0].offset), "s"(p.mat[NM - 1].offset), "s"(p.eps));
-  const uint32_t rres = p.R[min(row0 + min(lane, RPW - 1), M - 1)];  // epilogue operand
+  uint32_t rres[NR];  // epilogue operands
+#pragma unroll
+  for (int n = 0; n < NR; ++n)
+    rres[n] = p.R[(n == 0 ? 0 : (size_t)min(n, p.N - 1) * M) + min(row0 + min(lane, RPW - 1), M - 1)];
   const uint4 gc = *reinterpret_cast<const uint4*>(p.G + 8 * (size_t)(norm ? min(tid, KD - 1) : 0));
 
   // 2b. (attention prologue) every load of the attention, before any waits:
@@ -434,20 +444,24 @@ __global__ __launch_bounds__(GEMV_THREADS) void nf4_gemv_kernel(
     }
   } else if (!norm) {
 #pragma unroll
-    for (int i = 0; i < XC_MAX; ++i) {
-      const int c = tid + i * nthr;
-      if (i < XN && c < KD) xs[c] = xc[i];
-    }
-    // rows longer than XC_MAX chunks a thread (K > 12288): the rest of x is
-    // loaded here, after the weight rows were requested, so this wait also
-    // waits for them - only those long rows pay it
-    for (int i = XC_MAX; i < XN; ++i) {
-      const int c = tid + i * nthr;
-      if (c < KD) xs[c] = *reinterpret_cast<const uint4*>(X + 8 * (size_t)c);
+    for (int n = 0; n < NR; ++n) {
+#pragma unroll
+      for (int i = 0; i < XC_MAX; ++i) {
+        const int c = tid + i * nthr;
+        if (i < XN && c < KD) xs[n * KD + c] = xc[i][n];
+      }
+      // rows longer than XC_MAX chunks a thread (K > 12288): the rest of x is
+      // loaded here, after the weight rows were requested, so this wait also
+      // waits for them - only those long rows pay it
+      for (int i = XC_MAX; i < XN; ++i) {
+        const int c = tid + i * nthr;
+        if (c < KD)
+          xs[n * KD + c] = *reinterpret_cast<const uint4*>(X + (n == 0 ? 0 : (size_t)min(n, p.N - 1) * K) + 8 * (size_t)c);
+      }
     }
   } else {
     float sq = 0.0f;
-    if (tid < KD) sq = dt == DT_BF16 ? sumsq8<DT_BF16>(xc[0], 0.0f) : sumsq8<DT_F16>(xc[0], 0.0f);
+    if (tid < KD) sq = dt == DT_BF16 ? sumsq8<DT_BF16>(xc[0][0], 0.0f) : sumsq8<DT_F16>(xc[0][0], 0.0f);
     sq = wave_sum_dpp(sq);
     if (lane == 0) wpart[wave] = sq;
   }
@@ -457,27 +471,28 @@ __global__ __launch_bounds__(GEMV_THREADS) void nf4_gemv_kernel(
 #pragma unroll
     for (int w2 = 1; w2 < NW; ++w2) ss = __fadd_rn(ss, wpart[w2]);
     const float r = rsqrt_rn(__fadd_rn(__fdiv_rn(ss, (float)K), p.eps));
-    if (tid < KD) xs[tid] = dt == DT_BF16 ? norm8<DT_BF16>(xc[0], gc, r) : norm8<DT_F16>(xc[0], gc, r);
+    if (tid < KD) xs[tid] = dt == DT_BF16 ? norm8<DT_BF16>(xc[0][0], gc, r) : norm8<DT_F16>(xc[0][0], gc, r);
     __syncthreads();
   }
 
   // x as fp32 (zero past the row's end: the clamped weight dword there is
   // finite, so its products are exactly +0)
-  F8 xf[J];
-  {
+  F8 xf[NR][J];
+#pragma unroll
+  for (int n = 0; n < NR; ++n) {
     uint4 xz[J];
 #pragma unroll
     for (int j = 0; j < J; ++j) {
       const int d = lane + 64 * (j * KS + ks);
-      const uint4 v = xs[min(d, KD - 1)];
+      const uint4 v = xs[n * KD + min(d, KD - 1)];
       xz[j] = d < KD ? v : make_uint4(0, 0, 0, 0);
     }
     if (dt == DT_BF16) {
 #pragma unroll
-      for (int j = 0; j < J; ++j) xf[j] = to_f32<DT_BF16>(xz[j]);
+      for (int j = 0; j < J; ++j) xf[n][j] = to_f32<DT_BF16>(xz[j]);
     } else {
 #pragma unroll
-      for (int j = 0; j < J; ++j) xf[j] = to_f32<DT_F16>(xz[j]);
+      for (int j = 0; j < J; ++j) xf[n][j] = to_f32<DT_F16>(xz[j]);
     }
   }
 
@@ -509,60 +524,70 @@ __global__ __launch_bounds__(GEMV_THREADS) void nf4_gemv_kernel(
   };
 #pragma unroll
   for (int t = 0; t < LA; ++t) lookup(t);
-  float tot[NM][RPW];
+  // outputs per weight row: NM weights (SwiGLU) or NR activation rows
+  constexpr int NO = NM * NR;
+  float tot[NO][RPW];
 #pragma unroll
   for (int m = 0; m < NM; ++m)
 #pragma unroll
     for (int r = 0; r < RPW; ++r) {
       if (m == 0 && r + PF < RPW) load_row(r + PF);
-      float acc = 0.0f;
+      float acc[NR];
+#pragma unroll
+      for (int n = 0; n < NR; ++n) acc[n] = 0.0f;
 #pragma unroll
       for (int j = 0; j < J; ++j) {
         const int t = (m * RPW + r) * J + j;
         if (t + LA < T) lookup(t + LA);
         __builtin_amdgcn_sched_barrier(0);
-        float q = __builtin_fmaf(h_lo(cp[t][0]), xf[j].v[0], 0.0f);
-        q = __builtin_fmaf(h_hi(cp[t][0]), xf[j].v[1], q);
-        q = __builtin_fmaf(h_lo(cp[t][1]), xf[j].v[2], q);
-        q = __builtin_fmaf(h_hi(cp[t][1]), xf[j].v[3], q);
-        q = __builtin_fmaf(h_lo(cp[t][2]), xf[j].v[4], q);
-        q = __builtin_fmaf(h_hi(cp[t][2]), xf[j].v[5], q);
-        q = __builtin_fmaf(h_lo(cp[t][3]), xf[j].v[6], q);
-        q = __builtin_fmaf(h_hi(cp[t][3]), xf[j].v[7], q);
-        acc = __builtin_fmaf(q, sc[t], acc);
+#pragma unroll
+        for (int n = 0; n < NR; ++n) {  // each activation row: the one-row chain
+          float q = __builtin_fmaf(h_lo(cp[t][0]), xf[n][j].v[0], 0.0f);
+          q = __builtin_fmaf(h_hi(cp[t][0]), xf[n][j].v[1], q);
+          q = __builtin_fmaf(h_lo(cp[t][1]), xf[n][j].v[2], q);
+          q = __builtin_fmaf(h_hi(cp[t][1]), xf[n][j].v[3], q);
+          q = __builtin_fmaf(h_lo(cp[t][2]), xf[n][j].v[4], q);
+          q = __builtin_fmaf(h_hi(cp[t][2]), xf[n][j].v[5], q);
+          q = __builtin_fmaf(h_lo(cp[t][3]), xf[n][j].v[6], q);
+          q = __builtin_fmaf(h_hi(cp[t][3]), xf[n][j].v[7], q);
+          acc[n] = __builtin_fmaf(q, sc[t], acc[n]);
+        }
       }
-      tot[m][r] = wave_sum_dpp(acc);
+#pragma unroll
+      for (int n = 0; n < NR; ++n) tot[m * NR + n][r] = wave_sum_dpp(acc[n]);
     }
 
   // 5. K-slices left to right, epilogue, store (lane r stores row r)
   if (KS > 1) {
     if (lane == 0) {
 #pragma unroll
-      for (int m = 0; m < NM; ++m)
+      for (int o = 0; o < NO; ++o)
 #pragma unroll
-        for (int r = 0; r < RPW; ++r) red[wave * NM * RPW + m * RPW + r] = tot[m][r];
+        for (int r = 0; r < RPW; ++r) red[wave * NO * RPW + o * RPW + r] = tot[o][r];
     }
     __syncthreads();
     if (ks != 0) return;
 #pragma unroll
-    for (int m = 0; m < NM; ++m)
+    for (int o = 0; o < NO; ++o)
 #pragma unroll
       for (int r = 0; r < RPW; ++r) {
-        float a = tot[m][r];
-        for (int k2 = 1; k2 < KS; ++k2) a = __fadd_rn(a, red[(wave + k2) * NM * RPW + m * RPW + r]);
-        tot[m][r] = a;
+        float a = tot[o][r];
+        for (int k2 = 1; k2 < KS; ++k2) a = __fadd_rn(a, red[(wave + k2) * NO * RPW + o * RPW + r]);
+        tot[o][r] = a;
       }
   }
-  float mine[NM];
+  float mine[NO];
 #pragma unroll
-  for (int m = 0; m < NM; ++m) {
-    mine[m] = tot[m][0];
+  for (int o = 0; o < NO; ++o) {
+    mine[o] = tot[o][0];
 #pragma unroll
-    for (int r = 1; r < RPW; ++r) mine[m] = lane == r ? tot[m][r] : mine[m];
+    for (int r = 1; r < RPW; ++r) mine[o] = lane == r ? tot[o][r] : mine[o];
   }
   if (lane < RPW && row0 + lane < M) {
     if constexpr (NM == 1) {
-      p.Y[row0 + lane] = epilogue16(dt, mine[0], p.epi, rres);
+#pragma unroll
+      for (int n = 0; n < NR; ++n)
+        if (n < p.N) p.Y[(size_t)n * M + row0 + lane] = epilogue16(dt, mine[n], p.epi, rres[n]);
     } else {
       // SwiGLU: w1's row is the gate operand of w3's row, as the two-launch form rounds it
       p.Y[row0 + lane] = epilogue16(dt, mine[1], 2, st16(dt, mine[0]));
@@ -588,10 +613,10 @@ static constexpr int kRPW2[] = {1, 2, 3, 4, 5};
 static constexpr int kCUs = GEMV_WG_SLOTS;  // workgroups resident at once
 static constexpr size_t kLdsPerCU = 160 * 1024;  // a workgroup's LDS must fit
 
-// Dynamic LDS of one workgroup (the table is static).
-static size_t gemv_dyn_lds(const GemvShape& g, int nm, int K, int bs_shift) {
+// Dynamic LDS of one workgroup (the table is static); nr activation rows.
+static size_t gemv_dyn_lds(const GemvShape& g, int nm, int K, int bs_shift, int nr = 1) {
   const size_t sc = (size_t)GEMV_WAVES * nm * g.RPW * 8 * g.J;  // scale slots
-  return 4 * (256 * (size_t)nm + GEMV_WAVES + (size_t)GEMV_WAVES * nm * g.RPW + sc) + 2 * (size_t)K;
+  return 4 * (256 * (size_t)nm + GEMV_WAVES + (size_t)GEMV_WAVES * nm * nr * g.RPW + sc) + 2 * (size_t)K * nr;
 }
 
 // K is split (KS a power of two) so that a lane's chunks J <= 8 leave the
@@ -599,14 +624,23 @@ static size_t gemv_dyn_lds(const GemvShape& g, int nm, int K, int bs_shift) {
 // workgroup per CU (every workgroup builds the 64 KiB table and stages x once,
 // so fewer, fuller workgroups pay less of that - measured faster than two
 // half-full workgroups per CU at every decode shape).
-static GemvShape gemv_shape(int M, int K, int nm = 1, int bs_shift = 6) {
+// The rows form (nr > 1 activation rows) holds x as fp32 for its J chunks of
+// every row through the dot loop: J * nr <= 20 keeps that within 160 VGPRs.
+// Two rows: every J fits, so the K split is the one-row launch's and each
+// row's result equals a one-row launch bit for bit. (Four rows a launch were
+// built and measured: faster than the few-row MFMA kernel only on the
+// smallest matrices, 10-35 % slower on the large ones.)
+static constexpr int kRowsXMax = 20;
+constexpr int GEMV_MAX_ROWS = 2;
+
+static GemvShape gemv_shape(int M, int K, int nm = 1, int bs_shift = 6, int nr = 1) {
   const int chunks = (K / 8 + 63) / 64;  // 64-dword chunks per row
   int KS = 0, J = 0, waste = 1 << 30;
   for (int ks = 1; ks <= GEMV_WAVES; ks *= 2) {
     int j = 0;
     for (int v : kJ)
       if (v >= (chunks + ks - 1) / ks) { j = v; break; }
-    if (j && ks * j - chunks < waste) { KS = ks; J = j; waste = ks * j - chunks; }
+    if (j && (nr == 1 || j * nr <= kRowsXMax) && ks * j - chunks < waste) { KS = ks; J = j; waste = ks * j - chunks; }
   }
   if (!KS) return {0, 0, 0};
   const int RG = GEMV_WAVES / KS;
@@ -620,22 +654,22 @@ static GemvShape gemv_shape(int M, int K, int nm = 1, int bs_shift = 6) {
   return g;
 }
 
-template <int J, int RPW, int NM, bool ATT = false>
+template <int J, int RPW, int NM, bool ATT = false, int NR = 1>
 static void launch_gemv(const GemvShape& g, const GemvParams& p, hipStream_t st, size_t extra_lds = 0) {
   const int rows_wg = (GEMV_WAVES / g.KS) * RPW;
   const int grid = (p.M + rows_wg - 1) / rows_wg;
   const uint32_t mk = (uint32_t)p.M | ((uint32_t)(p.K / 128) << 20);
   const uint32_t cfg = (uint32_t)g.KS | ((uint32_t)p.bs_shift << 4) | ((uint32_t)p.bs2_shift << 8) |
                        ((uint32_t)p.dt << 12) | ((uint32_t)p.nested << 14) | ((uint32_t)p.norm << 15);
-  hipLaunchKernelGGL((nf4_gemv_kernel<J, RPW, NM, ATT>), dim3(grid), dim3(GEMV_THREADS),
-                     gemv_dyn_lds(g, NM, p.K, p.bs_shift) + extra_lds, st, p.mat[0].W, p.X, p.LUT,
+  hipLaunchKernelGGL((nf4_gemv_kernel<J, RPW, NM, ATT, NR>), dim3(grid), dim3(GEMV_THREADS),
+                     gemv_dyn_lds(g, NM, p.K, p.bs_shift, NR) + extra_lds, st, p.mat[0].W, p.X, p.LUT,
                      p.mat[0].A8, p.mat[0].AMAX, p.mat[0].CODE2, mk, cfg, p);
 }
 
-template <int J, int NM>
+template <int J, int NM, int NR = 1>
 static int dispatch_rpw(const GemvShape& g, const GemvParams& p, hipStream_t st) {
 #define TTSP_R(RV) \
-  case RV: launch_gemv<J, RV, NM>(g, p, st); return 0;
+  case RV: launch_gemv<J, RV, NM, false, NR>(g, p, st); return 0;
   if constexpr (NM == 1) {
     switch (g.RPW) {
       TTSP_R(1) TTSP_R(2) TTSP_R(3) TTSP_R(4) TTSP_R(5) TTSP_R(6) TTSP_R(8)
@@ -650,10 +684,12 @@ static int dispatch_rpw(const GemvShape& g, const GemvParams& p, hipStream_t st)
 #undef TTSP_R
 }
 
-template <int NM>
+template <int NM, int NR = 1>
 static int dispatch_j(const GemvShape& g, const GemvParams& p, hipStream_t st) {
-#define TTSP_J(JV) \
-  case JV: return dispatch_rpw<JV, NM>(g, p, st);
+#define TTSP_J(JV)                                                            \
+  case JV:                                                                    \
+    if constexpr (NR == 1 || JV * NR <= kRowsXMax) return dispatch_rpw<JV, NM, NR>(g, p, st); \
+    else return (int)hipErrorInvalidValue;
   switch (g.J) {
     TTSP_J(1) TTSP_J(2) TTSP_J(3) TTSP_J(4) TTSP_J(5) TTSP_J(6) TTSP_J(8)
     default: return (int)hipErrorInvalidValue;
@@ -686,7 +722,7 @@ static int log2_exact(int v) {
 static int gemv_launch(const void* X, int dt, const void* G, float eps, const Nf4Mat& mat1,
                        const Nf4Mat* mat3, bool nested, const float* LUT, void* Y, const void* R,
                        int epi, int M, int K, int blocksize, int blocksize2, hipStream_t st,
-                       const AttnSrc* att = nullptr) {
+                       const AttnSrc* att = nullptr, int N = 1) {
   const int bs_shift = log2_exact(blocksize);
   const int bs2_shift = nested ? log2_exact(blocksize2) : 0;
   if (bs_shift < 6 || bs_shift > 15 || bs2_shift < 0 || bs2_shift > 15 || K % 128 || K % blocksize || M <= 0 ||
@@ -695,11 +731,13 @@ static int gemv_launch(const void* X, int dt, const void* G, float eps, const Nf
   if (dt != DT_F16 && dt != DT_BF16) return (int)hipErrorInvalidValue;
   if (epi < 0 || epi > 2 || (epi && !R) || (mat3 && epi)) return (int)hipErrorInvalidValue;
   const int nm = mat3 ? 2 : 1;
-  const GemvShape g = gemv_shape(M, K, nm, bs_shift);
+  if (N < 1 || N > GEMV_MAX_ROWS || (N > 1 && (G || mat3 || att))) return (int)hipErrorInvalidValue;
+  const int nr = N;
+  const GemvShape g = gemv_shape(M, K, nm, bs_shift, nr);
   if (!g.J) return (int)hipErrorInvalidValue;
   if (G && K / 8 > GEMV_THREADS) return (int)hipErrorInvalidValue;  // the norm: one chunk per thread
   const size_t att_bytes = att ? att_lds((int)((att->hcfg >> 8) & 255u), att->max_len) : 0;
-  if (LUT_BYTES + gemv_dyn_lds(g, nm, K, bs_shift) + att_bytes > kLdsPerCU) return (int)hipErrorInvalidValue;
+  if (LUT_BYTES + gemv_dyn_lds(g, nm, K, bs_shift, nr) + att_bytes > kLdsPerCU) return (int)hipErrorInvalidValue;
   if (att && (G || mat3)) return (int)hipErrorInvalidValue;
   if (nested && ((uintptr_t)mat1.CODE2 % 16 || (mat3 && (uintptr_t)mat3->CODE2 % 16)))
     return (int)hipErrorInvalidValue;  // code2 is read 16 bytes per lane
@@ -721,6 +759,7 @@ static int gemv_launch(const void* X, int dt, const void* G, float eps, const Nf
   p.eps = eps;
   p.M = M;
   p.K = K;
+  p.N = N;
   p.KS = g.KS;
   p.bs_shift = bs_shift;
   p.bs2_shift = bs2_shift;
@@ -729,27 +768,35 @@ static int gemv_launch(const void* X, int dt, const void* G, float eps, const Nf
   p.norm = G ? 1 : 0;
   p.epi = epi;
   p.att = att ? *att : AttnSrc{};
-  const int rc = att ? dispatch_att(g, p, st, att_bytes) : nm == 1 ? dispatch_j<1>(g, p, st) : dispatch_j<2>(g, p, st);
+  const int rc = att     ? dispatch_att(g, p, st, att_bytes)
+                 : nm == 2 ? dispatch_j<2>(g, p, st)
+                 : nr == 1 ? dispatch_j<1>(g, p, st)
+                           : dispatch_j<1, 2>(g, p, st);
   if (rc) return rc;
   TTSP_RETURN_LAUNCH();
 }
 
-// Whether the GEMV takes a one-weight launch of this shape (no norm): rows of
-// at most 64 chunks a lane-set (K <= 32768) whose LDS fits a CU. Larger rows
-// go to the tiled kernel.
-bool gemv_fits(int M, int K, int blocksize) {
+// Whether the GEMV takes a one-weight launch of this shape for N activation
+// rows (no norm): rows of at most 64 chunks a lane-set (K <= 32768; fewer
+// with several activation rows) whose LDS fits a CU. Larger rows go to the
+// tiled kernel.
+bool gemv_fits(int M, int K, int blocksize, int N) {
   const int bs_shift = log2_exact(blocksize);
   if (bs_shift < 6 || bs_shift > 15 || M <= 0 || K <= 0 || K % 128 || K % blocksize || M >= (1 << 20)) return false;
-  const GemvShape g = gemv_shape(M, K, 1, bs_shift);
-  return g.J && LUT_BYTES + gemv_dyn_lds(g, 1, K, bs_shift) <= kLdsPerCU;
+  if (N < 1 || N > GEMV_MAX_ROWS) return false;
+  const GemvShape g = gemv_shape(M, K, 1, bs_shift, N);
+  return g.J && LUT_BYTES + gemv_dyn_lds(g, 1, K, bs_shift, N) <= kLdsPerCU;
 }
 
-int gemv_n1(const void* X, int dt, const uint8_t* W, const uint8_t* A8, const float* AMAX,
-            const float* CODE2, float offset, const float* LUT, void* Y, const void* R, int epi,
-            int M, int K, int blocksize, int blocksize2, hipStream_t st) {
+// N (1..GEMV_MAX_ROWS) activation rows through the GEMV: every weight byte's
+// codes are looked up once, and each row gets the one-row arithmetic (its
+// result equals a one-row launch, bit for bit).
+int gemv_rows(const void* X, int dt, const uint8_t* W, const uint8_t* A8, const float* AMAX,
+              const float* CODE2, float offset, const float* LUT, void* Y, const void* R, int epi,
+              int M, int K, int N, int blocksize, int blocksize2, hipStream_t st) {
   const Nf4Mat m{reinterpret_cast<const uint32_t*>(W), A8, AMAX, CODE2, offset};
   return gemv_launch(X, dt, nullptr, 0.0f, m, nullptr, A8 != nullptr, LUT, Y, R, epi, M, K, blocksize,
-                     blocksize2, st);
+                     blocksize2, st, nullptr, N);
 }
 
 }  // namespace ttsp
@@ -762,6 +809,15 @@ extern "C" int ttsp_gemv_shape(int M, int K, int* J, int* KS, int* RPW) {
   if (KS) *KS = g.KS;
   if (RPW) *RPW = g.RPW;
   return g.J ? 0 : (int)hipErrorInvalidValue;
+}
+
+extern "C" int ttsp_gemv_rows_shape(int M, int K, int N, int* J, int* KS, int* RPW) {
+  const bool ok = gemv_fits(M, K, 64, N);
+  const GemvShape g = ok ? gemv_shape(M, K, 1, 6, N) : GemvShape{0, 0, 0};
+  if (J) *J = g.J;
+  if (KS) *KS = g.KS;
+  if (RPW) *RPW = g.RPW;
+  return ok ? 0 : (int)hipErrorInvalidValue;
 }
 
 extern "C" int ttsp_nf4_gemv_fused(const void* X, int x_dtype, const void* NORM_W, float eps,

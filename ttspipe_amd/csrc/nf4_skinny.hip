@@ -170,7 +170,12 @@ __global__ __launch_bounds__(64 * NW) void nf4_skinny_kernel(
   }
   // every wave writes the same code2 values (no branch on the wave)
   if constexpr (NESTED) reinterpret_cast<f32x4*>(code2_s)[lane] = c2v;
+  // (no arithmetic on the streamed operands may move above the barrier: each
+  // such use waits for its load, and the in-order counter for every load
+  // issued before it)
+  __builtin_amdgcn_sched_barrier(0);
   __syncthreads();
+  __builtin_amdgcn_sched_barrier(0);
   const unsigned char* tab = reinterpret_cast<const unsigned char*>(&lut2[0][0]);
   const uint32_t lane8 = 8u * (uint32_t)(lane & (SK_REP - 1));
   // rows n >= N of an X tile contribute zeros (their fragments are replaced)
