@@ -33,7 +33,9 @@ def test_prefill_spans_follow_the_buckets():
 
     top = PREFILL_BUCKETS[-1]
     assert prefill_spans(0) == []
-    assert prefill_spans(1) == [(0, 1, PREFILL_BUCKETS[0])]
+    assert PREFILL_BUCKETS[:6] == (1, 2, 4, 8, 16, 32)  # the reference's buckets (graphs.py:137)
+    assert prefill_spans(1) == [(0, 1, 1)]
+    assert [prefill_spans(n)[0][2] for n in (2, 3, 4, 5, 8, 9)] == [2, 4, 4, 8, 8, 16]
     assert prefill_spans(40) == [(0, 40, 64)]
     assert prefill_spans(top) == [(0, top, top)]
     assert prefill_spans(top + 1) == [(0, top, top), (top, 1, PREFILL_BUCKETS[0])]
@@ -265,12 +267,14 @@ def _tokens(model, n, seed):
 
 
 @pytest.mark.gpu
-def test_prompt_prefill_matches_position_by_position_decode(fresh):
-    """Prefill 40 positions at once, then decode the same positions one at a
-    time through the decode kernels: the KV rows and the last logits agree."""
+@pytest.mark.parametrize("start,n", [(8, 40), (8, 1), (9, 2), (10, 3), (11, 5), (12, 8)])
+def test_prompt_prefill_matches_position_by_position_decode(fresh, start, n):
+    """Prefill n positions at once (buckets 64, 1, 2, 4, 8, 8: the decode
+    block, the two-row GEMV, the few-row kernel), then decode the same
+    positions one at a time through the decode kernels: the KV rows and the
+    last logits agree."""
     m, cfg = fresh, fresh.cfg
-    start, n = 8, 40
-    toks = _tokens(m, n, 1)
+    toks = _tokens(m, n, 1 + n)
     assert m.prefill(toks, start, graphed=False)
     kv = [(b.attention.kv_cache.k_cache[:, :, start:start + n].clone(),
            b.attention.kv_cache.v_cache[:, :, start:start + n].clone()) for b in m.layers]
@@ -296,21 +300,29 @@ def test_prompt_prefill_matches_position_by_position_decode(fresh):
 
 
 @pytest.mark.gpu
-def test_graph_prefill_equals_the_eager_span(fresh):
+@pytest.mark.parametrize("n,bucket", [(100, 128), (1, 1), (2, 2), (3, 4), (6, 8)])
+def test_graph_prefill_equals_the_eager_span(fresh, n, bucket):
+    """One span padded to its bucket: three graph replays, each with eager
+    work and synchronisation between them, equal the eager span bit for bit
+    (logits, token and the K rows of every layer)."""
+    from ttspipe_amd.dualar import prefill_spans
+
     m = fresh
-    toks = _tokens(m, 100, 2)  # one span, padded to the 128 bucket
-    assert m.prefill(toks, 0, graphed=False)
+    assert prefill_spans(n) == [(0, n, bucket)]
+    toks = _tokens(m, n, 2 + n)
+    start = 5
+    assert m.prefill(toks, start, graphed=False)
     eager = (m.logits.clone(), int(m.prefill_token.item()),
-             [b.attention.kv_cache.k_cache[:, :, :100].clone() for b in m.layers])
-    m.capture_prefill([128])
+             [b.attention.kv_cache.k_cache[:, :, start:start + n].clone() for b in m.layers])
+    m.capture_prefill([bucket])
     for _ in range(3):
         m.logits.zero_()
         torch.cuda.synchronize()
-        assert m.prefill(toks, 0, graphed=True)
+        assert m.prefill(toks, start, graphed=True)
         torch.cuda.synchronize()
         assert torch.equal(m.logits, eager[0]) and int(m.prefill_token.item()) == eager[1]
         for kc, b in zip(eager[2], m.layers):
-            assert torch.equal(kc, b.attention.kv_cache.k_cache[:, :, :100])
+            assert torch.equal(kc, b.attention.kv_cache.k_cache[:, :, start:start + n])
 
 
 @pytest.mark.gpu

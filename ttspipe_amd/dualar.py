@@ -69,9 +69,11 @@ class DualARConfig:
 
 
 #: Padded span lengths a prompt is prefilled at; longer prompts go through in
-#: spans of the largest (the reference's buckets stop at 32 because its MMA
-#: kernel takes at most 32 rows, graphs.py:137; the GEMM here takes any).
-PREFILL_BUCKETS = (16, 32, 64, 128, 256, 512)
+#: spans of the largest. The reference pads to 1, 2, 4, 8, 16 or 32 rows
+#: (graphs.py:137; its MMA kernel takes at most 32); the GEMM here takes any
+#: row count, so the buckets go on to 512. A 1-position span runs the decode
+#: block (the GEMV), 2 positions the two-row GEMV, 4-64 the few-row kernel.
+PREFILL_BUCKETS = (1, 2, 4, 8, 16, 32, 64, 128, 256, 512)
 
 def prefill_spans(n: int):
     """(offset, real length, bucket) of each span an n-token prompt is
