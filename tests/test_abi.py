@@ -240,6 +240,31 @@ def test_benchmark_byte_counts():
     assert bench.fused_layer_bytes() == 52_186_204 - saved == 52_149_332
 
 
+def test_roofline_figures_are_keyed_to_the_launch_they_measured():
+    """bench.py's off-line GEMV figures (rocprof durations, counter traffic)
+    carry the launch they were measured on - shape, grid and a digest of the
+    kernel source - and are printed only while it matches the launch the bench
+    makes: the committed figures match the current kernel, and any other key
+    reads as stale."""
+    import bench
+
+    key = bench.gemv_launch_key(9728, 2560)
+    assert key == bench.GEMV_PROFILE["key"], "nf4_gemv.hip or its launch changed: re-profile and update GEMV_PROFILE"
+    kern = {"M": 9728, "K": 2560, "sec": 6e-6, "bytes": bench.nf4_bytes(9728, 2560, True), "gbs": 2145.4}
+    line = bench.roofline_entry(kern)
+    assert line["traffic"] == bench.GEMV_PROFILE["traffic_bytes"] and "stale" not in line
+    assert line["rocprof"]["median_us"] == bench.GEMV_PROFILE["rocprof_median_us"]
+    assert abs(line["frac"] - 2145.4 / 8000) < 1e-4
+    saved = dict(bench.GEMV_PROFILE["key"])
+    try:
+        bench.GEMV_PROFILE["key"]["source_sha16"] = "0" * 16
+        line = bench.roofline_entry(kern)
+        assert line["traffic"] is None and "rocprof" not in line and "stale" in line
+    finally:
+        bench.GEMV_PROFILE["key"].clear()
+        bench.GEMV_PROFILE["key"].update(saved)
+
+
 def test_dualar_specs_and_byte_account():
     from ttspipe_amd import dualar
 

@@ -634,3 +634,34 @@ def prefill_benchmark(n_tokens: int = 512, reps: int = 5, cfg: DualARConfig = Du
     torch.cuda.empty_cache()
     return {"tokens": n_tokens, "ms": round(ms, 3), "tokens_per_s": round(n_tokens / ms * 1e3, 1),
             "first_token": token, "layers": cfg.n_layer}
+
+
+def prefill_tail_benchmark(sizes=(1, 2, 4, 8, 16, 32), start: int = 512, reps: int = 20,
+                           cfg: DualARConfig = DualARConfig()) -> dict:
+    """ms to prefill a prompt tail of n tokens after `start` cached positions
+    (the case after a prefix-cache hit, reference streamgen.py:184-253), one
+    captured bucket graph per size, through the 36-layer slow transformer."""
+    import torch
+
+    model = SyntheticDualAR(cfg)
+    g = torch.Generator(device=model.device).manual_seed(cfg.seed + 1)
+    stream = torch.cuda.current_stream()
+    out = []
+    for n in sizes:
+        toks = torch.randint(0, cfg.codebook_size, (cfg.n_tokens, n), generator=g, device=model.device,
+                             dtype=torch.int32)
+        bucket = prefill_spans(n)[-1][2]
+        model.capture_prefill([bucket])
+        assert model.prefill(toks, start)
+        torch.cuda.synchronize()
+        torch.cuda._sleep(200_000)  # the host's first submission overlaps this, not the timed region
+        t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        t0.record(stream)
+        for _ in range(reps):
+            model.prefill(toks, start)
+        t1.record(stream)
+        t1.synchronize()
+        out.append({"tokens": n, "bucket": bucket, "ms": round(t0.elapsed_time(t1) / reps, 3)})
+    del model
+    torch.cuda.empty_cache()
+    return {"after_cached_positions": start, "layers": cfg.n_layer, "points": out}
