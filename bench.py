@@ -51,15 +51,19 @@ SPIN_CYCLES = 200_000
 #: WRITE_SIZE x 1.0): (6444.06 x 1.99925 + 22.81) KiB.
 #: rocprof_*_us: dispatch durations of that kernel in rocprofv3 --kernel-trace
 #: --stats -- python3 bench.py --only kernel (2156 graph-replayed dispatches).
-#: The tracer reads about 10 % above the untraced launch-to-launch interval
-#: (6.52 against 5.92 us in the same session), and 6.2-6.6 us across boxes.
+#: The tracer reads 3-10 % above the untraced launch-to-launch interval (6.04
+#: median against 5.89 us in the same session; 6.2-6.6 us means across boxes).
 GEMV_PROFILE = {
-    "key": {"M": 9728, "K": 2560, "J": 5, "KS": 1, "RPW": 5, "grid": 244, "source_sha16": "d0917e6fce1445d7"},
-    "traffic_bytes": 13_215_856,
-    "rocprof_mean_us": 6.549,
-    "rocprof_median_us": 6.519,
+    "key": {"M": 9728, "K": 2560, "J": 5, "KS": 1, "RPW": 5, "grid": 244, "source_sha16": "49b39e41fae50e2b"},
+    "traffic_bytes": 13_215_868,
+    "rocprof_mean_us": 6.190,
+    "rocprof_median_us": 6.039,
     "summary": "profiles/nf4_gemv_gate_9728x2560_bf16_nested.md",
 }
+
+
+#: the GEMV's translation unit: its source and the headers it includes
+GEMV_SOURCES = ("nf4_gemv.hip", "gemv_common.h", "attn_common.h", "ttsp_common.h")
 
 
 def gemv_launch_key(M: int, K: int) -> dict:
@@ -72,9 +76,11 @@ def gemv_launch_key(M: int, K: int) -> dict:
     J, KS, RPW = ctypes.c_int(), ctypes.c_int(), ctypes.c_int()
     _lib.load().ttsp_gemv_shape(M, K, ctypes.byref(J), ctypes.byref(KS), ctypes.byref(RPW))
     rows_wg = (8 // KS.value) * RPW.value
-    src = ROOT / "ttspipe_amd" / "csrc" / "nf4_gemv.hip"
+    h = hashlib.sha256()
+    for name in GEMV_SOURCES:
+        h.update((ROOT / "ttspipe_amd" / "csrc" / name).read_bytes())
     return {"M": M, "K": K, "J": J.value, "KS": KS.value, "RPW": RPW.value, "grid": -(-M // rows_wg),
-            "source_sha16": hashlib.sha256(src.read_bytes()).hexdigest()[:16]}
+            "source_sha16": h.hexdigest()[:16]}
 
 
 def spin():

@@ -33,6 +33,35 @@ extern "C" {
 enum { TTSP_F16 = 0, TTSP_BF16 = 1, TTSP_F32 = 2 };
 enum { TTSP_EPI_NONE = 0, TTSP_EPI_RESIDUAL = 1, TTSP_EPI_SILU_GATE = 2 };
 
+/* One NF4 weight as ttsp_nf4_gemm takes it (A8 == NULL: plain scales). */
+typedef struct ttsp_nf4_weight {
+  const uint8_t* W;
+  const uint8_t* A8;
+  const float* AMAX;
+  const float* CODE2;
+  float offset;
+} ttsp_nf4_weight;
+
+/* One fast-transformer layer for ttsp_fast_steps: its weights, RMSNorm
+ * weights (q_norm / k_norm NULL without head norms) and KV cache
+ * [n_kv][max_len][128]. */
+typedef struct ttsp_fast_layer {
+  ttsp_nf4_weight wqkv, wo, w1, w3, w2;
+  const void* attention_norm;
+  const void* ffn_norm;
+  const void* q_norm;
+  const void* k_norm;
+  void* k_cache;
+  void* v_cache;
+} ttsp_fast_layer;
+
+/* ttsp_fast_steps' barrier words: TTSP_FAST_SYNC_WORDS uint32, zero before the
+ * first launch; a launch leaves them zero except word TTSP_FAST_SYNC_FAILED,
+ * the count of barrier waits that gave up (sticky until the caller clears it). */
+enum { TTSP_FAST_SYNC_WORDS = 192, TTSP_FAST_SYNC_FAILED = 128 };
+
+#ifndef TTSP_HIP_TYPES_ONLY
+
 /* Y[N][M] = epi(X[N][K] . dequant(W)^T). N == 1 runs the HBM-bound GEMV (rows
  * of up to 32768 codes; a longer row takes the tiled kernel), N > 1 the MFMA
  * GEMM (LDS-staged dequantisation; from 256 to 512 rows on large shapes,
@@ -310,6 +339,45 @@ int ttsp_frame_advance(const int* tokens, int ntok, int* history, int rows, long
  * of the synthetic benchmark model on the device. */
 int ttsp_synth_fill(void* out, long long n, unsigned long long seed, int kind, float scale,
                     float offset, void* stream);
+
+/* The fast transformer's codebook steps in one launch: for step i = step0 ..
+ * step0 + n_steps - 1 (fast position i, rotary row F[i] of ftype), the
+ * n_layers decode blocks (ttsp_nf4_gemv_fused with the norm, the attention
+ * and wo as ttsp_attn_nf4_gemv, w1/w3 SwiGLU, w2 with the residual), the
+ * final norm (fast_norm) and head, then tokens[i + 1] = argmax of the logits
+ * (lowest index on ties), whose clamped row of emb [vocab][dim] is the next
+ * step's input; x0 [dim] is the first step's input. logits [vocab] keeps the
+ * last step's. The same bits as that launch sequence (one launch per block
+ * half, head and ttsp_argmax_embed per step). Workgroups meet at grid
+ * barriers in `sync` (TTSP_FAST_SYNC_WORDS words, zero before the first
+ * launch); a wait is bounded, and one that gives up counts in
+ * sync[TTSP_FAST_SYNC_FAILED] (the results are then not valid). work:
+ * ttsp_fast_steps_work_bytes() bytes of activations. Served shapes:
+ * ttsp_fast_steps_grid() > 0 (every phase unsplit along K as the GEMV runs
+ * it: dim and n_head * 128 of 1024 with FFN 3072, or all of them at most
+ * 512; <= 4 layers, <= 8 query heads, max_len <= 64); others, and grids the
+ * device cannot hold at once, return hipErrorInvalidValue. Positions must lie
+ * in [0, max_len). All weights share blocksize and nesting. Replaces: the
+ * codebook loop of sample_frame, app/engine/graphs.py:126-131 (per step:
+ * _fast_step over the fast layers and head, _sample, _fast_embed), greedy. */
+int ttsp_fast_steps(const ttsp_fast_layer* layers, int n_layers, const ttsp_nf4_weight* head,
+                    const void* fast_norm, const void* emb, const float* LUT, const void* F, int ftype,
+                    const void* x0, void* work, unsigned* sync, void* logits, int* tokens, int dim, int n_head,
+                    int n_kv, int inter, int vocab, int max_len, int step0, int n_steps, float eps,
+                    int blocksize, int blocksize2, int dtype, void* stream);
+
+/* Workgroups ttsp_fast_steps launches for these shapes, 0 when it does not
+ * serve them (host-only). Replaces: nothing separate (the reference always
+ * runs the loop as separate launches). */
+int ttsp_fast_steps_grid(int dim, int n_head, int n_kv, int inter, int vocab, int max_len, int n_layers,
+                         int blocksize);
+
+/* Bytes of ttsp_fast_steps' activation workspace (host-only). Replaces: the
+ * fast transformer's activation buffers inside the captured frame
+ * (graphs.py:126-131). */
+int ttsp_fast_steps_work_bytes(int dim, int n_head, int n_kv, int inter);
+
+#endif /* TTSP_HIP_TYPES_ONLY */
 
 #ifdef __cplusplus
 }

@@ -319,3 +319,84 @@ def test_dualar_oracle_decode_is_deterministic_and_in_range(orc):
     assert np.array_equal(a, b)
     assert (a[:, 0] < cfg.vocab_size).all() and (a[:, 1:] < cfg.codebook_size).all() and (a >= 0).all()
     assert (a[:, 1] == np.minimum(a[:, 0], cfg.codebook_size - 1)).all()
+
+
+def test_fast_steps_argument_blocks_match_the_header(tmp_path):
+    """`ttsp_nf4_weight` / `ttsp_fast_layer` as the C compiler lays them out
+    from the header, against the ctypes mirrors the Python side passes."""
+    import subprocess
+
+    from ttspipe_amd import _lib
+
+    src = tmp_path / "layout.c"
+    src.write_text(
+        '#include <stddef.h>\n#include <stdio.h>\n#include "ttsp_hip.h"\n'
+        "int main(void) {\n"
+        '  printf("%zu %zu %zu %zu %zu %zu\\n", sizeof(ttsp_nf4_weight), offsetof(ttsp_nf4_weight, offset),\n'
+        "         sizeof(ttsp_fast_layer), offsetof(ttsp_fast_layer, w2), offsetof(ttsp_fast_layer, attention_norm),\n"
+        "         offsetof(ttsp_fast_layer, v_cache));\n"
+        '  printf("%d %d\\n", TTSP_FAST_SYNC_WORDS, TTSP_FAST_SYNC_FAILED);\n'
+        "  return 0;\n}\n")
+    exe = tmp_path / "layout"
+    subprocess.run(["gcc", "-std=c99", f"-I{ROOT / 'include'}", str(src), "-o", str(exe)], check=True)
+    lines = subprocess.run([str(exe)], check=True, capture_output=True, text=True).stdout.split("\n")
+    got = [int(v) for v in lines[0].split()]
+    W, L = _lib.Nf4Weight, _lib.FastLayer
+    assert got == [ctypes.sizeof(W), W.offset.offset, ctypes.sizeof(L), L.w2.offset, L.attention_norm.offset,
+                   L.v_cache.offset]
+    assert [int(v) for v in lines[1].split()] == [_lib.FAST_SYNC_WORDS, _lib.FAST_SYNC_FAILED]
+
+
+def test_fast_steps_serves_the_fast_transformer_shapes():
+    """The one-launch codebook loop's shape plan (host-only): the benchmark's
+    fast transformer (d 1024, 8/2 heads, FFN 3072, codebook 4096) on 128
+    workgroups, the reduced model's on 64; shapes the GEMV would split along K,
+    more than 8 query heads, caches past one 64-position chunk, more than 4
+    layers and blocks under 64 codes are declined (0)."""
+    from ttspipe_amd import _lib
+    from ttspipe_amd.dualar import SMALL, DualARConfig
+
+    lib = _lib.load()
+
+    def grid(c, **kw):
+        a = dict(dim=c.fast_dim, n_head=c.fast_n_head, n_kv=c.fast_n_local_heads, inter=c.fast_intermediate_size,
+                 vocab=c.codebook_size, max_len=c.fast_max_len, n_layers=c.fast_n_layer, blocksize=64)
+        a.update(kw)
+        return lib.ttsp_fast_steps_grid(*a.values())
+
+    big = DualARConfig()
+    assert grid(big) == 128
+    assert grid(SMALL) == 64
+    for kw in ({"dim": 2560}, {"inter": 9728}, {"n_head": 16, "n_kv": 4}, {"max_len": 65}, {"n_layers": 5},
+               {"n_layers": 0}, {"blocksize": 32}, {"blocksize": 96}, {"n_head": 6, "n_kv": 4}, {"vocab": 0}):
+        assert grid(big, **kw) == 0, kw
+    # the phases' K splits as the GEMV's own plan gives them: all 1
+    for M, K in ((1536, 1024), (1024, 1024), (3072, 1024), (1024, 3072), (4096, 1024)):
+        assert _shape(M, K)[2] == 1
+    qkv = (big.fast_n_head + 2 * big.fast_n_local_heads) * 128
+    rb = lambda e: -(-2 * e // 256) * 256  # noqa: E731
+    assert lib.ttsp_fast_steps_work_bytes(1024, 8, 2, 3072) == rb(qkv) + 2 * rb(1024) + rb(3072)
+    assert lib.ttsp_fast_steps_work_bytes(0, 8, 2, 3072) == 0
+
+
+def test_fast_steps_rejects_bad_arguments_before_any_launch():
+    """Null pointers, positions past the cache and unserved shapes return
+    hipErrorInvalidValue (1) on the host."""
+    from ttspipe_amd import _lib
+
+    lib = _lib.load()
+    layers = (_lib.FastLayer * 4)()
+    head = _lib.Nf4Weight()
+    p = 4096  # never dereferenced: every case returns before a launch
+
+    def call(dim=1024, max_len=16, step0=1, n_steps=9, x0=p, n_layers=4):
+        return lib.ttsp_fast_steps(layers, n_layers, head, p, p, p, p, 1, x0, p, p, p, p, dim, 8, 2, 3072, 4096,
+                                   max_len, step0, n_steps, 1e-6, 64, 256, _lib.DT_BF16, None)
+
+    assert call(x0=None) == 1
+    assert call(step0=8, n_steps=9) == 1  # positions 8 .. 16 run past a 16-row cache
+    assert call(step0=-1) == 1
+    assert call(n_steps=0) == 1
+    assert call(dim=2560) == 1
+    assert call(n_layers=5) == 1
+    assert call() == 1  # the weights' pointers are NULL

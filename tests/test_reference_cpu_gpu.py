@@ -117,6 +117,7 @@ def test_teacher_forced_frames_agree_with_the_reference_cpu_path(which, frames):
 
     cfg = SMALL if which == "small" else DualARConfig()
     model = SyntheticDualAR(cfg)
+    assert not model.use_fast_steps  # the per-head logits come from the per-launch heads
     cpu = CpuReferenceDualAR(cfg, weights_from_gpu_model(model))
     log = []
     orig = SyntheticDualAR._fused

@@ -29,6 +29,25 @@ _i = ctypes.c_int
 _f = ctypes.c_float
 _ll = ctypes.c_longlong
 
+
+
+class Nf4Weight(ctypes.Structure):
+    """`ttsp_nf4_weight`: one NF4 weight's device pointers (A8 NULL: plain scales)."""
+
+    _fields_ = [("W", _vp), ("A8", _vp), ("AMAX", _vp), ("CODE2", _vp), ("offset", _f)]
+
+
+class FastLayer(ctypes.Structure):
+    """`ttsp_fast_layer`: one fast-transformer layer for `ttsp_fast_steps`."""
+
+    _fields_ = [("wqkv", Nf4Weight), ("wo", Nf4Weight), ("w1", Nf4Weight), ("w3", Nf4Weight), ("w2", Nf4Weight),
+                ("attention_norm", _vp), ("ffn_norm", _vp), ("q_norm", _vp), ("k_norm", _vp), ("k_cache", _vp),
+                ("v_cache", _vp)]
+
+
+#: `ttsp_fast_steps`' barrier words and the index of its failed-wait count.
+FAST_SYNC_WORDS, FAST_SYNC_FAILED = 192, 128
+
 #: name -> argtypes (restype is int for all of them)
 SIGNATURES: dict[str, list] = {
     "ttsp_nf4_gemm": [_vp, _i, _vp, _vp, _vp, _vp, _f, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _vp],
@@ -65,6 +84,10 @@ SIGNATURES: dict[str, list] = {
     "ttsp_argmax_embed": [_vp, _i, _i, _vp, _vp, _vp, _i, _i, _vp, _vp],
     "ttsp_frame_advance": [_vp, _i, _vp, _i, _vp, _vp, _vp, _i, _i, _vp, _vp],
     "ttsp_synth_fill": [_vp, _ll, ctypes.c_ulonglong, _i, _f, _f, _vp],
+    "ttsp_fast_steps": [ctypes.POINTER(FastLayer), _i, ctypes.POINTER(Nf4Weight), _vp, _vp, _vp, _vp, _i, _vp, _vp,
+                        _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _i, _i, _f, _i, _i, _i, _vp],
+    "ttsp_fast_steps_grid": [_i, _i, _i, _i, _i, _i, _i, _i],
+    "ttsp_fast_steps_work_bytes": [_i, _i, _i, _i],
 }
 
 

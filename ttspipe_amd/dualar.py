@@ -314,6 +314,12 @@ class SyntheticDualAR:
         self.logits = torch.empty(1, cfg.vocab_size, dtype=bf, device=dev)
         self.fast_h = torch.empty(1, 1, cfg.fast_dim, dtype=bf, device=dev)
         self.fast_logits = torch.empty(1, cfg.codebook_size, dtype=bf, device=dev)
+        # the codebook loop as one launch (ttsp_fast_steps), where it serves these
+        # shapes, on request: the same bits, but measured slower on MI355X than
+        # the graph-replayed launches (its grid barriers cost more than a launch)
+        self.use_fast_steps = False
+        self.fast_sync = torch.zeros(_lib.FAST_SYNC_WORDS, dtype=torch.int32, device=dev)
+        self._fast_args = self._fast_steps_args()
         self.graph = None
         # prompt prefill: the fork's causal mask rows, one captured graph per bucket
         self.causal = torch.tril(torch.ones(cfg.max_seq_len, cfg.max_seq_len, dtype=torch.bool, device=dev))
@@ -388,6 +394,97 @@ class SyntheticDualAR:
             raise RuntimeError("the fused matmul declined a head of the synthetic model")
         return y
 
+    def _fast_steps_args(self):
+        """`ttsp_fast_steps`' arguments for this model's fast transformer (the
+        codebook loop in one launch), or None where that launch does not serve
+        its shapes: the loop then runs launch by launch, with the same bits."""
+        import torch
+
+        cfg = self.cfg
+        n_steps = cfg.num_codebooks - 1
+        if n_steps < 1 or cfg.num_codebooks > cfg.fast_max_len:  # fast positions 1 .. n_steps
+            return None
+        lins = [self.fast_output]
+        for blk in self.fast_layers:
+            a, ff = blk.attention, blk.feed_forward
+            lins += [a.wqkv, a.wo, ff.w1, ff.w3, ff.w2]
+        fast = [getattr(lin, "_nf4_fast", None) for lin in lins]
+        if any(f is None for f in fast) or len({(f["bs"], f["bs2"], f["nested"]) for f in fast}) != 1:
+            return None
+        norms = [blk.attention_norm for blk in self.fast_layers] + [blk.ffn_norm for blk in self.fast_layers]
+        if cfg.qk_norm:
+            norms += [blk.attention.q_norm for blk in self.fast_layers] + [blk.attention.k_norm for blk in self.fast_layers]
+        if any(float(m.eps) != float(cfg.norm_eps) for m in norms):
+            return None
+        bs, bs2 = fast[0]["bs"], fast[0]["bs2"]
+        grid = self._lib.ttsp_fast_steps_grid(cfg.fast_dim, cfg.fast_n_head, cfg.fast_n_local_heads,
+                                              cfg.fast_intermediate_size, cfg.codebook_size, cfg.fast_max_len,
+                                              cfg.fast_n_layer, bs)
+        ftype = _lib.dtype_code(self.fast_freqs.dtype)
+        if grid <= 0 or ftype is None or not self.fast_freqs.is_contiguous():
+            return None
+
+        def weight(lin):
+            f = lin._nf4_fast
+            return _lib.Nf4Weight(f["w"], f["a8"] or None, f["amax"], f["code2"] or None, f["offset"])
+
+        layers = (_lib.FastLayer * cfg.fast_n_layer)()
+        for i, blk in enumerate(self.fast_layers):
+            a, ff = blk.attention, blk.feed_forward
+            layers[i] = _lib.FastLayer(
+                weight(a.wqkv), weight(a.wo), weight(ff.w1), weight(ff.w3), weight(ff.w2),
+                blk.attention_norm.weight.data_ptr(), blk.ffn_norm.weight.data_ptr(),
+                a.q_norm.weight.data_ptr() if cfg.qk_norm else None,
+                a.k_norm.weight.data_ptr() if cfg.qk_norm else None,
+                a.kv_cache.k_cache.data_ptr(), a.kv_cache.v_cache.data_ptr())
+        nbytes = self._lib.ttsp_fast_steps_work_bytes(cfg.fast_dim, cfg.fast_n_head, cfg.fast_n_local_heads,
+                                                     cfg.fast_intermediate_size)
+        work = torch.empty(nbytes, dtype=torch.uint8, device=self.device)
+        return {"layers": layers, "head": weight(self.fast_output), "work": work, "grid": grid, "ftype": ftype,
+                "lut": fast[0]["lut"], "bs": bs, "bs2": bs2, "n_steps": n_steps}
+
+    def fast_steps_failed(self) -> int:
+        """Grid-barrier waits of `ttsp_fast_steps` that gave up since the model
+        was built (0 unless the launch's workgroups were not all resident)."""
+        return int(self.fast_sync[_lib.FAST_SYNC_FAILED].item())
+
+    def check_fast_steps(self) -> None:
+        """Raise if a `ttsp_fast_steps` barrier wait gave up (its frames' tokens are then not valid)."""
+        n = self.fast_steps_failed()
+        if n:
+            raise RuntimeError(f"ttsp_fast_steps: {n} grid-barrier waits gave up; the decoded tokens are not valid")
+
+    def _codebook_steps(self, st) -> None:
+        """The codebook loop as one `ttsp_fast_steps` launch: steps 1 .. n-1 at
+        fast positions 1 .. n-1 from `fast_h`, tokens[2 ..] and fast_logits."""
+        cfg, f = self.cfg, self._fast_args
+        rc = self._lib.ttsp_fast_steps(
+            f["layers"], cfg.fast_n_layer, f["head"], self.tensors["fast_norm"].data_ptr(),
+            self.tensors["fast_embeddings"].data_ptr(), f["lut"].data_ptr(), self.fast_freqs.data_ptr(), f["ftype"],
+            self.fast_h.data_ptr(), f["work"].data_ptr(), self.fast_sync.data_ptr(), self.fast_logits.data_ptr(),
+            self.tokens.data_ptr(), cfg.fast_dim, cfg.fast_n_head, cfg.fast_n_local_heads, cfg.fast_intermediate_size,
+            cfg.codebook_size, cfg.fast_max_len, 1, f["n_steps"], float(cfg.norm_eps), f["bs"], f["bs2"],
+            _lib.DT_BF16, st)
+        self._check(rc, "ttsp_fast_steps")
+
+    def _codebook_loop(self, st) -> None:
+        """The codebook loop launch by launch: per step the fast blocks, the
+        fast head, the greedy token and (but for the last) its embedding row."""
+        cfg, lib = self.cfg, self._lib
+        emb = self.tensors["fast_embeddings"].data_ptr()
+        for i in range(1, cfg.num_codebooks):
+            x = self._run_blocks(self.fast_layers, self.fws, self.fast_h, self.fast_freqs[i], self.fast_mask,
+                                 self.fast_pos[i])
+            self._fused(self.fast_output, x.view(1, 1, -1), self.tensors["fast_norm"], cfg.norm_eps, self.fast_logits)
+            tok = self.tokens[i + 1:].data_ptr()
+            if i + 1 < cfg.num_codebooks:  # the token and the next codebook step's embedding
+                rc = lib.ttsp_argmax_embed(self.fast_logits.data_ptr(), cfg.codebook_size, _lib.DT_BF16, tok, None,
+                                           emb, cfg.codebook_size, cfg.fast_dim, self.fast_h.data_ptr(), st)
+                self._check(rc, "ttsp_argmax_embed")
+            else:
+                rc = lib.ttsp_argmax(self.fast_logits.data_ptr(), cfg.codebook_size, _lib.DT_BF16, tok, st)
+                self._check(rc, "ttsp_argmax")
+
     def step(self) -> None:
         """One frame: tokens (device) at position pos -> next frame's tokens; pos += 1."""
         cfg, lib, st = self.cfg, self._lib, _lib.stream()
@@ -412,18 +509,10 @@ class SyntheticDualAR:
                                    self.tokens[1:].data_ptr(), emb, cfg.codebook_size, cfg.fast_dim,
                                    self.fast_h.data_ptr(), st)
         self._check(rc, "ttsp_argmax_embed")
-        for i in range(1, cfg.num_codebooks):
-            x = self._run_blocks(self.fast_layers, self.fws, self.fast_h, self.fast_freqs[i], self.fast_mask,
-                                 self.fast_pos[i])
-            self._fused(self.fast_output, x.view(1, 1, -1), self.tensors["fast_norm"], cfg.norm_eps, self.fast_logits)
-            tok = self.tokens[i + 1:].data_ptr()
-            if i + 1 < cfg.num_codebooks:  # the token and the next codebook step's embedding
-                rc = lib.ttsp_argmax_embed(self.fast_logits.data_ptr(), cfg.codebook_size, _lib.DT_BF16, tok, None,
-                                           emb, cfg.codebook_size, cfg.fast_dim, self.fast_h.data_ptr(), st)
-                self._check(rc, "ttsp_argmax_embed")
-            else:
-                rc = lib.ttsp_argmax(self.fast_logits.data_ptr(), cfg.codebook_size, _lib.DT_BF16, tok, st)
-                self._check(rc, "ttsp_argmax")
+        if self.use_fast_steps and self._fast_args is not None:
+            self._codebook_steps(st)
+        else:
+            self._codebook_loop(st)
         # bookkeeping on the device: history row, step and position, the next rotary row
         rc = lib.ttsp_frame_advance(self.tokens.data_ptr(), cfg.n_tokens, self.history.data_ptr(),
                                     self.history.shape[0], self.step_index.data_ptr(), self.pos.data_ptr(),
@@ -547,6 +636,7 @@ class SyntheticDualAR:
             else:
                 self.step()
         torch.cuda.synchronize()
+        self.check_fast_steps()
         return self.history[:n_steps].cpu().numpy()
 
 
@@ -576,11 +666,15 @@ def step_bytes(cfg: DualARConfig, pos: int) -> int:
     return slow + fast_passes * sum(fast_layer) + prime + heads + slow_kv + fast_kv + emb + norms
 
 
-def benchmark(n_steps: int = 256, warmup: int = 8, cfg: DualARConfig = DualARConfig()) -> dict:
-    """ms per frame over `n_steps` graph-replayed greedy steps (one MI355X)."""
+def benchmark(n_steps: int = 256, warmup: int = 8, cfg: DualARConfig = DualARConfig(),
+              fast_steps: bool = False) -> dict:
+    """ms per frame over `n_steps` graph-replayed greedy steps (one MI355X);
+    fast_steps True runs the codebook loop as one `ttsp_fast_steps` launch."""
     import torch
 
     model = SyntheticDualAR(cfg)
+    model.use_fast_steps = fast_steps
+    one_launch = fast_steps and model._fast_args is not None
     model.reset(max(n_steps, warmup))  # the history the graph writes: grown before capture
     model.capture()
     model.reset(max(n_steps, warmup))
@@ -595,12 +689,13 @@ def benchmark(n_steps: int = 256, warmup: int = 8, cfg: DualARConfig = DualARCon
         model.graph.replay()
     end.record(stream)
     end.synchronize()
+    model.check_fast_steps()
     ms = start.elapsed_time(end) / n_steps
     hist = model.history[:n_steps].cpu().numpy()
     nbytes = sum(step_bytes(cfg, cfg.prefill_len + i) for i in range(n_steps)) / n_steps
     del model
     torch.cuda.empty_cache()
-    return {"ms_per_step": round(ms, 4), "steps": n_steps, "bytes_per_step": int(nbytes),
+    return {"ms_per_step": round(ms, 4), "steps": n_steps, "bytes_per_step": int(nbytes), "fast_steps": one_launch,
             "achieved_gbs": round(nbytes / (ms * 1e-3) / 1e9, 1),
             "tokens_first_step": hist[0].tolist(), "tokens_last_step": hist[-1].tolist(),
             "config": f"slow {cfg.n_layer}x d{cfg.dim} ({cfg.n_head}q/{cfg.n_local_heads}kv x{cfg.head_dim}, "
