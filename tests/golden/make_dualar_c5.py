@@ -18,7 +18,8 @@ records:
 * sha256 digests of the K and V cache rows written at frames 0, 128 and 255
   in slow layers 0, 17 and 35, and of the rotary tables the frame used.
 
-Run from the repository root (about 16 minutes on 8 cores):
+Run from the repository root (about 21 minutes on 8 cores; the fixture records the run's
+seconds in `cpu_seconds`: 1,260.6):
 
     python -m tests.golden.make_dualar_c5 [--frames 256]
 
