@@ -387,9 +387,43 @@ def bench_gemm(rows: int = 512, copies: int = 4, reps: int = 20):
         total_s += sec
         total_flop += flop
         del lins
-    return {"rows": rows, "projections": res, "layer_us": round(total_s * 1e6, 1),
-            "tflops": round(total_flop / total_s / 1e12, 1),
-            "pct_of_mfma_peak": round(100 * total_flop / total_s / 1e12 / MFMA_PEAK_TFLOPS, 2)}
+    out = {"rows": rows, "projections": res, "layer_us": round(total_s * 1e6, 1),
+           "tflops": round(total_flop / total_s / 1e12, 1),
+           "pct_of_mfma_peak": round(100 * total_flop / total_s / 1e12 / MFMA_PEAK_TFLOPS, 2)}
+    # gate and up as the prefill block runs them: one SwiGLU launch
+    (_, M, K), = [p for p in LAYER if p[0] == "gate"]
+    if lib.ttsp_nf4_gemm_swiglu_fits(M, K, rows, 64, 256, 1):
+        pairs = [(Linear(M, K, True, seed=700 + c, device=dev), Linear(M, K, True, seed=750 + c, device=dev))
+                 for c in range(copies)]
+        x = torch.randn(rows, K, device=dev).to(torch.bfloat16)
+        y = torch.empty(rows, M, dtype=torch.bfloat16, device=dev)
+
+        def body_sw():
+            st = torch.cuda.current_stream().cuda_stream
+            for l1, l3 in pairs:
+                rc = lib.ttsp_nf4_gemm_swiglu(x.data_ptr(), _lib.DT_BF16, l1.w.data_ptr(), l1.a8.data_ptr(),
+                                              l1.amax.data_ptr(), l1.code2.data_ptr(), l1.offset, l3.w.data_ptr(),
+                                              l3.a8.data_ptr(), l3.amax.data_ptr(), l3.code2.data_ptr(), l3.offset,
+                                              lut.data_ptr(), y.data_ptr(), M, K, rows, 64, 256, st)
+                if rc:
+                    raise RuntimeError(f"ttsp_nf4_gemm_swiglu failed: {rc}")
+
+        body_sw()
+        torch.cuda.synchronize()
+        graph = capture(body_sw)
+        stream = torch.cuda.current_stream()
+        time_graph(graph, 2, stream)
+        sec = time_graph(graph, reps, stream) / copies
+        flop = 2 * 2 * rows * M * K
+        sep = sum(r["us"] for r in res if r["name"] in ("gate", "up")) * 1e-6
+        layer = total_s - sep + sec
+        out["swiglu_gate_up"] = {"us": round(sec * 1e6, 2), "tflops": round(flop / sec / 1e12, 1),
+                                 "two_launches_us": round(sep * 1e6, 2)}
+        out["layer_us_with_one_swiglu_launch"] = round(layer * 1e6, 1)
+        out["pct_of_mfma_peak_with_one_swiglu_launch"] = round(
+            100 * total_flop / layer / 1e12 / MFMA_PEAK_TFLOPS, 2)
+        del pairs
+    return out
 
 
 def bench_small_n(ns=(1, 2, 4, 8, 16, 32), min_bytes: int = 2 * MALL_BYTES, replays: int = 20):

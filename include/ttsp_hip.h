@@ -95,6 +95,26 @@ int ttsp_nf4_gemm_split(const void* X, int x_dtype, const uint8_t* W, const uint
                         void* Y, const void* R, int epi, int M, int K, int N, int blocksize,
                         int blocksize2, float* work, int splits, void* stream);
 
+/* The SwiGLU pair of a multi-row forward in one launch:
+ * Y[N][M] = round(round(silu(round(X . W1^T))) * round(X . W3^T)), W1 and W3
+ * of one shape [M, K] with the same blocksize and nesting, every value the
+ * bits of ttsp_nf4_gemm(W1) then ttsp_nf4_gemm(W3, epi 2, R = the first's
+ * output). Served where both of those would run the direct-to-LDS kernel
+ * unsplit (ttsp_nf4_gemm_swiglu_fits; e.g. 385-512 rows of 9728 x 2560); other
+ * shapes return hipErrorInvalidValue and the caller runs the two launches.
+ * 16-byte aligned X, W1, W3. Replaces: w1 then w3 with the SwiGLU gate in
+ * the fork's FeedForward for S > 1 (the unfused block the reference runs
+ * there, fastpath.py:207-271, through nf4gemv.matmul twice). */
+int ttsp_nf4_gemm_swiglu(const void* X, int x_dtype, const uint8_t* W1, const uint8_t* A8_1,
+                         const float* AMAX_1, const float* CODE2_1, float offset_1, const uint8_t* W3,
+                         const uint8_t* A8_3, const float* AMAX_3, const float* CODE2_3, float offset_3,
+                         const float* LUT, void* Y, int M, int K, int N, int blocksize, int blocksize2,
+                         void* stream);
+
+/* 1 where ttsp_nf4_gemm_swiglu serves [M, K] weights over N rows (nested:
+ * double-quant scales), else 0. Host-only. Replaces: nothing separate. */
+int ttsp_nf4_gemm_swiglu_fits(int M, int K, int N, int blocksize, int blocksize2, int nested);
+
 /* The batch-1 matmuls of a decode block in one launch each (K <= 32768,
  * K <= 4096 with NORM_W; ttsp_gemv_shape says whether a shape fits):
  *   W3 == NULL: Y = epi(n(X) . dequant(W1)^T), epi as ttsp_nf4_gemm;

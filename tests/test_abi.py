@@ -400,3 +400,27 @@ def test_fast_steps_rejects_bad_arguments_before_any_launch():
     assert call(dim=2560) == 1
     assert call(n_layers=5) == 1
     assert call() == 1  # the weights' pointers are NULL
+
+
+def test_swiglu_gemm_plan_on_the_host():
+    """`ttsp_nf4_gemm_swiglu_fits`: one launch where both GEMMs of the pair
+    would run the direct-to-LDS kernel unsplit (up to 512 rows, >= 512 tiles
+    of 64 x 128 with fewer than 64 K-steps: 385-512 rows of 9728 x 2560),
+    nowhere else; the entry rejects a
+    shape it does not serve before any launch."""
+    from ttspipe_amd import _lib
+
+    lib = _lib.load()
+    fits = lib.ttsp_nf4_gemm_swiglu_fits
+    assert fits(9728, 2560, 512, 64, 256, 1) == 1
+    assert fits(9728, 2560, 400, 64, 256, 0) == 1
+    assert fits(9730, 2560, 500, 64, 256, 1) == 1
+    for args in ((2560, 9728, 512, 64, 256, 1), (9728, 2560, 128, 64, 256, 1), (9728, 2560, 256, 64, 256, 1), (9728, 2560, 513, 64, 256, 1),
+                 (1536, 1024, 512, 64, 256, 1), (9728, 2560, 512, 64, 16, 1), (9728, 2560, 512, 32, 256, 1),
+                 (9728, 2560, 512, 96, 256, 0), (9728, 2500, 512, 64, 256, 1)):
+        assert fits(*args) == 0, args
+    p = 4096
+    assert lib.ttsp_nf4_gemm_swiglu(p, 1, p, p, p, p, 0.0, p, p, p, p, 0.0, p, p, 2560, 9728, 512, 64, 256,
+                                    None) == 1
+    assert lib.ttsp_nf4_gemm_swiglu(p, 1, p, p, p, p, 0.0, p, None, p, p, 0.0, p, p, 9728, 2560, 512, 64, 256,
+                                    None) == 1  # one weight nested, the other plain

@@ -589,3 +589,49 @@ def test_prequantised_checkpoint_serves_the_same_bits(nf4, nested):
     for rows in (1, 24):
         x = from_bits(randn_bits(rows * K, dtype, seed=rows), dtype).view(rows, K)
         assert torch.equal(src(x).view(torch.int16), dst(x).view(torch.int16))
+
+
+# ------------------------------------------------------------ the SwiGLU pair as one GEMM launch
+
+
+@pytest.mark.parametrize("shape,rows,nested,dtype", [((9728, 2560), 512, True, torch.bfloat16),
+                                                     ((9728, 2560), 400, True, torch.bfloat16),
+                                                     ((9728, 2560), 512, False, torch.float16),
+                                                     ((9730, 2560), 500, True, torch.bfloat16),
+                                                     ((9730, 2560), 500, False, torch.float16)])
+def test_swiglu_gemm_equals_the_two_launches(nf4, shape, rows, nested, dtype):
+    """`matmul_swiglu` (one launch: the gate's waves and w3's waves of the
+    same rows meet in LDS) against `matmul(w1)` then `matmul(w3, epi=SILU_GATE)`,
+    bit for bit, including ragged tiles (9730 rows: M % 4 == 2 and a partial
+    64-row tile; 500 activation rows: a partial 128-row tile), plain and nested
+    scales, fp16 and bf16."""
+    from ttspipe_amd import _lib
+
+    M, K = shape
+    lib = _lib.load()
+    assert lib.ttsp_nf4_gemm_swiglu_fits(M, K, rows, 64, 256, int(nested)) == 1
+    w1 = to_linear(random_layer(M, K, nested, seed=M + rows), dtype)
+    w3 = to_linear(random_layer(M, K, nested, seed=M + rows + 1), dtype)
+    x = from_bits(randn_bits(rows * K, dtype, seed=rows + 5, scale=2.0), dtype).view(1, rows, K)
+    got = nf4.matmul_swiglu(w1, w3, x)
+    assert got is not None and got.shape == (1, rows, M)
+    g = nf4.matmul(w1, x)
+    ref = nf4.matmul(w3, x, epi=nf4.EPI_SILU_GATE, operand=g)
+    torch.cuda.synchronize()
+    gb, rb = bits(got), bits(ref)
+    assert np.array_equal(gb, rb), first_mismatch(gb, rb)
+    assert np.abs(o.to_f32(rb, dt_code(dtype))).max() > 0
+
+
+@pytest.mark.parametrize("shape,rows,bs2", [((2560, 9728), 512, 256), ((9728, 2560), 256, 256),
+                                            ((9728, 2560), 512, 16), ((1536, 1024), 512, 256)])
+def test_swiglu_gemm_declines_what_one_launch_does_not_serve(nf4, shape, rows, bs2):
+    """Shapes whose GEMMs the plan splits along K, row counts below the
+    direct-to-LDS kernel's, second-level groups a workgroup's K range could
+    cross twice, and tile counts below its unsplit rule: None (the caller runs
+    the two launches)."""
+    M, K = shape
+    w1 = to_linear(random_layer(M, K, True, seed=3, bs2=bs2), torch.bfloat16)
+    w3 = to_linear(random_layer(M, K, True, seed=4, bs2=bs2), torch.bfloat16)
+    x = from_bits(randn_bits(rows * K, torch.bfloat16, seed=9), torch.bfloat16).view(rows, K)
+    assert nf4.matmul_swiglu(w1, w3, x) is None

@@ -523,6 +523,21 @@ constexpr int GEMV_ROWS_N = 2;
 int gemm_skinny(const void* X, int dt, const uint8_t* W, const uint8_t* A8, const float* AMAX, const float* CODE2,
                 float offset, const float* LUT, void* Y, const void* RES, int epi, int M, int K, int N, int bs_shift,
                 int bs2_shift, hipStream_t st);
+int gemm_dl_swiglu(const void* X, int dt, const uint8_t* W1, const uint8_t* A8_1, const float* AMAX_1,
+                   const float* CODE2_1, float offset_1, const uint8_t* W3, const uint8_t* A8_3,
+                   const float* AMAX_3, const float* CODE2_3, float offset_3, const float* LUT, void* Y, int M, int K,
+                   int N, int bs_shift, int bs2_shift, hipStream_t st);
+
+// Whether the SwiGLU pair fits one launch of the direct-to-LDS kernel: where
+// each of its two GEMMs would run that kernel unsplit (so the one launch
+// gives their bits).
+static bool swiglu_fits(int M, int K, int N, int bs_shift, int bs2_shift, bool nested) {
+  if (M <= 0 || K <= 0 || K % 128 || N <= SKINNY_MAX_N) return false;
+  GemmPlan dl;
+  if (!dl_plan(M, K, N, &dl) || dl.splits != 1 || dl.shape != 4) return false;
+  // the plan's fallback to 64 x 128 tiles for small second-level groups
+  return !(nested && (long long)K > (1LL << (bs_shift + bs2_shift)));
+}
 
 }  // namespace ttsp
 
@@ -595,4 +610,33 @@ extern "C" int ttsp_nf4_gemm_split(const void* X, int x_dtype, const uint8_t* W,
   const bool vec = M % 8 == 0 && (uintptr_t)Y % 16 == 0 && (!epi || (uintptr_t)R % 16 == 0);
   return gemm_mfma(X, x_dtype, W, A8, AMAX, CODE2, offset, LUT, Y, R, epi | (vec ? 4 : 0), M, K, N, bs_shift,
                    bs2_shift, gemm_plan(M, K, N), work, stream);
+}
+
+static int log2_of(int v) {
+  int sh = 0;
+  while (sh < 30 && (1 << sh) < v) ++sh;
+  return (1 << sh) == v ? sh : -1;
+}
+
+extern "C" int ttsp_nf4_gemm_swiglu_fits(int M, int K, int N, int blocksize, int blocksize2, int nested) {
+  const int bs = log2_of(blocksize), bs2 = nested ? log2_of(blocksize2) : 0;
+  if (bs < 6 || bs2 < 0 || K % blocksize) return 0;
+  return swiglu_fits(M, K, N, bs, bs2, nested != 0) ? 1 : 0;
+}
+
+extern "C" int ttsp_nf4_gemm_swiglu(const void* X, int x_dtype, const uint8_t* W1, const uint8_t* A8_1,
+                                    const float* AMAX_1, const float* CODE2_1, float offset_1, const uint8_t* W3,
+                                    const uint8_t* A8_3, const float* AMAX_3, const float* CODE2_3,
+                                    float offset_3, const float* LUT, void* Y, int M, int K, int N, int blocksize,
+                                    int blocksize2, hipStream_t stream) {
+  int bs_shift, bs2_shift;
+  if (int rc = gemm_args(X, W1, A8_1, AMAX_1, CODE2_1, LUT, Y, nullptr, 0, M, K, N, blocksize, blocksize2,
+                         &bs_shift, &bs2_shift))
+    return rc;
+  if (!W3 || !AMAX_3 || (A8_3 != nullptr) != (A8_1 != nullptr) || (A8_3 && !CODE2_3))
+    return (int)hipErrorInvalidValue;
+  if ((uintptr_t)X % 16 || (uintptr_t)W1 % 16 || (uintptr_t)W3 % 16) return (int)hipErrorInvalidValue;
+  if (!swiglu_fits(M, K, N, bs_shift, bs2_shift, A8_1 != nullptr)) return (int)hipErrorInvalidValue;
+  return gemm_dl_swiglu(X, x_dtype, W1, A8_1, AMAX_1, CODE2_1, offset_1, W3, A8_3, AMAX_3, CODE2_3, offset_3, LUT, Y,
+                        M, K, N, bs_shift, bs2_shift, stream);
 }

@@ -125,15 +125,30 @@ __device__ __forceinline__ uint16_t dl_epi(float y, uint16_t r, int ep) {
   return Elem<DT>::store(v);
 }
 
-template <int DT, bool NESTED, int W>
+// The SwiGLU form's second weight (w3): its codes and scales as the first's.
+struct DlMat {
+  const uint8_t* W;
+  const uint8_t* A8;
+  const float* AMAX;
+  const float* CODE2;
+  float offset;
+};
+
+// SW: the SwiGLU form. Waves 0 .. W/2 - 1 take rows of the first weight (w1,
+// the gate), waves W/2 .. W - 1 the same rows of the second (m3, w3); the
+// gate's rounded outputs meet w3's in LDS and the workgroup stores
+// round(round(silu(g)) * round(u)), the two launches' bits.
+template <int DT, bool NESTED, int W, bool SW = false>
 __global__ __launch_bounds__(64 * W) void nf4_gemm_dl_kernel(
     const uint16_t* __restrict__ X, const uint8_t* __restrict__ Wt, const uint8_t* __restrict__ A8,
     const float* __restrict__ AMAX, const float* __restrict__ CODE2, float offset, const float* __restrict__ LUT,
     uint16_t* __restrict__ Y, const uint16_t* __restrict__ R, int epi, int M, int K, int N, int bs_shift,
-    int bs2_shift, float* __restrict__ YP) {
+    int bs2_shift, float* __restrict__ YP, const DlMat m3 = DlMat{}) {
   // the buffer-resource type exists in device code only
 #if defined(__HIP_DEVICE_COMPILE__)
-  constexpr int BM = 32 * W;
+  constexpr int BM = 32 * W;   // weight rows the waves take (SW: BM / 2 of each weight)
+  constexpr int BMO = SW ? BM / 2 : BM;  // output rows a workgroup
+  static_assert(!SW || W % 2 == 0, "the SwiGLU form splits the waves in two");
   constexpr int STAGE = BSTAGE + W * CH + (NESTED ? 0 : W * 256);
   static_assert(16 % W == 0, "activation loads split evenly over the waves");
   constexpr int CPW = 16 / W;
@@ -142,11 +157,20 @@ __global__ __launch_bounds__(64 * W) void nf4_gemm_dl_kernel(
   __shared__ __align__(16) uint8_t ring0[STAGE];
   __shared__ __align__(16) uint8_t ring1[STAGE];
   __shared__ float2 lut2_s[256];
-  __shared__ float code2_s[NESTED ? 256 : 1];
+  __shared__ float code2_s[NESTED ? (SW ? 512 : 256) : 1];
   __shared__ uint8_t a8_s[NESTED ? BM * DL_MAX_STEPS : 1];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int m0 = blockIdx.x * BM, n0 = blockIdx.y * BN;
+  const int m0 = blockIdx.x * BMO, n0 = blockIdx.y * BN;
+  // this wave's weight (SW: the second half of the waves takes w3). The
+  // choice is made on the wave index read from one lane, so the compiler
+  // knows it is uniform: the weight's buffer resource stays in scalar
+  // registers (as a per-lane value it would wrap each load in a loop).
+  const bool w3 = SW && __builtin_amdgcn_readfirstlane(wave) >= W / 2;
+  const uint8_t* const Wm = w3 ? m3.W : Wt;
+  const uint8_t* const A8m = w3 ? m3.A8 : A8;
+  const float* const AMm = w3 ? m3.AMAX : AMAX;
+  const float offm = w3 ? m3.offset : offset;
   // split-K (gridDim.z > 1): workgroup z takes K-steps [z S, z S + S) and
   // writes fp32 partial sums to YP[z][n][m]
   const int nsteps = K / KT / gridDim.z, kbase = blockIdx.z * nsteps * KT;
@@ -154,6 +178,7 @@ __global__ __launch_bounds__(64 * W) void nf4_gemm_dl_kernel(
   for (int i = tid; i < 256; i += 64 * W) {
     lut2_s[i] = make_float2(LUT[i >> 4], LUT[i & 15]);
     if constexpr (NESTED) code2_s[i] = CODE2[i];
+    if constexpr (NESTED && SW) code2_s[256 + i] = m3.CODE2[i];
   }
   // nested: the workgroup's scale bytes, entry r * DL_MAX_STEPS + j for row
   // r, step j; lane l takes step l (steps past the range repeat the last,
@@ -167,8 +192,10 @@ __global__ __launch_bounds__(64 * W) void nf4_gemm_dl_kernel(
     uint32_t v[PER];
 #pragma unroll
     for (int u = 0; u < PER; ++u) {
-      const int row = min(m0 + wave + u * W, M - 1);
-      v[u] = A8[((long long)row * K + kbase + j * KT) >> bs_shift];
+      const int vr = wave + u * W;  // (SW: rows BMO .. BM - 1 are w3's)
+      const bool second = SW && vr >= BMO;
+      const int row = min(m0 + vr - (second ? BMO : 0), M - 1);
+      v[u] = (second ? m3.A8 : A8)[((long long)row * K + kbase + j * KT) >> bs_shift];
     }
 #pragma unroll
     for (int u = 0; u < PER; ++u) a8_s[(wave + u * W) * DL_MAX_STEPS + lane] = (uint8_t)v[u];
@@ -177,22 +204,22 @@ __global__ __launch_bounds__(64 * W) void nf4_gemm_dl_kernel(
   // before jsw and from jsw on (a workgroup's K range crosses at most one
   // second-level group: 64 steps of 64 codes < one group of >= 256 blocks)
   const int rl = 32 * wave + (lane & 31);
-  const int arow = min(m0 + rl, M - 1);
+  const int arow = min(m0 + rl - (w3 ? BMO : 0), M - 1);
   float amax_lo = 0.0f, amax_hi = 0.0f;
   int jsw = nsteps;
   if constexpr (NESTED) {
     const long long e0 = (long long)arow * K + kbase;
     const long long g0 = (e0 >> bs_shift) >> bs2_shift;
-    amax_lo = AMAX[g0];
+    amax_lo = AMm[g0];
     const long long enext = ((g0 + 1) << bs2_shift) << bs_shift;  // first element of the next group
     jsw = (int)min((long long)nsteps, (enext - e0 + KT - 1) / KT);
-    amax_hi = jsw < nsteps ? AMAX[g0 + 1] : amax_lo;
+    amax_hi = jsw < nsteps ? AMm[g0 + 1] : amax_lo;
   }
 
   const __amdgpu_buffer_rsrc_t xr =
       __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(X), (short)0, (int)((size_t)N * K * 2), 0x00020000);
   const __amdgpu_buffer_rsrc_t wr =
-      __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(Wt), (short)0, (int)((size_t)M * K / 2), 0x00020000);
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(Wm), (short)0, (int)((size_t)M * K / 2), 0x00020000);
   // activation load j of this wave: rows 8 q .. 8 q + 7 (q = wave CPW + j),
   // lane l row 8 q + l / 8 and LDS slot l % 8, i.e. segment (l % 8) ^ ((t >> 1) & 7)
   uint32_t xoff[CPW];
@@ -207,7 +234,7 @@ __global__ __launch_bounds__(64 * W) void nf4_gemm_dl_kernel(
   // plain: lane l's absmax of row l % 32 (block (row K + k) >> bs_shift: the
   // row's part per lane, the step's part uniform, both whole blocks)
   const __amdgpu_buffer_rsrc_t ar = __builtin_amdgcn_make_buffer_rsrc(
-      const_cast<float*>(AMAX), (short)0, NESTED ? 0 : (int)(((size_t)M * K >> bs_shift) * 4), 0x00020000);
+      const_cast<float*>(AMm), (short)0, NESTED ? 0 : (int)(((size_t)M * K >> bs_shift) * 4), 0x00020000);
   const uint32_t aoff = (uint32_t)(((long long)arow * K) >> bs_shift) * 4u;
 
   f32x16_v acc[4];
@@ -238,7 +265,7 @@ __global__ __launch_bounds__(64 * W) void nf4_gemm_dl_kernel(
     float sc = 0.0f;  // plain: read inside the step
     if constexpr (NESTED) {
       const float am = s < jsw ? amax_lo : amax_hi;
-      sc = __fadd_rn(__fmul_rn(code2_s[a8_s[rl * DL_MAX_STEPS + s]], am), offset);
+      sc = __fadd_rn(__fmul_rn(code2_s[(w3 ? 256 : 0) + a8_s[rl * DL_MAX_STEPS + s]], am), offm);
     }
     dl_step<DT, W, CPW, !NESTED>(rd, dst, lut2_s, xr, wr, ar, xoff, woff, aoff, k0n * 2, k0n / 2,
                                  (k0n >> bs_shift) * 4, wave, lane, sc, acc);
@@ -254,6 +281,46 @@ __global__ __launch_bounds__(64 * W) void nf4_gemm_dl_kernel(
   // accumulator r of lane l is (row 8 (r / 4) + 4 (l / 32) + r % 4, column
   // l % 32): 4 consecutive weight rows m of one activation row n per lane
   const bool v4 = (M & 3) == 0;
+  if constexpr (SW) {
+    // the gate waves' outputs, rounded, to LDS - in the stage the last step
+    // read (free once every wave is past it; the other stage takes that
+    // step's unread refill) - then w3's waves combine them with their own
+    static_assert((W / 2) * 4 * 16 * 64 * 2 <= STAGE, "gate outputs exceed the ring stage");
+    uint16_t* g_s = reinterpret_cast<uint16_t*>(nsteps % 2 == 0 ? ring1 : ring0);  // [W / 2][4][16][64]
+    const int hw = w3 ? wave - W / 2 : wave;
+    __syncthreads();
+    if (!w3) {
+#pragma unroll
+      for (int b = 0; b < 4; ++b)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) g_s[((hw * 4 + b) * 16 + r) * 64 + lane] = Elem<DT>::store(acc[b][r]);
+    }
+    __syncthreads();
+    if (!w3) return;
+    const bool vec = v4 && (epi & 8);  // Y 8-byte aligned (host)
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+      const int n = n0 + 32 * b + (lane & 31);
+      if (n >= N) continue;
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int m = m0 + 32 * hw + 8 * g + 4 * (lane >> 5);
+        const size_t o = (size_t)n * M + m;
+        uint16_t ov[4];
+#pragma unroll
+        for (int c = 0; c < 4; ++c)
+          ov[c] = dl_epi<DT>(Elem<DT>::load(Elem<DT>::store(acc[b][4 * g + c])),
+                             g_s[((hw * 4 + b) * 16 + 4 * g + c) * 64 + lane], 2);
+        if (vec && m + 4 <= M) {
+          *reinterpret_cast<uint2*>(Y + o) =
+              make_uint2((uint32_t)ov[0] | ((uint32_t)ov[1] << 16), (uint32_t)ov[2] | ((uint32_t)ov[3] << 16));
+        } else {
+          for (int c = 0; c < 4 && m + c < M; ++c) Y[o + c] = ov[c];
+        }
+      }
+    }
+    return;
+  }
   if (YP) {
     float* yp = YP + (size_t)blockIdx.z * N * M;
 #pragma unroll
@@ -316,11 +383,29 @@ int launch_dl(const void* X, const uint8_t* Wt, const uint8_t* A8, const float* 
   if (A8)
     hipLaunchKernelGGL((nf4_gemm_dl_kernel<DT, true, W>), grid, dim3(64 * W), 0, st, (const uint16_t*)X, Wt, A8,
                        AMAX, CODE2, offset, LUT, (uint16_t*)Y, (const uint16_t*)R, epi, M, K, N, bs_shift,
-                       bs2_shift, YP);
+                       bs2_shift, YP, DlMat{});
   else
     hipLaunchKernelGGL((nf4_gemm_dl_kernel<DT, false, W>), grid, dim3(64 * W), 0, st, (const uint16_t*)X, Wt, A8,
                        AMAX, CODE2, offset, LUT, (uint16_t*)Y, (const uint16_t*)R, epi, M, K, N, bs_shift,
-                       bs2_shift, YP);
+                       bs2_shift, YP, DlMat{});
+  TTSP_RETURN_LAUNCH();
+}
+
+// The SwiGLU form: 4 waves, 64 output rows of both weights a workgroup.
+template <int DT>
+int launch_dl_swiglu(const void* X, const uint8_t* W1, const uint8_t* A8, const float* AMAX, const float* CODE2,
+                     float offset, const DlMat& m3, const float* LUT, void* Y, int epi, int M, int K, int N,
+                     int bs_shift, int bs2_shift, hipStream_t st) {
+  constexpr int W = 4, BMO = 32 * W / 2;
+  const dim3 grid((M + BMO - 1) / BMO, (N + BN - 1) / BN, 1);
+  if (A8)
+    hipLaunchKernelGGL((nf4_gemm_dl_kernel<DT, true, W, true>), grid, dim3(64 * W), 0, st, (const uint16_t*)X, W1,
+                       A8, AMAX, CODE2, offset, LUT, (uint16_t*)Y, (const uint16_t*)nullptr, epi, M, K, N, bs_shift,
+                       bs2_shift, (float*)nullptr, m3);
+  else
+    hipLaunchKernelGGL((nf4_gemm_dl_kernel<DT, false, W, true>), grid, dim3(64 * W), 0, st, (const uint16_t*)X, W1,
+                       A8, AMAX, CODE2, offset, LUT, (uint16_t*)Y, (const uint16_t*)nullptr, epi, M, K, N, bs_shift,
+                       bs2_shift, (float*)nullptr, m3);
   TTSP_RETURN_LAUNCH();
 }
 
@@ -358,6 +443,25 @@ int gemm_dl(const void* X, int dt, const uint8_t* W, const uint8_t* A8, const fl
     return launch_dl<DT_F16, 4>(X, W, A8, AMAX, CODE2, offset, LUT, Y, R, e, M, K, N, bs_shift, bs2_shift, splits,
                                 yp, st);
   }
+  return (int)hipErrorInvalidValue;
+}
+
+// Y = round(round(silu(X . W1^T)) * round(X . W3^T)) in one unsplit launch
+// (the two launches' bits where they run this kernel unsplit: the caller
+// checks the plan). Both weights share blocksize and nesting.
+int gemm_dl_swiglu(const void* X, int dt, const uint8_t* W1, const uint8_t* A8_1, const float* AMAX_1,
+                   const float* CODE2_1, float offset_1, const uint8_t* W3, const uint8_t* A8_3,
+                   const float* AMAX_3, const float* CODE2_3, float offset_3, const float* LUT, void* Y, int M, int K,
+                   int N, int bs_shift, int bs2_shift, hipStream_t st) {
+  if (!gemm_dl_fits(M, K, N, 1)) return (int)hipErrorInvalidValue;
+  const DlMat m3{W3, A8_3, AMAX_3, CODE2_3, offset_3};
+  const int e = (uintptr_t)Y % 8 == 0 ? 8 : 0;
+  if (dt == DT_BF16)
+    return launch_dl_swiglu<DT_BF16>(X, W1, A8_1, AMAX_1, CODE2_1, offset_1, m3, LUT, Y, e, M, K, N, bs_shift,
+                                     bs2_shift, st);
+  if (dt == DT_F16)
+    return launch_dl_swiglu<DT_F16>(X, W1, A8_1, AMAX_1, CODE2_1, offset_1, m3, LUT, Y, e, M, K, N, bs_shift,
+                                    bs2_shift, st);
   return (int)hipErrorInvalidValue;
 }
 

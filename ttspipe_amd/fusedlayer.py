@@ -244,8 +244,9 @@ def prefill_block(block, x, freqs_cis, mask, input_pos):
     wqkv GEMM, q/k head norms + rotary + KV-cache write for every row in one
     launch (the decode step's kernel over rows; the fork's modules when the
     cache or tables do not fit it), one-launch causal attention, wo GEMM with
-    the residual add in its epilogue, RMSNorm, w1 GEMM, w3 GEMM with the
-    SwiGLU gate in its epilogue, w2 GEMM with the residual add (reference: the
+    the residual add in its epilogue, RMSNorm, w1 and w3 GEMMs with the
+    SwiGLU gate (one launch where it serves the shape, else w3's epilogue), w2 GEMM with
+    the residual add (reference: the
     unfused block the reference runs for S > 1, fastpath.py:207-271 and
     fusedlayer.py:198).
     """
@@ -302,8 +303,11 @@ def prefill_block(block, x, freqs_cis, mask, input_pos):
     y = y.transpose(1, 2).contiguous().view(bsz, n, nh * hd)
     h = nf4gemv.matmul(a.wo, y, epi=nf4gemv.EPI_RESIDUAL, operand=x)
     hn = None if h is None else fusedops.rms_norm(h, fn.weight, fn.eps)
-    g = None if hn is None else nf4gemv.matmul(ff.w1, hn)
-    u = None if g is None else nf4gemv.matmul(ff.w3, hn, epi=nf4gemv.EPI_SILU_GATE, operand=g)
+    # w1 and w3 with the SwiGLU gate in one launch where it serves the shape, else two
+    u = None if hn is None else nf4gemv.matmul_swiglu(ff.w1, ff.w3, hn)
+    if u is None and hn is not None:
+        g = nf4gemv.matmul(ff.w1, hn)
+        u = None if g is None else nf4gemv.matmul(ff.w3, hn, epi=nf4gemv.EPI_SILU_GATE, operand=g)
     out = None if u is None else nf4gemv.matmul(ff.w2, u, epi=nf4gemv.EPI_RESIDUAL, operand=h)
     if out is None:
         raise RuntimeError("prefill_block: a GEMM declined after the KV cache was written")

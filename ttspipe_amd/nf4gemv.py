@@ -292,6 +292,43 @@ def matmul_fused(module, x, *, norm_weight=None, eps: float = 1e-6, module3=None
     return out.view(*x.shape[:-1], M)
 
 
+def matmul_swiglu(module1, module3, x, *, out=None):
+    """silu(x W1^T) * (x W3^T) for several rows in one launch, rounded as the
+    two-launch form `matmul(w3, x, epi=EPI_SILU_GATE, operand=matmul(w1, x))`
+    and with its bits; None where one launch does not serve the shape (it
+    serves where both GEMMs would run the direct-to-LDS kernel unsplit, e.g.
+    385 to 512 rows of 9728 x 2560)."""
+    import torch
+
+    if not (prepare(module1) and prepare(module3)):
+        return None
+    f1, f3 = module1._nf4_fast, module3._nf4_fast
+    dt = _lib.dtype_code(x.dtype)
+    if dt not in (_lib.DT_F16, _lib.DT_BF16) or x.device.type != "cuda":
+        return None
+    K, M = f1["K"], f1["M"]
+    if (f3["M"], f3["K"], f3["nested"], f3["bs"], f3["bs2"]) != (M, K, f1["nested"], f1["bs"], f1["bs2"]):
+        return None
+    if x.shape[-1] != K or not x.is_contiguous() or x.data_ptr() % 16:
+        return None
+    rows = x.numel() // K
+    lib = _lib.lib()
+    if not lib.ttsp_nf4_gemm_swiglu_fits(M, K, rows, f1["bs"], f1["bs2"], int(f1["nested"])):
+        return None
+    if out is None:
+        out = torch.empty((rows, M), dtype=x.dtype, device=x.device)
+    elif out.dtype != x.dtype or out.numel() != rows * M or not out.is_contiguous():
+        return None
+    rc = lib.ttsp_nf4_gemm_swiglu(
+        x.data_ptr(), dt, f1["w"], f1["a8"], f1["amax"], f1["code2"], f1["offset"],
+        f3["w"], f3["a8"], f3["amax"], f3["code2"], f3["offset"], f1["lut"].data_ptr(), out.data_ptr(),
+        M, K, rows, f1["bs"], f1["bs2"], _lib.stream())
+    if rc:
+        raise RuntimeError(f"ttsp_nf4_gemm_swiglu failed: hipError_t {rc}")
+    _stats["fast"] += 2
+    return out.view(*x.shape[:-1], M)
+
+
 def _classes():
     """Linear4bit classes to patch: ours, and bitsandbytes' where it is importable."""
     from ttspipe_amd.quant import Linear4bit
