@@ -300,21 +300,22 @@ def test_prompt_prefill_matches_position_by_position_decode(fresh, start, n):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("start", [5, 0])
 @pytest.mark.parametrize("n,bucket", [(100, 128), (1, 1), (2, 2), (3, 4), (6, 8)])
-def test_graph_prefill_equals_the_eager_span(fresh, n, bucket):
+def test_graph_prefill_equals_the_eager_span(fresh, n, bucket, start):
     """One span padded to its bucket: three graph replays, each with eager
     work and synchronisation between them, equal the eager span bit for bit
-    (logits, token and the K rows of every layer)."""
+    (logits, token and the K rows of every layer); at position 0 through the
+    graphs whose attention window ends with the span."""
     from ttspipe_amd.dualar import prefill_spans
 
     m = fresh
     assert prefill_spans(n) == [(0, n, bucket)]
     toks = _tokens(m, n, 2 + n)
-    start = 5
     assert m.prefill(toks, start, graphed=False)
     eager = (m.logits.clone(), int(m.prefill_token.item()),
              [b.attention.kv_cache.k_cache[:, :, start:start + n].clone() for b in m.layers])
-    m.capture_prefill([bucket])
+    m.capture_prefill([bucket], first=start == 0)
     for _ in range(3):
         m.logits.zero_()
         torch.cuda.synchronize()
@@ -364,12 +365,14 @@ def _assert_same_prefill(m, eager, upto):
 
 @pytest.mark.gpu
 def test_graphed_prefill_captures_buckets_without_touching_live_kv(roomy):
-    """A 600-token prompt with no bucket captured beforehand: the second span's
+    """A 600-token prompt with no bucket captured beforehand: the first span
+    (at position 0) takes its own window's 512 graph; the second span's
     bucket (128) is captured after the first span's KV rows are written, and
     its warm-up runs at positions 0..127; the result must equal the eager
     prefill, KV rows and logits bit for bit."""
     m = roomy
     m.prefill_graphs.clear()
+    m.prefill_first_graphs.clear()
     initial = _kv_state(m, m.cfg.max_seq_len)
     toks = _tokens(m, 600, 5)
     assert m.prefill(toks, 0, graphed=False)
@@ -378,7 +381,8 @@ def test_graphed_prefill_captures_buckets_without_touching_live_kv(roomy):
     _set_kv(m, initial)
     assert m.prefill(toks, 0, graphed=True)
     torch.cuda.synchronize()
-    assert sorted(m.prefill_graphs) == [128, 512]
+    # (the span at position 0 takes the graph whose window ends with it)
+    assert sorted(m.prefill_first_graphs) == [512] and sorted(m.prefill_graphs) == [128]
     _assert_same_prefill(m, eager, 600)
 
 
@@ -399,3 +403,37 @@ def test_graphed_prefill_after_an_eager_one_keeps_its_context(roomy):
     torch.cuda.synchronize()
     assert 128 in m.prefill_graphs
     _assert_same_prefill(m, eager, 164)
+
+
+@pytest.mark.gpu
+def test_first_span_window_matches_the_whole_cache_window(roomy):
+    """A 300-token prompt at position 0 through the window that ends with the
+    span (the default there) and through the whole-cache window: the keys past
+    the span are masked either way, so the KV rows and the last logits agree
+    within the reference's 2e-2 block bar (the attention's key split differs
+    with the window, and with it the roundings); layer 0's K/V rows, written
+    before any attention, are identical."""
+    import numpy as np
+
+    m = roomy
+    toks = _tokens(m, 300, 9)
+    initial = _kv_state(m, m.cfg.max_seq_len)
+    got = {}
+    for name, width in (("span", 512), ("cache", None)):
+        _set_kv(m, initial)
+        inp = torch.empty(m.cfg.n_tokens, 512, dtype=torch.int32, device=m.device)
+        inp[:, :300].copy_(toks)
+        inp[:, 300:].copy_(toks[:, -1:].expand(-1, 212))
+        pos = torch.arange(512, dtype=torch.long, device=m.device)
+        last = torch.tensor([299], dtype=torch.long, device=m.device)
+        m.prefill_forward(inp, pos, last, width)
+        torch.cuda.synchronize()
+        got[name] = (m.logits.float().cpu().numpy(), _kv_state(m, 300))
+    (la, kva), (lb, kvb) = got["span"], got["cache"]
+    assert np.linalg.norm(la - lb) / np.linalg.norm(lb) < 2e-2
+    assert torch.equal(kva[0][0], kvb[0][0]) and torch.equal(kva[0][1], kvb[0][1])
+    for (ka, va), (kb, vb) in zip(kva, kvb):
+        for a, b in ((ka, kb), (va, vb)):
+            a, b = a.float(), b.float()
+            assert float((a - b).norm() / b.norm()) < 2e-2
+    _set_kv(m, initial)

@@ -324,6 +324,7 @@ class SyntheticDualAR:
         # prompt prefill: the fork's causal mask rows, one captured graph per bucket
         self.causal = torch.tril(torch.ones(cfg.max_seq_len, cfg.max_seq_len, dtype=torch.bool, device=dev))
         self.prefill_graphs = {}
+        self.prefill_first_graphs = {}
         self.prefill_token = torch.zeros(1, dtype=torch.int32, device=dev)
         self.reset()
 
@@ -522,23 +523,27 @@ class SyntheticDualAR:
 
     # ---------------------------------------------------------------- prefill
 
-    def prefill_forward(self, inp, pos, last) -> None:
+    def prefill_forward(self, inp, pos, last, width: int | None = None) -> None:
         """The slow transformer over a prompt span: `inp` (n_tokens, n) int32
         token rows at positions `pos` (n,) int64 write their KV entries; the
         final norm and output head run on span index `last` (1,) int64, whose
         greedy token lands in `prefill_token` and logits in `logits`
         (reference: DecodeGraphs._prefill_body, graphs.py:219-231, through
-        BaseTransformer.forward_generate with the whole cache as the window)."""
+        BaseTransformer.forward_generate with the whole cache as the window).
+        `width`: the attention window, the first `width` cache positions
+        (default the whole cache; a span that starts at position 0 sees
+        nothing past its own end, so its window can stop there)."""
         import torch
 
         cfg = self.cfg
+        width = cfg.max_seq_len if width is None else width
         n = inp.shape[1]
         rows = torch.clamp(inp.long(), 0, cfg.vocab_size - 1)
         rows = rows + (torch.arange(cfg.n_tokens, device=inp.device) * cfg.vocab_size).view(-1, 1)
         emb = self.tensors["embeddings"].view(-1, cfg.dim).index_select(0, rows.reshape(-1))
         x = emb.view(cfg.n_tokens, n, cfg.dim).float().sum(0).to(self.dtype).view(1, n, cfg.dim)
         freqs = self.freqs.index_select(0, pos)
-        mask = self.causal.index_select(0, pos).view(1, 1, n, cfg.max_seq_len)
+        mask = self.causal.index_select(0, pos)[None, None, :, :width]
         for blk in self.layers:
             x = blk(x, freqs, mask, pos)
         h = x.index_select(1, last)
@@ -547,8 +552,11 @@ class SyntheticDualAR:
                                    _lib.stream())
         self._check(rc, "ttsp_argmax")
 
-    def capture_prefill(self, buckets=None) -> None:
-        """One graph per padded span length (after an eager warm-up of each).
+    def capture_prefill(self, buckets=None, first: bool = False) -> None:
+        """One graph per padded span length (after an eager warm-up of each);
+        `first`: the graphs for a span at position 0, whose attention window
+        ends with the span (`prefill_first_graphs`), else the whole-cache ones
+        (`prefill_graphs`).
 
         The warm-up runs the span at positions 0..b-1, which writes those KV
         rows of every slow layer; they are saved first and put back after, so
@@ -557,24 +565,26 @@ class SyntheticDualAR:
         next span anyway)."""
         import torch
 
+        graphs = self.prefill_first_graphs if first else self.prefill_graphs
         for b in buckets or PREFILL_BUCKETS:
-            if b in self.prefill_graphs or b > self.cfg.max_seq_len:
+            if b in graphs or b > self.cfg.max_seq_len:
                 continue
+            width = b if first else None
             inp = torch.zeros(self.cfg.n_tokens, b, dtype=torch.int32, device=self.device)
             pos = torch.arange(b, dtype=torch.long, device=self.device)
             last = torch.zeros(1, dtype=torch.long, device=self.device)
             saved = [(blk.attention.kv_cache.k_cache[:, :, :b].clone(), blk.attention.kv_cache.v_cache[:, :, :b].clone())
                      for blk in self.layers]
-            self.prefill_forward(inp, pos, last)
+            self.prefill_forward(inp, pos, last, width)
             torch.cuda.synchronize()
             g = torch.cuda.CUDAGraph()
             with torch.cuda.graph(g):
-                self.prefill_forward(inp, pos, last)
+                self.prefill_forward(inp, pos, last, width)
             for blk, (kc, vc) in zip(self.layers, saved):
                 blk.attention.kv_cache.k_cache[:, :, :b].copy_(kc)
                 blk.attention.kv_cache.v_cache[:, :, :b].copy_(vc)
             del saved
-            self.prefill_graphs[b] = (g, inp, pos, last)
+            graphs[b] = (g, inp, pos, last)
 
     def prefill(self, tokens, start: int, graphed: bool = True) -> bool:
         """KV entries for `tokens` (n_tokens, n) int32 at [start, start + n),
@@ -582,7 +592,9 @@ class SyntheticDualAR:
         padding repeats the last real token; its KV entries land past the
         prompt, where decoding overwrites them before reading them); the last
         real position's token in `prefill_token`. False (nothing done) when
-        the padded span runs past the cache (reference: graphs.py:304-335)."""
+        the padded span runs past the cache (reference: graphs.py:304-335).
+        A span at position 0 attends over its own positions only (the window
+        of the reference's causal mask there), not the whole cache."""
         import torch
 
         n = tokens.shape[-1]
@@ -590,10 +602,12 @@ class SyntheticDualAR:
         if not spans or start + spans[-1][0] + spans[-1][2] > self.cfg.max_seq_len:
             return False
         for off, size, b in spans:
+            first = start + off == 0
             if graphed:
-                if b not in self.prefill_graphs:
-                    self.capture_prefill([b])
-                g, inp, pos, last = self.prefill_graphs[b]
+                graphs = self.prefill_first_graphs if first else self.prefill_graphs
+                if b not in graphs:
+                    self.capture_prefill([b], first=first)
+                g, inp, pos, last = graphs[b]
             else:
                 inp = torch.empty(self.cfg.n_tokens, b, dtype=torch.int32, device=self.device)
                 pos = torch.empty(b, dtype=torch.long, device=self.device)
@@ -605,7 +619,7 @@ class SyntheticDualAR:
             if graphed:
                 g.replay()
             else:
-                self.prefill_forward(inp, pos, last)
+                self.prefill_forward(inp, pos, last, b if first else None)
         return True
 
     def capture(self) -> None:
