@@ -665,7 +665,7 @@ def main() -> int:
     ap.add_argument("--skip-cpu", action="store_true")
     ap.add_argument("--skip-decode", action="store_true")
     ap.add_argument("--only", choices=["layer", "kernel", "c1", "copy", "decode", "gemm", "pattn", "prefill",
-                                       "smalln", "normrope"],
+                                       "prefill512", "smalln", "normrope"],
                     default=None,
                     help="run one GPU measurement only (for profiling runs)")
     ap.add_argument("--decode-steps", type=int, default=256, help="greedy frames the decode benchmark times")
@@ -700,11 +700,12 @@ def main() -> int:
         out["smalln"] = bench_small_n()
     if args.only in (None, "normrope"):
         out["normrope"] = bench_norm_rope()
-    if args.only in (None, "prefill"):
+    if args.only in (None, "prefill", "prefill512"):
         from ttspipe_amd import dualar
 
         out["prefill"] = dualar.prefill_benchmark(512)
-        out["prefill_tail"] = dualar.prefill_tail_benchmark()
+        if args.only != "prefill512":  # (the 512-token prompt alone: its kernel trace)
+            out["prefill_tail"] = dualar.prefill_tail_benchmark()
     decode = None
     if args.only in (None, "decode") and not args.skip_decode:
         from ttspipe_amd import dualar
