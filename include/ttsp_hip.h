@@ -95,6 +95,20 @@ int ttsp_nf4_gemm_split(const void* X, int x_dtype, const uint8_t* W, const uint
                         void* Y, const void* R, int epi, int M, int K, int N, int blocksize,
                         int blocksize2, float* work, int splits, void* stream);
 
+/* ttsp_nf4_gemm_split (splits > 1) whose reduce also writes the RMSNorm of
+ * each output row: Y as ttsp_nf4_gemm_split, and YN[n] = rms_norm(Y[n], G,
+ * eps), bit-identical to ttsp_rms_norm on Y. The reduce, the epilogue and the
+ * norm are one launch (a workgroup per row). Requires M % 8 == 0, M <= 4096 and
+ * 16-byte aligned Y, YN, G, work (and R with an epilogue); else
+ * hipErrorInvalidValue. Replaces: wo / w2 of a multi-row block
+ * (nf4gemv.matmul, app/engine/nf4gemv.py:460-477) followed by the next
+ * RMSNorm launch (fusedops.rms_norm, app/engine/fusedops.py:169-196). */
+int ttsp_nf4_gemm_split_norm(const void* X, int x_dtype, const uint8_t* W, const uint8_t* A8,
+                             const float* AMAX, const float* CODE2, float offset, const float* LUT,
+                             void* Y, const void* R, int epi, int M, int K, int N, int blocksize,
+                             int blocksize2, float* work, int splits, const void* G, float eps,
+                             void* YN, void* stream);
+
 /* The SwiGLU pair of a multi-row forward in one launch:
  * Y[N][M] = round(round(silu(round(X . W1^T))) * round(X . W3^T)), W1 and W3
  * of one shape [M, K] with the same blocksize and nesting, every value the

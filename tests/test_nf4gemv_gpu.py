@@ -635,3 +635,53 @@ def test_swiglu_gemm_declines_what_one_launch_does_not_serve(nf4, shape, rows, b
     w3 = to_linear(random_layer(M, K, True, seed=4, bs2=bs2), torch.bfloat16)
     x = from_bits(randn_bits(rows * K, torch.bfloat16, seed=9), torch.bfloat16).view(rows, K)
     assert nf4.matmul_swiglu(w1, w3, x) is None
+
+
+@pytest.mark.parametrize("shape,rows,splits,epi,nested,dtype", [
+    ((2560, 4096), 512, 4, 1, True, torch.bfloat16),   # wo of a 512-row span
+    ((2560, 9728), 512, 4, 1, True, torch.bfloat16),   # w2 of a 512-row span
+    ((2560, 9728), 64, 4, 1, False, torch.float16),
+    ((1024, 4096), 128, 8, 0, True, torch.float16),
+    ((1536, 1024), 300, 2, 2, True, torch.bfloat16),
+    ((512, 1024), 64, 2, 1, True, torch.bfloat16)])
+def test_split_gemm_with_the_next_norm_equals_the_two_launches(nf4, shape, rows, splits, epi, nested, dtype):
+    """`matmul_norm` (the split-K reduce, its epilogue and the RMSNorm of each
+    output row in one launch) against `matmul` then `fusedops.rms_norm`, bit
+    for bit: 2, 4 and 8 splits, every epilogue, fp16 and bf16, plain and
+    nested scales, a row count that is not a multiple of four."""
+    from ttspipe_amd import _lib, fusedops
+
+    M, K = shape
+    assert _lib.load().ttsp_nf4_gemm_splits(M, K, rows) == splits
+    assert fusedops.install()
+    lin = to_linear(random_layer(M, K, nested, seed=M + K + rows), dtype)
+    assert nf4.prepare(lin)
+    x = from_bits(randn_bits(rows * K, dtype, seed=rows + 11, scale=0.5), dtype).view(1, rows, K)
+    r = from_bits(randn_bits(rows * M, dtype, seed=rows + 12), dtype).view(1, rows, M) if epi else None
+    g = torch.rand(M, generator=torch.Generator().manual_seed(M)).add(0.5).to(dtype).cuda()
+    eps = 1e-5
+    got = nf4.matmul_norm(lin, x, g, eps, epi=epi, operand=r)
+    assert got is not None
+    y, yn = got
+    ref = nf4.matmul(lin, x, epi=epi, operand=r)
+    ref_n = fusedops.rms_norm(ref, g, eps)
+    assert ref_n is not None
+    torch.cuda.synchronize()
+    for a, b in ((y, ref), (yn, ref_n)):
+        ab, bb = bits(a), bits(b)
+        assert np.array_equal(ab, bb), first_mismatch(ab, bb)
+    nb = o.to_f32(bits(ref_n), dt_code(dtype)).reshape(rows, M)
+    assert np.all(np.isfinite(nb)) and np.abs(nb).max() > 0
+
+
+@pytest.mark.parametrize("shape,rows", [((1540, 2560), 512), ((4096, 2560), 512), ((6144, 2560), 256),
+                                        ((2560, 9728), 16), ((2560, 9728), 1)])
+def test_split_gemm_norm_declines_what_it_does_not_serve(nf4, shape, rows):
+    """M % 8 != 0, an unsplit plan, M over 4096, the few-row and one-row
+    paths: None (the caller runs the GEMM and the norm separately)."""
+    M, K = shape
+    lin = to_linear(random_layer(M, K, True, seed=5), torch.bfloat16)
+    assert nf4.prepare(lin)
+    x = from_bits(randn_bits(rows * K, torch.bfloat16, seed=6), torch.bfloat16).view(rows, K)
+    g = torch.ones(M, dtype=torch.bfloat16, device="cuda")
+    assert nf4.matmul_norm(lin, x, g, 1e-6) is None

@@ -266,6 +266,39 @@ def _tokens(model, n, seed):
                          dtype=torch.int32)
 
 
+def _prefill_state(m):
+    from tests.gpuutil import bits
+
+    torch.cuda.synchronize()
+    return [bits(t).copy() for b in m.layers for t in (b.attention.kv_cache.k_cache, b.attention.kv_cache.v_cache)
+            ] + [bits(m.logits).copy()]
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("n,start", [(64, 0), (40, 8)])
+def test_chained_norms_equal_the_separate_norm_launches(fresh, monkeypatch, n, start):
+    """The prompt's blocks handing each other the next RMSNorm from w2's (and
+    wo's) split-K reduce against the same blocks with every norm a launch of
+    its own (`matmul_norm` declined): every KV row and the logits bit for bit."""
+    import numpy as np
+
+    from ttspipe_amd import nf4gemv
+
+    m = fresh
+    toks = _tokens(m, n, 70 + n)
+    pos = torch.arange(start, start + n, device="cuda")
+    last = torch.tensor([n - 1], device="cuda")
+    calls = nf4gemv.stats()["fast"]
+    m.prefill_forward(toks, pos, last)
+    chained = _prefill_state(m)
+    assert nf4gemv.stats()["fast"] > calls
+    monkeypatch.setattr(nf4gemv, "matmul_norm", lambda *a, **k: None)
+    m.prefill_forward(toks, pos, last)
+    separate = _prefill_state(m)
+    for i, (a, b) in enumerate(zip(chained, separate)):
+        assert np.array_equal(a, b), f"state {i} differs"
+
+
 @pytest.mark.gpu
 @pytest.mark.parametrize("start,n", [(8, 40), (8, 1), (9, 2), (10, 3), (11, 5), (12, 8)])
 def test_prompt_prefill_matches_position_by_position_decode(fresh, start, n):

@@ -53,6 +53,8 @@ SIGNATURES: dict[str, list] = {
     "ttsp_nf4_gemm": [_vp, _i, _vp, _vp, _vp, _vp, _f, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _vp],
     "ttsp_nf4_gemm_splits": [_i, _i, _i],
     "ttsp_nf4_gemm_split": [_vp, _i, _vp, _vp, _vp, _vp, _f, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _vp, _i, _vp],
+    "ttsp_nf4_gemm_split_norm": [_vp, _i, _vp, _vp, _vp, _vp, _f, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _vp, _i,
+                                 _vp, _f, _vp, _vp],
     "ttsp_nf4_gemm_swiglu": [_vp, _i, _vp, _vp, _vp, _vp, _f, _vp, _vp, _vp, _vp, _f, _vp, _vp, _i, _i, _i, _i, _i,
                              _vp],
     "ttsp_nf4_gemm_swiglu_fits": [_i, _i, _i, _i, _i, _i],

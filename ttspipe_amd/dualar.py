@@ -535,6 +535,8 @@ class SyntheticDualAR:
         nothing past its own end, so its window can stop there)."""
         import torch
 
+        from ttspipe_amd import fusedlayer
+
         cfg = self.cfg
         width = cfg.max_seq_len if width is None else width
         n = inp.shape[1]
@@ -544,8 +546,16 @@ class SyntheticDualAR:
         x = emb.view(cfg.n_tokens, n, cfg.dim).float().sum(0).to(self.dtype).view(1, n, cfg.dim)
         freqs = self.freqs.index_select(0, pos)
         mask = self.causal.index_select(0, pos)[None, None, :, :width]
-        for blk in self.layers:
-            x = blk(x, freqs, mask, pos)
+        # each block hands the next its attention RMSNorm, written by w2's
+        # split-K reduce where that serves the span length
+        xn = None
+        for i, blk in enumerate(self.layers):
+            nxt = self.layers[i + 1].attention_norm if i + 1 < len(self.layers) else None
+            r = fusedlayer.prefill_block_chain(blk, x, freqs, mask, pos, xn=xn, next_norm=nxt)
+            if r is None:
+                x, xn = blk(x, freqs, mask, pos), None
+            else:
+                x, xn = r
         h = x.index_select(1, last)
         self._fused(self.output, h, self.tensors["norm"], cfg.norm_eps, self.logits)
         rc = self._lib.ttsp_argmax(self.logits.data_ptr(), cfg.vocab_size, _lib.DT_BF16, self.prefill_token.data_ptr(),

@@ -239,6 +239,19 @@ def _prefill_eligible(block, x, mask, input_pos) -> bool:
 
 def prefill_block(block, x, freqs_cis, mask, input_pos):
     """`TransformerBlock.forward` for several positions (B = 1, S > 1), or None.
+    The block of `prefill_block_chain` without a carried norm."""
+    r = prefill_block_chain(block, x, freqs_cis, mask, input_pos)
+    return None if r is None else r[0]
+
+
+def prefill_block_chain(block, x, freqs_cis, mask, input_pos, *, xn=None, next_norm=None):
+    """`(out, out_n)`: the block's output for several positions (B = 1, S > 1)
+    and, with `next_norm` (an RMSNorm module), `next_norm(out)` for the next
+    block (else None); None when the block declines.
+    `xn`, if given, is this block's `attention_norm(x)` (a previous call's
+    `out_n`), whose launch is then skipped; where the split-K reduce of wo and
+    w2 serves the shape it writes the following RMSNorm too
+    (`nf4gemv.matmul_norm`), bit for bit the separate launch.
 
     The fork's block in its own order with the prefill kernels: RMSNorm,
     wqkv GEMM, q/k head norms + rotary + KV-cache write for every row in one
@@ -261,7 +274,8 @@ def prefill_block(block, x, freqs_cis, mask, input_pos):
     bsz, n, _ = x.shape
     nh, nkv, hd = a.n_head, a.n_local_heads, a.head_dim
     an, fn = block.attention_norm, block.ffn_norm
-    xn = fusedops.rms_norm(x, an.weight, an.eps)
+    if xn is None:
+        xn = fusedops.rms_norm(x, an.weight, an.eps)
     qkv = None if xn is None else nf4gemv.matmul(a.wqkv, xn)
     if qkv is None:
         return None
@@ -301,18 +315,31 @@ def prefill_block(block, x, freqs_cis, mask, input_pos):
     if y is None:
         y = fastpath.decode_attention(q, k, v, mask, nh, nkv, hd)
     y = y.transpose(1, 2).contiguous().view(bsz, n, nh * hd)
-    h = nf4gemv.matmul(a.wo, y, epi=nf4gemv.EPI_RESIDUAL, operand=x)
-    hn = None if h is None else fusedops.rms_norm(h, fn.weight, fn.eps)
+    hh = nf4gemv.matmul_norm(a.wo, y, fn.weight, fn.eps, epi=nf4gemv.EPI_RESIDUAL, operand=x)
+    if hh is not None:
+        h, hn = hh
+    else:
+        h = nf4gemv.matmul(a.wo, y, epi=nf4gemv.EPI_RESIDUAL, operand=x)
+        hn = None if h is None else fusedops.rms_norm(h, fn.weight, fn.eps)
     # w1 and w3 with the SwiGLU gate in one launch where it serves the shape, else two
     u = None if hn is None else nf4gemv.matmul_swiglu(ff.w1, ff.w3, hn)
     if u is None and hn is not None:
         g = nf4gemv.matmul(ff.w1, hn)
         u = None if g is None else nf4gemv.matmul(ff.w3, hn, epi=nf4gemv.EPI_SILU_GATE, operand=g)
-    out = None if u is None else nf4gemv.matmul(ff.w2, u, epi=nf4gemv.EPI_RESIDUAL, operand=h)
+    oo = None
+    if u is not None and next_norm is not None:
+        oo = nf4gemv.matmul_norm(ff.w2, u, next_norm.weight, next_norm.eps, epi=nf4gemv.EPI_RESIDUAL, operand=h)
+    if oo is not None:
+        out, out_n = oo
+    else:
+        out = None if u is None else nf4gemv.matmul(ff.w2, u, epi=nf4gemv.EPI_RESIDUAL, operand=h)
+        out_n = None
+        if out is not None and next_norm is not None:
+            out_n = fusedops.rms_norm(out, next_norm.weight, next_norm.eps)
     if out is None:
         raise RuntimeError("prefill_block: a GEMM declined after the KV cache was written")
     _stats["prefill"] += 1
-    return out
+    return out, out_n
 
 
 def install() -> bool:

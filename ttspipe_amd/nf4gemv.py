@@ -222,6 +222,58 @@ def matmul(module, x, *, epi: int = EPI_NONE, operand=None, out=None):
     return out.view(*x.shape[:-1], M)
 
 
+#: Widest output row whose RMSNorm the split-K reduce folds in (eight 8-value
+#: chunks per lane of one wave).
+NORM_MAX_M = 4096
+
+
+def matmul_norm(module, x, norm_weight, eps: float, *, epi: int = EPI_NONE, operand=None):
+    """`(y, rms_norm(y))` for several rows with the norm folded into the
+    split-K reduce, or None where that form does not serve the call (one row,
+    an unsplit shape, M over NORM_MAX_M); y is `matmul(module, x, epi=epi,
+    operand=operand)` and the second output is `fusedops.rms_norm(y,
+    norm_weight, eps)`, both bit for bit."""
+    import torch
+
+    fast = getattr(module, "_nf4_fast", None)
+    if fast is None:
+        return None
+    dt = _lib.dtype_code(x.dtype)
+    if dt not in (_lib.DT_F16, _lib.DT_BF16) or x.device.type != "cuda":
+        return None
+    K, M = fast["K"], fast["M"]
+    if x.shape[-1] != K or not x.is_contiguous() or x.data_ptr() % 16 or M % 8 or M > NORM_MAX_M:
+        return None
+    rows = x.numel() // K
+    if rows < 2:
+        return None
+    if (norm_weight.dtype != x.dtype or norm_weight.numel() != M or not norm_weight.is_contiguous()
+            or norm_weight.data_ptr() % 16 or norm_weight.device != x.device):
+        return None
+    if epi != EPI_NONE:
+        if operand is None or operand.numel() != rows * M or operand.dtype != x.dtype:
+            return None
+        if operand.device != x.device or not operand.is_contiguous() or operand.data_ptr() % 16:
+            return None
+    lib = _lib.lib()
+    splits = lib.ttsp_nf4_gemm_splits(M, K, rows)
+    if splits not in (2, 4, 8):
+        return None
+    out = torch.empty((rows, M), dtype=x.dtype, device=x.device)
+    out_n = torch.empty((rows, M), dtype=x.dtype, device=x.device)
+    work = torch.empty(splits * rows * M, dtype=torch.float32, device=x.device)
+    rc = lib.ttsp_nf4_gemm_split_norm(
+        x.data_ptr(), dt, fast["w"], fast["a8"], fast["amax"], fast["code2"], fast["offset"],
+        fast["lut"].data_ptr(), out.data_ptr(), _lib.ptr(operand) if epi else 0, epi, M, K, rows,
+        fast["bs"], fast["bs2"], work.data_ptr(), splits, norm_weight.data_ptr(), float(eps), out_n.data_ptr(),
+        _lib.stream())
+    if rc:
+        raise RuntimeError(f"ttsp_nf4_gemm_split_norm failed: hipError_t {rc}")
+    _stats["fast"] += 1
+    shape = (*x.shape[:-1], M)
+    return out.view(shape), out_n.view(shape)
+
+
 #: Widest input whose RMSNorm the single-row kernel folds in (one 8-value
 #: chunk per thread of its 512).
 NORM_MAX_K = 4096
