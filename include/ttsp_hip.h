@@ -95,6 +95,15 @@ int ttsp_nf4_gemm_split(const void* X, int x_dtype, const uint8_t* W, const uint
                         void* Y, const void* R, int epi, int M, int K, int N, int blocksize,
                         int blocksize2, float* work, int splits, void* stream);
 
+/* The K-split launch of ttsp_nf4_gemm_split without its reduce: work gets
+ * the fp32 partial sums, split z of output row n at work + (z*N + n)*M, for
+ * a consumer that adds them in split order (ttsp_qk_rope_kv_rows_partials).
+ * splits must equal ttsp_nf4_gemm_splits(M, K, N) > 1; work 16-byte aligned.
+ * Replaces: as ttsp_nf4_gemm_split. */
+int ttsp_nf4_gemm_partials(const void* X, int x_dtype, const uint8_t* W, const uint8_t* A8,
+                           const float* AMAX, const float* CODE2, float offset, const float* LUT, int M,
+                           int K, int N, int blocksize, int blocksize2, float* work, int splits, void* stream);
+
 /* ttsp_nf4_gemm_split (splits > 1) whose reduce also writes the RMSNorm of
  * each output row: Y as ttsp_nf4_gemm_split, and YN[n] = rms_norm(Y[n], G,
  * eps), bit-identical to ttsp_rms_norm on Y. The reduce, the epilogue and the
@@ -206,6 +215,16 @@ int ttsp_qk_rope_kv(const void* QKV, const void* QW, const void* KW, float eps, 
 int ttsp_qk_rope_kv_rows(const void* QKV, long long qkv_row_stride, const void* QW, const void* KW,
                          float eps, const void* F, int ftype, const long long* POS, void* Q, void* KC,
                          void* VC, int nh, int nkv, int max_len, int rows, int dtype, void* stream);
+
+/* ttsp_qk_rope_kv_rows reading a K-split GEMM's fp32 partial sums instead of
+ * its output: split z of row r at YP + (z*rows + r)*(nh + 2*nkv)*128 (what
+ * ttsp_nf4_gemm_partials writes), summed in split order and rounded as
+ * ttsp_nf4_gemm_split's reduce rounds them, so every write equals
+ * ttsp_nf4_gemm_split then ttsp_qk_rope_kv_rows bit for bit; 2 <= splits <= 8.
+ * Replaces: as ttsp_qk_rope_kv_rows, with the wqkv GEMM's reduce folded in. */
+int ttsp_qk_rope_kv_rows_partials(const float* YP, int splits, const void* QW, const void* KW, float eps,
+                                  const void* F, int ftype, const long long* POS, void* Q, void* KC, void* VC,
+                                  int nh, int nkv, int max_len, int rows, int dtype, void* stream);
 
 /* Grouped-query decode attention of Q [nh*128] over cache positions
  * [0, min(POS[0] + 1, max_len)), split into nchunk chunks of
@@ -343,6 +362,15 @@ int ttsp_prefill_attention_split(const void* Q, long long q_seq_stride, long lon
  * embed). */
 int ttsp_embed_sum(const void* E, const int* tok, int ntok, int vocab, int D, void* out, int dtype,
                    void* stream);
+
+/* ttsp_embed_sum for `rows` positions: out[r][d] = round(sum_{c < ntok}
+ * E[(c*vocab + tok[c*tok_stride + r]) * D + d]) (tok int32 [ntok][tok_stride]
+ * on the device, each clamped into [0, vocab)); row r has the bits of a
+ * one-position ttsp_embed_sum of column r. Replaces: the summed codebook
+ * embeddings of a prompt span (the prompt's embed in the fork's
+ * forward_generate, reached through app/engine/graphs.py:219-231). */
+int ttsp_embed_sum_rows(const void* E, const int* tok, long long tok_stride, int ntok, int rows, int vocab,
+                        int D, void* out, int dtype, void* stream);
 
 /* out[0] = argmax(X[0..n)), lowest index on ties: greedy decoding in place of
  * the sampler (app/engine/graphs.py:57-73, fusedsample.py). */

@@ -164,6 +164,40 @@ def test_argmax_embed_equals_argmax_then_embed(dtype, n, vocab, D):
         assert int(tok[0]) == int((x.float() == top).nonzero()[0])  # the lowest index holding the maximum
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("ntok,rows,vocab,D,pad", [(11, 512, 4096, 2560, 0), (5, 37, 512, 512, 3),
+                                                   (3, 9, 64, 1000, 0), (1, 4, 16, 8, 1)])
+def test_embed_sum_rows_equals_the_one_position_sum(dtype, ntok, rows, vocab, D, pad):
+    """ttsp_embed_sum_rows == ttsp_embed_sum of each token column, bit for
+    bit (16-byte and one-value paths: D = 1000 is not a multiple of 8), with
+    tokens outside the tables (clamped), -0.0 entries, a padded token stride;
+    and a sample of rows against the oracle's embed_sum."""
+    from oracle import oracle as o
+    from ttspipe_amd import _lib
+
+    lib, st = _lib.lib(), _lib.stream()
+    dt = _lib.dtype_code(dtype)
+    g = torch.Generator(device="cuda").manual_seed(ntok * rows + D)
+    E = torch.randn(ntok * vocab, D, device="cuda", generator=g).to(dtype)
+    E[:, ::5] = -0.0
+    tok = torch.randint(-3, vocab + 3, (ntok, rows + pad), device="cuda", generator=g, dtype=torch.int32)
+    out = torch.empty(rows, D, dtype=dtype, device="cuda")
+    _lib.check(lib.ttsp_embed_sum_rows(E.data_ptr(), tok.data_ptr(), rows + pad, ntok, rows, vocab, D,
+                                       out.data_ptr(), dt, st), "embed_sum_rows")
+    ref = torch.empty(rows, D, dtype=dtype, device="cuda")
+    col = torch.empty(rows, ntok, dtype=torch.int32, device="cuda")
+    col.copy_(tok[:, :rows].t())
+    for r in range(rows):
+        _lib.check(lib.ttsp_embed_sum(E.data_ptr(), col[r].data_ptr(), ntok, vocab, D, ref[r].data_ptr(), dt, st),
+                   "embed_sum")
+    torch.cuda.synchronize()
+    assert torch.equal(out.view(torch.int16), ref.view(torch.int16))
+    Eb = E.view(torch.int16).cpu().numpy().view(np.uint16)
+    for r in sorted({0, rows // 2, rows - 1}):
+        want = o.embed_sum(Eb, col[r].cpu().numpy(), vocab, D, dt)
+        assert np.array_equal(out[r].view(torch.int16).cpu().numpy().view(np.uint16), want)
+
+
 def test_frame_advance_equals_the_torch_bookkeeping():
     """ttsp_frame_advance == history.index_copy_(0, step, tokens),
     step.add_(1), pos.add_(1), index_select(freqs, 0, pos): three frames in a

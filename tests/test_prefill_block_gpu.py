@@ -78,6 +78,63 @@ def test_prefill_block_matches_the_unpatched_block(qk_norm):
     assert torch.equal(ours_v, vc[:, :, 24:64])  # V rows are copied as they are
 
 
+@pytest.mark.gpu
+@pytest.mark.parametrize("qk_norm,rows", [(True, 40), (False, 100)])
+def test_prefill_block_folded_reduces_equal_the_separate_launches(monkeypatch, qk_norm, rows):
+    """A block whose wqkv, wo and w2 all take K splits (d = 1024, 8 q / 2 kv
+    heads, FFN 2048): wqkv's partial sums added inside the head-norm / rotary
+    / KV kernel and the RMSNorms written by wo's and w2's reduces, against
+    the block with a reduce and a norm launch of their own: the output, the
+    next norm's output and every cache row bit for bit."""
+    from tests.gpuutil import bits
+    from tests.test_fused_gpu import _block
+    from ttspipe_amd import _lib, fusedlayer, fusedops, nf4gemv
+    from ttspipe_amd.llama import precompute_freqs_cis
+
+    assert nf4gemv.install() and fusedops.install()
+    lib = _lib.load()
+    assert min(lib.ttsp_nf4_gemm_splits(1536, 1024, rows), lib.ttsp_nf4_gemm_splits(1024, 1024, rows),
+               lib.ttsp_nf4_gemm_splits(1024, 2048, rows)) > 1
+    block, _ = _block(torch.bfloat16, qk_norm, dim=1024, n_head=8, n_local_heads=2, inter=2048, max_len=128, seed=4)
+    kc, vc = block.attention.kv_cache.k_cache, block.attention.kv_cache.v_cache
+    kc.normal_()
+    vc.normal_()
+    saved = (kc.clone(), vc.clone())
+    start = 128 - rows
+    pos = torch.arange(start, 128, device="cuda")
+    mask = torch.tril(torch.ones(128, 128, dtype=torch.bool, device="cuda"))[None, None, pos]
+    freqs = precompute_freqs_cis(128, 128, 1e6).cuda()[pos].contiguous()
+    x = torch.randn(1, rows, 1024, device="cuda").to(torch.bfloat16)
+
+    def run():
+        kc.copy_(saved[0])
+        vc.copy_(saved[1])
+        r = fusedlayer.prefill_block_chain(block, x, freqs, mask, pos, next_norm=block.attention_norm)
+        assert r is not None and r[1] is not None
+        torch.cuda.synchronize()
+        return [bits(t).copy() for t in (*r, kc, vc)]
+
+    used = []
+
+    def spy(fn, tag):
+        def wrapped(*a, **k):
+            r = fn(*a, **k)
+            used.append((tag, r is not None))
+            return r
+        return wrapped
+
+    monkeypatch.setattr(nf4gemv, "matmul_partials", spy(nf4gemv.matmul_partials, "partials"))
+    monkeypatch.setattr(nf4gemv, "matmul_norm", spy(nf4gemv.matmul_norm, "norm"))
+    folded = run()
+    assert used == [("partials", True), ("norm", True), ("norm", True)]
+    monkeypatch.setattr(nf4gemv, "matmul_norm", lambda *a, **k: None)
+    monkeypatch.setattr(nf4gemv, "matmul_partials", lambda *a, **k: None)
+    separate = run()
+    for name, a_, b_ in zip(["out", "out_n", "k_cache", "v_cache"], folded, separate):
+        assert np.array_equal(a_, b_), name
+    assert not np.array_equal(separate[2], bits(saved[0]))  # the span was written
+
+
 # ------------------------------------------------ against an fp64 block
 
 REF_BAR = 3e-3  # rel-norm of the block output against the fp64 block with the fork's roundings
@@ -278,8 +335,10 @@ def _prefill_state(m):
 @pytest.mark.parametrize("n,start", [(64, 0), (40, 8)])
 def test_chained_norms_equal_the_separate_norm_launches(fresh, monkeypatch, n, start):
     """The prompt's blocks handing each other the next RMSNorm from w2's (and
-    wo's) split-K reduce against the same blocks with every norm a launch of
-    its own (`matmul_norm` declined): every KV row and the logits bit for bit."""
+    wo's) split-K reduce, and wqkv's partial sums going straight to the
+    head-norm / rotary / KV kernel, against the same blocks with every norm
+    and reduce a launch of its own (`matmul_norm`, `matmul_partials`
+    declined): every KV row and the logits bit for bit."""
     import numpy as np
 
     from ttspipe_amd import nf4gemv
@@ -293,6 +352,7 @@ def test_chained_norms_equal_the_separate_norm_launches(fresh, monkeypatch, n, s
     chained = _prefill_state(m)
     assert nf4gemv.stats()["fast"] > calls
     monkeypatch.setattr(nf4gemv, "matmul_norm", lambda *a, **k: None)
+    monkeypatch.setattr(nf4gemv, "matmul_partials", lambda *a, **k: None)
     m.prefill_forward(toks, pos, last)
     separate = _prefill_state(m)
     for i, (a, b) in enumerate(zip(chained, separate)):

@@ -53,6 +53,7 @@ SIGNATURES: dict[str, list] = {
     "ttsp_nf4_gemm": [_vp, _i, _vp, _vp, _vp, _vp, _f, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _vp],
     "ttsp_nf4_gemm_splits": [_i, _i, _i],
     "ttsp_nf4_gemm_split": [_vp, _i, _vp, _vp, _vp, _vp, _f, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _vp, _i, _vp],
+    "ttsp_nf4_gemm_partials": [_vp, _i, _vp, _vp, _vp, _vp, _f, _vp, _i, _i, _i, _i, _i, _vp, _i, _vp],
     "ttsp_nf4_gemm_split_norm": [_vp, _i, _vp, _vp, _vp, _vp, _f, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _vp, _i,
                                  _vp, _f, _vp, _vp],
     "ttsp_nf4_gemm_swiglu": [_vp, _i, _vp, _vp, _vp, _vp, _f, _vp, _vp, _vp, _vp, _f, _vp, _vp, _i, _i, _i, _i, _i,
@@ -75,6 +76,8 @@ SIGNATURES: dict[str, list] = {
     "ttsp_attn_decode_qkv_noalloc": [_vp, _vp, _vp, _f, _vp, _i, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _f, _i, _vp],
     "ttsp_attn_decode_qkv_noalloc_max_slots": [],
     "ttsp_qk_rope_kv_rows": [_vp, _ll, _vp, _vp, _f, _vp, _i, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _vp],
+    "ttsp_qk_rope_kv_rows_partials": [_vp, _i, _vp, _vp, _f, _vp, _i, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i,
+                                      _vp],
     "ttsp_prefill_attention": [_vp, _ll, _ll, _vp, _ll, _ll, _vp, _ll, _ll, _vp, _ll, _vp, _i, _i, _i, _i, _f, _i,
                                _vp],
     "ttsp_prefill_max_groups": [],
@@ -85,6 +88,7 @@ SIGNATURES: dict[str, list] = {
     "ttsp_sample_max_top_k": [],
     "ttsp_sample_max_vocab": [],
     "ttsp_embed_sum": [_vp, _vp, _i, _i, _i, _vp, _i, _vp],
+    "ttsp_embed_sum_rows": [_vp, _vp, _ll, _i, _i, _i, _i, _vp, _i, _vp],
     "ttsp_argmax": [_vp, _i, _i, _vp, _vp],
     "ttsp_argmax_embed": [_vp, _i, _i, _vp, _vp, _vp, _i, _i, _vp, _vp],
     "ttsp_frame_advance": [_vp, _i, _vp, _i, _vp, _vp, _vp, _i, _i, _vp, _vp],

@@ -5,6 +5,8 @@
 // counter-based fill that materialises seeded synthetic weights on the device.
 #include "ttsp_common.h"
 
+#include <type_traits>
+
 namespace ttsp {
 
 // out[d] = round(sum_{c < ntok} E[(c * vocab + tok[c]) * D + d]), fp32 sum in
@@ -22,6 +24,69 @@ __global__ __launch_bounds__(256) void embed_sum_kernel(const uint16_t* __restri
     acc = __fadd_rn(acc, Elem<DT>::load(E[((size_t)c * vocab + t) * D + d]));
   }
   out[d] = Elem<DT>::store(acc);
+}
+
+// embed_sum_kernel for several rows: row r sums tables c < ntok at token
+// tok[c * tok_stride + r], the same fp32 adds in codebook order. V = 8: a
+// thread per 8 consecutive values (16-byte loads; D % 8 == 0 and E, out
+// 16-byte aligned), V = 1: a thread per value. Up to EMB_ROWS_T tables the
+// token loads, then the table loads, are all issued before the first add.
+constexpr int EMB_ROWS_T = 16;
+template <int DT, int V>
+__global__ __launch_bounds__(256) void embed_sum_rows_kernel(const uint16_t* __restrict__ E,
+                                                            const int* __restrict__ tok, long long tok_stride,
+                                                            int ntok, int rows, int vocab, int D,
+                                                            uint16_t* __restrict__ out) {
+  using Vec = typename std::conditional<V == 8, uint4, uint16_t>::type;
+  const int per_row = D / V;
+  const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= (long long)per_row * rows) return;
+  const int r = (int)(i / per_row), d = (int)(i % per_row) * V;
+  float acc[V];
+#pragma unroll
+  for (int k = 0; k < V; ++k) acc[k] = 0.0f;
+  auto add = [&](const Vec& w) {
+    if constexpr (V == 8) {
+      const uint32_t u[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        acc[2 * k] = __fadd_rn(acc[2 * k], Elem<DT>::load(u[k]));
+        acc[2 * k + 1] = __fadd_rn(acc[2 * k + 1], Elem<DT>::load(u[k] >> 16));
+      }
+    } else {
+      acc[0] = __fadd_rn(acc[0], Elem<DT>::load(w));
+    }
+  };
+  auto row_of = [&](int c) {
+    int t = tok[c * tok_stride + r];
+    t = t < 0 ? 0 : (t >= vocab ? vocab - 1 : t);
+    return reinterpret_cast<const Vec*>(E + ((size_t)c * vocab + t) * D + d);
+  };
+  if (ntok <= EMB_ROWS_T) {
+    const Vec* src[EMB_ROWS_T];
+    Vec w[EMB_ROWS_T];
+#pragma unroll
+    for (int c = 0; c < EMB_ROWS_T; ++c)
+      if (c < ntok) src[c] = row_of(c);
+#pragma unroll
+    for (int c = 0; c < EMB_ROWS_T; ++c)
+      if (c < ntok) w[c] = *src[c];
+#pragma unroll
+    for (int c = 0; c < EMB_ROWS_T; ++c)
+      if (c < ntok) add(w[c]);
+  } else {
+    for (int c = 0; c < ntok; ++c) add(*row_of(c));
+  }
+  uint16_t* o = out + (size_t)r * D + d;
+  if constexpr (V == 8) {
+    uint32_t w[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+      w[k] = (uint32_t)Elem<DT>::store(acc[2 * k]) | ((uint32_t)Elem<DT>::store(acc[2 * k + 1]) << 16);
+    *reinterpret_cast<uint4*>(o) = make_uint4(w[0], w[1], w[2], w[3]);
+  } else {
+    o[0] = Elem<DT>::store(acc[0]);
+  }
 }
 
 // Index of the largest of X[0..n), the lowest index on ties (NaN never wins;
@@ -151,6 +216,30 @@ extern "C" int ttsp_embed_sum(const void* E, const int* tok, int ntok, int vocab
                        ntok, vocab, D, (uint16_t*)out);
   else
     return (int)hipErrorInvalidValue;
+  TTSP_RETURN_LAUNCH();
+}
+
+extern "C" int ttsp_embed_sum_rows(const void* E, const int* tok, long long tok_stride, int ntok, int rows,
+                                   int vocab, int D, void* out, int dtype, hipStream_t stream) {
+  if (ntok <= 0 || rows <= 0 || vocab <= 0 || D <= 0 || tok_stride < rows || !E || !tok || !out)
+    return (int)hipErrorInvalidValue;
+  const bool vec = D % 8 == 0 && (uintptr_t)E % 16 == 0 && (uintptr_t)out % 16 == 0;
+  const long long threads = (long long)(vec ? D / 8 : D) * rows;
+  if (threads > (1LL << 31) - 256) return (int)hipErrorInvalidValue;
+  const dim3 grid((unsigned)((threads + 255) / 256));
+#define TTSP_ER(DTV, VV)                                                                                    \
+  hipLaunchKernelGGL((embed_sum_rows_kernel<DTV, VV>), grid, dim3(256), 0, stream, (const uint16_t*)E, tok, \
+                     tok_stride, ntok, rows, vocab, D, (uint16_t*)out)
+  if (dtype == DT_F16) {
+    if (vec) TTSP_ER(DT_F16, 8);
+    else TTSP_ER(DT_F16, 1);
+  } else if (dtype == DT_BF16) {
+    if (vec) TTSP_ER(DT_BF16, 8);
+    else TTSP_ER(DT_BF16, 1);
+  } else {
+    return (int)hipErrorInvalidValue;
+  }
+#undef TTSP_ER
   TTSP_RETURN_LAUNCH();
 }
 

@@ -33,32 +33,50 @@ namespace ttsp {
 // arithmetic (head_norm_rope), so both paths give the same bits. A q head goes
 // to Q, a k head to KC[kv][pos], a v head is copied to VC[kv][pos]. Row
 // blockIdx.y reads its own QKV row, rotary row and position; the rotary table
-// is read a dword at a time (4-byte aligned).
+// is read a dword at a time (4-byte aligned). P: the row is a K-split GEMM's
+// fp32 partial sums (split z of row r at YP[(z * rows + r) * qkv_rs]), added
+// in split order and rounded as the split GEMM's own reduce does.
 constexpr int QKV_WAVES = 4;
 
-template <int DT>
+template <int DT, bool P = false>
 __global__ __launch_bounds__(64 * QKV_WAVES) void qk_rope_kv_kernel(
     const uint16_t* __restrict__ QKV, const uint16_t* __restrict__ QW,
     const uint16_t* __restrict__ KW, float eps, const void* __restrict__ F, int ftype,
     const long long* __restrict__ POS, uint16_t* __restrict__ Q, uint16_t* __restrict__ KC,
-    uint16_t* __restrict__ VC, int nh, int nkv, int max_len, int qkv_rs) {
+    uint16_t* __restrict__ VC, int nh, int nkv, int max_len, int qkv_rs, const float* __restrict__ YP = nullptr,
+    int splits = 0) {
   const int lane = threadIdx.x & 63;
   const int head = blockIdx.x * QKV_WAVES + (threadIdx.x >> 6);
   const int row = blockIdx.y;
   if (head >= nh + 2 * nkv) return;
   const long long pos = POS[row];
   if (pos < 0 || pos >= max_len) return;  // no cache slot to write: leave everything untouched
-  const uint16_t* src = QKV + (size_t)row * qkv_rs + (size_t)head * HD;
+  float lo, hi;
+  if constexpr (P) {
+    const size_t o = (size_t)row * qkv_rs + (size_t)head * HD, zs = (size_t)gridDim.y * qkv_rs;
+    lo = YP[o + lane];
+    hi = YP[o + lane + 64];
+    for (int z = 1; z < splits; ++z) {
+      lo += YP[z * zs + o + lane];
+      hi += YP[z * zs + o + lane + 64];
+    }
+    lo = Elem<DT>::load(Elem<DT>::store(lo));
+    hi = Elem<DT>::load(Elem<DT>::store(hi));
+  }
+  const uint16_t* src = P ? nullptr : QKV + (size_t)row * qkv_rs + (size_t)head * HD;
   if (head >= nh + nkv) {
     uint16_t* v = VC + ((long long)(head - nh - nkv) * max_len + pos) * HD;
-    v[lane] = src[lane];
-    v[lane + 64] = src[lane + 64];
+    v[lane] = P ? (uint16_t)Elem<DT>::store(lo) : src[lane];
+    v[lane + 64] = P ? (uint16_t)Elem<DT>::store(hi) : src[lane + 64];
     return;
   }
   const bool is_q = head < nh;
   const uint16_t* w = is_q ? QW : KW;
   const RopeF f = load_rope((const uint8_t*)F + (size_t)row * HD * (ftype == DT_F32 ? 4 : 2), ftype, lane);
-  float lo = Elem<DT>::load(src[lane]), hi = Elem<DT>::load(src[lane + 64]);
+  if constexpr (!P) {
+    lo = Elem<DT>::load(src[lane]);
+    hi = Elem<DT>::load(src[lane + 64]);
+  }
   const uint16_t nwl = w ? w[lane] : 0, nwh = w ? w[lane + 64] : 0;
   head_norm_rope<DT>(lo, hi, w != nullptr, nwl, nwh, eps, f, lane);
   uint16_t* dst = is_q ? Q + (size_t)row * nh * HD + (size_t)head * HD
@@ -385,6 +403,25 @@ extern "C" int ttsp_qk_rope_kv_rows(const void* QKV, long long qkv_row_stride, c
   else if (dtype == DT_BF16) TTSP_QKR(DT_BF16);
   else return (int)hipErrorInvalidValue;
 #undef TTSP_QKR
+  TTSP_RETURN_LAUNCH();
+}
+
+extern "C" int ttsp_qk_rope_kv_rows_partials(const float* YP, int splits, const void* QW, const void* KW, float eps,
+                                             const void* F, int ftype, const long long* POS, void* Q, void* KC,
+                                             void* VC, int nh, int nkv, int max_len, int rows, int dtype,
+                                             hipStream_t stream) {
+  if (nh <= 0 || nkv <= 0 || max_len <= 0 || ftype < 0 || ftype > 2 || rows <= 0 || rows > 65535 || !YP ||
+      splits < 2 || splits > 8 || (uintptr_t)F % 4)
+    return (int)hipErrorInvalidValue;
+  const int qkv_rs = (nh + 2 * nkv) * HD;
+#define TTSP_QKP(DTV)                                                                                           \
+  hipLaunchKernelGGL((qk_rope_kv_kernel<DTV, true>), dim3((nh + 2 * nkv + QKV_WAVES - 1) / QKV_WAVES, rows),      \
+                     dim3(64 * QKV_WAVES), 0, stream, nullptr, (const uint16_t*)QW, (const uint16_t*)KW, eps, F, \
+                     ftype, POS, (uint16_t*)Q, (uint16_t*)KC, (uint16_t*)VC, nh, nkv, max_len, qkv_rs, YP, splits)
+  if (dtype == DT_F16) TTSP_QKP(DT_F16);
+  else if (dtype == DT_BF16) TTSP_QKP(DT_BF16);
+  else return (int)hipErrorInvalidValue;
+#undef TTSP_QKP
   TTSP_RETURN_LAUNCH();
 }
 

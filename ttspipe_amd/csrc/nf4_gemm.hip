@@ -713,6 +713,21 @@ extern "C" int ttsp_nf4_gemm_swiglu(const void* X, int x_dtype, const uint8_t* W
                         M, K, N, bs_shift, bs2_shift, stream);
 }
 
+extern "C" int ttsp_nf4_gemm_partials(const void* X, int x_dtype, const uint8_t* W, const uint8_t* A8,
+                                      const float* AMAX, const float* CODE2, float offset, const float* LUT, int M,
+                                      int K, int N, int blocksize, int blocksize2, float* work, int splits,
+                                      hipStream_t stream) {
+  if (N <= 1 || splits < 2 || splits != ttsp_nf4_gemm_splits(M, K, N) || !work || (uintptr_t)work % 16)
+    return (int)hipErrorInvalidValue;
+  int bs_shift, bs2_shift;
+  // (Y is not written: the split launch stops at its partial sums)
+  if (int rc = gemm_args(X, W, A8, AMAX, CODE2, LUT, work, nullptr, 0, M, K, N, blocksize, blocksize2, &bs_shift,
+                         &bs2_shift))
+    return rc;
+  return gemm_mfma(X, x_dtype, W, A8, AMAX, CODE2, offset, LUT, nullptr, nullptr, 0, M, K, N, bs_shift, bs2_shift,
+                   gemm_plan(M, K, N), work, stream, false);
+}
+
 extern "C" int ttsp_nf4_gemm_split_norm(const void* X, int x_dtype, const uint8_t* W, const uint8_t* A8,
                                         const float* AMAX, const float* CODE2, float offset, const float* LUT,
                                         void* Y, const void* R, int epi, int M, int K, int N, int blocksize,

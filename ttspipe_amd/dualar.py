@@ -540,10 +540,14 @@ class SyntheticDualAR:
         cfg = self.cfg
         width = cfg.max_seq_len if width is None else width
         n = inp.shape[1]
-        rows = torch.clamp(inp.long(), 0, cfg.vocab_size - 1)
-        rows = rows + (torch.arange(cfg.n_tokens, device=inp.device) * cfg.vocab_size).view(-1, 1)
-        emb = self.tensors["embeddings"].view(-1, cfg.dim).index_select(0, rows.reshape(-1))
-        x = emb.view(cfg.n_tokens, n, cfg.dim).float().sum(0).to(self.dtype).view(1, n, cfg.dim)
+        if inp.dtype != torch.int32 or inp.shape[0] != cfg.n_tokens or inp.stride(1) != 1:
+            raise ValueError("inp must be int32 (n_tokens, n) with contiguous rows")
+        # every position's summed codebook embeddings, as a decode step sums them
+        x = torch.empty(1, n, cfg.dim, dtype=self.dtype, device=inp.device)
+        rc = self._lib.ttsp_embed_sum_rows(self.tensors["embeddings"].data_ptr(), inp.data_ptr(), inp.stride(0),
+                                           cfg.n_tokens, n, cfg.vocab_size, cfg.dim, x.data_ptr(),
+                                           _lib.dtype_code(self.dtype), _lib.stream())
+        self._check(rc, "ttsp_embed_sum_rows")
         freqs = self.freqs.index_select(0, pos)
         mask = self.causal.index_select(0, pos)[None, None, :, :width]
         # each block hands the next its attention RMSNorm, written by w2's
@@ -728,7 +732,7 @@ def benchmark(n_steps: int = 256, warmup: int = 8, cfg: DualARConfig = DualARCon
                       f"{cfg.num_codebooks} codebooks of {cfg.codebook_size}, KV from {cfg.prefill_len}"}
 
 
-def prefill_benchmark(n_tokens: int = 512, reps: int = 5, cfg: DualARConfig = DualARConfig()) -> dict:
+def prefill_benchmark(n_tokens: int = 512, reps: int = 20, cfg: DualARConfig = DualARConfig()) -> dict:
     """ms to prefill an `n_tokens` prompt (one captured bucket graph per span)
     through the slow transformer, from position 0, synthetic tokens."""
     import torch

@@ -255,8 +255,9 @@ def prefill_block_chain(block, x, freqs_cis, mask, input_pos, *, xn=None, next_n
 
     The fork's block in its own order with the prefill kernels: RMSNorm,
     wqkv GEMM, q/k head norms + rotary + KV-cache write for every row in one
-    launch (the decode step's kernel over rows; the fork's modules when the
-    cache or tables do not fit it), one-launch causal attention, wo GEMM with
+    launch (the decode step's kernel over rows, which also adds a K-split
+    wqkv's partial sums; the fork's modules when the cache or tables do not
+    fit it), one-launch causal attention, wo GEMM with
     the residual add in its epilogue, RMSNorm, w1 and w3 GEMMs with the
     SwiGLU gate (one launch where it serves the shape, else w3's epilogue), w2 GEMM with
     the residual add (reference: the
@@ -276,8 +277,7 @@ def prefill_block_chain(block, x, freqs_cis, mask, input_pos, *, xn=None, next_n
     an, fn = block.attention_norm, block.ffn_norm
     if xn is None:
         xn = fusedops.rms_norm(x, an.weight, an.eps)
-    qkv = None if xn is None else nf4gemv.matmul(a.wqkv, xn)
-    if qkv is None:
+    if xn is None:
         return None
     kc, vc = a.kv_cache.k_cache, a.kv_cache.v_cache
     max_len = kc.shape[2]
@@ -285,17 +285,35 @@ def prefill_block_chain(block, x, freqs_cis, mask, input_pos, *, xn=None, next_n
     rows_ok = (ftype is not None and freqs_cis.is_contiguous() and freqs_cis.numel() == n * hd
                and input_pos.dtype == torch.long and input_pos.is_contiguous() and kc.is_contiguous()
                and vc.is_contiguous() and kc.dtype == x.dtype and tuple(kc.shape) == (1, nkv, max_len, hd))
+    # a K-split wqkv hands its fp32 partial sums straight to the head-norm /
+    # rotary / KV kernel, which adds them as the split's own reduce would
+    part = None
+    if rows_ok and a.wqkv._nf4_fast["M"] == (nh + 2 * nkv) * hd:
+        part = nf4gemv.matmul_partials(a.wqkv, xn)
+    qkv = None
+    if part is None:
+        qkv = nf4gemv.matmul(a.wqkv, xn)
+        if qkv is None:
+            return None
     if rows_ok:
         # head norms, rotary and the KV write for every row in one launch
         q = torch.empty(bsz, n, nh, hd, dtype=x.dtype, device=x.device)
         qn, kn = (a.q_norm, a.k_norm) if a.attention_qk_norm else (None, None)
         eps = float(qn.eps) if qn is not None else 0.0
-        rc = _lib.lib().ttsp_qk_rope_kv_rows(
-            qkv.data_ptr(), qkv.shape[-1], _lib.ptr(None if qn is None else qn.weight),
-            _lib.ptr(None if kn is None else kn.weight), eps, freqs_cis.data_ptr(), ftype, input_pos.data_ptr(),
-            q.data_ptr(), kc.data_ptr(), vc.data_ptr(), nh, nkv, max_len, n, _lib.dtype_code(x.dtype),
-            _lib.stream())
-        _lib.check(rc, "ttsp_qk_rope_kv_rows")
+        qw, kw = _lib.ptr(None if qn is None else qn.weight), _lib.ptr(None if kn is None else kn.weight)
+        if part is not None:
+            work, splits = part
+            rc = _lib.lib().ttsp_qk_rope_kv_rows_partials(
+                work.data_ptr(), splits, qw, kw, eps, freqs_cis.data_ptr(), ftype, input_pos.data_ptr(),
+                q.data_ptr(), kc.data_ptr(), vc.data_ptr(), nh, nkv, max_len, n, _lib.dtype_code(x.dtype),
+                _lib.stream())
+            _lib.check(rc, "ttsp_qk_rope_kv_rows_partials")
+        else:
+            rc = _lib.lib().ttsp_qk_rope_kv_rows(
+                qkv.data_ptr(), qkv.shape[-1], qw, kw, eps, freqs_cis.data_ptr(), ftype, input_pos.data_ptr(),
+                q.data_ptr(), kc.data_ptr(), vc.data_ptr(), nh, nkv, max_len, n, _lib.dtype_code(x.dtype),
+                _lib.stream())
+            _lib.check(rc, "ttsp_qk_rope_kv_rows")
         q, k, v = q.transpose(1, 2), kc, vc
     else:
         q, k, v = qkv.split([nh * hd, nkv * hd, nkv * hd], dim=-1)

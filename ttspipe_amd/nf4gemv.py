@@ -227,6 +227,39 @@ def matmul(module, x, *, epi: int = EPI_NONE, operand=None, out=None):
 NORM_MAX_M = 4096
 
 
+def matmul_partials(module, x):
+    """`(work, splits)`: the K-split launch of `matmul(module, x)` without its
+    reduce, work the fp32 partial sums [splits, rows, M] for a consumer that
+    adds them in split order; None where the shape runs unsplit (or the
+    kernels do not take the call)."""
+    import torch
+
+    fast = getattr(module, "_nf4_fast", None)
+    if fast is None:
+        return None
+    dt = _lib.dtype_code(x.dtype)
+    if dt not in (_lib.DT_F16, _lib.DT_BF16) or x.device.type != "cuda":
+        return None
+    K, M = fast["K"], fast["M"]
+    if x.shape[-1] != K or not x.is_contiguous() or x.data_ptr() % 16:
+        return None
+    rows = x.numel() // K
+    if rows < 2:
+        return None
+    lib = _lib.lib()
+    splits = lib.ttsp_nf4_gemm_splits(M, K, rows)
+    if splits < 2:
+        return None
+    work = torch.empty(splits, rows, M, dtype=torch.float32, device=x.device)
+    rc = lib.ttsp_nf4_gemm_partials(
+        x.data_ptr(), dt, fast["w"], fast["a8"], fast["amax"], fast["code2"], fast["offset"],
+        fast["lut"].data_ptr(), M, K, rows, fast["bs"], fast["bs2"], work.data_ptr(), splits, _lib.stream())
+    if rc:
+        raise RuntimeError(f"ttsp_nf4_gemm_partials failed: hipError_t {rc}")
+    _stats["fast"] += 1
+    return work, splits
+
+
 def matmul_norm(module, x, norm_weight, eps: float, *, epi: int = EPI_NONE, operand=None):
     """`(y, rms_norm(y))` for several rows with the norm folded into the
     split-K reduce, or None where that form does not serve the call (one row,
