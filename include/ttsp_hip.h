@@ -237,6 +237,18 @@ int ttsp_attn_decode(const void* Q, const void* KC, const void* VC, const long l
                      float* PL, float* PACC, void* Y, int nh, int nkv, int max_len, int nchunk,
                      float scale, int dtype, void* stream);
 
+/* ttsp_attn_decode for `rows` query rows at once: row r reads Q + r*nh*128
+ * and POS[r], attends over cache positions [0, min(POS[r] + 1, max_len)) and
+ * writes Y + r*nh*128; scratch PM, PL [rows * nh * nchunk], PACC
+ * [rows * nh * nchunk * 128]. Each row's result is the one-position entry's
+ * for that row, bit for bit (a causal prompt span whose K/V rows are already
+ * in the cache). Replaces: the grouped decode attention the reference runs for
+ * a span of up to 64 positions (fastpath.py:133-174, 243-250), for a causal
+ * mask. */
+int ttsp_attn_decode_rows(const void* Q, const void* KC, const void* VC, const long long* POS, float* PM,
+                          float* PL, float* PACC, void* Y, int nh, int nkv, int max_len, int nchunk,
+                          float scale, int rows, int dtype, void* stream);
+
 /* qk_rope_kv and the decode attention in one pass: the head norms and rotary
  * of the query heads are applied inside the attention workgroups (from QKV),
  * the new position's K/V row is computed, written to KC/VC[kv][POS[0]] and used

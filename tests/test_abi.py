@@ -199,6 +199,8 @@ def test_invalid_arguments_are_rejected_before_any_launch():
     assert lib.ttsp_nf4_gemm(8, 1, 8, None, 8, None, 0.0, 8, 8, None, 1, 64, 128, 1, 64, 256, None) == 1
     assert lib.ttsp_nf4_dequant(8, None, 8, None, 0.0, 8, 8, 1, -1, 64, 256, None) == 1
     assert lib.ttsp_attn_decode(8, 8, 8, 8, 8, 8, 8, 8, 32, 7, 64, 1, 0.1, 1, None) == 1  # nh % nkv
+    assert lib.ttsp_attn_decode_rows(8, 8, 8, 8, 8, 8, 8, 8, 32, 8, 64, 1, 0.1, 0, 1, None) == 1  # no rows
+    assert lib.ttsp_attn_decode_rows(8, 8, 8, 8, 8, 8, 8, 8, 32, 8, 64, 1, 0.1, 70000, 1, None) == 1
     assert lib.ttsp_attn_chunk() == 64
     # the frame's glue: empty rows, tables or histories, missing pointers, an unknown dtype
     assert lib.ttsp_argmax_embed(8, 0, 1, 8, None, 8, 16, 8, 8, None) == 1

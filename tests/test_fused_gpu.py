@@ -203,6 +203,44 @@ def test_decode_attention_bit_exact(hip, orc, L, dtype):
     assert relative_error(o.to_f32(bits(y), dt), ref) < 5e-3
 
 
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("positions,max_len,nh,nkv,nchunk", [
+    ([512, 513], 2304, 32, 8, 36),                  # a 2-token tail after 512 cached positions
+    ([0, 1, 2, 3, 4], 8, 8, 2, 1),                  # a first span: the window ends with it
+    ([60, 61, 62, 63, 64, 65, 66, 67], 128, 4, 1, 2),  # a span across a chunk edge
+    (list(range(2290, 2304)), 2304, 32, 8, 36),     # the cache's last positions
+    ([7, 300, 41, 2000, 64, 65], 2304, 16, 4, 36)])  # rows in any order, one a row
+def test_decode_attention_rows_equal_one_position_each(hip, orc, dtype, positions, max_len, nh, nkv, nchunk):
+    """ttsp_attn_decode_rows == ttsp_attn_decode for each row's position, bit
+    for bit, and row 0 against the oracle's emulation."""
+    from ttspipe_amd import _lib
+
+    S, dt = len(positions), dt_code(dtype)
+    qb = randn_bits(S * nh * 128, dtype, seed=S + nh, scale=2.0)
+    kcb = randn_bits(nkv * max_len * 128, dtype, seed=S + 1)
+    vcb = randn_bits(nkv * max_len * 128, dtype, seed=S + 2)
+    f32 = dict(dtype=torch.float32, device="cuda")
+    qd, kd, vd = from_bits(qb, dtype), from_bits(kcb, dtype), from_bits(vcb, dtype)
+    posd = torch.tensor(positions, dtype=torch.long, device="cuda")
+    pm, pl = torch.empty(S * nh * nchunk, **f32), torch.empty(S * nh * nchunk, **f32)
+    pacc = torch.empty(S * nh * nchunk * 128, **f32)
+    y = torch.empty(S, nh * 128, dtype=dtype, device="cuda")
+    rc = hip.ttsp_attn_decode_rows(qd.data_ptr(), kd.data_ptr(), vd.data_ptr(), posd.data_ptr(), pm.data_ptr(),
+                                   pl.data_ptr(), pacc.data_ptr(), y.data_ptr(), nh, nkv, max_len, nchunk,
+                                   float(128**-0.5), S, dt, _lib.stream())
+    assert rc == 0
+    for r, p in enumerate(positions):
+        one = torch.empty(nh * 128, dtype=dtype, device="cuda")
+        pr = torch.tensor([p], dtype=torch.long, device="cuda")
+        rc = hip.ttsp_attn_decode(qd[r * nh * 128:].data_ptr(), kd.data_ptr(), vd.data_ptr(), pr.data_ptr(),
+                                  pm.data_ptr(), pl.data_ptr(), pacc.data_ptr(), one.data_ptr(), nh, nkv, max_len,
+                                  nchunk, float(128**-0.5), dt, _lib.stream())
+        assert rc == 0
+        assert np.array_equal(bits(y[r]), bits(one)), (r, p)
+    expect = orc.attn_emul(qb[:nh * 128], kcb, vcb, positions[0], nh, nkv, max_len, nchunk, 128**-0.5, dt)
+    assert np.array_equal(bits(y[0]), expect), first_mismatch(bits(y[0]), expect)
+
+
 @pytest.mark.parametrize("qk_norm", [True, False])
 @pytest.mark.parametrize("dtype", DTYPES)
 @pytest.mark.parametrize("pos,max_len,nh,nkv", [(0, 2304, 32, 8), (37, 2304, 32, 8), (63, 2304, 32, 8),

@@ -98,13 +98,15 @@ __global__ __launch_bounds__(1024) void attn_partial_kernel(
   uint16_t* v_s = k_s + ACHUNK * KPAD;                       // [ACHUNK][HD]
 
   const int kh = blockIdx.x, c = blockIdx.y;
+  const int row = blockIdx.z;  // query row of the rows form: Q, POS and the partials by row (0: one position)
   const int tid = threadIdx.x, nthr = blockDim.x;
   const int g = tid >> 6, lane = tid & 63;
-  const int qh = kh * groups + g;
+  const int qh = kh * groups + g, nh = (int)gridDim.x * groups;
+  Q += (size_t)row * nh * HD;
   // Positions [0, L) are live; the cache holds max_len of them.
-  const long long L = min(POS[0] + 1, (long long)max_len);
+  const long long L = min(POS[row] + 1, (long long)max_len);
   const long long j0 = (long long)c * ACHUNK;
-  const size_t slot = (size_t)qh * nchunk + c;
+  const size_t slot = ((size_t)row * nh + qh) * nchunk + c;
   if (j0 >= L) {
     if (lane == 0) {
       PM[slot] = -1e30f;
@@ -164,7 +166,8 @@ __global__ __launch_bounds__(HD) void attn_combine_kernel(const float* __restric
                                                           uint16_t* __restrict__ Y, int nchunk) {
   __shared__ __align__(16) float wl_s[CMAX][2];  // per chunk: w_c, l_c
   __shared__ float mx_s[2];
-  const int qh = blockIdx.x, d = threadIdx.x, lane = d & 63;
+  // head blockIdx.x of query row blockIdx.y (the rows form; 0 for one position)
+  const int qh = blockIdx.y * gridDim.x + blockIdx.x, d = threadIdx.x, lane = d & 63;
   const float* acc = PACC + (size_t)qh * nchunk * HD + d;
   float cur[CMB];
 #pragma unroll
@@ -422,6 +425,31 @@ extern "C" int ttsp_qk_rope_kv_rows_partials(const float* YP, int splits, const 
   else if (dtype == DT_BF16) TTSP_QKP(DT_BF16);
   else return (int)hipErrorInvalidValue;
 #undef TTSP_QKP
+  TTSP_RETURN_LAUNCH();
+}
+
+extern "C" int ttsp_attn_decode_rows(const void* Q, const void* KC, const void* VC, const long long* POS,
+                                     float* PM, float* PL, float* PACC, void* Y, int nh, int nkv, int max_len,
+                                     int nchunk, float scale, int rows, int dtype, hipStream_t stream) {
+  if (nh <= 0 || nkv <= 0 || nh % nkv || nchunk <= 0 || max_len <= 0 || rows <= 0 || rows > 65535 || !Q || !KC ||
+      !VC || !POS || !PM || !PL || !PACC || !Y)
+    return (int)hipErrorInvalidValue;
+  const int groups = nh / nkv;
+  if (groups > 16 || nchunk > CMAX) return (int)hipErrorInvalidValue;
+  const size_t shmem = sizeof(float) * (size_t)groups * (HD + ACHUNK) +
+                       sizeof(uint16_t) * (size_t)ACHUNK * (KPAD + HD);
+#define TTSP_AR(DTV)                                                                                    \
+  do {                                                                                                  \
+    hipLaunchKernelGGL(attn_partial_kernel<DTV>, dim3(nkv, nchunk, rows), dim3(64 * groups), shmem, stream, \
+                       (const uint16_t*)Q, (const uint16_t*)KC, (const uint16_t*)VC, POS, PM, PL, PACC,    \
+                       groups, max_len, nchunk, scale);                                                 \
+    hipLaunchKernelGGL(attn_combine_kernel<DTV>, dim3(nh, rows), dim3(HD), 0, stream, PM, PL, PACC,     \
+                       (uint16_t*)Y, nchunk);                                                           \
+  } while (0)
+  if (dtype == DT_F16) TTSP_AR(DT_F16);
+  else if (dtype == DT_BF16) TTSP_AR(DT_BF16);
+  else return (int)hipErrorInvalidValue;
+#undef TTSP_AR
   TTSP_RETURN_LAUNCH();
 }
 

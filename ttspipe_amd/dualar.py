@@ -555,7 +555,7 @@ class SyntheticDualAR:
         xn = None
         for i, blk in enumerate(self.layers):
             nxt = self.layers[i + 1].attention_norm if i + 1 < len(self.layers) else None
-            r = fusedlayer.prefill_block_chain(blk, x, freqs, mask, pos, xn=xn, next_norm=nxt)
+            r = fusedlayer.prefill_block_chain(blk, x, freqs, mask, pos, xn=xn, next_norm=nxt, causal=True)
             if r is None:
                 x, xn = blk(x, freqs, mask, pos), None
             else:

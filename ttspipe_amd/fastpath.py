@@ -12,15 +12,18 @@ the matrix cores) for any number of new positions: the reference runs
 `decode_attention` for up to `GROUPED_MAX_QUERY` queries and torch's
 `scaled_dot_product_attention` with the boolean mask beyond
 (app/engine/fastpath.py:244-268). It declines (returns None) what it does not
-take, and the caller then runs `decode_attention`.
+take, and the caller then runs `decode_attention`. `causal_rows_attention`
+serves a short span whose mask is known to be causal with the decode step's
+attention kernels, row by row.
 """
 
 from __future__ import annotations
 
 GROUPED_MAX_QUERY = 64
 HEAD_DIM = 128
+CHUNK = 64  # cache positions per chunk of the decode attention (ttsp_attn_chunk)
 
-_stats = {"prefill_attn": 0, "prefill_declined": 0}
+_stats = {"prefill_attn": 0, "prefill_declined": 0, "causal_rows": 0}
 
 
 def stats() -> dict:
@@ -92,6 +95,47 @@ def prefill_attention(q, k, v, mask, n_head, n_local_heads, head_dim, out=None, 
     _lib.check(rc, "ttsp_prefill_attention_split")
     _stats["prefill_attn"] += 1
     return out.view(1, seqlen, n_head, head_dim).transpose(1, 2)
+
+
+#: Longest causal span `causal_rows_attention` serves (the grouped decode
+#: attention row by row); longer spans take `prefill_attention`.
+CAUSAL_ROWS_MAX = 8
+
+
+def causal_rows_attention(q, k_cache, v_cache, input_pos, n_head, n_local_heads, width):
+    """Attention of S query rows (q contiguous (1, S, n_head, 128)) at
+    positions `input_pos` (int64 (S,)) over the cache (1, n_local_heads,
+    max_len, 128) with the causal mask - row i sees positions 0 .. pos[i],
+    which must lie below `width`, the mask's key count - as the decode step's
+    attention computes each row (bit for bit the one-position result). Returns
+    (1, S, n_head * 128); None when declined (shapes, dtypes, S >
+    CAUSAL_ROWS_MAX)."""
+    import torch
+
+    from ttspipe_amd import _lib
+
+    if not _lib.gpu_present():
+        return None
+    S = q.shape[1] if q.dim() == 4 else 0
+    if (S < 1 or S > CAUSAL_ROWS_MAX or q.shape != (1, S, n_head, HEAD_DIM) or not q.is_contiguous()
+            or k_cache.dim() != 4 or k_cache.shape[0] != 1 or k_cache.shape[1] != n_local_heads
+            or k_cache.shape[3] != HEAD_DIM or v_cache.shape != k_cache.shape or not k_cache.is_contiguous()
+            or not v_cache.is_contiguous() or k_cache.dtype != q.dtype or v_cache.dtype != q.dtype
+            or input_pos.dtype != torch.long or input_pos.numel() != S or not input_pos.is_contiguous()
+            or n_head % n_local_heads or _lib.dtype_code(q.dtype) not in (_lib.DT_F16, _lib.DT_BF16)):
+        return None
+    max_len = k_cache.shape[2]
+    nchunk = -(-min(width, max_len) // CHUNK)
+    pm = torch.empty(2 * S * n_head * nchunk, dtype=torch.float32, device=q.device)
+    pacc = torch.empty(S * n_head * nchunk * HEAD_DIM, dtype=torch.float32, device=q.device)
+    y = torch.empty(1, S, n_head * HEAD_DIM, dtype=q.dtype, device=q.device)
+    rc = _lib.lib().ttsp_attn_decode_rows(
+        q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), input_pos.data_ptr(), pm.data_ptr(),
+        pm[S * n_head * nchunk:].data_ptr(), pacc.data_ptr(), y.data_ptr(), n_head, n_local_heads, max_len, nchunk,
+        float(HEAD_DIM**-0.5), S, _lib.dtype_code(q.dtype), _lib.stream())
+    _lib.check(rc, "ttsp_attn_decode_rows")
+    _stats["causal_rows"] += 1
+    return y
 
 
 def prefill_work_floats(seqlen: int, n_head: int, splits: int) -> int:

@@ -244,14 +244,18 @@ def prefill_block(block, x, freqs_cis, mask, input_pos):
     return None if r is None else r[0]
 
 
-def prefill_block_chain(block, x, freqs_cis, mask, input_pos, *, xn=None, next_norm=None):
+def prefill_block_chain(block, x, freqs_cis, mask, input_pos, *, xn=None, next_norm=None, causal=False):
     """`(out, out_n)`: the block's output for several positions (B = 1, S > 1)
     and, with `next_norm` (an RMSNorm module), `next_norm(out)` for the next
     block (else None); None when the block declines.
     `xn`, if given, is this block's `attention_norm(x)` (a previous call's
     `out_n`), whose launch is then skipped; where the split-K reduce of wo and
     w2 serves the shape it writes the following RMSNorm too
-    (`nf4gemv.matmul_norm`), bit for bit the separate launch.
+    (`nf4gemv.matmul_norm`), bit for bit the separate launch. `causal`: the
+    caller's promise that the mask is the causal one (row i allows keys
+    0 .. input_pos[i], all below the mask's width); a span of up to
+    `fastpath.CAUSAL_ROWS_MAX` rows then attends row by row as the decode
+    step does (`fastpath.causal_rows_attention`), without reading the mask.
 
     The fork's block in its own order with the prefill kernels: RMSNorm,
     wqkv GEMM, q/k head norms + rotary + KV-cache write for every row in one
@@ -314,6 +318,7 @@ def prefill_block_chain(block, x, freqs_cis, mask, input_pos, *, xn=None, next_n
                 q.data_ptr(), kc.data_ptr(), vc.data_ptr(), nh, nkv, max_len, n, _lib.dtype_code(x.dtype),
                 _lib.stream())
             _lib.check(rc, "ttsp_qk_rope_kv_rows")
+        q_rows = q
         q, k, v = q.transpose(1, 2), kc, vc
     else:
         q, k, v = qkv.split([nh * hd, nkv * hd, nkv * hd], dim=-1)
@@ -327,12 +332,17 @@ def prefill_block_chain(block, x, freqs_cis, mask, input_pos, *, xn=None, next_n
             fq, fk = apply_rotary_emb(q, freqs_cis), apply_rotary_emb(k, freqs_cis)
         q, k, v = (t.transpose(1, 2) for t in (fq, fk, v))
         k, v = a.kv_cache.update(input_pos, k, v)
-    if mask.shape[-1] < k.shape[2]:
-        k, v = k[:, :, : mask.shape[-1]], v[:, :, : mask.shape[-1]]
-    y = fastpath.prefill_attention(q, k, v, mask, nh, nkv, hd)
+    y = None
+    if causal and rows_ok:
+        # a short causal span: each row as the decode step attends (no mask reads)
+        y = fastpath.causal_rows_attention(q_rows, kc, vc, input_pos, nh, nkv, mask.shape[-1])
     if y is None:
-        y = fastpath.decode_attention(q, k, v, mask, nh, nkv, hd)
-    y = y.transpose(1, 2).contiguous().view(bsz, n, nh * hd)
+        if mask.shape[-1] < k.shape[2]:
+            k, v = k[:, :, : mask.shape[-1]], v[:, :, : mask.shape[-1]]
+        y = fastpath.prefill_attention(q, k, v, mask, nh, nkv, hd)
+        if y is None:
+            y = fastpath.decode_attention(q, k, v, mask, nh, nkv, hd)
+        y = y.transpose(1, 2).contiguous().view(bsz, n, nh * hd)
     hh = nf4gemv.matmul_norm(a.wo, y, fn.weight, fn.eps, epi=nf4gemv.EPI_RESIDUAL, operand=x)
     if hh is not None:
         h, hn = hh
