@@ -79,8 +79,8 @@ def test_prefill_block_matches_the_unpatched_block(qk_norm):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("qk_norm,rows", [(True, 40), (False, 100)])
-def test_prefill_block_folded_reduces_equal_the_separate_launches(monkeypatch, qk_norm, rows):
+@pytest.mark.parametrize("qk_norm,rows,dtype", [(True, 40, torch.bfloat16), (False, 100, torch.float16)])
+def test_prefill_block_folded_reduces_equal_the_separate_launches(monkeypatch, qk_norm, rows, dtype):
     """A block whose wqkv, wo and w2 all take K splits (d = 1024, 8 q / 2 kv
     heads, FFN 2048): wqkv's partial sums added inside the head-norm / rotary
     / KV kernel and the RMSNorms written by wo's and w2's reduces, against
@@ -95,7 +95,7 @@ def test_prefill_block_folded_reduces_equal_the_separate_launches(monkeypatch, q
     lib = _lib.load()
     assert min(lib.ttsp_nf4_gemm_splits(1536, 1024, rows), lib.ttsp_nf4_gemm_splits(1024, 1024, rows),
                lib.ttsp_nf4_gemm_splits(1024, 2048, rows)) > 1
-    block, _ = _block(torch.bfloat16, qk_norm, dim=1024, n_head=8, n_local_heads=2, inter=2048, max_len=128, seed=4)
+    block, _ = _block(dtype, qk_norm, dim=1024, n_head=8, n_local_heads=2, inter=2048, max_len=128, seed=4)
     kc, vc = block.attention.kv_cache.k_cache, block.attention.kv_cache.v_cache
     kc.normal_()
     vc.normal_()
@@ -104,7 +104,7 @@ def test_prefill_block_folded_reduces_equal_the_separate_launches(monkeypatch, q
     pos = torch.arange(start, 128, device="cuda")
     mask = torch.tril(torch.ones(128, 128, dtype=torch.bool, device="cuda"))[None, None, pos]
     freqs = precompute_freqs_cis(128, 128, 1e6).cuda()[pos].contiguous()
-    x = torch.randn(1, rows, 1024, device="cuda").to(torch.bfloat16)
+    x = torch.randn(1, rows, 1024, device="cuda").to(dtype)
 
     def run():
         kc.copy_(saved[0])
@@ -308,6 +308,59 @@ def test_rows_kernel_equals_the_one_position_kernel(dtype):
     torch.cuda.synchronize()
     assert torch.equal(q1, q2) and torch.equal(kc1, kc2) and torch.equal(vc1, vc2)
     assert not torch.equal(q1[3], torch.zeros_like(q1[3])) and torch.equal(q1[5], torch.zeros_like(q1[5]))
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("K,rows,splits,dtype,qk_norm", [(1024, 40, 2, torch.float16, True),
+                                                         (2048, 64, 4, torch.bfloat16, True),
+                                                         (4096, 100, 8, torch.bfloat16, False)])
+def test_rows_kernel_from_split_partials_equals_reduce_then_rows(K, rows, splits, dtype, qk_norm):
+    """wqkv's K-split partial sums added inside the head-norm / rotary / KV
+    kernel (`matmul_partials` + ttsp_qk_rope_kv_rows_partials) against the
+    split GEMM's own reduce then ttsp_qk_rope_kv_rows: Q, K and V cache bit
+    for bit at 2, 4 and 8 splits, fp16 and bf16, with and without the head
+    norms, positions in any order and one past the cache (nothing written)."""
+    from tests.nf4data import random_layer, to_linear
+    from ttspipe_amd import _lib, nf4gemv
+    from ttspipe_amd.llama import precompute_freqs_cis
+
+    nh, nkv, hd, max_len = 8, 2, 128, 256
+    M = (nh + 2 * nkv) * hd
+    lib, st = _lib.load(), _lib.stream()
+    assert lib.ttsp_nf4_gemm_splits(M, K, rows) == splits
+    assert nf4gemv.install()
+    lin = to_linear(random_layer(M, K, True, seed=K + rows), dtype)
+    assert nf4gemv.prepare(lin)
+    g = torch.Generator().manual_seed(rows)
+    x = torch.randn(rows, K, generator=g).mul(0.5).to(dtype).cuda()
+    pos = torch.randperm(max_len, generator=g)[:rows].cuda()
+    pos[rows // 2] = max_len + 3  # past the cache: the row writes nothing
+    freqs = precompute_freqs_cis(max_len + 8, hd, 1e6).cuda()[pos].contiguous()
+    qw = (torch.rand(hd, generator=g) + 0.5).to(dtype).cuda() if qk_norm else None
+    kw = (torch.rand(hd, generator=g) + 0.5).to(dtype).cuda() if qk_norm else None
+    dt = _lib.dtype_code(dtype)
+    kc1 = torch.randn(1, nkv, max_len, hd, generator=g).to(dtype).cuda()
+    vc1 = torch.randn(1, nkv, max_len, hd, generator=g).to(dtype).cuda()
+    kc2, vc2 = kc1.clone(), vc1.clone()
+    q1 = torch.zeros(rows, nh, hd, dtype=dtype, device="cuda")
+    q2 = torch.zeros_like(q1)
+    qkv = nf4gemv.matmul(lin, x)
+    rc = lib.ttsp_qk_rope_kv_rows(qkv.data_ptr(), M, _lib.ptr(qw), _lib.ptr(kw), 1e-6, freqs.data_ptr(), _lib.DT_BF16,
+                                  pos.data_ptr(), q1.data_ptr(), kc1.data_ptr(), vc1.data_ptr(), nh, nkv, max_len,
+                                  rows, dt, st)
+    assert rc == 0
+    work, got_splits = nf4gemv.matmul_partials(lin, x)
+    assert got_splits == splits
+    rc = lib.ttsp_qk_rope_kv_rows_partials(work.data_ptr(), splits, _lib.ptr(qw), _lib.ptr(kw), 1e-6,
+                                           freqs.data_ptr(), _lib.DT_BF16, pos.data_ptr(), q2.data_ptr(),
+                                           kc2.data_ptr(), vc2.data_ptr(), nh, nkv, max_len, rows, dt, st)
+    assert rc == 0
+    torch.cuda.synchronize()
+    assert torch.equal(q1.view(torch.int16), q2.view(torch.int16))
+    assert torch.equal(kc1.view(torch.int16), kc2.view(torch.int16))
+    assert torch.equal(vc1.view(torch.int16), vc2.view(torch.int16))
+    assert torch.equal(q2[rows // 2], torch.zeros_like(q2[rows // 2]))
+    assert not torch.equal(q2[0], torch.zeros_like(q2[0]))
 
 
 @pytest.fixture(scope="module")
