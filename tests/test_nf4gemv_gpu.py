@@ -685,3 +685,38 @@ def test_split_gemm_norm_declines_what_it_does_not_serve(nf4, shape, rows):
     x = from_bits(randn_bits(rows * K, torch.bfloat16, seed=6), torch.bfloat16).view(rows, K)
     g = torch.ones(M, dtype=torch.bfloat16, device="cuda")
     assert nf4.matmul_norm(lin, x, g, 1e-6) is None
+
+
+def _row_slice(layer, r0, r1):
+    """Rows r0 .. r1 - 1 of a nested layer as a layer of their own (r0 and r1
+    on second-level group boundaries)."""
+    K, bs, bs2 = layer["K"], layer["bs"], layer["bs2"]
+    b0, b1 = r0 * K // bs, r1 * K // bs
+    assert b0 % bs2 == 0 and b1 % bs2 == 0
+    out = dict(layer)
+    out.update(M=r1 - r0, W=layer["W"][r0 * K // 2:r1 * K // 2], A8=layer["A8"][b0:b1],
+               AMAX=layer["AMAX"][b0 // bs2:b1 // bs2])
+    return out
+
+
+@pytest.mark.parametrize("rows", [3, 4, 8])
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_three_tile_workgroups_equal_the_one_tile_launch(nf4, rows, dtype):
+    """9728 x 2560 at up to 8 rows runs three row tiles a workgroup; each
+    output row is the same fixed function of its weight row as in a
+    one-tile-a-workgroup launch (1024-row slices of the same bytes), bit for
+    bit, across the slice boundaries."""
+    M, K = 9728, 2560
+    layer = random_layer(M, K, True, seed=rows)
+    full = to_linear(layer, dtype)
+    assert nf4.prepare(full)
+    x = from_bits(randn_bits(rows * K, dtype, seed=rows + 40), dtype).view(rows, K)
+    y = nf4.matmul(full, x)
+    assert y is not None
+    for r0 in (0, 4096, 8704):
+        part = to_linear(_row_slice(layer, r0, r0 + 1024), dtype)
+        assert nf4.prepare(part)
+        ys = nf4.matmul(part, x)
+        torch.cuda.synchronize()
+        a, b = bits(y[:, r0:r0 + 1024].contiguous()), bits(ys)
+        assert np.array_equal(a, b), (r0, first_mismatch(a, b))

@@ -76,26 +76,41 @@ __device__ __forceinline__ uint32_t sk_pack2(float lo, float hi) {
     return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, sk_f16x2));
 }
 
-// MS: the wave's step budget (its K run is at most MS steps).
-template <int DT, int R, int NT, int NW, int MS, bool NESTED>
-__global__ __launch_bounds__(64 * NW) void nf4_skinny_kernel(
+// MS: the wave's step budget (its K run is at most MS steps). TG: row-tile
+// groups a workgroup (NW waves each, one table for all): the grid's
+// workgroups split the row tiles evenly (workgroup b takes tiles
+// b T / G .. (b + 1) T / G - 1, at most TG of them; a group past them repeats
+// the first tile's loads and stores nothing), so a matrix of 2-3 tiles a CU
+// runs in one round of workgroups instead of two and a tail.
+template <int DT, int R, int NT, int NW, int MS, bool NESTED, int TG = 1>
+__global__ __launch_bounds__(64 * NW * TG) void nf4_skinny_kernel(
     const uint16_t* __restrict__ X, const uint8_t* __restrict__ W, const uint8_t* __restrict__ A8,
     const float* __restrict__ AMAX, const float* __restrict__ CODE2, float offset, const float* __restrict__ LUT,
     uint16_t* __restrict__ Y, const uint16_t* __restrict__ RES, int epi, int M, int K, int N, int bs_shift,
     int bs2_shift) {
   // byte e -> (code of its high nibble, code of its low nibble), copy j at
   // [e][j]; after the loop the same memory holds each wave's partial sums
-  static_assert(NW * R * NT * 64 * sizeof(f32x4) <= SK_LDS, "partial sums exceed the table's LDS");
+  constexpr int NWT = NW * TG;  // waves a workgroup
+  static_assert(NWT * R * NT * 64 * sizeof(f32x4) <= SK_LDS, "partial sums exceed the table's LDS");
   __shared__ __align__(16) unsigned char lds[SK_LDS];
   __shared__ __align__(16) float code2_s[NESTED ? 256 : 4];
   float2 (*lut2)[SK_REP] = reinterpret_cast<float2 (*)[SK_REP]>(lds);
   f32x4 (*part)[R * NT][64] = reinterpret_cast<f32x4 (*)[R * NT][64]>(lds);
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int grp = TG > 1 ? wave / NW : 0, wk = TG > 1 ? wave % NW : wave;  // row-tile group, K run
   const int m = lane & 15, q = lane >> 4;
-  const int row0 = blockIdx.x * 16 * R;
+  int tile = blockIdx.x;
+  bool own = true;  // the group has a tile of its own (its stores happen)
+  if constexpr (TG > 1) {
+    const int T = (M + 16 * R - 1) / (16 * R), G = (int)gridDim.x;
+    const int b0 = (int)((long long)blockIdx.x * T / G), b1 = (int)((long long)(blockIdx.x + 1) * T / G);
+    own = b0 + grp < b1;
+    tile = own ? b0 + grp : b0;
+  }
+  const int row0 = tile * 16 * R;
   const int steps = K >> 7;  // 128-code steps per row
-  const int s0 = wave * steps / NW, s1 = (wave + 1) * steps / NW;
+  const int s0 = wk * steps / NW, s1 = (wk + 1) * steps / NW;
   const size_t rowbytes = (size_t)K >> 1;
   const int nblk = K >> bs_shift;
 
@@ -163,8 +178,10 @@ __global__ __launch_bounds__(64 * NW) void nf4_skinny_kernel(
   // (straight-line: a loop or a branch around these uses of loaded values
   // would make the compiler wait for every load first)
 #pragma unroll
-  for (int k = 0; k < 64 / NW; ++k) {
-    const int e = 4 * (wave + NW * k) + (lane >> 4), j = 2 * (lane & 15);
+  for (int k = 0; k < (64 + NWT - 1) / NWT; ++k) {
+    // (64 % NWT != 0: the last round's waves past entry group 63 rewrite it with the same values)
+    const int eg = 64 % NWT == 0 ? wave + NWT * k : min(wave + NWT * k, 63);
+    const int e = 4 * eg + (lane >> 4), j = 2 * (lane & 15);
     const float hi = __shfl(c16, e >> 4), lo = __shfl(c16, e & 15);
     *reinterpret_cast<float4*>(&lut2[e][j]) = make_float4(hi, lo, hi, lo);
   }
@@ -217,7 +234,8 @@ __global__ __launch_bounds__(64 * NW) void nf4_skinny_kernel(
     if (j + SK_PF < MS) load_x(xs, s0 + j + SK_PF);
   }
 
-  // K runs in wave order; wave w finishes the row tiles r with r % NW == w
+  // K runs in wave order within a group; wave w of a group finishes its row
+  // tiles r with r % NW == w
   __syncthreads();  // every wave is past its last lookup: the table's memory takes the partial sums
 #pragma unroll
   for (int r = 0; r < R; ++r)
@@ -227,21 +245,21 @@ __global__ __launch_bounds__(64 * NW) void nf4_skinny_kernel(
   const int ep = epi & 3;
 #pragma unroll
   for (int r = 0; r < R; ++r) {
-    if (r % NW != wave) continue;
+    if (r % NW != wk) continue;
     const int row = row0 + 16 * r + m;
 #pragma unroll
     for (int c = 0; c < NT; ++c) {
-      f32x4 v = part[0][r * NT + c][lane];
+      f32x4 v = part[grp * NW][r * NT + c][lane];
 #pragma unroll
       for (int w = 1; w < NW; ++w) {
-        const f32x4 o = part[w][r * NT + c][lane];
+        const f32x4 o = part[grp * NW + w][r * NT + c][lane];
 #pragma unroll
         for (int i = 0; i < 4; ++i) v[i] = __fadd_rn(v[i], o[i]);
       }
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int n = 16 * c + 4 * q + i;
-        if (n >= N || row >= M) continue;
+        if (n >= N || row >= M || !own) continue;
         const size_t o = (size_t)n * M + row;
         const float y = Elem<DT>::load(Elem<DT>::store(v[i]));
         float out = y;
@@ -255,25 +273,29 @@ __global__ __launch_bounds__(64 * NW) void nf4_skinny_kernel(
 
 int skinny_max_k(int N);
 
-template <int DT, int R, int NT, int NW, int MS>
+template <int DT, int R, int NT, int NW, int MS, int TG = 1>
 static void launch_skinny(const void* X, const uint8_t* W, const uint8_t* A8, const float* AMAX, const float* CODE2,
                           float offset, const float* LUT, void* Y, const void* RES, int epi, int M, int K, int N,
                           int bs_shift, int bs2_shift, hipStream_t st) {
-  const dim3 grid((M + 16 * R - 1) / (16 * R));
+  const int tiles = (M + 16 * R - 1) / (16 * R);
+  const dim3 grid((tiles + TG - 1) / TG);  // TG tiles a workgroup (the last may hold fewer)
   if (A8)
-    hipLaunchKernelGGL((nf4_skinny_kernel<DT, R, NT, NW, MS, true>), grid, dim3(64 * NW), 0, st, (const uint16_t*)X,
-                       W, A8, AMAX, CODE2, offset, LUT, (uint16_t*)Y, (const uint16_t*)RES, epi, M, K, N, bs_shift,
-                       bs2_shift);
+    hipLaunchKernelGGL((nf4_skinny_kernel<DT, R, NT, NW, MS, true, TG>), grid, dim3(64 * NW * TG), 0, st,
+                       (const uint16_t*)X, W, A8, AMAX, CODE2, offset, LUT, (uint16_t*)Y, (const uint16_t*)RES, epi,
+                       M, K, N, bs_shift, bs2_shift);
   else
-    hipLaunchKernelGGL((nf4_skinny_kernel<DT, R, NT, NW, MS, false>), grid, dim3(64 * NW), 0, st, (const uint16_t*)X,
-                       W, A8, AMAX, CODE2, offset, LUT, (uint16_t*)Y, (const uint16_t*)RES, epi, M, K, N, bs_shift,
-                       bs2_shift);
+    hipLaunchKernelGGL((nf4_skinny_kernel<DT, R, NT, NW, MS, false, TG>), grid, dim3(64 * NW * TG), 0, st,
+                       (const uint16_t*)X, W, A8, AMAX, CODE2, offset, LUT, (uint16_t*)Y, (const uint16_t*)RES, epi,
+                       M, K, N, bs_shift, bs2_shift);
 }
 
 // Launch shape. NW: the fewest waves (4, 8, 16) whose K runs fit SK_MAXS
 // steps; with fewer than 256 row tiles and runs of more than 5 steps at 4
-// waves, at least 8 (more waves per row tile). MS: the step budget, 5 when
-// the runs fit it (fewer repeated loads), else SK_MAXS. R: with 512 or more
+// waves, at least 8 (more waves per row tile). MS: the step budget; one row
+// tile a workgroup takes the smallest of 2, 3, 4, 5, 6, 8, 10 that holds the
+// run (every step past the run repeats a load: 2560 x 4096, runs of 4, 6.1
+// against 7.0 us with MS = 5 at 4 rows, 7.7 against 9.1 at 16), the other
+// forms 5 when the runs fit it, else SK_MAXS. R: with 512 or more
 // row tiles, several tiles a workgroup (each X fragment then serves R of them:
 // the activation traffic, which binds from 16 rows up, drops by R) - 4 for
 // 17-32 rows and 2 otherwise with 4 waves, 2 from 9 rows with 8 - else 1.
@@ -302,7 +324,27 @@ static bool skinny_shape(const void* X, const uint8_t* W, const uint8_t* A8, con
     if (ms5) TTSP_L(RV, NWV, 5); \
     else TTSP_L(RV, NWV, SK_MAXS); \
   } while (0)
+#define TTSP_MS1(NWV)                    \
+  do {                                   \
+    if (run <= 2) TTSP_L(1, NWV, 2);     \
+    else if (run <= 3) TTSP_L(1, NWV, 3); \
+    else if (run <= 4) TTSP_L(1, NWV, 4); \
+    else if (run <= 5) TTSP_L(1, NWV, 5); \
+    else if (run <= 6) TTSP_L(1, NWV, 6); \
+    else if (run <= 8) TTSP_L(1, NWV, 8); \
+    else TTSP_L(1, NWV, SK_MAXS);        \
+  } while (0)
   const bool many = tiles >= 2 * 256;
+  // 2-3 row tiles a CU, up to 8 rows: three tiles a workgroup (12 waves, one
+  // table) run in one round instead of two and a tail (9728 x 2560: 9.4
+  // against 10.4 us at 4 rows, 10.5 against 10.7 at 8; 16 rows tie)
+  if constexpr (NT == 1) {
+    if (many && tiles < 3 * 256 && N <= 8 && nw == 4 && ms5) {
+      launch_skinny<DT, 1, 1, 4, 5, 3>(X, W, A8, AMAX, CODE2, offset, LUT, Y, RES, epi, M, K, N, bs_shift, bs2_shift,
+                                        st);
+      return true;
+    }
+  }
   if constexpr (NT == 2) {
     if (many && nw == 4 && ms5) { TTSP_L(4, 4, 5); return true; }
   }
@@ -313,10 +355,11 @@ static bool skinny_shape(const void* X, const uint8_t* W, const uint8_t* A8, con
     if (r2 && nw == 4) { TTSP_MS(2, 4); return true; }
     if (r2) { TTSP_MS(2, 8); return true; }
   }
-  if (nw == 4) TTSP_MS(1, 4);
-  else if (nw == 8) TTSP_MS(1, 8);
-  else if constexpr (NT == 1) TTSP_MS(1, 16);  // 1024 threads: 128 registers a lane, enough for one X tile only
+  if (nw == 4) TTSP_MS1(4);
+  else if (nw == 8) TTSP_MS1(8);
+  else if constexpr (NT == 1) TTSP_MS1(16);  // 1024 threads: 128 registers a lane, enough for one X tile only
   else return false;
+#undef TTSP_MS1
 #undef TTSP_MS
 #undef TTSP_L
   return true;
