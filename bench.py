@@ -358,7 +358,9 @@ def bench_gemm(rows: int = 512, copies: int = 4, reps: int = 20):
     dev = torch.device("cuda", 0)
     lut = torch.tensor(NF4_CODE, dtype=torch.float32, device=dev)
     res, total_s, total_flop = [], 0.0, 0
-    for i, (name, M, K) in enumerate(LAYER):
+    # the seven projections of the reference's table, then wqkv as the
+    # prefill block runs it (q, k and v rows of one weight, one launch)
+    for i, (name, M, K) in enumerate(LAYER + [("qkv", 6144, 2560)]):
         lins = [Linear(M, K, True, seed=500 + 10 * i + c, device=dev) for c in range(copies)]
         x = torch.randn(rows, K, device=dev).to(torch.bfloat16)
         y = torch.empty(rows, M, dtype=torch.bfloat16, device=dev)
@@ -384,8 +386,9 @@ def bench_gemm(rows: int = 512, copies: int = 4, reps: int = 20):
         flop = 2 * rows * M * K
         res.append({"name": name, "M": M, "K": K, "k_splits": splits, "us": round(sec * 1e6, 2),
                     "tflops": round(flop / sec / 1e12, 1)})
-        total_s += sec
-        total_flop += flop
+        if name != "qkv":
+            total_s += sec
+            total_flop += flop
         del lins
     out = {"rows": rows, "projections": res, "layer_us": round(total_s * 1e6, 1),
            "tflops": round(total_flop / total_s / 1e12, 1),
@@ -422,6 +425,12 @@ def bench_gemm(rows: int = 512, copies: int = 4, reps: int = 20):
         out["layer_us_with_one_swiglu_launch"] = round(layer * 1e6, 1)
         out["pct_of_mfma_peak_with_one_swiglu_launch"] = round(
             100 * total_flop / layer / 1e12 / MFMA_PEAK_TFLOPS, 2)
+        # the prefill block's four launches: wqkv, wo, the SwiGLU pair, w2
+        us = {r["name"]: r["us"] * 1e-6 for r in res}
+        block = us["qkv"] + us["o"] + sec + us["down"]
+        out["prefill_block_launches_us"] = round(block * 1e6, 1)
+        out["pct_of_mfma_peak_prefill_block_launches"] = round(
+            100 * total_flop / block / 1e12 / MFMA_PEAK_TFLOPS, 2)
         del pairs
     return out
 
