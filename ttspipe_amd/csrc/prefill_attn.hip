@@ -15,9 +15,11 @@
 // O^T += V^T P^T straight from registers: the V^T fragments come from V's
 // row-major tile through the transposing LDS read, in the key order the
 // score layout gives P^T, so neither V nor P is transposed by hand. Scores, running max and sum are fp32 (in log2 units: the scale and
-// log2 e fold into one multiply-add before the hardware exp2);
-// probabilities are rounded to the activation type for the matrix core; O
-// is divided by the sum once at the end.
+// log2 e fold into one multiply-add before the hardware exp2); the
+// reference max the exponentials subtract moves only when a query's running
+// max outgrows it by more than 8 (so terms stay below 2^8 and O is rarely
+// rescaled); probabilities are rounded to the activation type for the matrix
+// core; O is divided by the sum once at the end.
 //
 // Staging is a two-deep pipeline: block group t + 2 is loaded into registers
 // (buffer loads, never under a branch, so the waits count them exactly)
@@ -352,8 +354,11 @@ __global__ __launch_bounds__(64 * G * NS) void prefill_attn_kernel(const Prefill
 #pragma unroll
       for (int r = 0; r < 16; ++r) bm = fmaxf(bm, s[r]);
       bm = fmaxf(bm, __shfl_xor(bm, 32, 64)) * a.scale2;
+      // the reference max moves only when the running max outgrows it by more
+      // than 2^8 (terms then stay below 256), so O's rescale is rare
       const float mnew = fmaxf(mrun, bm);
-      const float mref = mnew == -__builtin_inff() ? 0.0f : mnew;  // nothing seen yet: all terms 0
+      const float mkeep = mnew > mrun + 8.0f ? mnew : mrun;
+      const float mref = mkeep == -__builtin_inff() ? 0.0f : mkeep;  // nothing seen yet: all terms 0
       const float alpha = pa_exp2(mrun - mref);
       float ps = 0.0f;
       u32x4 pf[2];  // P^T fragments (B operand): keys 16 c + {4h .. 4h + 3, 8 + 4h .. 8 + 4h + 3}
@@ -370,8 +375,8 @@ __global__ __launch_bounds__(64 * G * NS) void prefill_attn_kernel(const Prefill
       }
       ps += __shfl_xor(ps, 32, 64);
       lrun = lrun * alpha + ps;
-      mrun = mnew;
-      // O^T = alpha O^T + V^T P^T (the rescale skipped while no lane's max moved)
+      mrun = mkeep;
+      // O^T = alpha O^T + V^T P^T (the rescale skipped while no lane's reference moved)
       if (__any(alpha != 1.0f)) {
 #pragma unroll
         for (int d = 0; d < HD / 32; ++d)
