@@ -148,7 +148,11 @@ __global__ __launch_bounds__(64 * G * NS) void prefill_attn_kernel(const Prefill
   constexpr int KPT = (NKP + NT - 1) / NT, VPT = (NVP + NT - 1) / NT, MPT = (NMP + NT - 1) / NT;
   constexpr int STAGE = 2 * NS * PA_BLK;
   constexpr int MERGE = NS > 1 ? G * 66 * 64 * 4 : 0;  // split 1's o (64 floats), m, l per lane
-  __shared__ __align__(16) uint8_t lds[STAGE > MERGE ? STAGE : MERGE];
+  constexpr int OROW = HD + 8;  // the staged output tile's row stride (elements): 272 bytes
+  constexpr int FROW = HD + 4;  // SPLIT: the staged fp32 partial rows' stride (floats): 528 bytes
+  // after the merge slots: each head's 32 output rows (SPLIT: its 32 fp32 partial rows)
+  constexpr int OUT = SPLIT ? G * PA_QB * FROW * 4 : G * PA_QB * OROW * 2;
+  __shared__ __align__(16) uint8_t lds[STAGE > MERGE + OUT ? STAGE : MERGE + OUT];
   __shared__ int wmax[NW];  // the mask scan's per-wave result
   __shared__ int full[3];   // per block group (mod 3): every key of its mask tiles allowed
   const int kh = blockIdx.x, q0 = blockIdx.y * PA_QB;
@@ -422,25 +426,34 @@ __global__ __launch_bounds__(64 * G * NS) void prefill_attn_kernel(const Prefill
       for (int r = 0; r < 16; ++r) o[d][r] = o[d][r] * f1 + mg[(16 * d + r) * 64] * f2;
   }
   if constexpr (SPLIT) {  // O unnormalised, max and sum of this split, for the merge kernel
-    if (i < a.S) {
-      float* wo = a.WO + (((size_t)z * a.S + i) * a.nh + head) * HD;
+    // O staged as this head's 32 rows in LDS (read back by this wave only)
+    // and stored as whole 512-byte rows, 16 bytes a lane
+    float* of = reinterpret_cast<float*>(lds + MERGE) + (size_t)gw * PA_QB * FROW;
 #pragma unroll
-      for (int d = 0; d < HD / 32; ++d)
+    for (int d = 0; d < HD / 32; ++d)
 #pragma unroll
-        for (int g = 0; g < 4; ++g)
-          *reinterpret_cast<float4*>(wo + 32 * d + 8 * g + 4 * h) =
-              make_float4(o[d][4 * g], o[d][4 * g + 1], o[d][4 * g + 2], o[d][4 * g + 3]);
-      if (h == 0) {
-        float* ml = a.WO + (size_t)gridDim.z * a.S * a.nh * HD + (((size_t)z * a.S + i) * a.nh + head) * 2;
-        *reinterpret_cast<float2*>(ml) = make_float2(mrun, lrun);
-      }
+      for (int g = 0; g < 4; ++g)
+        *reinterpret_cast<float4*>(of + ql * FROW + 32 * d + 8 * g + 4 * h) =
+            make_float4(o[d][4 * g], o[d][4 * g + 1], o[d][4 * g + 2], o[d][4 * g + 3]);
+#pragma unroll
+    for (int k = 0; k < PA_QB * HD / 4 / 64; ++k) {
+      const int e = lane + 64 * k, r = e >> 5, cc = (e & 31) * 4;
+      const float4 v = *reinterpret_cast<const float4*>(of + r * FROW + cc);
+      if (q0 + r < a.S)
+        *reinterpret_cast<float4*>(a.WO + (((size_t)z * a.S + q0 + r) * a.nh + head) * HD + cc) = v;
+    }
+    if (i < a.S && h == 0) {
+      float* ml = a.WO + (size_t)gridDim.z * a.S * a.nh * HD + (((size_t)z * a.S + i) * a.nh + head) * 2;
+      *reinterpret_cast<float2*>(ml) = make_float2(mrun, lrun);
     }
     return;
   }
-  // Y[i][head][dim] = O^T[dim][i] / l (a row with no allowed key: 0 / 0, as the reference's softmax)
-  if (i < a.S) {
+  // Y[i][head][dim] = O^T[dim][i] / l (a row with no allowed key: 0 / 0, as the reference's softmax),
+  // staged as this head's 32 rows in LDS (the wave reads back only what it
+  // wrote: no barrier) and stored as whole 256-byte rows, 16 bytes a lane
+  {
     const float inv = 1.0f / lrun;
-    uint16_t* yr = a.Y + ((size_t)i * a.nh + head) * HD;
+    uint16_t* ot = reinterpret_cast<uint16_t*>(lds + MERGE) + (size_t)gw * PA_QB * OROW;
 #pragma unroll
     for (int d = 0; d < HD / 32; ++d)
 #pragma unroll
@@ -448,8 +461,14 @@ __global__ __launch_bounds__(64 * G * NS) void prefill_attn_kernel(const Prefill
         uint2 w;
         w.x = pa_pack<DT>(o[d][4 * g] * inv, o[d][4 * g + 1] * inv);
         w.y = pa_pack<DT>(o[d][4 * g + 2] * inv, o[d][4 * g + 3] * inv);
-        *reinterpret_cast<uint2*>(yr + 32 * d + 8 * g + 4 * h) = w;
+        *reinterpret_cast<uint2*>(ot + ql * OROW + 32 * d + 8 * g + 4 * h) = w;
       }
+#pragma unroll
+    for (int k = 0; k < PA_QB * HD / 8 / 64; ++k) {
+      const int e = lane + 64 * k, r = e >> 4, cc = (e & 15) * 8;
+      const uint4 v = *reinterpret_cast<const uint4*>(ot + r * OROW + cc);
+      if (q0 + r < a.S) *reinterpret_cast<uint4*>(a.Y + ((size_t)(q0 + r) * a.nh + head) * HD + cc) = v;
+    }
   }
 }
 
