@@ -321,6 +321,96 @@ __global__ __launch_bounds__(64 * W) void nf4_gemm_dl_kernel(
     }
     return;
   }
+  // Two-wave tiles' outputs leave as whole rows: staged as [n][m] in the
+  // stage the last step read (no load refills it; the other stage takes that
+  // step's unread refill, which is not written into) and stored 16 bytes a
+  // lane, so each store instruction writes whole 128-byte lines of output
+  // rows instead of 8- or 16-byte pieces of 32 rows.
+  uint8_t* const rd_last = nsteps % 2 == 0 ? ring1 : ring0;
+  if constexpr (W == 2) {
+    __syncthreads();
+    if (YP) {
+      // fp32 partials, 64 activation rows at a time (a 64 x 64 block at a
+      // 68-float row pitch fills the stage): both waves stage, then store
+      constexpr int FR = 68;
+      static_assert(64 * FR * 4 <= STAGE, "the partial block exceeds the ring stage");
+      float* f_s = reinterpret_cast<float*>(rd_last);
+      float* yp = YP + (size_t)blockIdx.z * N * M;
+#pragma unroll
+      for (int half = 0; half < 2; ++half) {
+#pragma unroll
+        for (int bb = 0; bb < 2; ++bb)
+#pragma unroll
+          for (int g = 0; g < 4; ++g) {
+            const int b = 2 * half + bb;
+            *reinterpret_cast<float4*>(f_s + (32 * bb + (lane & 31)) * FR + 32 * wave + 8 * g + 4 * (lane >> 5)) =
+                make_float4(acc[b][4 * g], acc[b][4 * g + 1], acc[b][4 * g + 2], acc[b][4 * g + 3]);
+          }
+        __syncthreads();
+#pragma unroll
+        for (int k = 0; k < 64 * 64 / 4 / 128; ++k) {
+          const int e = tid + 128 * k, nl = e >> 4, ml = (e & 15) * 4;
+          const int n = n0 + 64 * half + nl, m = m0 + ml;
+          if (n < N) {
+            const float4 v = *reinterpret_cast<const float4*>(f_s + nl * FR + ml);
+            const size_t o = (size_t)n * M + m;
+            if (v4 && m + 4 <= M) {
+              *reinterpret_cast<float4*>(yp + o) = v;
+            } else {
+              const float vv[4] = {v.x, v.y, v.z, v.w};
+              for (int c = 0; c < 4 && m + c < M; ++c) yp[o + c] = vv[c];
+            }
+          }
+        }
+        __syncthreads();  // the block's reads before the next half's writes
+      }
+      return;
+    }
+    // the rounded outputs at a 72-element row pitch (both waves' 32 columns)
+    constexpr int HR = 72;
+    static_assert(BN * HR * 2 <= STAGE, "the output block exceeds the ring stage");
+    uint16_t* h_s = reinterpret_cast<uint16_t*>(rd_last);
+#pragma unroll
+    for (int b = 0; b < 4; ++b)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const uint32_t lo = (uint32_t)Elem<DT>::store(acc[b][4 * g]) | ((uint32_t)Elem<DT>::store(acc[b][4 * g + 1]) << 16);
+        const uint32_t hi =
+            (uint32_t)Elem<DT>::store(acc[b][4 * g + 2]) | ((uint32_t)Elem<DT>::store(acc[b][4 * g + 3]) << 16);
+        *reinterpret_cast<uint2*>(h_s + (32 * b + (lane & 31)) * HR + 32 * wave + 8 * g + 4 * (lane >> 5)) =
+            make_uint2(lo, hi);
+      }
+    __syncthreads();
+    const int ep = epi & 3;
+    const bool vec = (M & 7) == 0 && (epi & 16);  // rows of Y and R 16-byte aligned (host: Y, R)
+#pragma unroll
+    for (int k = 0; k < BN * 64 / 8 / 128; ++k) {
+      const int e = tid + 128 * k, nl = e >> 3, ml = (e & 7) * 8;
+      const int n = n0 + nl, m = m0 + ml;
+      if (n >= N) continue;
+      const uint4 v = *reinterpret_cast<const uint4*>(h_s + nl * HR + ml);
+      const size_t o = (size_t)n * M + m;
+      const uint32_t vw[4] = {v.x, v.y, v.z, v.w};
+      if (vec && m + 8 <= M) {
+        uint4 rv = make_uint4(0u, 0u, 0u, 0u);
+        if (ep) rv = *reinterpret_cast<const uint4*>(R + o);
+        const uint32_t rw[4] = {rv.x, rv.y, rv.z, rv.w};
+        uint32_t owd[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const uint16_t lo = dl_epi<DT>(Elem<DT>::load(vw[q] & 0xffffu), (uint16_t)rw[q], ep);
+          const uint16_t hi = dl_epi<DT>(Elem<DT>::load(vw[q] >> 16), (uint16_t)(rw[q] >> 16), ep);
+          owd[q] = (uint32_t)lo | ((uint32_t)hi << 16);
+        }
+        *reinterpret_cast<uint4*>(Y + o) = make_uint4(owd[0], owd[1], owd[2], owd[3]);
+      } else {
+        for (int c = 0; c < 8 && m + c < M; ++c)
+          Y[o + c] = dl_epi<DT>(Elem<DT>::load((uint16_t)(vw[c >> 1] >> (16 * (c & 1)))), ep ? R[o + c] : (uint16_t)0,
+                                ep);
+      }
+    }
+    return;
+  }
   if (YP) {
     float* yp = YP + (size_t)blockIdx.z * N * M;
 #pragma unroll
@@ -420,14 +510,15 @@ bool gemm_dl_fits(int M, int K, int N, int splits) {
 
 // waves: 2 (64 weight rows a workgroup) or 4 (128). splits > 1 writes fp32
 // partials to YP (the caller reduces them and applies the epilogue); else
-// epi as nf4_gemm_kernel's (bit 2: vectorised output; 8-byte alignment of Y
-// and R is checked here).
+// epi as nf4_gemm_kernel's (bit 2: vectorised output; 8- and 16-byte
+// alignment of Y and R is checked here).
 int gemm_dl(const void* X, int dt, const uint8_t* W, const uint8_t* A8, const float* AMAX, const float* CODE2,
             float offset, const float* LUT, void* Y, const void* R, int epi, int M, int K, int N, int bs_shift,
             int bs2_shift, int waves, int splits, float* YP, hipStream_t st) {
   if (!gemm_dl_fits(M, K, N, splits) || (splits > 1 && !YP)) return (int)hipErrorInvalidValue;
   const bool al8 = (uintptr_t)Y % 8 == 0 && (!(epi & 3) || (uintptr_t)R % 8 == 0);
-  const int e = (epi & 3) | (al8 ? 8 : 0);
+  const bool al16 = (uintptr_t)Y % 16 == 0 && (!(epi & 3) || (uintptr_t)R % 16 == 0);
+  const int e = (epi & 3) | (al8 ? 8 : 0) | (al16 ? 16 : 0);
   float* yp = splits > 1 ? YP : nullptr;
   if (dt == DT_BF16) {
     if (waves == 2)
