@@ -368,6 +368,21 @@ int ttsp_prefill_attention_split(const void* Q, long long q_seq_stride, long lon
                                  int nkv, int L, float scale, int dtype, float* work, int splits,
                                  void* stream);
 
+/* ttsp_prefill_attention_split with the causal mask at the rows' positions:
+ * pos (int64, S entries on the device) in place of the mask, query i
+ * allowing keys j <= min(pos[i], L - 1). The mask is computed in the kernel
+ * rather than read (no mask rows, no scan of them), and the same keys are
+ * masked, so Y is bit for bit ttsp_prefill_attention_split's with mask row i
+ * = causal_mask[pos[i]][0 .. L). Null pos returns hipErrorInvalidValue.
+ * Replaces: scaled_dot_product_attention with the mask forward_generate
+ * builds, causal_mask[..., input_pos, :max_seq_len] (app/engine/fastpath.py:9,
+ * 244-268; the prefill of app/engine/graphs.py:219-228). */
+int ttsp_prefill_attention_causal(const void* Q, long long q_seq_stride, long long q_head_stride,
+                                  const void* K, long long k_seq_stride, long long k_head_stride,
+                                  const void* V, long long v_seq_stride, long long v_head_stride,
+                                  const long long* pos, void* Y, int S, int nh, int nkv, int L, float scale,
+                                  int dtype, float* work, int splits, void* stream);
+
 /* out[d] = round(sum_{c < ntok} E[(c*vocab + tok[c]) * D + d]) (tok int32 on the
  * device, clamped into [0, vocab)). Replaces: the codebook-embedding lookup of
  * a decode step (app/engine/graphs.py:124-131 via the fork's _fast_embed /

@@ -314,3 +314,95 @@ def test_attention_forward_takes_the_kernel_for_a_prefill():
     # roundings, which wo then mixes
     rel = ((ours.float() - theirs.float()).norm() / theirs.float().norm()).item()
     assert rel < 2e-2
+
+
+CAUSAL_CASES = [  # (S, prefix, nh, nkv, window past the span): the masked kernel's own shapes
+    (512, 0, 32, 8, 0),       # the 512-token prompt, its window ending with the span
+    (512, 0, 32, 8, 1792),    # the same over the whole cache (2304 positions)
+    (512, 1536, 32, 8, 0),    # after a cached prefix: two key splits
+    (64, 2000, 32, 8, 0),     # a short run over a long prefix: 16 key splits
+    (100, 37, 8, 2, 5),       # ragged query and key blocks
+    (33, 0, 6, 2, 0),         # three heads per kv head (one key split a workgroup)
+    (9, 3, 8, 1, 40),         # eight heads per kv head
+    (1, 0, 4, 4, 0),          # one row, one key
+]
+
+
+@pytest.mark.parametrize("S,prefix,nh,nkv,extra", CAUSAL_CASES)
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_causal_positions_equal_the_causal_mask_bit_for_bit(S, prefix, nh, nkv, extra, dtype):
+    """`positions=` (the mask computed from the rows' positions in the kernel)
+    against the masked kernel with the fork's causal rows at those positions,
+    which it must equal bit for bit (the same keys masked, the same blocks
+    taken whole), and against fp64."""
+    from ttspipe_amd import fastpath
+
+    L = prefix + S + extra
+    q, k, v, _ = _setup(S, prefix, nh, nkv, dtype, seed=S + prefix + extra)
+    g = torch.Generator().manual_seed(L)
+    kc, vc = (torch.randn(1, nkv, L, D, generator=g).to(dtype).cuda() for _ in "kv")
+    kc[:, :, : prefix + S], vc[:, :, : prefix + S] = k, v
+    Lp = (L + 255) // 256 * 256  # the masked kernel takes 16-byte aligned mask rows
+    causal = torch.tril(torch.ones(Lp, Lp, dtype=torch.bool, device="cuda"))
+    pos = torch.arange(prefix, prefix + S, device="cuda")
+    mask = causal[None, None, pos, :Lp][..., :L]
+    masked = _run(q, kc, vc, mask, nh, nkv)
+    got = fastpath.prefill_attention(q, kc, vc, None, nh, nkv, D, positions=pos)
+    assert got is not None
+    assert torch.equal(got.view(torch.int16), masked.view(torch.int16))
+    assert relative_error(got[0].float().cpu().numpy(), _fp64(q, kc, vc, mask)) < TOL
+
+
+def test_causal_positions_in_any_order_and_past_the_window():
+    """Rows need not be consecutive: each row's own position sets its keys
+    (positions at or past L allow every key), bit for bit the mask that
+    states the same."""
+    from ttspipe_amd import fastpath
+
+    S, nh, nkv, L = 80, 8, 2, 300
+    q, _, _, _ = _setup(S, 0, nh, nkv, torch.bfloat16, seed=11)
+    g = torch.Generator().manual_seed(12)
+    k = torch.randn(1, nkv, L, D, generator=g).to(torch.bfloat16).cuda()
+    v = torch.randn(1, nkv, L, D, generator=g).to(torch.bfloat16).cuda()
+    pos = torch.randint(0, L + 40, (S,), generator=g).cuda()
+    mask = (torch.arange(L + 20, device="cuda")[None, :] <= pos[:, None])[None, None, :, :L]  # 16-byte rows
+    masked = _run(q, k, v, mask, nh, nkv)
+    got = fastpath.prefill_attention(q, k, v, None, nh, nkv, D, positions=pos)
+    assert torch.equal(got.view(torch.int16), masked.view(torch.int16))
+
+
+def test_causal_positions_declines_and_argument_checks():
+    from ttspipe_amd import _lib, fastpath
+
+    q, k, v, mask = _setup(16, 4, 8, 2, torch.bfloat16)
+    pos = torch.arange(4, 20, device="cuda")
+    assert fastpath.prefill_attention(q, k, v, None, 8, 2, D, positions=pos.int()) is None
+    assert fastpath.prefill_attention(q, k, v, None, 8, 2, D, positions=pos[:15]) is None
+    assert fastpath.prefill_attention(q, k, v, None, 8, 2, D, positions=pos.cpu()) is None
+    assert fastpath.prefill_attention(q, k, v, None, 8, 2, D) is None
+    hip = _lib.load()
+    p = q.data_ptr()
+    rc = hip.ttsp_prefill_attention_causal(p, 1024, 128, p, 256, 4096, p, 256, 4096, None, p, 16, 8, 2, 20, 0.088, 1,
+                                           None, 1, None)
+    assert rc != 0
+
+
+def test_causal_positions_captured_in_a_graph_replay_identically():
+    from ttspipe_amd import fastpath
+
+    for S, prefix in ((96, 40), (64, 2000)):
+        q, k, v, _ = _setup(S, prefix, 32, 8, torch.bfloat16, seed=5)
+        pos = torch.arange(prefix, prefix + S, device="cuda")
+        out = torch.empty(1, S, 32 * D, dtype=torch.bfloat16, device="cuda")
+        work = torch.empty(fastpath.prefill_work_floats(S, 32, 16), device="cuda")
+        eager = fastpath.prefill_attention(q, k, v, None, 32, 8, D, positions=pos).clone()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            fastpath.prefill_attention(q, k, v, None, 32, 8, D, out=out, work=work, positions=pos)
+        for _ in range(3):
+            out.zero_()
+            work.zero_()
+            torch.cuda.synchronize()
+            graph.replay()
+            torch.cuda.synchronize()
+            assert torch.equal(out.view(1, S, 32, D).transpose(1, 2), eager)

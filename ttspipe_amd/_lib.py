@@ -85,6 +85,8 @@ SIGNATURES: dict[str, list] = {
     "ttsp_prefill_attention_splits": [_i, _i, _i],
     "ttsp_prefill_attention_split": [_vp, _ll, _ll, _vp, _ll, _ll, _vp, _ll, _ll, _vp, _ll, _vp, _i, _i, _i, _i, _f,
                                      _i, _vp, _i, _vp],
+    "ttsp_prefill_attention_causal": [_vp, _ll, _ll, _vp, _ll, _ll, _vp, _ll, _ll, _vp, _vp, _i, _i, _i, _i, _f, _i,
+                                      _vp, _i, _vp],
     "ttsp_sample_topk": [_vp, _i, _i, _vp, _vp, _vp, _vp, _vp, _vp],
     "ttsp_sample_max_top_k": [],
     "ttsp_sample_max_vocab": [],

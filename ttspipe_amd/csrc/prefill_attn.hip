@@ -129,6 +129,7 @@ struct PrefillArgs {
   int S, nh, nkv, L;
   float scale2;  // scale * log2(e): scores in log2 units
   float* WO;     // SPLIT: unnormalised O [z][i][head][128], then m, l [z][i][head]
+  const long long* POS;  // CAUSAL: the S query rows' positions (M unused)
 };
 
 // LDS of one staged key block: K rows, V rows, mask tile (bytes)
@@ -141,20 +142,27 @@ constexpr int PA_BLK = PA_KT + PA_VT + PA_MT;
 // taking the z-th of gridDim.z equal runs of the key blocks that hold keys
 // 0 .. last (the mask scan's result, the same in every split), and writing
 // partials to WO; its first staging loads then wait for the scan.
-template <int DT, int G, int NS, bool SPLIT>
+// CAUSAL: the mask is the causal one at the rows' positions (row i allows
+// keys 0 .. POS[i], and none at or past L), so it is computed instead of
+// read: no mask tiles, no scan, each wave takes the workgroup's last key
+// (and the first key some row may not see) from its own 32 position loads.
+// The same keys are masked and the same blocks flagged whole as with the
+// causal mask's bytes, so the results are those bits.
+template <int DT, int G, int NS, bool SPLIT, bool CAUSAL = false>
 __global__ __launch_bounds__(64 * G * NS) void prefill_attn_kernel(const PrefillArgs a) {
   constexpr int NT = 64 * G * NS, NW = NT / 64;
-  constexpr int NKP = NS * PA_KB * (HD / 8), NVP = NKP, NMP = NS * PA_QB * 2;
-  constexpr int KPT = (NKP + NT - 1) / NT, VPT = (NVP + NT - 1) / NT, MPT = (NMP + NT - 1) / NT;
-  constexpr int STAGE = 2 * NS * PA_BLK;
+  constexpr int NKP = NS * PA_KB * (HD / 8), NVP = NKP, NMP = CAUSAL ? 0 : NS * PA_QB * 2;
+  constexpr int KPT = (NKP + NT - 1) / NT, VPT = (NVP + NT - 1) / NT, MPT = NMP ? (NMP + NT - 1) / NT : 1;
+  constexpr int BLK = CAUSAL ? PA_KT + PA_VT : PA_BLK;  // LDS of one staged key block
+  constexpr int STAGE = 2 * NS * BLK;
   constexpr int MERGE = NS > 1 ? G * 66 * 64 * 4 : 0;  // split 1's o (64 floats), m, l per lane
   constexpr int OROW = HD + 8;  // the staged output tile's row stride (elements): 272 bytes
   constexpr int FROW = HD + 4;  // SPLIT: the staged fp32 partial rows' stride (floats): 528 bytes
   // after the merge slots: each head's 32 output rows (SPLIT: its 32 fp32 partial rows)
   constexpr int OUT = SPLIT ? G * PA_QB * FROW * 4 : G * PA_QB * OROW * 2;
   __shared__ __align__(16) uint8_t lds[STAGE > MERGE + OUT ? STAGE : MERGE + OUT];
-  __shared__ int wmax[NW];  // the mask scan's per-wave result
-  __shared__ int full[3];   // per block group (mod 3): every key of its mask tiles allowed
+  __shared__ int wmax[CAUSAL ? 1 : NW];  // the mask scan's per-wave result
+  __shared__ int full[CAUSAL ? 1 : 3];   // per block group (mod 3): every key of its mask tiles allowed
   const int kh = blockIdx.x, q0 = blockIdx.y * PA_QB;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int gw = wave % G, split = wave / G;
@@ -171,13 +179,17 @@ __global__ __launch_bounds__(64 * G * NS) void prefill_attn_kernel(const Prefill
   // L - 1 (bounds are checked per dword; the piece lies in the same page as
   // that byte, and its bytes past L are cleared)
   const __amdgpu_buffer_rsrc_t mr =
-      pa_rsrc(a.M + (size_t)q0 * a.m_ss, (uint32_t)((nq - 1) * a.m_ss + ((L + 15) & ~15)));
+      pa_rsrc(CAUSAL ? nullptr : a.M + (size_t)q0 * a.m_ss, CAUSAL ? 0u : (uint32_t)((nq - 1) * a.m_ss + ((L + 15) & ~15)));
 
   // the mask scan's first step, issued before everything else: thread
   // (row r, k) reads the k-th 16-byte piece from the end of row r
+  // (CAUSAL: this lane's row position instead)
   constexpr int PER = NT / PA_QB;
   const int ncg = (L + 15) / 16, srow = tid % PA_QB, scg0 = ncg - 1 - tid / PA_QB;
-  const u32x4 scan0 = pa_ld16(mr, (uint32_t)(min(srow, nq - 1) * a.m_ss + 16 * max(scg0, 0)));
+  u32x4 scan0 = {0u, 0u, 0u, 0u};
+  long long pos_i = 0;
+  if constexpr (CAUSAL) pos_i = a.POS[min(i, a.S - 1)];
+  else scan0 = pa_ld16(mr, (uint32_t)(min(srow, nq - 1) * a.m_ss + 16 * max(scg0, 0)));
   __builtin_amdgcn_sched_barrier(0);  // keep it first, so waiting for it waits for nothing else
 
   // Q^T fragments (B operand): column = query ql, dims 16 kc + 8 h .. + 7
@@ -211,11 +223,13 @@ __global__ __launch_bounds__(64 * G * NS) void prefill_attn_kernel(const Prefill
       const int j = min(kb0 + NS * t * PA_KB + blk * PA_KB + q / (HD / 8), L - 1), e = (q % (HD / 8)) * 8;
       r.v[n] = pa_ld16(vr, (uint32_t)(j * a.v_ss + e) * 2);
     }
+    if constexpr (!CAUSAL) {
 #pragma unroll
-    for (int n = 0; n < MPT; ++n) {
-      const int p = min(tid + n * NT, NMP - 1), blk = p / (PA_QB * 2), q = p % (PA_QB * 2);
-      const int c = min(kb0 + NS * t * PA_KB + blk * PA_KB + 16 * (q & 1), 16 * (ncg - 1));
-      r.m[n] = pa_ld16(mr, (uint32_t)(min(q >> 1, nq - 1) * a.m_ss + c));
+      for (int n = 0; n < MPT; ++n) {
+        const int p = min(tid + n * NT, NMP - 1), blk = p / (PA_QB * 2), q = p % (PA_QB * 2);
+        const int c = min(kb0 + NS * t * PA_KB + blk * PA_KB + 16 * (q & 1), 16 * (ncg - 1));
+        r.m[n] = pa_ld16(mr, (uint32_t)(min(q >> 1, nq - 1) * a.m_ss + c));
+      }
     }
   };
   auto store = [&](const Regs& r, int t) {
@@ -224,7 +238,7 @@ __global__ __launch_bounds__(64 * G * NS) void prefill_attn_kernel(const Prefill
     for (int n = 0; n < KPT; ++n) {
       const int p = tid + n * NT, blk = p / (PA_KB * (HD / 8)), q = p % (PA_KB * (HD / 8));
       if (NKP % NT == 0 || p < NKP) {
-        uint8_t* base = lds + (size_t)(buf * NS + blk) * PA_BLK;
+        uint8_t* base = lds + (size_t)(buf * NS + blk) * BLK;
         *reinterpret_cast<u32x4*>(base + 2 * ((q / (HD / 8)) * PA_KROW + (q % (HD / 8)) * 8)) = r.k[n];
       }
     }
@@ -232,18 +246,20 @@ __global__ __launch_bounds__(64 * G * NS) void prefill_attn_kernel(const Prefill
     for (int n = 0; n < VPT; ++n) {
       const int p = tid + n * NT, blk = p / (PA_KB * (HD / 8)), q = p % (PA_KB * (HD / 8));
       if (NVP % NT == 0 || p < NVP) {
-        uint8_t* base = lds + (size_t)(buf * NS + blk) * PA_BLK + PA_KT;
+        uint8_t* base = lds + (size_t)(buf * NS + blk) * BLK + PA_KT;
         *reinterpret_cast<u32x4*>(base + 2 * ((q / (HD / 8)) * PA_VROW + (q % (HD / 8)) * 8)) = r.v[n];
       }
     }
+    if constexpr (!CAUSAL) {
 #pragma unroll
-    for (int n = 0; n < MPT; ++n) {
-      const int p = tid + n * NT, blk = p / (PA_QB * 2), q = p % (PA_QB * 2);
-      if (NMP % NT == 0 || p < NMP) {
-        const u32x4 m = pa_mask_tail(r.m[n], kb0 + NS * t * PA_KB + blk * PA_KB + 16 * (q & 1), L);
-        *reinterpret_cast<u32x4*>(lds + (size_t)(buf * NS + blk) * PA_BLK + PA_KT + PA_VT + (q >> 1) * PA_MROW +
-                                  16 * (q & 1)) = m;
-        if ((q >> 1) < nq && !pa_all_set(m)) full[t % 3] = 0;  // rows past nq are never used
+      for (int n = 0; n < MPT; ++n) {
+        const int p = tid + n * NT, blk = p / (PA_QB * 2), q = p % (PA_QB * 2);
+        if (NMP % NT == 0 || p < NMP) {
+          const u32x4 m = pa_mask_tail(r.m[n], kb0 + NS * t * PA_KB + blk * PA_KB + 16 * (q & 1), L);
+          *reinterpret_cast<u32x4*>(lds + (size_t)(buf * NS + blk) * BLK + PA_KT + PA_VT + (q >> 1) * PA_MROW +
+                                    16 * (q & 1)) = m;
+          if ((q >> 1) < nq && !pa_all_set(m)) full[t % 3] = 0;  // rows past nq are never used
+        }
       }
     }
   };
@@ -258,7 +274,16 @@ __global__ __launch_bounds__(64 * G * NS) void prefill_attn_kernel(const Prefill
   // piece, then (only where it holds no allowed key) the rest of the row
   // backwards; the maximum over the workgroup through one slot per wave
   int hit = -1;
-  if (srow < nq && scg0 >= 0) {
+  // CAUSAL: the last key this lane's row sees (-1: none), and the lowest such
+  // key over the workgroup's rows, below which every block is whole
+  const int klast = CAUSAL ? (int)min(pos_i, (long long)L - 1) : 0;
+  int kwhole = 0;
+  if constexpr (CAUSAL) {
+    hit = klast;
+    kwhole = ql < nq ? klast : L;
+#pragma unroll
+    for (int o = 16; o >= 1; o >>= 1) kwhole = min(kwhole, __shfl_xor(kwhole, o, 64));
+  } else if (srow < nq && scg0 >= 0) {
     u32x4 v = pa_mask_tail(scan0, 16 * scg0, L);
     for (int cg = scg0;;) {
 #pragma unroll
@@ -271,12 +296,15 @@ __global__ __launch_bounds__(64 * G * NS) void prefill_attn_kernel(const Prefill
   }
 #pragma unroll
   for (int o = 32; o >= 1; o >>= 1) hit = max(hit, __shfl_xor(hit, o, 64));
-  if (lane == 0) wmax[wave] = hit;
-  if (tid == 0) full[0] = full[1] = 1;
-  __syncthreads();
-  int last = -1;
+  int last = hit;  // CAUSAL: every wave holds the workgroup's value
+  if constexpr (!CAUSAL) {
+    if (lane == 0) wmax[wave] = hit;
+    if (tid == 0) full[0] = full[1] = 1;
+    __syncthreads();
+    last = -1;
 #pragma unroll
-  for (int w = 0; w < NW; ++w) last = max(last, wmax[w]);
+    for (int w = 0; w < NW; ++w) last = max(last, wmax[w]);
+  }
   // this workgroup's key blocks: all blocks holding keys 0 .. last, or split
   // z's run of them
   const int live = (last + PA_KB) / PA_KB;
@@ -310,12 +338,15 @@ __global__ __launch_bounds__(64 * G * NS) void prefill_attn_kernel(const Prefill
   auto step = [&](int t, Regs& rl, const Regs& rw) {
     const int buf = t & 1, b = NS * t + split;
     load(rl, t + 2);  // also past the last group: clamped rows, never stored
-    if (tid == 0) full[(t + 2) % 3] = 1;  // group t - 1 used this slot before the last barrier
+    if (!CAUSAL && tid == 0) full[(t + 2) % 3] = 1;  // group t - 1 used this slot before the last barrier
     if (b < nkb) {
-      const uint8_t* base = lds + (size_t)(buf * NS + split) * PA_BLK;
+      const uint8_t* base = lds + (size_t)(buf * NS + split) * BLK;
       const uint16_t* ks = reinterpret_cast<const uint16_t*>(base);
       const uint8_t* ms = base + PA_KT + PA_VT;
-      const bool all = __builtin_amdgcn_readfirstlane(full[t % 3]) != 0;
+      // (CAUSAL: the group's blocks whole when its last key is below every row's
+      // last key, as the causal mask's tiles are then all set)
+      const int gend = kb0 + (NS * t + NS) * PA_KB - 1;
+      const bool all = CAUSAL ? gend <= kwhole : __builtin_amdgcn_readfirstlane(full[t % 3]) != 0;
       // S^T = K Q^T for keys 32 b .. 32 b + 31
       pa_f32x16 s;
 #pragma unroll
@@ -345,13 +376,22 @@ __global__ __launch_bounds__(64 * G * NS) void prefill_attn_kernel(const Prefill
       // the whole group is allowed; the online softmax of query ql over this
       // lane and lane ^ 32, in log2 units
       if (!all) {
-        const uint8_t* mrow = ms + ql * PA_MROW + 4 * h;
+        if constexpr (CAUSAL) {
+          const int k0 = kb0 + b * PA_KB + 4 * h;  // key of s[0]
 #pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          const uint32_t mw = *reinterpret_cast<const uint32_t*>(mrow + 8 * g);
+          for (int g = 0; g < 4; ++g)
 #pragma unroll
-          for (int c = 0; c < 4; ++c)
-            if (((mw >> (8 * c)) & 0xffu) == 0) s[4 * g + c] = -__builtin_inff();
+            for (int c = 0; c < 4; ++c)
+              if (k0 + 8 * g + c > klast) s[4 * g + c] = -__builtin_inff();
+        } else {
+          const uint8_t* mrow = ms + ql * PA_MROW + 4 * h;
+#pragma unroll
+          for (int g = 0; g < 4; ++g) {
+            const uint32_t mw = *reinterpret_cast<const uint32_t*>(mrow + 8 * g);
+#pragma unroll
+            for (int c = 0; c < 4; ++c)
+              if (((mw >> (8 * c)) & 0xffu) == 0) s[4 * g + c] = -__builtin_inff();
+          }
         }
       }
       float bm = -__builtin_inff();
@@ -542,13 +582,46 @@ using namespace ttsp;
 
 extern "C" int ttsp_prefill_max_groups() { return PA_MAX_GROUPS; }
 
+// the kernel for `groups` query heads per kv head: two key splits for 1, 2
+// and 4 heads per kv head (at most 8 waves, two a SIMD at ~240 registers),
+// one otherwise
+template <int DT, bool CAUSAL>
+static int prefill_dispatch(int groups, dim3 grid, int splits, const PrefillArgs& a, hipStream_t stream) {
+#define TTSP_PA_G(G)                                                                                         \
+  case G:                                                                                                    \
+    if (splits > 1)                                                                                          \
+      hipLaunchKernelGGL((prefill_attn_kernel<DT, G, PA_SPLITS(G), true, CAUSAL>), grid,                     \
+                         dim3(64 * G * PA_SPLITS(G)), 0, stream, a);                                         \
+    else                                                                                                     \
+      hipLaunchKernelGGL((prefill_attn_kernel<DT, G, PA_SPLITS(G), false, CAUSAL>), grid,                    \
+                         dim3(64 * G * PA_SPLITS(G)), 0, stream, a);                                         \
+    return 0;
+  switch (groups) {
+    TTSP_PA_G(1)
+    TTSP_PA_G(2)
+    TTSP_PA_G(3)
+    TTSP_PA_G(4)
+    TTSP_PA_G(5)
+    TTSP_PA_G(6)
+    TTSP_PA_G(7)
+    TTSP_PA_G(8)
+    default:
+      return (int)hipErrorInvalidValue;
+  }
+#undef TTSP_PA_G
+}
+
+// mask: bool rows (mask_row_stride bytes apart), or null with pos, the S
+// rows' positions, for the causal mask at those positions
 static int prefill_launch(const void* Q, long long q_seq_stride, long long q_head_stride, const void* K,
                           long long k_seq_stride, long long k_head_stride, const void* V, long long v_seq_stride,
-                          long long v_head_stride, const void* mask, long long mask_row_stride, void* Y, int S,
-                          int nh, int nkv, int L, float scale, int dtype, float* work, int splits,
+                          long long v_head_stride, const void* mask, long long mask_row_stride, const long long* pos,
+                          void* Y, int S, int nh, int nkv, int L, float scale, int dtype, float* work, int splits,
                           hipStream_t stream) {
-  if (!Q || !K || !V || !mask || !Y || S <= 0 || nh <= 0 || nkv <= 0 || nh % nkv || L <= 0 ||
-      nh / nkv > PA_MAX_GROUPS || S > (1 << 20) || mask_row_stride < L || splits < 1 || splits > 16)
+  const bool causal = pos != nullptr;
+  if (causal) mask = nullptr, mask_row_stride = 0;
+  if (!Q || !K || !V || (!causal && !mask) || !Y || S <= 0 || nh <= 0 || nkv <= 0 || nh % nkv || L <= 0 ||
+      nh / nkv > PA_MAX_GROUPS || S > (1 << 20) || (!causal && mask_row_stride < L) || splits < 1 || splits > 16)
     return (int)hipErrorInvalidValue;
   // 16-byte pieces: every row start and the bases aligned
   const long long st[6] = {q_seq_stride, q_head_stride, k_seq_stride, k_head_stride, v_seq_stride, v_head_stride};
@@ -566,41 +639,19 @@ static int prefill_launch(const void* Q, long long q_seq_stride, long long q_hea
   PrefillArgs a{(const uint16_t*)Q, (const uint16_t*)K, (const uint16_t*)V, (const uint8_t*)mask, (uint16_t*)Y,
                 q_seq_stride, q_head_stride, (int)k_seq_stride, (int)k_head_stride, (int)v_seq_stride,
                 (int)v_head_stride, (int)mask_row_stride, S, nh, nkv, L, scale * PA_LOG2E,
-                splits > 1 ? work : nullptr};
+                splits > 1 ? work : nullptr, pos};
   const int groups = nh / nkv;
   const dim3 grid(nkv, (S + PA_QB - 1) / PA_QB, splits);
-  // two key splits for 1, 2 and 4 heads per kv head (at most 8 waves, two a
-  // SIMD at ~240 registers), one otherwise
-#define TTSP_PA_G(DTV, G)                                                                                   \
-  case G:                                                                                                   \
-    if (splits > 1)                                                                                         \
-      hipLaunchKernelGGL((prefill_attn_kernel<DTV, G, PA_SPLITS(G), true>), grid, dim3(64 * G * PA_SPLITS(G)), \
-                         0, stream, a);                                                                     \
-    else                                                                                                    \
-      hipLaunchKernelGGL((prefill_attn_kernel<DTV, G, PA_SPLITS(G), false>), grid, dim3(64 * G * PA_SPLITS(G)), \
-                         0, stream, a);                                                                     \
-    break;
-#define TTSP_PA(DTV)                           \
-  switch (groups) {                            \
-    TTSP_PA_G(DTV, 1)                          \
-    TTSP_PA_G(DTV, 2)                          \
-    TTSP_PA_G(DTV, 3)                          \
-    TTSP_PA_G(DTV, 4)                          \
-    TTSP_PA_G(DTV, 5)                          \
-    TTSP_PA_G(DTV, 6)                          \
-    TTSP_PA_G(DTV, 7)                          \
-    TTSP_PA_G(DTV, 8)                          \
-    default: return (int)hipErrorInvalidValue; \
-  }
-  if (dtype == DT_F16) {
-    TTSP_PA(DT_F16)
-  } else if (dtype == DT_BF16) {
-    TTSP_PA(DT_BF16)
-  } else {
+  int rc;
+  if (dtype == DT_F16)
+    rc = causal ? prefill_dispatch<DT_F16, true>(groups, grid, splits, a, stream)
+                : prefill_dispatch<DT_F16, false>(groups, grid, splits, a, stream);
+  else if (dtype == DT_BF16)
+    rc = causal ? prefill_dispatch<DT_BF16, true>(groups, grid, splits, a, stream)
+                : prefill_dispatch<DT_BF16, false>(groups, grid, splits, a, stream);
+  else
     return (int)hipErrorInvalidValue;
-  }
-#undef TTSP_PA
-#undef TTSP_PA_G
+  if (rc) return rc;
   if (splits > 1) {
     const long long n = (long long)S * nh * (HD / 8);
     const dim3 mg((unsigned)((n + 255) / 256));
@@ -632,7 +683,8 @@ extern "C" int ttsp_prefill_attention(const void* Q, long long q_seq_stride, lon
                                       const void* mask, long long mask_row_stride, void* Y, int S, int nh,
                                       int nkv, int L, float scale, int dtype, hipStream_t stream) {
   return prefill_launch(Q, q_seq_stride, q_head_stride, K, k_seq_stride, k_head_stride, V, v_seq_stride,
-                        v_head_stride, mask, mask_row_stride, Y, S, nh, nkv, L, scale, dtype, nullptr, 1, stream);
+                        v_head_stride, mask, mask_row_stride, nullptr, Y, S, nh, nkv, L, scale, dtype, nullptr, 1,
+                        stream);
 }
 
 extern "C" int ttsp_prefill_attention_splits(int S, int nkv, int L) {
@@ -647,5 +699,16 @@ extern "C" int ttsp_prefill_attention_split(const void* Q, long long q_seq_strid
                                             int nkv, int L, float scale, int dtype, float* work, int splits,
                                             hipStream_t stream) {
   return prefill_launch(Q, q_seq_stride, q_head_stride, K, k_seq_stride, k_head_stride, V, v_seq_stride,
-                        v_head_stride, mask, mask_row_stride, Y, S, nh, nkv, L, scale, dtype, work, splits, stream);
+                        v_head_stride, mask, mask_row_stride, nullptr, Y, S, nh, nkv, L, scale, dtype, work, splits,
+                        stream);
+}
+
+extern "C" int ttsp_prefill_attention_causal(const void* Q, long long q_seq_stride, long long q_head_stride,
+                                             const void* K, long long k_seq_stride, long long k_head_stride,
+                                             const void* V, long long v_seq_stride, long long v_head_stride,
+                                             const long long* pos, void* Y, int S, int nh, int nkv, int L,
+                                             float scale, int dtype, float* work, int splits, hipStream_t stream) {
+  if (!pos) return (int)hipErrorInvalidValue;
+  return prefill_launch(Q, q_seq_stride, q_head_stride, K, k_seq_stride, k_head_stride, V, v_seq_stride,
+                        v_head_stride, nullptr, 0, pos, Y, S, nh, nkv, L, scale, dtype, work, splits, stream);
 }

@@ -30,12 +30,14 @@ def stats() -> dict:
     return dict(_stats)
 
 
-def _prefill_eligible(q, k, v, mask, n_head, n_local_heads, head_dim) -> bool:
+def _prefill_eligible(q, k, v, mask, n_head, n_local_heads, head_dim, positions=None) -> bool:
     import torch
 
     from ttspipe_amd import _lib
 
-    if head_dim != HEAD_DIM or mask is None or not q.is_cuda or q.dim() != 4 or k.dim() != 4 or v.dim() != 4:
+    if head_dim != HEAD_DIM or (mask is None and positions is None) or not q.is_cuda or q.dim() != 4:
+        return False
+    if k.dim() != 4 or v.dim() != 4:
         return False
     if q.dtype not in (torch.float16, torch.bfloat16) or k.dtype != q.dtype or v.dtype != q.dtype:
         return False
@@ -47,15 +49,18 @@ def _prefill_eligible(q, k, v, mask, n_head, n_local_heads, head_dim) -> bool:
     L = k.shape[2]
     if k.shape != (1, n_local_heads, L, head_dim) or v.shape != k.shape:
         return False
-    if mask.dtype != torch.bool or mask.dim() != 4 or tuple(mask.shape) != (1, 1, seqlen, L) or not mask.is_cuda:
-        return False
     for t in (q, k, v):
         if t.stride(3) != 1 or t.stride(1) % 8 or t.stride(2) % 8 or t.data_ptr() % 16:
             return False
+    if positions is not None:
+        return (positions.dtype == torch.long and positions.is_cuda and positions.is_contiguous()
+                and positions.numel() == seqlen)
+    if mask.dtype != torch.bool or mask.dim() != 4 or tuple(mask.shape) != (1, 1, seqlen, L) or not mask.is_cuda:
+        return False
     return mask.stride(3) == 1 and mask.stride(2) % 16 == 0 and mask.stride(2) >= L and mask.data_ptr() % 16 == 0
 
 
-def prefill_attention(q, k, v, mask, n_head, n_local_heads, head_dim, out=None, work=None):
+def prefill_attention(q, k, v, mask, n_head, n_local_heads, head_dim, out=None, work=None, positions=None):
     """`decode_attention` in one launch: q (1, n_head, S, 128), k/v (1,
     n_local_heads, L, 128) with the last dim contiguous (any seq/head strides
     that keep rows 16-byte aligned, e.g. the KV cache sliced to L), mask bool
@@ -66,12 +71,16 @@ def prefill_attention(q, k, v, mask, n_head, n_local_heads, head_dim, out=None, 
     reference's softmax over all -inf scores. A short run over a long cache
     splits its keys over several workgroups (`ttsp_prefill_attention_splits`)
     through an fp32 workspace: `work=` may supply one of at least
-    `prefill_work_floats(...)` elements, else it is allocated per call."""
+    `prefill_work_floats(...)` elements, else it is allocated per call.
+    `positions` (int64 (S,), contiguous): the causal mask at those positions
+    (row i allows keys 0 .. positions[i], none at or past L) is computed in
+    the kernel instead of read, and `mask` is not read (it may be None); the
+    result is bit for bit the one `mask` = those causal rows gives."""
     import torch
 
     from ttspipe_amd import _lib
 
-    if not _lib.gpu_present() or not _prefill_eligible(q, k, v, mask, n_head, n_local_heads, head_dim):
+    if not _lib.gpu_present() or not _prefill_eligible(q, k, v, mask, n_head, n_local_heads, head_dim, positions):
         _stats["prefill_declined"] += 1
         return None
     seqlen, L = q.shape[2], k.shape[2]
@@ -87,12 +96,19 @@ def prefill_attention(q, k, v, mask, n_head, n_local_heads, head_dim, out=None, 
     elif splits > 1 and (work.dtype != torch.float32 or work.numel() < need or not work.is_contiguous()
                          or work.data_ptr() % 16):
         raise ValueError(f"work must be a contiguous 16-byte aligned fp32 tensor of at least {need} elements")
-    rc = lib.ttsp_prefill_attention_split(
-        q.data_ptr(), q.stride(2), q.stride(1), k.data_ptr(), k.stride(2), k.stride(1), v.data_ptr(), v.stride(2),
-        v.stride(1), mask.data_ptr(), mask.stride(2), out.data_ptr(), seqlen, n_head, n_local_heads, L,
-        float(head_dim**-0.5), _lib.dtype_code(q.dtype), work.data_ptr() if splits > 1 else None, splits,
-        _lib.stream())
-    _lib.check(rc, "ttsp_prefill_attention_split")
+    wp = work.data_ptr() if splits > 1 else None
+    if positions is not None:
+        rc = lib.ttsp_prefill_attention_causal(
+            q.data_ptr(), q.stride(2), q.stride(1), k.data_ptr(), k.stride(2), k.stride(1), v.data_ptr(),
+            v.stride(2), v.stride(1), positions.data_ptr(), out.data_ptr(), seqlen, n_head, n_local_heads, L,
+            float(head_dim**-0.5), _lib.dtype_code(q.dtype), wp, splits, _lib.stream())
+        _lib.check(rc, "ttsp_prefill_attention_causal")
+    else:
+        rc = lib.ttsp_prefill_attention_split(
+            q.data_ptr(), q.stride(2), q.stride(1), k.data_ptr(), k.stride(2), k.stride(1), v.data_ptr(),
+            v.stride(2), v.stride(1), mask.data_ptr(), mask.stride(2), out.data_ptr(), seqlen, n_head, n_local_heads,
+            L, float(head_dim**-0.5), _lib.dtype_code(q.dtype), wp, splits, _lib.stream())
+        _lib.check(rc, "ttsp_prefill_attention_split")
     _stats["prefill_attn"] += 1
     return out.view(1, seqlen, n_head, head_dim).transpose(1, 2)
 

@@ -255,7 +255,8 @@ def prefill_block_chain(block, x, freqs_cis, mask, input_pos, *, xn=None, next_n
     caller's promise that the mask is the causal one (row i allows keys
     0 .. input_pos[i], all below the mask's width); a span of up to
     `fastpath.CAUSAL_ROWS_MAX` rows then attends row by row as the decode
-    step does (`fastpath.causal_rows_attention`), without reading the mask.
+    step does (`fastpath.causal_rows_attention`), and a longer one computes
+    the mask from `input_pos` in the attention kernel; neither reads it.
 
     The fork's block in its own order with the prefill kernels: RMSNorm,
     wqkv GEMM, q/k head norms + rotary + KV-cache write for every row in one
@@ -339,7 +340,8 @@ def prefill_block_chain(block, x, freqs_cis, mask, input_pos, *, xn=None, next_n
     if y is None:
         if mask.shape[-1] < k.shape[2]:
             k, v = k[:, :, : mask.shape[-1]], v[:, :, : mask.shape[-1]]
-        y = fastpath.prefill_attention(q, k, v, mask, nh, nkv, hd)
+        # a causal span's mask follows from its positions: computed in the kernel, not read
+        y = fastpath.prefill_attention(q, k, v, mask, nh, nkv, hd, positions=input_pos if causal else None)
         if y is None:
             y = fastpath.decode_attention(q, k, v, mask, nh, nkv, hd)
         y = y.transpose(1, 2).contiguous().view(bsz, n, nh * hd)
