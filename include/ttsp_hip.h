@@ -373,7 +373,9 @@ int ttsp_prefill_attention_split(const void* Q, long long q_seq_stride, long lon
  * allowing keys j <= min(pos[i], L - 1). The mask is computed in the kernel
  * rather than read (no mask rows, no scan of them), and the same keys are
  * masked, so Y is bit for bit ttsp_prefill_attention_split's with mask row i
- * = causal_mask[pos[i]][0 .. L). Null pos returns hipErrorInvalidValue.
+ * = causal_mask[pos[i]][0 .. L), except with nh / nkv = 4, splits = 1 and
+ * nkv * ceil(S / 32) >= 128, where four key splits a workgroup merge (the
+ * same attention to fp32 rounding). Null pos returns hipErrorInvalidValue.
  * Replaces: scaled_dot_product_attention with the mask forward_generate
  * builds, causal_mask[..., input_pos, :max_seq_len] (app/engine/fastpath.py:9,
  * 244-268; the prefill of app/engine/graphs.py:219-228). */

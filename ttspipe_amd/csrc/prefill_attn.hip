@@ -148,26 +148,32 @@ constexpr int PA_BLK = PA_KT + PA_VT + PA_MT;
 // (and the first key some row may not see) from its own 32 position loads.
 // The same keys are masked and the same blocks flagged whole as with the
 // causal mask's bytes, so the results are those bits.
-template <int DT, int G, int NS, bool SPLIT, bool CAUSAL = false>
-__global__ __launch_bounds__(64 * G * NS) void prefill_attn_kernel(const PrefillArgs a) {
-  constexpr int NT = 64 * G * NS, NW = NT / 64;
+// GW: the query heads a workgroup takes, of the G that share a kv head
+// (G / GW workgroups a kv head and query block, each staging the kv head's
+// keys for its own heads).
+template <int DT, int G, int NS, bool SPLIT, bool CAUSAL = false, int GW = G>
+__global__ __launch_bounds__(64 * GW * NS) void prefill_attn_kernel(const PrefillArgs a) {
+  static_assert(G % GW == 0, "a kv head's query heads split evenly over its workgroups");
+  static_assert((NS & (NS - 1)) == 0, "the key splits merge in halving rounds");
+  constexpr int NT = 64 * GW * NS, NW = NT / 64;
   constexpr int NKP = NS * PA_KB * (HD / 8), NVP = NKP, NMP = CAUSAL ? 0 : NS * PA_QB * 2;
   constexpr int KPT = (NKP + NT - 1) / NT, VPT = (NVP + NT - 1) / NT, MPT = NMP ? (NMP + NT - 1) / NT : 1;
   constexpr int BLK = CAUSAL ? PA_KT + PA_VT : PA_BLK;  // LDS of one staged key block
   constexpr int STAGE = 2 * NS * BLK;
-  constexpr int MERGE = NS > 1 ? G * 66 * 64 * 4 : 0;  // split 1's o (64 floats), m, l per lane
+  // the first merge round's slots: each giving split's o (64 floats), m, l per lane
+  constexpr int MERGE = NS > 1 ? (NS / 2) * GW * 66 * 64 * 4 : 0;
   constexpr int OROW = HD + 8;  // the staged output tile's row stride (elements): 272 bytes
   constexpr int FROW = HD + 4;  // SPLIT: the staged fp32 partial rows' stride (floats): 528 bytes
   // after the merge slots: each head's 32 output rows (SPLIT: its 32 fp32 partial rows)
-  constexpr int OUT = SPLIT ? G * PA_QB * FROW * 4 : G * PA_QB * OROW * 2;
+  constexpr int OUT = SPLIT ? GW * PA_QB * FROW * 4 : GW * PA_QB * OROW * 2;
   __shared__ __align__(16) uint8_t lds[STAGE > MERGE + OUT ? STAGE : MERGE + OUT];
   __shared__ int wmax[CAUSAL ? 1 : NW];  // the mask scan's per-wave result
   __shared__ int full[CAUSAL ? 1 : 3];   // per block group (mod 3): every key of its mask tiles allowed
-  const int kh = blockIdx.x, q0 = blockIdx.y * PA_QB;
+  const int kh = blockIdx.x / (G / GW), q0 = blockIdx.y * PA_QB;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int gw = wave % G, split = wave / G;
+  const int gw = wave % GW, split = wave / GW;
   const int h = lane >> 5, ql = lane & 31;
-  const int head = kh * G + gw;
+  const int head = kh * G + (int)(blockIdx.x % (G / GW)) * GW + gw;
   const int i = q0 + ql;  // this lane's query
   const int nq = min(PA_QB, a.S - q0);
   const int L = a.L;
@@ -440,30 +446,38 @@ __global__ __launch_bounds__(64 * G * NS) void prefill_attn_kernel(const Prefill
     if (t + 1 < nit) step(t + 1, rs[1], rs[0]);
   }
   if constexpr (NS > 1) {
-    // merge split 1 into split 0 through LDS (same lane layout in both), then
-    // split 0 writes; the staging buffers are free after the loop's last barrier
-    static_assert(NS == 2, "one merge round");
-    float* mg = reinterpret_cast<float*>(lds) + gw * 66 * 64 + lane;
-    if (split == 1) {
+    // splits st .. 2 st - 1 hand their o, m, l to splits 0 .. st - 1 through
+    // LDS (same lane layout in both), st halving down to 1, then split 0
+    // writes; the staging buffers are free after the loop's last barrier.
+    // Every wave takes every barrier; only split 0 goes on.
 #pragma unroll
-      for (int d = 0; d < HD / 32; ++d)
+    for (int st = NS / 2; st >= 1; st /= 2) {
+      const bool give = split >= st && split < 2 * st, take = split < st;
+      float* mg = reinterpret_cast<float*>(lds) + (size_t)((give ? split - st : split) * GW + gw) * 66 * 64 + lane;
+      if (give) {
 #pragma unroll
-        for (int r = 0; r < 16; ++r) mg[(16 * d + r) * 64] = o[d][r];
-      mg[64 * 64] = mrun;
-      mg[65 * 64] = lrun;
+        for (int d = 0; d < HD / 32; ++d)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) mg[(16 * d + r) * 64] = o[d][r];
+        mg[64 * 64] = mrun;
+        mg[65 * 64] = lrun;
+      }
+      __syncthreads();
+      if (take) {
+        const float m2 = mg[64 * 64], l2 = mg[65 * 64];
+        const float mm = fmaxf(mrun, m2);
+        const float mref = mm == -__builtin_inff() ? 0.0f : mm;
+        const float f1 = pa_exp2(mrun - mref), f2 = pa_exp2(m2 - mref);
+        lrun = lrun * f1 + l2 * f2;
+        mrun = mm;  // o and lrun are now relative to the merged max (the key-split merge reads it)
+#pragma unroll
+        for (int d = 0; d < HD / 32; ++d)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) o[d][r] = o[d][r] * f1 + mg[(16 * d + r) * 64] * f2;
+      }
+      if (st > 1) __syncthreads();  // the next round writes the slots again
     }
-    __syncthreads();
-    if (split == 1) return;
-    const float m2 = mg[64 * 64], l2 = mg[65 * 64];
-    const float mm = fmaxf(mrun, m2);
-    const float mref = mm == -__builtin_inff() ? 0.0f : mm;
-    const float f1 = pa_exp2(mrun - mref), f2 = pa_exp2(m2 - mref);
-    lrun = lrun * f1 + l2 * f2;
-    mrun = mm;  // o and lrun are now relative to the merged max (the key-split merge reads it)
-#pragma unroll
-    for (int d = 0; d < HD / 32; ++d)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) o[d][r] = o[d][r] * f1 + mg[(16 * d + r) * 64] * f2;
+    if (split != 0) return;
   }
   if constexpr (SPLIT) {  // O unnormalised, max and sum of this split, for the merge kernel
     // O staged as this head's 32 rows in LDS (read back by this wave only)
@@ -584,9 +598,22 @@ extern "C" int ttsp_prefill_max_groups() { return PA_MAX_GROUPS; }
 
 // the kernel for `groups` query heads per kv head: two key splits for 1, 2
 // and 4 heads per kv head (at most 8 waves, two a SIMD at ~240 registers),
-// one otherwise
+// one otherwise. The causal form with 4 heads per kv head and no key split
+// over workgroups, once the (kv head, query block) pairs fill half the CUs,
+// takes two workgroups of 2 heads and 4 key splits each instead (its LDS
+// holds four key blocks a stage without the mask tiles): all CUs busy and
+// half the serial key steps, for twice the key staging (512 causal rows,
+// 32 / 8 heads: 14.5 against 15.9 us; with fewer rows, or with key splits,
+// the staging costs more than it saves).
 template <int DT, bool CAUSAL>
 static int prefill_dispatch(int groups, dim3 grid, int splits, const PrefillArgs& a, hipStream_t stream) {
+  if constexpr (CAUSAL) {
+    if (groups == 4 && splits == 1 && (long long)grid.x * grid.y >= 128) {
+      grid.x *= 2;
+      hipLaunchKernelGGL((prefill_attn_kernel<DT, 4, 4, false, true, 2>), grid, dim3(64 * 2 * 4), 0, stream, a);
+      return 0;
+    }
+  }
 #define TTSP_PA_G(G)                                                                                         \
   case G:                                                                                                    \
     if (splits > 1)                                                                                          \

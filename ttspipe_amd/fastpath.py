@@ -75,7 +75,10 @@ def prefill_attention(q, k, v, mask, n_head, n_local_heads, head_dim, out=None, 
     `positions` (int64 (S,), contiguous): the causal mask at those positions
     (row i allows keys 0 .. positions[i], none at or past L) is computed in
     the kernel instead of read, and `mask` is not read (it may be None); the
-    result is bit for bit the one `mask` = those causal rows gives."""
+    result is bit for bit the one `mask` = those causal rows gives, except
+    where the kernel takes four in-workgroup key splits (4 query heads per kv
+    head, no split over workgroups, at least 128 (kv head, 32-row block)
+    pairs), whose merge order rounds differently."""
     import torch
 
     from ttspipe_amd import _lib
