@@ -552,8 +552,10 @@ def bench_prefill_attention(cases=((512, 0), (512, 1536), (64, 2000)), n_head: i
     causal mask, as the HIP path runs it (one launch, or a key split and its
     merge for a short run over a long cache); torch's
     scaled_dot_product_attention with the same boolean mask (the reference's
-    path beyond 64 positions) timed beside it. FLOPs count the allowed
-    (query, key) pairs: 4 * 128 per pair and head."""
+    path beyond 64 positions) timed beside it, and the causal form the
+    prefill block runs (`positions=`: the mask computed from the rows'
+    positions, `us_causal`). FLOPs count the allowed (query, key) pairs:
+    4 * 128 per pair and head."""
     import torch
     import torch.nn.functional as F
 
@@ -572,18 +574,23 @@ def bench_prefill_attention(cases=((512, 0), (512, 1536), (64, 2000)), n_head: i
         vc = torch.randn(1, n_kv, max_len, 128, device=dev, generator=g).to(torch.bfloat16)
         k, v = kc[:, :, :L], vc[:, :, :L]
         causal = torch.tril(torch.ones(max_len, max_len, dtype=torch.bool, device=dev))
-        mask = causal[None, None, torch.arange(prefix, L, device=dev)][..., :L]
+        pos = torch.arange(prefix, L, device=dev)
+        mask = causal[None, None, pos][..., :L]
         y = torch.empty(1, rows, n_head * 128, dtype=torch.bfloat16, device=dev)
 
         def ours():
             if fastpath.prefill_attention(q, k, v, mask, n_head, n_kv, 128, out=y, work=work) is None:
                 raise RuntimeError("prefill attention declined")
 
+        def ours_causal():
+            if fastpath.prefill_attention(q, k, v, None, n_head, n_kv, 128, out=y, work=work, positions=pos) is None:
+                raise RuntimeError("prefill attention declined")
+
         def sdpa():
             F.scaled_dot_product_attention(q, k, v, attn_mask=mask, enable_gqa=True)
 
         times = {}
-        for name, fn in (("hip", ours), ("sdpa", sdpa)):
+        for name, fn in (("hip", ours), ("causal", ours_causal), ("sdpa", sdpa)):
             fn()
             torch.cuda.synchronize()
             graph = capture(lambda fn=fn: [fn() for _ in range(4)])
@@ -595,6 +602,9 @@ def bench_prefill_attention(cases=((512, 0), (512, 1536), (64, 2000)), n_head: i
         out.append({"rows": rows, "prefix": prefix, "key_splits": splits, "us": round(times["hip"] * 1e6, 2),
                     "tflops": round(flop / times["hip"] / 1e12, 1),
                     "pct_of_mfma_peak": round(100 * flop / times["hip"] / 1e12 / MFMA_PEAK_TFLOPS, 2),
+                    "us_causal": round(times["causal"] * 1e6, 2),
+                    "tflops_causal": round(flop / times["causal"] / 1e12, 1),
+                    "pct_of_mfma_peak_causal": round(100 * flop / times["causal"] / 1e12 / MFMA_PEAK_TFLOPS, 2),
                     "torch_sdpa_us": round(times["sdpa"] * 1e6, 1)})
     return out
 
