@@ -361,72 +361,64 @@ __global__ __launch_bounds__(256) void nf4_gemm_reduce_kernel(const float* __res
 // in one launch: Y is nf4_gemm_reduce_kernel's output, YN = rms_norm(Y, G, eps)
 // with rms_norm_kernel's order (chunk c of 8 values by lane c % 64 in step
 // c / 64, each chunk an fma chain of squares, DPP sums, steps left to right).
-// One workgroup of four waves per output row: wave w holds steps w and w + 4
-// in registers, the step sums meet in LDS. M % 8 == 0, M <= 64 * 8 * NRM_CH.
+// One workgroup per output row with a wave per step (64 * ceil(M / 512)
+// threads, at most 8 waves): each wave issues all of its loads - the splits'
+// partials, the residual and the norm weight - before using any, so the row
+// costs one memory round trip; the step sums meet in LDS.
+// M % 8 == 0, M <= 64 * 8 * NRM_CH.
 constexpr int NRM_CH = 8;
 template <int DT, int S>
-__global__ __launch_bounds__(256) void nf4_gemm_reduce_norm_kernel(const float* __restrict__ YP,
-                                                                   uint16_t* __restrict__ Y,
-                                                                   const uint16_t* __restrict__ R, int epi, int M,
-                                                                   int N, const uint16_t* __restrict__ G, float eps,
-                                                                   uint16_t* __restrict__ YN) {
+__global__ __launch_bounds__(64 * NRM_CH) void nf4_gemm_reduce_norm_kernel(const float* __restrict__ YP,
+                                                                          uint16_t* __restrict__ Y,
+                                                                          const uint16_t* __restrict__ R, int epi,
+                                                                          int M, int N,
+                                                                          const uint16_t* __restrict__ G, float eps,
+                                                                          uint16_t* __restrict__ YN) {
   __shared__ float step_sum[NRM_CH];
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63, j = threadIdx.x >> 6;  // this wave's step
   const int n = blockIdx.x;
   const int nc = M >> 3, ep = epi & 3, nsteps = (nc + 63) >> 6;
-  uint4 h[NRM_CH / 4];
+  const int c = min(lane + 64 * j, nc - 1);
+  const size_t o = (size_t)n * M + 8 * (size_t)c;
+  float4 p[S][2];
 #pragma unroll
-  for (int t = 0; t < NRM_CH / 4; ++t) {
-    const int j = wave + 4 * t;
-    if (j >= nsteps) break;  // wave-uniform
-    const int c = min(lane + 64 * j, nc - 1);
-    const size_t o = (size_t)n * M + 8 * (size_t)c;
-    float4 p[S][2];
-#pragma unroll
-    for (int z = 0; z < S; ++z) {
-      const float4* q = reinterpret_cast<const float4*>(YP + (size_t)z * N * M + o);
-      p[z][0] = q[0];
-      p[z][1] = q[1];
-    }
-    const uint4 rv = ep ? *reinterpret_cast<const uint4*>(R + o) : make_uint4(0, 0, 0, 0);
-    const uint32_t rw[4] = {rv.x, rv.y, rv.z, rv.w};
-    uint32_t ow[4];
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      uint32_t h2[2];
-#pragma unroll
-      for (int u = 0; u < 2; ++u) {
-        const int e = 2 * q + u;  // element of the chunk, in the reduce kernel's order
-        float a = e < 4 ? (&p[0][0].x)[e] : (&p[0][1].x)[e - 4];
-#pragma unroll
-        for (int z = 1; z < S; ++z) a += e < 4 ? (&p[z][0].x)[e] : (&p[z][1].x)[e - 4];
-        const float y = Elem<DT>::load(Elem<DT>::store(a));
-        const float r = Elem<DT>::load(rw[q] >> (16 * u));
-        float v = y;
-        if (ep == 1) v = __fadd_rn(r, y);
-        else if (ep == 2) v = __fmul_rn(Elem<DT>::load(Elem<DT>::store(silu_rn(r))), y);
-        h2[u] = Elem<DT>::store(v);
-      }
-      ow[q] = h2[0] | (h2[1] << 16);
-    }
-    h[t] = make_uint4(ow[0], ow[1], ow[2], ow[3]);
-    if (lane + 64 * j < nc) *reinterpret_cast<uint4*>(Y + o) = h[t];
-    const float part = wave_sum_dpp(lane + 64 * j < nc ? sumsq8<DT>(h[t], 0.0f) : 0.0f);
-    if (lane == 0) step_sum[j] = part;
+  for (int z = 0; z < S; ++z) {
+    const float4* q = reinterpret_cast<const float4*>(YP + (size_t)z * N * M + o);
+    p[z][0] = q[0];
+    p[z][1] = q[1];
   }
+  const uint4 rv = ep ? *reinterpret_cast<const uint4*>(R + o) : make_uint4(0, 0, 0, 0);
+  const uint4 gv = *reinterpret_cast<const uint4*>(G + 8 * (size_t)c);
+  const uint32_t rw[4] = {rv.x, rv.y, rv.z, rv.w};
+  uint32_t ow[4];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    uint32_t h2[2];
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int e = 2 * q + u;  // element of the chunk, in the reduce kernel's order
+      float a = e < 4 ? (&p[0][0].x)[e] : (&p[0][1].x)[e - 4];
+#pragma unroll
+      for (int z = 1; z < S; ++z) a += e < 4 ? (&p[z][0].x)[e] : (&p[z][1].x)[e - 4];
+      const float y = Elem<DT>::load(Elem<DT>::store(a));
+      const float r = Elem<DT>::load(rw[q] >> (16 * u));
+      float v = y;
+      if (ep == 1) v = __fadd_rn(r, y);
+      else if (ep == 2) v = __fmul_rn(Elem<DT>::load(Elem<DT>::store(silu_rn(r))), y);
+      h2[u] = Elem<DT>::store(v);
+    }
+    ow[q] = h2[0] | (h2[1] << 16);
+  }
+  const uint4 h = make_uint4(ow[0], ow[1], ow[2], ow[3]);
+  const bool own = lane + 64 * j < nc;
+  if (own) *reinterpret_cast<uint4*>(Y + o) = h;
+  const float part = wave_sum_dpp(own ? sumsq8<DT>(h, 0.0f) : 0.0f);
+  if (lane == 0) step_sum[j] = part;
   __syncthreads();
   float ss = step_sum[0];
-  for (int j = 1; j < nsteps; ++j) ss = __fadd_rn(ss, step_sum[j]);
+  for (int k = 1; k < nsteps; ++k) ss = __fadd_rn(ss, step_sum[k]);
   const float rr = rsqrt_rn(__fadd_rn(__fdiv_rn(ss, (float)M), eps));
-#pragma unroll
-  for (int t = 0; t < NRM_CH / 4; ++t) {
-    const int j = wave + 4 * t;
-    if (j >= nsteps) break;
-    const int c = lane + 64 * j;
-    if (c < nc)
-      *reinterpret_cast<uint4*>(YN + (size_t)n * M + 8 * (size_t)c) =
-          norm8<DT>(h[t], *reinterpret_cast<const uint4*>(G + 8 * (size_t)c), rr);
-  }
+  if (own) *reinterpret_cast<uint4*>(YN + o) = norm8<DT>(h, gv, rr);
 }
 
 template <int DT, int BM, int BN, int WM, int WN, int PF>
@@ -747,9 +739,9 @@ extern "C" int ttsp_nf4_gemm_split_norm(const void* X, int x_dtype, const uint8_
   if (int rc = gemm_mfma(X, x_dtype, W, A8, AMAX, CODE2, offset, LUT, Y, R, epi, M, K, N, bs_shift, bs2_shift,
                          gemm_plan(M, K, N), work, stream, false))
     return rc;
-  const dim3 grid((unsigned)N);
+  const dim3 grid((unsigned)N), block((unsigned)(64 * ((M / 8 + 63) / 64)));
 #define TTSP_RN(DTV, SV)                                                                                      \
-  hipLaunchKernelGGL((nf4_gemm_reduce_norm_kernel<DTV, SV>), grid, dim3(256), 0, stream, work, (uint16_t*)Y, \
+  hipLaunchKernelGGL((nf4_gemm_reduce_norm_kernel<DTV, SV>), grid, block, 0, stream, work, (uint16_t*)Y, \
                      (const uint16_t*)R, epi, M, N, (const uint16_t*)G, eps, (uint16_t*)YN)
 #define TTSP_RS(DTV)                  \
   if (splits == 2) TTSP_RN(DTV, 2);   \
