@@ -165,6 +165,44 @@ def test_argmax_embed_equals_argmax_then_embed(dtype, n, vocab, D):
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("n", [1, 7, 8, 9, 4096, 4103, 32768, 40000])
+@pytest.mark.parametrize("offset", [0, 1, 3])
+def test_argmax_is_the_lowest_index_of_the_maximum(dtype, n, offset):
+    """ttsp_argmax against torch: the lowest index holding the maximum, with
+    ties inside one 8-value chunk and across chunks and threads, NaN entries
+    (never chosen), an all -inf row (index 0), lengths off the chunk size and
+    logits that do not start 16-byte aligned (offset values in)."""
+    from ttspipe_amd import _lib
+
+    lib, st = _lib.lib(), _lib.stream()
+    dt = _lib.dtype_code(dtype)
+    g = torch.Generator(device="cuda").manual_seed(n * 3 + offset)
+    for case in range(5):
+        base = torch.randn(n + offset, device="cuda", generator=g).to(dtype)
+        x = base[offset:]
+        if case == 1 and n > 1:  # ties: two in one chunk, one in another chunk, one in another thread's chunk
+            top = x.float().max().to(dtype)
+            for i in {n - 1, n // 2, min(n - 1, n // 2 + 1), min(n - 1, 8 * 1024 + 3)}:
+                x[i] = top
+        if case == 2:  # NaN entries, one of them first
+            x[0] = float("nan")
+            x[n // 3] = float("nan")
+        if case == 3:
+            x.fill_(-float("inf"))
+        if case == 4 and n > 8:  # the maximum in the tail past the last whole chunk
+            x[n - 1] = 100.0
+        out = torch.full((1,), -5, dtype=torch.int32, device="cuda")
+        _lib.check(lib.ttsp_argmax(x.data_ptr(), n, dt, out.data_ptr(), st), "argmax")
+        xf = x.float()
+        finite = xf[~xf.isnan()]
+        if case == 3 or finite.numel() == 0 or finite.max() == -float("inf"):
+            want = 0  # nothing beats -inf
+        else:
+            want = int((xf == finite.max()).nonzero()[0])
+        assert int(out[0]) == want, (case, int(out[0]), want)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("ntok,rows,vocab,D,pad", [(11, 512, 4096, 2560, 0), (5, 37, 512, 512, 3),
                                                    (3, 9, 64, 1000, 0), (1, 4, 16, 8, 1)])
 def test_embed_sum_rows_equals_the_one_position_sum(dtype, ntok, rows, vocab, D, pad):

@@ -91,16 +91,43 @@ __global__ __launch_bounds__(256) void embed_sum_rows_kernel(const uint16_t* __r
 
 // Index of the largest of X[0..n), the lowest index on ties (NaN never wins;
 // 0 when nothing beats -inf), valid in thread 0 after the call. One workgroup.
+// A thread scans 8-element chunks (16-byte loads when X is 16-byte aligned),
+// four chunks' loads issued before the first compare, in rising index order.
 template <int DT>
 __device__ __forceinline__ int block_argmax(const uint16_t* __restrict__ X, int n) {
   __shared__ float bv[16];
   __shared__ int bi[16];
-  const int tid = threadIdx.x;
+  const int tid = threadIdx.x, nthr = blockDim.x;
   float best = -__builtin_inff();
   int idx = 0x7fffffff;
-  for (int i = tid; i < n; i += blockDim.x) {
-    const float v = Elem<DT>::load(X[i]);
-    if (v > best) { best = v; idx = i; }
+  if ((reinterpret_cast<uintptr_t>(X) & 15) == 0) {
+    const int nch = n >> 3;  // whole chunks; the tail below
+    constexpr int U = 4;
+    for (int c0 = tid; c0 < nch; c0 += U * nthr) {
+      uint4 v[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) v[u] = *reinterpret_cast<const uint4*>(X + 8 * (size_t)min(c0 + u * nthr, nch - 1));
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int c = c0 + u * nthr;
+        if (c >= nch) break;
+        const uint32_t w[4] = {v[u].x, v[u].y, v[u].z, v[u].w};
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const float x = Elem<DT>::load((uint16_t)(w[e >> 1] >> (16 * (e & 1))));
+          if (x > best) { best = x; idx = 8 * c + e; }
+        }
+      }
+    }
+    for (int i = 8 * nch + tid; i < n; i += nthr) {
+      const float x = Elem<DT>::load(X[i]);
+      if (x > best) { best = x; idx = i; }
+    }
+  } else {
+    for (int i = tid; i < n; i += nthr) {
+      const float x = Elem<DT>::load(X[i]);
+      if (x > best) { best = x; idx = i; }
+    }
   }
   for (int off = 32; off >= 1; off >>= 1) {
     const float ov = __shfl_xor(best, off, 64);
