@@ -9,25 +9,9 @@
 
 namespace ttsp {
 
-// out[d] = round(sum_{c < ntok} E[(c * vocab + tok[c]) * D + d]), fp32 sum in
-// codebook order. ntok == 1 is a plain row gather.
-template <int DT>
-__global__ __launch_bounds__(256) void embed_sum_kernel(const uint16_t* __restrict__ E,
-                                                       const int* __restrict__ tok, int ntok,
-                                                       int vocab, int D, uint16_t* __restrict__ out) {
-  const int d = blockIdx.x * blockDim.x + threadIdx.x;
-  if (d >= D) return;
-  float acc = 0.0f;
-  for (int c = 0; c < ntok; ++c) {
-    int t = tok[c];
-    t = t < 0 ? 0 : (t >= vocab ? vocab - 1 : t);
-    acc = __fadd_rn(acc, Elem<DT>::load(E[((size_t)c * vocab + t) * D + d]));
-  }
-  out[d] = Elem<DT>::store(acc);
-}
-
-// embed_sum_kernel for several rows: row r sums tables c < ntok at token
-// tok[c * tok_stride + r], the same fp32 adds in codebook order. V = 8: a
+// out[r][d] = round(sum_{c < ntok} E[(c * vocab + t) * D + d]) with t =
+// tok[c * tok_stride + r] clamped into [0, vocab): each row's fp32 sum in
+// codebook order (one row: a decode step's embedding sum). V = 8: a
 // thread per 8 consecutive values (16-byte loads; D % 8 == 0 and E, out
 // 16-byte aligned), V = 1: a thread per value. Up to EMB_ROWS_T tables the
 // token loads, then the table loads, are all issued before the first add.
@@ -231,21 +215,6 @@ __global__ __launch_bounds__(256) void synth_fill_kernel(void* __restrict__ out,
 
 using namespace ttsp;
 
-extern "C" int ttsp_embed_sum(const void* E, const int* tok, int ntok, int vocab, int D, void* out,
-                              int dtype, hipStream_t stream) {
-  if (ntok <= 0 || vocab <= 0 || D <= 0) return (int)hipErrorInvalidValue;
-  const dim3 grid((D + 255) / 256);
-  if (dtype == DT_F16)
-    hipLaunchKernelGGL(embed_sum_kernel<DT_F16>, grid, dim3(256), 0, stream, (const uint16_t*)E, tok,
-                       ntok, vocab, D, (uint16_t*)out);
-  else if (dtype == DT_BF16)
-    hipLaunchKernelGGL(embed_sum_kernel<DT_BF16>, grid, dim3(256), 0, stream, (const uint16_t*)E, tok,
-                       ntok, vocab, D, (uint16_t*)out);
-  else
-    return (int)hipErrorInvalidValue;
-  TTSP_RETURN_LAUNCH();
-}
-
 extern "C" int ttsp_embed_sum_rows(const void* E, const int* tok, long long tok_stride, int ntok, int rows,
                                    int vocab, int D, void* out, int dtype, hipStream_t stream) {
   if (ntok <= 0 || rows <= 0 || vocab <= 0 || D <= 0 || tok_stride < rows || !E || !tok || !out)
@@ -268,6 +237,13 @@ extern "C" int ttsp_embed_sum_rows(const void* E, const int* tok, long long tok_
   }
 #undef TTSP_ER
   TTSP_RETURN_LAUNCH();
+}
+
+// one position: the rows kernel with one row (every token load, then every
+// table load, issued before the first add)
+extern "C" int ttsp_embed_sum(const void* E, const int* tok, int ntok, int vocab, int D, void* out,
+                              int dtype, hipStream_t stream) {
+  return ttsp_embed_sum_rows(E, tok, 1, ntok, 1, vocab, D, out, dtype, stream);
 }
 
 extern "C" int ttsp_argmax_embed(const void* X, int n, int dtype, int* tok, int* tok2, const void* E, int vocab,
