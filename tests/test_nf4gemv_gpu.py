@@ -643,12 +643,16 @@ def test_swiglu_gemm_declines_what_one_launch_does_not_serve(nf4, shape, rows, b
     ((2560, 9728), 64, 4, 1, False, torch.float16),
     ((1024, 4096), 128, 8, 0, True, torch.float16),
     ((1536, 1024), 300, 2, 2, True, torch.bfloat16),
-    ((512, 1024), 64, 2, 1, True, torch.bfloat16)])
+    ((512, 1024), 64, 2, 1, True, torch.bfloat16),
+    ((4096, 4096), 128, 4, 1, True, torch.bfloat16),  # eight waves a row, the largest M served
+    ((520, 2048), 128, 4, 1, True, torch.float16),    # a last step of one 8-value chunk
+    ((4088, 2048), 64, 4, 0, False, torch.bfloat16)])
 def test_split_gemm_with_the_next_norm_equals_the_two_launches(nf4, shape, rows, splits, epi, nested, dtype):
     """`matmul_norm` (the split-K reduce, its epilogue and the RMSNorm of each
     output row in one launch) against `matmul` then `fusedops.rms_norm`, bit
     for bit: 2, 4 and 8 splits, every epilogue, fp16 and bf16, plain and
-    nested scales, a row count that is not a multiple of four."""
+    nested scales, a row count that is not a multiple of four, rows of one
+    to eight 512-column steps (a wave each) and a ragged last step."""
     from ttspipe_amd import _lib, fusedops
 
     M, K = shape
