@@ -197,10 +197,12 @@ def test_fp64_block_reference_catches_planted_mistakes(qk_norm):
         assert rel_norm(_ref(c, qk_norm, m)[0], ref) > 2 * REF_BAR, m
 
 
-def _block_against_fp64(dtype, qk_norm, **shape):
+def _block_against_fp64(dtype, qk_norm, causal=False, **shape):
     """The fused prefill block of `_ref_inputs(dtype, qk_norm, **shape)`'s
     shape on the GPU against the fp64 block: (rel-norm of the output, K-row
-    and V-row error in ulps of each head row's largest element)."""
+    and V-row error in ulps of each head row's largest element). `causal`:
+    through `prefill_block_chain(..., causal=True)`, the attention computing
+    the causal mask from the positions."""
     from tests.refblock import rel_norm
     from tests.test_fused_gpu import _block
     from ttspipe_amd import fusedlayer, fusedops, nf4gemv
@@ -221,7 +223,13 @@ def _block_against_fp64(dtype, qk_norm, **shape):
     mask = torch.tril(torch.ones(length, length, dtype=torch.bool, device="cuda"))[None, None, pos]
     before = fusedlayer.stats()["prefill"]
     with torch.inference_mode():
-        ours = block(dev(c["xb"], (1, rows, D)), c["freqs"].cuda(), mask, pos)
+        if causal:
+            r = fusedlayer.prefill_block_chain(block, dev(c["xb"], (1, rows, D)), c["freqs"].cuda(), mask, pos,
+                                               causal=True)
+            assert r is not None
+            ours = r[0]
+        else:
+            ours = block(dev(c["xb"], (1, rows, D)), c["freqs"].cuda(), mask, pos)
     assert fusedlayer.stats()["prefill"] == before + 1
     ref, k_ref, v_ref = _ref(c, qk_norm)
     got = ours.double().cpu().numpy().reshape(rows, D)
@@ -271,6 +279,58 @@ def test_random_block_shapes_match_an_fp64_block(case):
     where = f"{shape} {dtype} qk_norm={qk_norm}: rel {rel:.2e}, K {k_ulps:.1f} ulp, V {v_ulps:.1f} ulp"
     assert rel < REF_BAR, where
     assert k_ulps <= 1.0 and v_ulps <= 1.0, where
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_causal_512_row_block_matches_an_fp64_block(dtype):
+    """A 512-row first span with 32 query / 8 kv heads through the causal
+    chain, whose attention then takes two-head workgroups with four key
+    splits each: the same bars against the fp64 block."""
+    from ttspipe_amd import fastpath
+
+    before = fastpath.stats()["prefill_attn"]
+    rel, k_ulps, v_ulps = _block_against_fp64(dtype, True, causal=True, nh=32, nkv=8, D=1024, inter=1024, start=0,
+                                              rows=512, length=512, seed=71)
+    assert fastpath.stats()["prefill_attn"] == before + 1
+    print(f"causal 512-row block vs fp64 block: rel {rel:.2e}, K rows {k_ulps:.1f} ulp, V rows {v_ulps:.1f} ulp")
+    assert rel < REF_BAR
+    assert k_ulps <= 1.0 and v_ulps <= 1.0
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("rows,start,nh,nkv", [(100, 37, 32, 8), (64, 200, 8, 2), (20, 0, 6, 3)])
+def test_causal_chain_equals_the_masked_chain(rows, start, nh, nkv):
+    """`prefill_block_chain(..., causal=True)` (the mask computed from the
+    positions) against the same chain reading the causal mask's bytes: the
+    block output, its carried norm and the new K/V rows bit for bit (shapes
+    on the two-split attention form)."""
+    from tests.test_fused_gpu import _block
+    from ttspipe_amd import fusedlayer, fusedops, nf4gemv
+
+    assert nf4gemv.install() and fusedops.install() and fusedlayer.install()
+    dtype, D, length = torch.bfloat16, 512, 512
+    block, _ = _block(dtype, True, dim=D, n_head=nh, n_local_heads=nkv, inter=1024, max_len=length, seed=rows)
+    kv = block.attention.kv_cache
+    g = torch.Generator().manual_seed(start)
+    kv.k_cache.copy_(torch.randn(kv.k_cache.shape, generator=g).to(dtype))
+    kv.v_cache.copy_(torch.randn(kv.v_cache.shape, generator=g).to(dtype))
+    x = torch.randn(1, rows, D, generator=g).to(dtype).cuda()
+    pos = torch.arange(start, start + rows, device="cuda")
+    from ttspipe_amd.llama import precompute_freqs_cis
+
+    freqs = precompute_freqs_cis(length, 128, 10000.0, dtype=dtype).cuda()[pos].contiguous()
+    mask = torch.tril(torch.ones(length, length, dtype=torch.bool, device="cuda"))[None, None, pos]
+    outs = []
+    with torch.inference_mode():
+        for causal in (False, True):
+            r = fusedlayer.prefill_block_chain(block, x, freqs, mask, pos, next_norm=block.ffn_norm, causal=causal)
+            assert r is not None
+            k_rows = kv.k_cache[0, :, start : start + rows].clone()
+            v_rows = kv.v_cache[0, :, start : start + rows].clone()
+            outs.append([t.clone() for t in r] + [k_rows, v_rows])
+    for a, b in zip(*outs):
+        assert torch.equal(a.view(torch.int16), b.view(torch.int16))
 
 
 @pytest.mark.gpu
