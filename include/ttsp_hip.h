@@ -156,6 +156,18 @@ int ttsp_nf4_gemv_fused(const void* X, int x_dtype, const void* NORM_W, float ep
                         const void* R, int epi, int M, int K, int blocksize, int blocksize2,
                         void* stream);
 
+/* ttsp_nf4_gemv_fused's one-weight form for N = 1 or 2 activation rows (X
+ * [N][K], R and Y [N][M]): each row normalised with NORM_W (if given) as
+ * ttsp_rms_norm does, every weight byte's codes looked up once for both rows,
+ * each row's result bit for bit its own one-row launch. Replaces: the
+ * rms_norm -> matmul pairs of the unfused block the reference runs for a
+ * short prompt span (app/engine/fastpath.py:207-271 with
+ * app/engine/nf4gemv.py:459-477). */
+int ttsp_nf4_gemv_fused_rows(const void* X, int x_dtype, const void* NORM_W, float eps, const uint8_t* W,
+                             const uint8_t* A8, const float* AMAX, const float* CODE2, float offset,
+                             const float* LUT, void* Y, const void* R, int epi, int M, int K, int N,
+                             int blocksize, int blocksize2, void* stream);
+
 /* out[k] = round(LUT[q_k] * s_{k / blocksize}) for the n flattened codes, one
  * rounding, out_dtype TTSP_F16/BF16/F32. Replaces: the dequantisation inside
  * nf4_mma (app/engine/nf4gemv.py:154-188) and bitsandbytes' dequantize_4bit

@@ -518,6 +518,41 @@ def test_norm_folded_into_the_matmul_is_bit_exact(nf4, orc, shape, nested, dtype
     assert np.array_equal(bits(y), expect), f"M={M} K={K}: {first_mismatch(bits(y), expect)}"
 
 
+@pytest.mark.parametrize("shape", FUSED_SHAPES)
+@pytest.mark.parametrize("nested", [True, False])
+@pytest.mark.parametrize("epi", [0, 1, 2])
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_norm_folded_into_two_rows_is_bit_exact(nf4, orc, shape, nested, epi, dtype):
+    """Two rows through `matmul_fused` with the norm folded in (one launch,
+    each weight byte looked up once for both rows): each row bit for bit the
+    oracle's norm then GEMV (and its epilogue), and the two one-row launches."""
+    M, K = shape
+    if K > nf4.NORM_MAX_K:
+        return
+    layer = random_layer(M, K, nested, seed=M + 5 * K + epi)
+    lin = to_linear(layer, dtype)
+    assert nf4.prepare(lin)
+    dt = dt_code(dtype)
+    xb = [randn_bits(K, dtype, seed=K + 11 + r, scale=2.0 + r) for r in range(2)]
+    rb = [randn_bits(M, dtype, seed=M + 21 + r) for r in range(2)]
+    gb = o.from_f32((np.random.default_rng(K + 3).random(K) * 0.5 + 0.75).astype(np.float32), dt)
+    g = from_bits(gb, dtype)
+    x2 = from_bits(np.concatenate(xb), dtype).view(1, 2, K)
+    r2 = from_bits(np.concatenate(rb), dtype).view(1, 2, M) if epi else None
+    y = nf4.matmul_fused(lin, x2, norm_weight=g, eps=1e-6, epi=epi, operand=r2)
+    assert y is not None and y.shape == (1, 2, M)
+    J, KS, _ = gemv_shape(M, K)
+    for r in range(2):
+        xn = orc.rms_norm_emul(xb[r], gb, 1, K, 1e-6, dt)
+        kw = dict(R=rb[r], epi=epi) if epi else {}
+        expect = orc.gemv_emul(xn, dt, **oracle_args(layer), M=M, K=K, bs=64, KS=KS, J=J, bs2=layer["bs2"] or 256,
+                               **kw)
+        assert np.array_equal(bits(y[0, r]), expect), f"row {r} M={M} K={K}: {first_mismatch(bits(y[0, r]), expect)}"
+        one = nf4.matmul_fused(lin, x2[:, r : r + 1].contiguous(), norm_weight=g, eps=1e-6, epi=epi,
+                               operand=None if r2 is None else r2[:, r : r + 1].contiguous())
+        assert np.array_equal(bits(one), bits(y[0, r]))
+
+
 @pytest.mark.parametrize("shape", [(9728, 2560), (3072, 1024), (1000, 2560), (64, 128)])
 @pytest.mark.parametrize("norm", [True, False])
 @pytest.mark.parametrize("dtype", DTYPES)
@@ -562,7 +597,9 @@ def test_fused_form_declines_what_it_cannot_serve(nf4):
     assert nf4.prepare(a) and nf4.prepare(b)
     x = torch.randn(1, 2560, device="cuda", dtype=torch.bfloat16)
     assert nf4.matmul_fused(a, x, module3=b) is None  # shapes differ
-    assert nf4.matmul_fused(a, torch.randn(2, 2560, device="cuda", dtype=torch.bfloat16)) is None  # two rows
+    assert nf4.matmul_fused(a, torch.randn(3, 2560, device="cuda", dtype=torch.bfloat16)) is None  # three rows
+    two = torch.randn(2, 2560, device="cuda", dtype=torch.bfloat16)
+    assert nf4.matmul_fused(a, two, module3=a) is None  # the SwiGLU pair takes one row
     assert nf4.matmul_fused(a, x, norm_weight=torch.ones(2560, device="cuda", dtype=torch.float16)) is None
 
 

@@ -334,6 +334,47 @@ def test_causal_chain_equals_the_masked_chain(rows, start, nh, nkv):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("causal", [True, False])
+def test_two_row_chain_with_folded_norms_equals_the_norm_launches(monkeypatch, causal):
+    """Two blocks chained over a 2-row span: with the RMSNorms folded into the
+    wqkv and w1 / w3 GEMVs (no norm launch) against the same chain running
+    them as launches (the carried norm, then w1 and w3 on it): both blocks'
+    outputs and the new K/V rows bit for bit."""
+    from tests.test_fused_gpu import _block
+    from ttspipe_amd import fusedlayer, fusedops, nf4gemv
+    from ttspipe_amd.llama import precompute_freqs_cis
+
+    assert nf4gemv.install() and fusedops.install() and fusedlayer.install()
+    dtype, D, length, start, rows = torch.bfloat16, 512, 256, 30, 2
+    block, _ = _block(dtype, True, dim=D, n_head=8, n_local_heads=2, inter=1024, max_len=length, seed=5)
+    kv = block.attention.kv_cache
+    g = torch.Generator().manual_seed(6)
+    kc0 = torch.randn(kv.k_cache.shape, generator=g).to(dtype).cuda()
+    vc0 = torch.randn(kv.v_cache.shape, generator=g).to(dtype).cuda()
+    x = torch.randn(1, rows, D, generator=g).to(dtype).cuda()
+    pos = torch.arange(start, start + rows, device="cuda")
+    freqs = precompute_freqs_cis(length, 128, 10000.0, dtype=dtype).cuda()[pos].contiguous()
+    mask = torch.tril(torch.ones(length, length, dtype=torch.bool, device="cuda"))[None, None, pos]
+    outs = []
+    for fold in (False, True):
+        monkeypatch.setattr(nf4gemv, "FUSED_MAX_ROWS", 2 if fold else 1)
+        kv.k_cache.copy_(kc0)
+        kv.v_cache.copy_(vc0)
+        calls = nf4gemv.stats()["fast"]
+        with torch.inference_mode():
+            o1, n1 = fusedlayer.prefill_block_chain(block, x, freqs, mask, pos, next_norm=block.attention_norm,
+                                                    causal=causal)
+            assert (n1 is None) == fold
+            o2, _ = fusedlayer.prefill_block_chain(block, o1, freqs, mask, pos, xn=n1, causal=causal)
+        if fold:
+            assert nf4gemv.stats()["fast"] >= calls + 6  # wqkv, w1, w3 of each block through the fused GEMV
+        outs.append([o1.clone(), o2.clone(), kv.k_cache[0, :, start : start + rows].clone(),
+                     kv.v_cache[0, :, start : start + rows].clone()])
+    for a, b in zip(*outs):
+        assert torch.equal(a.view(torch.int16), b.view(torch.int16))
+
+
+@pytest.mark.gpu
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 def test_rows_kernel_equals_the_one_position_kernel(dtype):
     """ttsp_qk_rope_kv_rows over a run of positions (in any order, one out of

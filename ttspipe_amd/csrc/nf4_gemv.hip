@@ -102,7 +102,7 @@ struct GemvParams {
 
 
 
-// Dynamic LDS after the static table: code2 [NM][256], norm partials [8],
+// Dynamic LDS after the static table: code2 [NM][256], norm partials [NR][8],
 // K-slice partials [8][NM*NR*RPW], the resolved scales [8 waves][NM][RPW][8 J]
 // (16-byte aligned), then x as staged [NR][K/8].
 // The leading scalar arguments are what the first loads need (weight 0's
@@ -127,8 +127,8 @@ __global__ __launch_bounds__(GEMV_THREADS) void nf4_gemv_kernel(
   __shared__ __align__(16) uint32_t lut_rep[256 * LUT_REP];
   extern __shared__ __align__(16) unsigned char lds_dyn[];
   float* code2_s = reinterpret_cast<float*>(lds_dyn);  // [NM][256]
-  float* wpart = code2_s + NM * 256;                   // [NW] norm partial sums
-  float* red = wpart + NW;                             // [NW][NM*NR*RPW]
+  float* wpart = code2_s + NM * 256;                   // [NR][NW] norm partial sums
+  float* red = wpart + NR * NW;                        // [NW][NM*NR*RPW]
   float* srow = red + NW * NM * NR * RPW;              // [NW][NM][RPW][8 J] scale slots
 
   const int tid = threadIdx.x;
@@ -183,7 +183,7 @@ __global__ __launch_bounds__(GEMV_THREADS) void nf4_gemv_kernel(
   // x (and the norm weight): staged once per workgroup, chunk c = tid + 512 i
   // of each activation row by thread tid (one chunk per thread unless
   // K > 4096, where there is no norm); rows past N repeat row N - 1 (the rows
-  // form: NR > 1, one weight, no norm)
+  // form: NR > 1, one weight, a norm of each row if any)
   const int XN = uniform((KD + nthr - 1) / nthr);
   uint4 xc[XC_MAX][NR];
   // (chunks past XN stay unset and unread: a zero-initialised chunk would make
@@ -376,19 +376,26 @@ __global__ __launch_bounds__(GEMV_THREADS) void nf4_gemv_kernel(
           xs[n * KD + c] = *reinterpret_cast<const uint4*>(X + (n == 0 ? 0 : (size_t)min(n, p.N - 1) * K) + 8 * (size_t)c);
       }
     }
-  } else {
-    float sq = 0.0f;
-    if (tid < KD) sq = dt == DT_BF16 ? sumsq8<DT_BF16>(xc[0][0], 0.0f) : sumsq8<DT_F16>(xc[0][0], 0.0f);
-    sq = wave_sum_dpp(sq);
-    if (lane == 0) wpart[wave] = sq;
+  } else {  // each activation row's sum of squares, wave w taking its chunks 64 w .. 64 w + 63
+#pragma unroll
+    for (int n = 0; n < NR; ++n) {
+      float sq = 0.0f;
+      if (tid < KD) sq = dt == DT_BF16 ? sumsq8<DT_BF16>(xc[0][n], 0.0f) : sumsq8<DT_F16>(xc[0][n], 0.0f);
+      sq = wave_sum_dpp(sq);
+      if (lane == 0) wpart[n * NW + wave] = sq;
+    }
   }
   __syncthreads();
-  if (norm) {  // the 64-chunk partial sums left to right, then each thread's chunk
-    float ss = wpart[0];
+  if (norm) {  // per row: the 64-chunk partial sums left to right, then each thread's chunk
 #pragma unroll
-    for (int w2 = 1; w2 < NW; ++w2) ss = __fadd_rn(ss, wpart[w2]);
-    const float r = rsqrt_rn(__fadd_rn(__fdiv_rn(ss, (float)K), p.eps));
-    if (tid < KD) xs[tid] = dt == DT_BF16 ? norm8<DT_BF16>(xc[0][0], gc, r) : norm8<DT_F16>(xc[0][0], gc, r);
+    for (int n = 0; n < NR; ++n) {
+      float ss = wpart[n * NW];
+#pragma unroll
+      for (int w2 = 1; w2 < NW; ++w2) ss = __fadd_rn(ss, wpart[n * NW + w2]);
+      const float r = rsqrt_rn(__fadd_rn(__fdiv_rn(ss, (float)K), p.eps));
+      if (tid < KD)
+        xs[n * KD + tid] = dt == DT_BF16 ? norm8<DT_BF16>(xc[0][n], gc, r) : norm8<DT_F16>(xc[0][n], gc, r);
+    }
     __syncthreads();
   }
 
@@ -533,7 +540,8 @@ static constexpr size_t kLdsPerCU = 160 * 1024;  // a workgroup's LDS must fit
 // Dynamic LDS of one workgroup (the table is static); nr activation rows.
 static size_t gemv_dyn_lds(const GemvShape& g, int nm, int K, int bs_shift, int nr = 1) {
   const size_t sc = (size_t)GEMV_WAVES * nm * g.RPW * 8 * g.J;  // scale slots
-  return 4 * (256 * (size_t)nm + GEMV_WAVES + (size_t)GEMV_WAVES * nm * nr * g.RPW + sc) + 2 * (size_t)K * nr;
+  return 4 * (256 * (size_t)nm + (size_t)GEMV_WAVES * nr + (size_t)GEMV_WAVES * nm * nr * g.RPW + sc) +
+         2 * (size_t)K * nr;
 }
 
 // K is split (KS a power of two) so that a lane's chunks J <= 8 leave the
@@ -648,7 +656,7 @@ static int gemv_launch(const void* X, int dt, const void* G, float eps, const Nf
   if (dt != DT_F16 && dt != DT_BF16) return (int)hipErrorInvalidValue;
   if (epi < 0 || epi > 2 || (epi && !R) || (mat3 && epi)) return (int)hipErrorInvalidValue;
   const int nm = mat3 ? 2 : 1;
-  if (N < 1 || N > GEMV_MAX_ROWS || (N > 1 && (G || mat3 || att))) return (int)hipErrorInvalidValue;
+  if (N < 1 || N > GEMV_MAX_ROWS || (N > 1 && (mat3 || att))) return (int)hipErrorInvalidValue;
   const int nr = N;
   const GemvShape g = gemv_shape(M, K, nm, bs_shift, nr);
   if (!g.J) return (int)hipErrorInvalidValue;
@@ -753,6 +761,19 @@ extern "C" int ttsp_nf4_gemv_fused(const void* X, int x_dtype, const void* NORM_
   const Nf4Mat m3{reinterpret_cast<const uint32_t*>(W3), A8_3, AMAX_3, CODE2_3, offset_3};
   return gemv_launch(X, x_dtype, NORM_W, eps, m1, &m3, nested, LUT, Y, R, epi, M, K, blocksize, blocksize2,
                      stream);
+}
+
+extern "C" int ttsp_nf4_gemv_fused_rows(const void* X, int x_dtype, const void* NORM_W, float eps, const uint8_t* W,
+                                        const uint8_t* A8, const float* AMAX, const float* CODE2, float offset,
+                                        const float* LUT, void* Y, const void* R, int epi, int M, int K, int N,
+                                        int blocksize, int blocksize2, hipStream_t stream) {
+  if (!X || !W || !AMAX || !LUT || !Y || M <= 0 || K <= 0 || N < 1 || N > GEMV_MAX_ROWS)
+    return (int)hipErrorInvalidValue;
+  const bool nested = A8 != nullptr;
+  if (nested && !CODE2) return (int)hipErrorInvalidValue;
+  const Nf4Mat m{reinterpret_cast<const uint32_t*>(W), A8, AMAX, CODE2, offset};
+  return gemv_launch(X, x_dtype, NORM_W, eps, m, nullptr, nested, LUT, Y, R, epi, M, K, blocksize, blocksize2,
+                     stream, nullptr, N);
 }
 
 extern "C" int ttsp_attn_nf4_gemv(const void* QKV, const void* QW, const void* KW, float eps, const void* F,

@@ -247,7 +247,9 @@ def prefill_block(block, x, freqs_cis, mask, input_pos):
 def prefill_block_chain(block, x, freqs_cis, mask, input_pos, *, xn=None, next_norm=None, causal=False):
     """`(out, out_n)`: the block's output for several positions (B = 1, S > 1)
     and, with `next_norm` (an RMSNorm module), `next_norm(out)` for the next
-    block (else None); None when the block declines.
+    block (else None, and None for a span of up to `nf4gemv.FUSED_MAX_ROWS`
+    rows, whose next block folds that norm into its wqkv GEMV); None when the
+    block declines.
     `xn`, if given, is this block's `attention_norm(x)` (a previous call's
     `out_n`), whose launch is then skipped; where the split-K reduce of wo and
     w2 serves the shape it writes the following RMSNorm too
@@ -280,10 +282,16 @@ def prefill_block_chain(block, x, freqs_cis, mask, input_pos, *, xn=None, next_n
     bsz, n, _ = x.shape
     nh, nkv, hd = a.n_head, a.n_local_heads, a.head_dim
     an, fn = block.attention_norm, block.ffn_norm
-    if xn is None:
+    # a span of up to FUSED_MAX_ROWS rows takes the GEMV with each row's
+    # RMSNorm folded in, as the decode step does: no norm launch runs
+    fold = n <= nf4gemv.FUSED_MAX_ROWS
+    qkv = None
+    if xn is None and fold:
+        qkv = nf4gemv.matmul_fused(a.wqkv, x, norm_weight=an.weight, eps=an.eps)
+    if qkv is None and xn is None:
         xn = fusedops.rms_norm(x, an.weight, an.eps)
-    if xn is None:
-        return None
+        if xn is None:
+            return None
     kc, vc = a.kv_cache.k_cache, a.kv_cache.v_cache
     max_len = kc.shape[2]
     ftype = _lib.dtype_code(freqs_cis.dtype)
@@ -293,10 +301,9 @@ def prefill_block_chain(block, x, freqs_cis, mask, input_pos, *, xn=None, next_n
     # a K-split wqkv hands its fp32 partial sums straight to the head-norm /
     # rotary / KV kernel, which adds them as the split's own reduce would
     part = None
-    if rows_ok and a.wqkv._nf4_fast["M"] == (nh + 2 * nkv) * hd:
+    if qkv is None and rows_ok and a.wqkv._nf4_fast["M"] == (nh + 2 * nkv) * hd:
         part = nf4gemv.matmul_partials(a.wqkv, xn)
-    qkv = None
-    if part is None:
+    if part is None and qkv is None:
         qkv = nf4gemv.matmul(a.wqkv, xn)
         if qkv is None:
             return None
@@ -350,9 +357,18 @@ def prefill_block_chain(block, x, freqs_cis, mask, input_pos, *, xn=None, next_n
         h, hn = hh
     else:
         h = nf4gemv.matmul(a.wo, y, epi=nf4gemv.EPI_RESIDUAL, operand=x)
-        hn = None if h is None else fusedops.rms_norm(h, fn.weight, fn.eps)
+        hn = None
+    u = None
+    if hh is None and fold and h is not None:  # w1 and w3 each with the FFN norm folded in
+        g = nf4gemv.matmul_fused(ff.w1, h, norm_weight=fn.weight, eps=fn.eps)
+        if g is not None:
+            u = nf4gemv.matmul_fused(ff.w3, h, norm_weight=fn.weight, eps=fn.eps, epi=nf4gemv.EPI_SILU_GATE,
+                                     operand=g)
+    if u is None and hn is None and h is not None:
+        hn = fusedops.rms_norm(h, fn.weight, fn.eps)
     # w1 and w3 with the SwiGLU gate in one launch where it serves the shape, else two
-    u = None if hn is None else nf4gemv.matmul_swiglu(ff.w1, ff.w3, hn)
+    if u is None and hn is not None:
+        u = nf4gemv.matmul_swiglu(ff.w1, ff.w3, hn)
     if u is None and hn is not None:
         g = nf4gemv.matmul(ff.w1, hn)
         u = None if g is None else nf4gemv.matmul(ff.w3, hn, epi=nf4gemv.EPI_SILU_GATE, operand=g)
@@ -364,7 +380,7 @@ def prefill_block_chain(block, x, freqs_cis, mask, input_pos, *, xn=None, next_n
     else:
         out = None if u is None else nf4gemv.matmul(ff.w2, u, epi=nf4gemv.EPI_RESIDUAL, operand=h)
         out_n = None
-        if out is not None and next_norm is not None:
+        if out is not None and next_norm is not None and not fold:  # (a short span's next block folds it)
             out_n = fusedops.rms_norm(out, next_norm.weight, next_norm.eps)
     if out is None:
         raise RuntimeError("prefill_block: a GEMM declined after the KV cache was written")
