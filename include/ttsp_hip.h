@@ -156,17 +156,20 @@ int ttsp_nf4_gemv_fused(const void* X, int x_dtype, const void* NORM_W, float ep
                         const void* R, int epi, int M, int K, int blocksize, int blocksize2,
                         void* stream);
 
-/* ttsp_nf4_gemv_fused's one-weight form for N = 1 or 2 activation rows (X
- * [N][K], R and Y [N][M]): each row normalised with NORM_W (if given) as
- * ttsp_rms_norm does, every weight byte's codes looked up once for both rows,
- * each row's result bit for bit its own one-row launch. Replaces: the
- * rms_norm -> matmul pairs of the unfused block the reference runs for a
- * short prompt span (app/engine/fastpath.py:207-271 with
+/* ttsp_nf4_gemv_fused for N = 1 or 2 activation rows (X [N][K], R and Y
+ * [N][M]): each row normalised with NORM_W (if given) as ttsp_rms_norm does,
+ * with one weight or the SwiGLU pair (W3 != NULL, epi 0), every weight
+ * byte's codes looked up once for both rows, each row's result bit for bit
+ * its own one-row launch. Replaces: the rms_norm -> matmul and w1 -> w3
+ * (silu gate) launches of the unfused block the reference runs for a short
+ * prompt span (app/engine/fastpath.py:207-271 with
  * app/engine/nf4gemv.py:459-477). */
-int ttsp_nf4_gemv_fused_rows(const void* X, int x_dtype, const void* NORM_W, float eps, const uint8_t* W,
-                             const uint8_t* A8, const float* AMAX, const float* CODE2, float offset,
-                             const float* LUT, void* Y, const void* R, int epi, int M, int K, int N,
-                             int blocksize, int blocksize2, void* stream);
+int ttsp_nf4_gemv_fused_rows(const void* X, int x_dtype, const void* NORM_W, float eps, const uint8_t* W1,
+                             const uint8_t* A8_1, const float* AMAX_1, const float* CODE2_1, float offset_1,
+                             const uint8_t* W3, const uint8_t* A8_3, const float* AMAX_3,
+                             const float* CODE2_3, float offset_3, const float* LUT, void* Y,
+                             const void* R, int epi, int M, int K, int N, int blocksize, int blocksize2,
+                             void* stream);
 
 /* out[k] = round(LUT[q_k] * s_{k / blocksize}) for the n flattened codes, one
  * rounding, out_dtype TTSP_F16/BF16/F32. Replaces: the dequantisation inside

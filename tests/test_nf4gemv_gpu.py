@@ -574,6 +574,36 @@ def test_swiglu_pair_in_one_launch_is_bit_exact(nf4, orc, shape, norm, dtype):
     assert np.array_equal(bits(y), expect), f"M={M} K={K}: {first_mismatch(bits(y), expect)}"
 
 
+@pytest.mark.parametrize("shape", [(9728, 2560), (3072, 1024), (1000, 2560), (64, 128)])
+@pytest.mark.parametrize("norm", [True, False])
+@pytest.mark.parametrize("nested", [True, False])
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_swiglu_pair_over_two_rows_is_bit_exact(nf4, orc, shape, norm, nested, dtype):
+    """The SwiGLU pair over two rows in one launch (norm folded or not): each
+    row bit for bit the oracle's w1, then w3 with the gate epilogue, and the
+    one-row launch of that row."""
+    M, K = shape
+    l1, l3 = random_layer(M, K, nested, seed=M + 11), random_layer(M, K, nested, seed=M + 12)
+    w1, w3 = to_linear(l1, dtype), to_linear(l3, dtype)
+    assert nf4.prepare(w1) and nf4.prepare(w3)
+    dt = dt_code(dtype)
+    xb = [randn_bits(K, dtype, seed=K + 31 + r) for r in range(2)]
+    gb = o.from_f32((np.random.default_rng(K + 7).random(K) + 0.5).astype(np.float32), dt)
+    g = from_bits(gb, dtype) if norm else None
+    x2 = from_bits(np.concatenate(xb), dtype).view(1, 2, K)
+    y = nf4.matmul_fused(w1, x2, norm_weight=g, eps=1e-6, module3=w3)
+    assert y is not None and y.shape == (1, 2, M)
+    J, KS, _ = gemv_shape(M, K)
+    for r in range(2):
+        xin = orc.rms_norm_emul(xb[r], gb, 1, K, 1e-6, dt) if norm else xb[r]
+        g1 = orc.gemv_emul(xin, dt, **oracle_args(l1), M=M, K=K, bs=64, KS=KS, J=J, bs2=l1["bs2"] or 256)
+        expect = orc.gemv_emul(xin, dt, **oracle_args(l3), M=M, K=K, bs=64, KS=KS, J=J, bs2=l3["bs2"] or 256, R=g1,
+                               epi=2)
+        assert np.array_equal(bits(y[0, r]), expect), f"row {r} M={M} K={K}: {first_mismatch(bits(y[0, r]), expect)}"
+        one = nf4.matmul_fused(w1, x2[:, r : r + 1].contiguous(), norm_weight=g, eps=1e-6, module3=w3)
+        assert np.array_equal(bits(one), bits(y[0, r]))
+
+
 @pytest.mark.parametrize("dtype", DTYPES)
 def test_norm_folded_with_residual_epilogue(nf4, orc, dtype):
     M, K = 2560, 4096
@@ -599,7 +629,7 @@ def test_fused_form_declines_what_it_cannot_serve(nf4):
     assert nf4.matmul_fused(a, x, module3=b) is None  # shapes differ
     assert nf4.matmul_fused(a, torch.randn(3, 2560, device="cuda", dtype=torch.bfloat16)) is None  # three rows
     two = torch.randn(2, 2560, device="cuda", dtype=torch.bfloat16)
-    assert nf4.matmul_fused(a, two, module3=a) is None  # the SwiGLU pair takes one row
+    assert nf4.matmul_fused(a, two, module3=b) is None  # shapes differ, two rows
     assert nf4.matmul_fused(a, x, norm_weight=torch.ones(2560, device="cuda", dtype=torch.float16)) is None
 
 

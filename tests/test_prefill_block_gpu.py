@@ -367,7 +367,7 @@ def test_two_row_chain_with_folded_norms_equals_the_norm_launches(monkeypatch, c
             assert (n1 is None) == fold
             o2, _ = fusedlayer.prefill_block_chain(block, o1, freqs, mask, pos, xn=n1, causal=causal)
         if fold:
-            assert nf4gemv.stats()["fast"] >= calls + 6  # wqkv, w1, w3 of each block through the fused GEMV
+            assert nf4gemv.stats()["fast"] >= calls + 6  # wqkv and the w1 / w3 pair of each block, fused
         outs.append([o1.clone(), o2.clone(), kv.k_cache[0, :, start : start + rows].clone(),
                      kv.v_cache[0, :, start : start + rows].clone()])
     for a, b in zip(*outs):

@@ -61,8 +61,8 @@ SIGNATURES: dict[str, list] = {
     "ttsp_nf4_gemm_swiglu_fits": [_i, _i, _i, _i, _i, _i],
     "ttsp_nf4_gemv_fused": [_vp, _i, _vp, _f, _vp, _vp, _vp, _vp, _f, _vp, _vp, _vp, _vp, _f, _vp, _vp, _vp,
                             _i, _i, _i, _i, _i, _vp],
-    "ttsp_nf4_gemv_fused_rows": [_vp, _i, _vp, _f, _vp, _vp, _vp, _vp, _f, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i,
-                                 _vp],
+    "ttsp_nf4_gemv_fused_rows": [_vp, _i, _vp, _f, _vp, _vp, _vp, _vp, _f, _vp, _vp, _vp, _vp, _f, _vp, _vp, _vp,
+                                 _i, _i, _i, _i, _i, _i, _vp],
     "ttsp_nf4_dequant": [_vp, _vp, _vp, _vp, _f, _vp, _vp, _i, _ll, _i, _i, _vp],
     "ttsp_gemv_shape": [_i, _i, ctypes.POINTER(_i), ctypes.POINTER(_i), ctypes.POINTER(_i)],
     "ttsp_gemv_rows_shape": [_i, _i, _i, ctypes.POINTER(_i), ctypes.POINTER(_i), ctypes.POINTER(_i)],

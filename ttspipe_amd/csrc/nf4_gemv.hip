@@ -183,7 +183,7 @@ __global__ __launch_bounds__(GEMV_THREADS) void nf4_gemv_kernel(
   // x (and the norm weight): staged once per workgroup, chunk c = tid + 512 i
   // of each activation row by thread tid (one chunk per thread unless
   // K > 4096, where there is no norm); rows past N repeat row N - 1 (the rows
-  // form: NR > 1, one weight, a norm of each row if any)
+  // form: NR > 1, a norm of each row if any)
   const int XN = uniform((KD + nthr - 1) / nthr);
   uint4 xc[XC_MAX][NR];
   // (chunks past XN stay unset and unread: a zero-initialised chunk would make
@@ -514,7 +514,9 @@ __global__ __launch_bounds__(GEMV_THREADS) void nf4_gemv_kernel(
         if (n < p.N) p.Y[(size_t)n * M + row0 + lane] = epilogue16(dt, mine[n], p.epi, rres[n]);
     } else {
       // SwiGLU: w1's row is the gate operand of w3's row, as the two-launch form rounds it
-      p.Y[row0 + lane] = epilogue16(dt, mine[1], 2, st16(dt, mine[0]));
+#pragma unroll
+      for (int n = 0; n < NR; ++n)
+        if (n < p.N) p.Y[(size_t)n * M + row0 + lane] = epilogue16(dt, mine[NR + n], 2, st16(dt, mine[n]));
     }
   }
 }
@@ -656,7 +658,7 @@ static int gemv_launch(const void* X, int dt, const void* G, float eps, const Nf
   if (dt != DT_F16 && dt != DT_BF16) return (int)hipErrorInvalidValue;
   if (epi < 0 || epi > 2 || (epi && !R) || (mat3 && epi)) return (int)hipErrorInvalidValue;
   const int nm = mat3 ? 2 : 1;
-  if (N < 1 || N > GEMV_MAX_ROWS || (N > 1 && (mat3 || att))) return (int)hipErrorInvalidValue;
+  if (N < 1 || N > GEMV_MAX_ROWS || (N > 1 && att)) return (int)hipErrorInvalidValue;
   const int nr = N;
   const GemvShape g = gemv_shape(M, K, nm, bs_shift, nr);
   if (!g.J) return (int)hipErrorInvalidValue;
@@ -694,7 +696,7 @@ static int gemv_launch(const void* X, int dt, const void* G, float eps, const Nf
   p.epi = epi;
   p.att = att ? *att : AttnSrc{};
   const int rc = att     ? dispatch_att(g, p, st, att_bytes)
-                 : nm == 2 ? dispatch_j<2>(g, p, st)
+                 : nm == 2 ? (nr == 1 ? dispatch_j<2>(g, p, st) : dispatch_j<2, 2>(g, p, st))
                  : nr == 1 ? dispatch_j<1>(g, p, st)
                            : dispatch_j<1, 2>(g, p, st);
   if (rc) return rc;
@@ -763,17 +765,24 @@ extern "C" int ttsp_nf4_gemv_fused(const void* X, int x_dtype, const void* NORM_
                      stream);
 }
 
-extern "C" int ttsp_nf4_gemv_fused_rows(const void* X, int x_dtype, const void* NORM_W, float eps, const uint8_t* W,
-                                        const uint8_t* A8, const float* AMAX, const float* CODE2, float offset,
-                                        const float* LUT, void* Y, const void* R, int epi, int M, int K, int N,
-                                        int blocksize, int blocksize2, hipStream_t stream) {
-  if (!X || !W || !AMAX || !LUT || !Y || M <= 0 || K <= 0 || N < 1 || N > GEMV_MAX_ROWS)
+extern "C" int ttsp_nf4_gemv_fused_rows(const void* X, int x_dtype, const void* NORM_W, float eps,
+                                        const uint8_t* W1, const uint8_t* A8_1, const float* AMAX_1,
+                                        const float* CODE2_1, float offset_1, const uint8_t* W3,
+                                        const uint8_t* A8_3, const float* AMAX_3, const float* CODE2_3,
+                                        float offset_3, const float* LUT, void* Y, const void* R, int epi, int M,
+                                        int K, int N, int blocksize, int blocksize2, hipStream_t stream) {
+  if (!X || !W1 || !AMAX_1 || !LUT || !Y || M <= 0 || K <= 0 || N < 1 || N > GEMV_MAX_ROWS)
     return (int)hipErrorInvalidValue;
-  const bool nested = A8 != nullptr;
-  if (nested && !CODE2) return (int)hipErrorInvalidValue;
-  const Nf4Mat m{reinterpret_cast<const uint32_t*>(W), A8, AMAX, CODE2, offset};
-  return gemv_launch(X, x_dtype, NORM_W, eps, m, nullptr, nested, LUT, Y, R, epi, M, K, blocksize, blocksize2,
-                     stream, nullptr, N);
+  const bool nested = A8_1 != nullptr;
+  if (nested && !CODE2_1) return (int)hipErrorInvalidValue;
+  const Nf4Mat m1{reinterpret_cast<const uint32_t*>(W1), A8_1, AMAX_1, CODE2_1, offset_1};
+  if (!W3)
+    return gemv_launch(X, x_dtype, NORM_W, eps, m1, nullptr, nested, LUT, Y, R, epi, M, K, blocksize, blocksize2,
+                       stream, nullptr, N);
+  if (!AMAX_3 || (A8_3 != nullptr) != nested || (nested && !CODE2_3)) return (int)hipErrorInvalidValue;
+  const Nf4Mat m3{reinterpret_cast<const uint32_t*>(W3), A8_3, AMAX_3, CODE2_3, offset_3};
+  return gemv_launch(X, x_dtype, NORM_W, eps, m1, &m3, nested, LUT, Y, R, epi, M, K, blocksize, blocksize2, stream,
+                     nullptr, N);
 }
 
 extern "C" int ttsp_attn_nf4_gemv(const void* QKV, const void* QW, const void* KW, float eps, const void* F,

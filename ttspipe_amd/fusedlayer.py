@@ -359,11 +359,13 @@ def prefill_block_chain(block, x, freqs_cis, mask, input_pos, *, xn=None, next_n
         h = nf4gemv.matmul(a.wo, y, epi=nf4gemv.EPI_RESIDUAL, operand=x)
         hn = None
     u = None
-    if hh is None and fold and h is not None:  # w1 and w3 each with the FFN norm folded in
-        g = nf4gemv.matmul_fused(ff.w1, h, norm_weight=fn.weight, eps=fn.eps)
-        if g is not None:
-            u = nf4gemv.matmul_fused(ff.w3, h, norm_weight=fn.weight, eps=fn.eps, epi=nf4gemv.EPI_SILU_GATE,
-                                     operand=g)
+    if hh is None and fold and h is not None:  # w1 and w3 with the FFN norm folded in: one launch, else two
+        u = nf4gemv.matmul_fused(ff.w1, h, norm_weight=fn.weight, eps=fn.eps, module3=ff.w3)
+        if u is None:
+            g = nf4gemv.matmul_fused(ff.w1, h, norm_weight=fn.weight, eps=fn.eps)
+            if g is not None:
+                u = nf4gemv.matmul_fused(ff.w3, h, norm_weight=fn.weight, eps=fn.eps, epi=nf4gemv.EPI_SILU_GATE,
+                                         operand=g)
     if u is None and hn is None and h is not None:
         hn = fusedops.rms_norm(h, fn.weight, fn.eps)
     # w1 and w3 with the SwiGLU gate in one launch where it serves the shape, else two

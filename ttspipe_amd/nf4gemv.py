@@ -319,15 +319,14 @@ def gemv_fits(M: int, K: int) -> bool:
     return _lib.lib().ttsp_gemv_shape(M, K, None, None, None) == 0
 
 
-#: Most activation rows `matmul_fused` takes in one launch (one weight; the
-#: SwiGLU pair takes one row).
+#: Most activation rows `matmul_fused` takes in one launch.
 FUSED_MAX_ROWS = 2
 
 
 def matmul_fused(module, x, *, norm_weight=None, eps: float = 1e-6, module3=None, epi: int = EPI_NONE,
                  operand=None, out=None):
-    """One input row (up to `FUSED_MAX_ROWS` with one weight) through
-    `module` in a single launch, or None if not applicable.
+    """Up to `FUSED_MAX_ROWS` input rows through `module` in a single launch
+    (each weight byte looked up once for all of them), or None if not applicable.
 
     `norm_weight` folds the fork's RMSNorm of each row in (bit-identical to
     `fusedops.rms_norm` then `matmul`); `module3` (same shape and scales
@@ -346,7 +345,7 @@ def matmul_fused(module, x, *, norm_weight=None, eps: float = 1e-6, module3=None
     rows = x.numel() // K if x.shape[-1] == K else 0
     if rows < 1 or rows > FUSED_MAX_ROWS or not x.is_contiguous() or x.data_ptr() % 16:
         return None
-    if rows > 1 and (module3 is not None or _lib.lib().ttsp_gemv_rows_shape(M, K, rows, None, None, None)):
+    if rows > 1 and _lib.lib().ttsp_gemv_rows_shape(M, K, rows, None, None, None):
         return None
     if not gemv_fits(M, K):
         return None
@@ -373,16 +372,16 @@ def matmul_fused(module, x, *, norm_weight=None, eps: float = 1e-6, module3=None
         out = torch.empty((rows, M), dtype=x.dtype, device=x.device)
     elif out.dtype != x.dtype or out.numel() != rows * M or not out.is_contiguous():
         return None
+    f3 = fast3 or {"w": 0, "a8": 0, "amax": 0, "code2": 0, "offset": 0.0}
     if rows > 1:
         rc = _lib.lib().ttsp_nf4_gemv_fused_rows(
             x.data_ptr(), dt, _lib.ptr(norm_weight), float(eps), fast["w"], fast["a8"], fast["amax"], fast["code2"],
-            fast["offset"], fast["lut"].data_ptr(), out.data_ptr(), _lib.ptr(operand) if epi else 0, epi, M, K, rows,
-            fast["bs"], fast["bs2"], _lib.stream())
+            fast["offset"], f3["w"], f3["a8"], f3["amax"], f3["code2"], f3["offset"], fast["lut"].data_ptr(),
+            out.data_ptr(), _lib.ptr(operand) if epi else 0, epi, M, K, rows, fast["bs"], fast["bs2"], _lib.stream())
         if rc:
             raise RuntimeError(f"ttsp_nf4_gemv_fused_rows failed: hipError_t {rc}")
-        _stats["fast"] += 1
+        _stats["fast"] += 2 if fast3 is not None else 1
         return out.view(*x.shape[:-1], M)
-    f3 = fast3 or {"w": 0, "a8": 0, "amax": 0, "code2": 0, "offset": 0.0}
     rc = _lib.lib().ttsp_nf4_gemv_fused(
         x.data_ptr(), dt, _lib.ptr(norm_weight), float(eps),
         fast["w"], fast["a8"], fast["amax"], fast["code2"], fast["offset"],
