@@ -54,10 +54,10 @@ SPIN_CYCLES = 200_000
 #: The tracer reads 3-10 % above the untraced launch-to-launch interval (6.04
 #: median against 5.89 us in the same session; 6.2-6.6 us means across boxes).
 GEMV_PROFILE = {
-    "key": {"M": 9728, "K": 2560, "J": 5, "KS": 1, "RPW": 5, "grid": 244, "source_sha16": "f9a19336d714b6f4"},
-    "traffic_bytes": 13_217_840,
-    "rocprof_mean_us": 6.213,
-    "rocprof_median_us": 5.959,
+    "key": {"M": 9728, "K": 2560, "J": 5, "KS": 1, "RPW": 5, "grid": 244, "source_sha16": "066d1767a696e109"},
+    "traffic_bytes": 13_211_723,
+    "rocprof_mean_us": 6.245,
+    "rocprof_median_us": 6.119,
     "summary": "profiles/nf4_gemv_gate_9728x2560_bf16_nested.md",
 }
 
