@@ -264,6 +264,21 @@ int ttsp_attn_decode_rows(const void* Q, const void* KC, const void* VC, const l
                           float* PL, float* PACC, void* Y, int nh, int nkv, int max_len, int nchunk,
                           float scale, int rows, int dtype, void* stream);
 
+/* ttsp_qk_rope_kv_rows then ttsp_attn_decode_rows, for up to 8 rows, in one
+ * attention launch and its merge: QKV row r at QKV + r*qkv_rs (the wqkv
+ * output, qkv_rs >= (nh + 2 nkv) * 128), rotary row r at F + r*128 values
+ * (F 4-byte aligned, ftype as ttsp_rope), positions POS[rows]. Each
+ * (kv head, chunk, row) workgroup computes its row's query head and every span
+ * row its chunk holds (q/k head norms with QW / KW if given, rotary), and
+ * writes its own row's K/V to the cache; Y and the cache rows are bit for bit
+ * those of the two entry points. Scratch as ttsp_attn_decode_rows.
+ * Replaces: the same reference steps as those two (a short causal prompt
+ * span, fusedlayer.py:56-92 and fastpath.py:133-174). */
+int ttsp_attn_decode_qkv_rows(const void* QKV, int qkv_rs, const void* QW, const void* KW, float eps,
+                              const void* F, int ftype, const long long* POS, void* KC, void* VC, float* PM,
+                              float* PL, float* PACC, void* Y, int nh, int nkv, int max_len, int nchunk,
+                              float scale, int rows, int dtype, void* stream);
+
 /* qk_rope_kv and the decode attention in one pass: the head norms and rotary
  * of the query heads are applied inside the attention workgroups (from QKV),
  * the new position's K/V row is computed, written to KC/VC[kv][POS[0]] and used

@@ -243,6 +243,64 @@ def test_decode_attention_rows_equal_one_position_each(hip, orc, dtype, position
 
 @pytest.mark.parametrize("qk_norm", [True, False])
 @pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("positions,max_len,nh,nkv", [
+    ([37], 2304, 32, 8),                             # one row
+    ([512, 513], 2304, 32, 8),                       # a 2-token tail after 512 cached positions
+    ([60, 61, 62, 63, 64, 65, 66, 67], 128, 4, 1),  # eight rows across a chunk edge
+    ([2297, 2298, 2299, 2300, 2301, 2302, 2303], 2304, 16, 4),  # the cache's last positions
+    ([7, 300, 41, 2000, 64, 65], 2304, 8, 2),        # rows in any order, one a chunk's first position
+    ([0, 1, 2], 16, 8, 8)])                          # one head per kv head, a one-chunk cache
+def test_rows_attention_from_qkv_equals_the_rows_kernels(hip, qk_norm, dtype, positions, max_len, nh, nkv):
+    """ttsp_attn_decode_qkv_rows (each workgroup computing its row's query and
+    the span rows its chunk holds) == ttsp_qk_rope_kv_rows then
+    ttsp_attn_decode_rows, bit for bit: the output and every cache row."""
+    from ttspipe_amd import _lib
+    from ttspipe_amd.llama import precompute_freqs_cis
+
+    S, dt = len(positions), dt_code(dtype)
+    nchunk = -(-max_len // 64)
+    rs = (nh + 2 * nkv) * 128
+    qkvb = randn_bits(S * rs, dtype, seed=S + nh, scale=2.0)
+    qwb = o.from_f32((np.random.default_rng(7).random(128) + 0.5).astype(np.float32), dt)
+    kwb = o.from_f32((np.random.default_rng(8).random(128) + 0.5).astype(np.float32), dt)
+    table = precompute_freqs_cis(max_len, 128, 1e6)
+    freqs = table[torch.tensor(positions)].contiguous().cuda()
+    kcb = randn_bits(nkv * max_len * 128, dtype, seed=S + 12)
+    vcb = randn_bits(nkv * max_len * 128, dtype, seed=S + 13)
+    qkv = from_bits(qkvb, dtype)
+    qw = from_bits(qwb, dtype) if qk_norm else None
+    kw = from_bits(kwb, dtype) if qk_norm else None
+    posd = torch.tensor(positions, dtype=torch.long, device="cuda")
+    f32 = dict(dtype=torch.float32, device="cuda")
+    outs = []
+    for fused in (True, False):
+        KC, VC = from_bits(kcb, dtype), from_bits(vcb, dtype)
+        pm, pl = torch.empty(S * nh * nchunk, **f32), torch.empty(S * nh * nchunk, **f32)
+        pacc = torch.empty(S * nh * nchunk * 128, **f32)
+        y = torch.empty(S, nh * 128, dtype=dtype, device="cuda")
+        if fused:
+            rc = hip.ttsp_attn_decode_qkv_rows(qkv.data_ptr(), rs, _lib.ptr(qw), _lib.ptr(kw), 1e-6, freqs.data_ptr(),
+                                               o.DT_BF16, posd.data_ptr(), KC.data_ptr(), VC.data_ptr(), pm.data_ptr(),
+                                               pl.data_ptr(), pacc.data_ptr(), y.data_ptr(), nh, nkv, max_len, nchunk,
+                                               float(128**-0.5), S, dt, _lib.stream())
+            assert rc == 0
+        else:
+            q = torch.empty(S, nh * 128, dtype=dtype, device="cuda")
+            rc = hip.ttsp_qk_rope_kv_rows(qkv.data_ptr(), rs, _lib.ptr(qw), _lib.ptr(kw), 1e-6, freqs.data_ptr(),
+                                          o.DT_BF16, posd.data_ptr(), q.data_ptr(), KC.data_ptr(), VC.data_ptr(), nh,
+                                          nkv, max_len, S, dt, _lib.stream())
+            assert rc == 0
+            rc = hip.ttsp_attn_decode_rows(q.data_ptr(), KC.data_ptr(), VC.data_ptr(), posd.data_ptr(), pm.data_ptr(),
+                                           pl.data_ptr(), pacc.data_ptr(), y.data_ptr(), nh, nkv, max_len, nchunk,
+                                           float(128**-0.5), S, dt, _lib.stream())
+            assert rc == 0
+        outs.append((bits(y), bits(KC), bits(VC)))
+    for a, b in zip(*outs):
+        assert np.array_equal(a, b), first_mismatch(a, b)
+
+
+@pytest.mark.parametrize("qk_norm", [True, False])
+@pytest.mark.parametrize("dtype", DTYPES)
 @pytest.mark.parametrize("pos,max_len,nh,nkv", [(0, 2304, 32, 8), (37, 2304, 32, 8), (63, 2304, 32, 8),
                                                 (64, 2304, 32, 8), (2047, 2304, 32, 8), (2303, 2304, 32, 8),
                                                 (0, 16, 8, 2), (9, 16, 8, 2), (15, 16, 8, 2), (100, 128, 4, 1),

@@ -334,6 +334,43 @@ def test_causal_chain_equals_the_masked_chain(rows, start, nh, nkv):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("rows,start", [(2, 30), (5, 60), (8, 0)])
+def test_short_causal_span_attention_from_qkv_equals_the_rows_kernels(monkeypatch, rows, start):
+    """A causal span of up to 8 rows with the head norms, rotary and KV write
+    inside the row-by-row attention launch, against the same chain with them
+    as their own launch first: the block output and the new K/V rows bit for
+    bit."""
+    from tests.test_fused_gpu import _block
+    from ttspipe_amd import fastpath, fusedlayer, fusedops, nf4gemv
+    from ttspipe_amd.llama import precompute_freqs_cis
+
+    assert nf4gemv.install() and fusedops.install() and fusedlayer.install()
+    dtype, D, length = torch.bfloat16, 512, 256
+    block, _ = _block(dtype, True, dim=D, n_head=8, n_local_heads=2, inter=1024, max_len=length, seed=rows)
+    kv = block.attention.kv_cache
+    g = torch.Generator().manual_seed(start)
+    kc0 = torch.randn(kv.k_cache.shape, generator=g).to(dtype).cuda()
+    vc0 = torch.randn(kv.v_cache.shape, generator=g).to(dtype).cuda()
+    x = torch.randn(1, rows, D, generator=g).to(dtype).cuda()
+    pos = torch.arange(start, start + rows, device="cuda")
+    freqs = precompute_freqs_cis(length, 128, 10000.0, dtype=dtype).cuda()[pos].contiguous()
+    mask = torch.tril(torch.ones(length, length, dtype=torch.bool, device="cuda"))[None, None, pos]
+    outs = []
+    orig = fastpath.causal_rows_attention_qkv
+    for fused in (True, False):
+        if not fused:
+            monkeypatch.setattr(fastpath, "causal_rows_attention_qkv", lambda *a, **k: None)
+        kv.k_cache.copy_(kc0)
+        kv.v_cache.copy_(vc0)
+        with torch.inference_mode():
+            out, _ = fusedlayer.prefill_block_chain(block, x, freqs, mask, pos, causal=True)
+        outs.append([out.clone(), kv.k_cache.clone(), kv.v_cache.clone()])
+    monkeypatch.setattr(fastpath, "causal_rows_attention_qkv", orig)
+    for a, b in zip(*outs):
+        assert torch.equal(a.view(torch.int16), b.view(torch.int16))
+
+
+@pytest.mark.gpu
 @pytest.mark.parametrize("causal", [True, False])
 def test_two_row_chain_with_folded_norms_equals_the_norm_launches(monkeypatch, causal):
     """Two blocks chained over a 2-row span: with the RMSNorms folded into the

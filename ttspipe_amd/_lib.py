@@ -79,6 +79,8 @@ SIGNATURES: dict[str, list] = {
     "ttsp_attn_decode_qkv_noalloc_max_slots": [],
     "ttsp_qk_rope_kv_rows": [_vp, _ll, _vp, _vp, _f, _vp, _i, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _vp],
     "ttsp_attn_decode_rows": [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _f, _i, _i, _vp],
+    "ttsp_attn_decode_qkv_rows": [_vp, _i, _vp, _vp, _f, _vp, _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i,
+                                  _f, _i, _i, _vp],
     "ttsp_qk_rope_kv_rows_partials": [_vp, _i, _vp, _vp, _f, _vp, _i, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i,
                                       _vp],
     "ttsp_prefill_attention": [_vp, _ll, _ll, _vp, _ll, _ll, _vp, _ll, _ll, _vp, _ll, _vp, _i, _i, _i, _i, _f, _i,

@@ -366,6 +366,143 @@ __global__ __launch_bounds__(1024) void attn_qkv_kernel(
   reinterpret_cast<float2*>(PACC + slot * HD)[lane] = make_float2(a0, a1);
 }
 
+// The rows form of attn_qkv_kernel, for a short causal span: rows r = 0 ..
+// nrows - 1 at positions POS[r], QKV row r at QKV + r qkv_rs and rotary row
+// r at F + r HD. Workgroup (kv head kh, chunk c, row r) takes query head
+// kh groups + w of row r in wave w, and stages every span row whose position
+// falls in its chunk from that row's QKV K/V heads (norm and rotary, as
+// qk_rope_kv_kernel), so no workgroup reads a cache row that another writes in
+// this launch; the wave that computes span row r in the chunk holding POS[r]
+// writes it to the cache. Partials go to slot (r nh + qh) nchunk + c for
+// attn_combine_kernel's rows form. The bits are those of qk_rope_kv_kernel
+// over the rows followed by attn_partial_kernel's rows form.
+constexpr int ATT_ROWS_MAX = 8;
+template <int DT>
+__global__ __launch_bounds__(1024) void attn_qkv_rows_kernel(
+    const uint16_t* __restrict__ QKV, int qkv_rs, const uint16_t* __restrict__ QW, const uint16_t* __restrict__ KW,
+    float eps, const void* __restrict__ F, int ftype, const long long* __restrict__ POS, int nrows,
+    uint16_t* __restrict__ KC, uint16_t* __restrict__ VC, float* __restrict__ PM, float* __restrict__ PL,
+    float* __restrict__ PACC, int nh, int nkv, int groups, int max_len, int nchunk, float scale) {
+  extern __shared__ __align__(16) float smem[];
+  float* q_s = smem;                                                   // [groups][HD]
+  float* p_s = q_s + groups * HD;                                      // [groups][ACHUNK]
+  uint16_t* k_s = reinterpret_cast<uint16_t*>(p_s + groups * ACHUNK);  // [ACHUNK][KPAD]
+  uint16_t* v_s = k_s + ACHUNK * KPAD;                                 // [ACHUNK][HD]
+
+  const int kh = blockIdx.x, c = blockIdx.y, r = blockIdx.z;
+  const int tid = threadIdx.x, nthr = blockDim.x;
+  const int g = tid >> 6, lane = tid & 63;
+  const int qh = kh * groups + g;
+  const long long j0 = (long long)c * ACHUNK;
+  const int fs = ftype == DT_F32 ? 4 : 2;  // bytes a rotary element
+  // every position of the span (lane j: row j), the query head with its norm
+  // weights and rotary row, then the chunk's cached K and V rows
+  const long long posl = POS[min(lane, nrows - 1)];
+  const bool qn = QW != nullptr, kn = KW != nullptr;
+  const uint16_t* qwp = qn ? QW : QKV;
+  const uint16_t* kwp = kn ? KW : QKV;
+  const uint16_t* qr = QKV + (size_t)r * qkv_rs + (size_t)qh * HD;
+  const uint16_t q0 = qr[lane], q1 = qr[lane + 64];
+  const uint16_t qw0 = qwp[lane], qw1 = qwp[lane + 64];
+  const uint16_t kw0 = kwp[lane], kw1 = kwp[lane + 64];
+  const RopeF rf = load_rope((const uint8_t*)F + (size_t)r * HD * fs, ftype, lane);
+  const uint16_t* kb = KC + (size_t)kh * max_len * HD;
+  const uint16_t* vb = VC + (size_t)kh * max_len * HD;
+  constexpr int NT = ACHUNK * (HD / 8);
+  constexpr int PER = NT / 256;
+  u32x4 kq[PER], vq[PER];
+#pragma unroll
+  for (int i = 0; i < PER; ++i) {
+    const int t = min(tid + i * nthr, NT - 1);
+    const long long row = min(j0 + t / (HD / 8), (long long)max_len - 1);
+    const int e = (t % (HD / 8)) * 8;
+    kq[i] = *reinterpret_cast<const u32x4*>(kb + (size_t)row * HD + e);
+    vq[i] = *reinterpret_cast<const u32x4*>(vb + (size_t)row * HD + e);
+  }
+  const long long pos = __shfl(posl, r, 64);
+  if (pos < 0 || pos >= max_len) return;  // no cache slot for it: nothing is written
+  const long long L = pos + 1;
+  const size_t slot = ((size_t)r * nh + qh) * nchunk + c;
+  if (j0 >= L) {  // a chunk past the row's live positions
+    if (lane == 0) {
+      PM[slot] = -1e30f;
+      PL[slot] = 0.0f;
+    }
+    return;
+  }
+  const int nvalid = (int)min((long long)ACHUNK, L - j0);
+  // chunk rows holding a span row (their cached values are stale: computed here instead)
+  uint64_t span = 0;
+  for (int j = 0; j < nrows; ++j) {
+    const long long pj = __shfl(posl, j, 64);
+    if (pj >= j0 && pj < j0 + ACHUNK && pj < max_len) span |= 1ull << (int)(pj - j0);
+  }
+
+  // this wave's query head of row r: norm, rotary, rounded as the stored Q, scaled
+  {
+    float lo = Elem<DT>::load(q0), hi = Elem<DT>::load(q1);
+    head_norm_rope<DT>(lo, hi, qn, qw0, qw1, eps, rf, lane);
+    q_s[g * HD + lane] = __fmul_rn(Elem<DT>::load(Elem<DT>::store(lo)), scale);
+    q_s[g * HD + lane + 64] = __fmul_rn(Elem<DT>::load(Elem<DT>::store(hi)), scale);
+  }
+  // the span rows in this chunk, wave w taking rows w, w + groups, ...: K
+  // normed and rotated as qk_rope_kv_kernel stores it, V as it is
+  for (int j = g; j < nrows; j += groups) {
+    const long long pj = __shfl(posl, j, 64);
+    if (pj < j0 || pj >= j0 + ACHUNK || pj >= max_len) continue;
+    const uint16_t* kr = QKV + (size_t)j * qkv_rs + (size_t)(nh + kh) * HD;
+    const uint16_t* vr = QKV + (size_t)j * qkv_rs + (size_t)(nh + nkv + kh) * HD;
+    const RopeF fj = load_rope((const uint8_t*)F + (size_t)j * HD * fs, ftype, lane);
+    float lo = Elem<DT>::load(kr[lane]), hi = Elem<DT>::load(kr[lane + 64]);
+    const uint16_t v0 = vr[lane], v1 = vr[lane + 64];
+    head_norm_rope<DT>(lo, hi, kn, kw0, kw1, eps, fj, lane);
+    const uint16_t klo = Elem<DT>::store(lo), khi = Elem<DT>::store(hi);
+    const int jj = (int)(pj - j0);
+    k_s[jj * KPAD + lane] = klo;
+    k_s[jj * KPAD + lane + 64] = khi;
+    v_s[jj * HD + lane] = v0;
+    v_s[jj * HD + lane + 64] = v1;
+    if (j == r) {  // row r's K/V into the cache (read by no workgroup of this launch)
+      const size_t row = ((size_t)kh * max_len + pj) * HD;
+      KC[row + lane] = klo;
+      KC[row + lane + 64] = khi;
+      VC[row + lane] = v0;
+      VC[row + lane + 64] = v1;
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < PER; ++i) {
+    const int t = tid + i * nthr;
+    const int j = t / (HD / 8), e = (t % (HD / 8)) * 8;
+    if (t < NT && !((span >> j) & 1ull)) {
+      *reinterpret_cast<u32x4*>(k_s + j * KPAD + e) = kq[i];
+      *reinterpret_cast<u32x4*>(v_s + j * HD + e) = vq[i];
+    }
+  }
+  for (int t = tid + PER * nthr; t < NT; t += nthr) {  // the rest, with fewer than 4 waves
+    const int j = t / (HD / 8), e = (t % (HD / 8)) * 8;
+    if ((span >> j) & 1ull) continue;
+    const long long jr = j0 + min(j, nvalid - 1);
+    *reinterpret_cast<u32x4*>(k_s + j * KPAD + e) = *reinterpret_cast<const u32x4*>(kb + (size_t)jr * HD + e);
+    *reinterpret_cast<u32x4*>(v_s + j * HD + e) = *reinterpret_cast<const u32x4*>(vb + (size_t)jr * HD + e);
+  }
+  __syncthreads();
+
+  const float s = score4<DT>(q_s + g * HD, k_s + lane * KPAD);
+  const bool valid = lane < nvalid;
+  const float m = wave_max_u(valid ? s : -3.0e38f);
+  const float p = valid ? exp_cw(__fsub_rn(s, m)) : 0.0f;
+  const float l = wave_sum_dpp(p);
+  p_s[g * ACHUNK + lane] = p;  // read back by this wave only: no barrier
+  float a0, a1;
+  pv4<DT>(p_s + g * ACHUNK, v_s, nvalid, lane, a0, a1);
+  if (lane == 0) {
+    PM[slot] = m;
+    PL[slot] = l;
+  }
+  reinterpret_cast<float2*>(PACC + slot * HD)[lane] = make_float2(a0, a1);
+}
+
 }  // namespace ttsp
 
 using namespace ttsp;
@@ -450,6 +587,35 @@ extern "C" int ttsp_attn_decode_rows(const void* Q, const void* KC, const void* 
   else if (dtype == DT_BF16) TTSP_AR(DT_BF16);
   else return (int)hipErrorInvalidValue;
 #undef TTSP_AR
+  TTSP_RETURN_LAUNCH();
+}
+
+extern "C" int ttsp_attn_decode_qkv_rows(const void* QKV, int qkv_rs, const void* QW, const void* KW, float eps,
+                                         const void* F, int ftype, const long long* POS, void* KC, void* VC,
+                                         float* PM, float* PL, float* PACC, void* Y, int nh, int nkv, int max_len,
+                                         int nchunk, float scale, int rows, int dtype, hipStream_t stream) {
+  if (!QKV || !F || !POS || !KC || !VC || !PM || !PL || !PACC || !Y || nh <= 0 || nkv <= 0 || nh % nkv ||
+      max_len <= 0 || nchunk <= 0 || rows < 1 || rows > ATT_ROWS_MAX || ftype < 0 || ftype > 2 || (uintptr_t)F % 4 ||
+      qkv_rs < (nh + 2 * nkv) * HD)
+    return (int)hipErrorInvalidValue;
+  const int groups = nh / nkv;
+  if (groups > 16 || nchunk > CMAX) return (int)hipErrorInvalidValue;
+  const size_t shmem = sizeof(float) * (size_t)groups * (HD + ACHUNK) +
+                       sizeof(uint16_t) * (size_t)ACHUNK * (KPAD + HD);
+  const uint16_t* qw = (const uint16_t*)QW;
+  const uint16_t* kw = (const uint16_t*)KW;
+#define TTSP_AQR(DTV)                                                                                           \
+  do {                                                                                                          \
+    hipLaunchKernelGGL(attn_qkv_rows_kernel<DTV>, dim3(nkv, nchunk, rows), dim3(64 * groups), shmem, stream,     \
+                       (const uint16_t*)QKV, qkv_rs, qw, kw, eps, F, ftype, POS, rows, (uint16_t*)KC,             \
+                       (uint16_t*)VC, PM, PL, PACC, nh, nkv, groups, max_len, nchunk, scale);                    \
+    hipLaunchKernelGGL(attn_combine_kernel<DTV>, dim3(nh, rows), dim3(HD), 0, stream, PM, PL, PACC,             \
+                       (uint16_t*)Y, nchunk);                                                                   \
+  } while (0)
+  if (dtype == DT_F16) TTSP_AQR(DT_F16);
+  else if (dtype == DT_BF16) TTSP_AQR(DT_BF16);
+  else return (int)hipErrorInvalidValue;
+#undef TTSP_AQR
   TTSP_RETURN_LAUNCH();
 }
 

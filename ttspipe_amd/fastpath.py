@@ -157,6 +157,53 @@ def causal_rows_attention(q, k_cache, v_cache, input_pos, n_head, n_local_heads,
     return y
 
 
+def causal_rows_attention_qkv(qkv, q_weight, k_weight, eps, freqs_cis, input_pos, k_cache, v_cache, n_head,
+                              n_local_heads, width):
+    """`causal_rows_attention` straight from the wqkv output: qkv (1, S,
+    (n_head + 2 n_local_heads) 128) contiguous, the q/k head-norm weights
+    (None: no head norms) and eps, the rows' rotary rows freqs_cis (S x 128
+    values, contiguous), positions input_pos (int64 (S,)). The head norms,
+    rotary and the KV-cache write of the S rows happen inside the attention
+    launch (each workgroup computes the span rows its chunk holds), with the
+    bits of the head-norm / rotary / KV kernel followed by
+    `causal_rows_attention`. Returns (1, S, n_head * 128); None when declined
+    (shapes, dtypes, S > CAUSAL_ROWS_MAX)."""
+    import torch
+
+    from ttspipe_amd import _lib
+
+    if not _lib.gpu_present():
+        return None
+    S = qkv.shape[1] if qkv.dim() == 3 else 0
+    width_qkv = (n_head + 2 * n_local_heads) * HEAD_DIM
+    ftype = _lib.dtype_code(freqs_cis.dtype)
+    if (S < 1 or S > CAUSAL_ROWS_MAX or qkv.shape != (1, S, width_qkv) or not qkv.is_contiguous()
+            or k_cache.dim() != 4 or k_cache.shape[0] != 1 or k_cache.shape[1] != n_local_heads
+            or k_cache.shape[3] != HEAD_DIM or v_cache.shape != k_cache.shape or not k_cache.is_contiguous()
+            or not v_cache.is_contiguous() or k_cache.dtype != qkv.dtype or v_cache.dtype != qkv.dtype
+            or input_pos.dtype != torch.long or input_pos.numel() != S or not input_pos.is_contiguous()
+            or n_head % n_local_heads or _lib.dtype_code(qkv.dtype) not in (_lib.DT_F16, _lib.DT_BF16)
+            or ftype is None or not freqs_cis.is_contiguous() or freqs_cis.numel() != S * HEAD_DIM
+            or freqs_cis.data_ptr() % 4):
+        return None
+    for w in (q_weight, k_weight):
+        if w is not None and (w.dtype != qkv.dtype or w.numel() != HEAD_DIM or not w.is_contiguous()):
+            return None
+    max_len = k_cache.shape[2]
+    nchunk = -(-min(width, max_len) // CHUNK)
+    pm = torch.empty(2 * S * n_head * nchunk, dtype=torch.float32, device=qkv.device)
+    pacc = torch.empty(S * n_head * nchunk * HEAD_DIM, dtype=torch.float32, device=qkv.device)
+    y = torch.empty(1, S, n_head * HEAD_DIM, dtype=qkv.dtype, device=qkv.device)
+    rc = _lib.lib().ttsp_attn_decode_qkv_rows(
+        qkv.data_ptr(), width_qkv, _lib.ptr(q_weight), _lib.ptr(k_weight), float(eps), freqs_cis.data_ptr(), ftype,
+        input_pos.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), pm.data_ptr(), pm[S * n_head * nchunk:].data_ptr(),
+        pacc.data_ptr(), y.data_ptr(), n_head, n_local_heads, max_len, nchunk, float(HEAD_DIM**-0.5), S,
+        _lib.dtype_code(qkv.dtype), _lib.stream())
+    _lib.check(rc, "ttsp_attn_decode_qkv_rows")
+    _stats["causal_rows"] += 1
+    return y
+
+
 def prefill_work_floats(seqlen: int, n_head: int, splits: int) -> int:
     """fp32 elements of the key-split workspace: per split, position and head
     the unnormalised output (128) and the running max and sum (2); 0 unsplit."""

@@ -307,7 +307,16 @@ def prefill_block_chain(block, x, freqs_cis, mask, input_pos, *, xn=None, next_n
         qkv = nf4gemv.matmul(a.wqkv, xn)
         if qkv is None:
             return None
-    if rows_ok:
+    y = None
+    if causal and rows_ok and part is None and n <= fastpath.CAUSAL_ROWS_MAX:
+        # a short causal span: the head norms, rotary and KV write inside the
+        # row-by-row attention launch (the decode step's form, no mask reads)
+        qn, kn = (a.q_norm, a.k_norm) if a.attention_qk_norm else (None, None)
+        y = fastpath.causal_rows_attention_qkv(qkv, None if qn is None else qn.weight,
+                                               None if kn is None else kn.weight,
+                                               float(qn.eps) if qn is not None else 0.0, freqs_cis, input_pos, kc,
+                                               vc, nh, nkv, mask.shape[-1])
+    if y is None and rows_ok:
         # head norms, rotary and the KV write for every row in one launch
         q = torch.empty(bsz, n, nh, hd, dtype=x.dtype, device=x.device)
         qn, kn = (a.q_norm, a.k_norm) if a.attention_qk_norm else (None, None)
@@ -328,7 +337,7 @@ def prefill_block_chain(block, x, freqs_cis, mask, input_pos, *, xn=None, next_n
             _lib.check(rc, "ttsp_qk_rope_kv_rows")
         q_rows = q
         q, k, v = q.transpose(1, 2), kc, vc
-    else:
+    elif y is None:
         q, k, v = qkv.split([nh * hd, nkv * hd, nkv * hd], dim=-1)
         q, k, v = q.view(bsz, n, nh, hd), k.view(bsz, n, nkv, hd), v.view(bsz, n, nkv, hd)
         if a.attention_qk_norm:
@@ -340,8 +349,7 @@ def prefill_block_chain(block, x, freqs_cis, mask, input_pos, *, xn=None, next_n
             fq, fk = apply_rotary_emb(q, freqs_cis), apply_rotary_emb(k, freqs_cis)
         q, k, v = (t.transpose(1, 2) for t in (fq, fk, v))
         k, v = a.kv_cache.update(input_pos, k, v)
-    y = None
-    if causal and rows_ok:
+    if y is None and causal and rows_ok:
         # a short causal span: each row as the decode step attends (no mask reads)
         y = fastpath.causal_rows_attention(q_rows, kc, vc, input_pos, nh, nkv, mask.shape[-1])
     if y is None:
