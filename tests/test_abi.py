@@ -407,8 +407,8 @@ def test_fast_steps_rejects_bad_arguments_before_any_launch():
 def test_swiglu_gemm_plan_on_the_host():
     """`ttsp_nf4_gemm_swiglu_fits`: one launch where both GEMMs of the pair
     would run the direct-to-LDS kernel unsplit (up to 512 rows, >= 512 tiles
-    of 64 x 128 with fewer than 64 K-steps: 385-512 rows of 9728 x 2560),
-    nowhere else; the entry rejects a
+    of 64 x 128 with fewer than 64 K-steps: 385-512 rows of 9728 x 2560) or
+    the few-row kernel (3-32 rows), nowhere else; the entry rejects a
     shape it does not serve before any launch."""
     from ttspipe_amd import _lib
 
@@ -421,6 +421,13 @@ def test_swiglu_gemm_plan_on_the_host():
                  (1536, 1024, 512, 64, 256, 1), (9728, 2560, 512, 64, 16, 1), (9728, 2560, 512, 32, 256, 1),
                  (9728, 2560, 512, 96, 256, 0), (9728, 2500, 512, 64, 256, 1)):
         assert fits(*args) == 0, args
+    # 3-32 rows where both GEMMs run the few-row kernel unsplit: its pair form
+    for rows in (3, 4, 8, 16, 17, 32):
+        assert fits(9728, 2560, rows, 64, 256, 1) == 1, rows
+        assert fits(2560, 9728, rows, 64, 256, 0) == 1, rows
+    for args in ((9728, 2560, 2, 64, 256, 1), (9728, 2560, 33, 64, 256, 1), (9728, 2560, 64, 64, 256, 1),
+                 (9728, 10368, 4, 64, 256, 1), (9728, 2560, 4, 32, 256, 1)):
+        assert fits(*args) == 0, args  # two rows (the GEMV), a K split, runs past 8 waves, 32-code blocks
     p = 4096
     assert lib.ttsp_nf4_gemm_swiglu(p, 1, p, p, p, p, 0.0, p, p, p, p, 0.0, p, p, 2560, 9728, 512, 64, 256,
                                     None) == 1

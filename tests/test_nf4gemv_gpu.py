@@ -690,6 +690,41 @@ def test_swiglu_gemm_equals_the_two_launches(nf4, shape, rows, nested, dtype):
     assert np.abs(o.to_f32(rb, dt_code(dtype))).max() > 0
 
 
+@pytest.mark.parametrize("shape,rows,nested,dtype", [((9728, 2560), 3, True, torch.bfloat16),
+                                                     ((9728, 2560), 4, True, torch.bfloat16),
+                                                     ((9728, 2560), 8, False, torch.float16),
+                                                     ((9728, 2560), 9, True, torch.bfloat16),
+                                                     ((9728, 2560), 16, True, torch.float16),
+                                                     ((9728, 2560), 17, True, torch.bfloat16),
+                                                     ((9728, 2560), 32, False, torch.bfloat16),
+                                                     ((9730, 2560), 5, True, torch.bfloat16),
+                                                     ((3072, 1024), 4, True, torch.bfloat16),
+                                                     ((1000, 4096), 12, False, torch.float16),
+                                                     ((512, 9728), 24, True, torch.bfloat16)])
+def test_swiglu_few_rows_equals_the_two_launches(nf4, shape, rows, nested, dtype):
+    """3-32 rows: `matmul_swiglu` runs the few-row kernel's pair form (each
+    row tile read from w1 and from w3 by one workgroup) with the bits of
+    `matmul(w1)` then `matmul(w3, epi=SILU_GATE)`: one and two X tiles, three
+    tiles a workgroup (4-8 rows of 9728 x 2560), ragged M, 8-wave K runs,
+    plain and nested scales, fp16 and bf16."""
+    from ttspipe_amd import _lib
+
+    M, K = shape
+    lib = _lib.load()
+    assert lib.ttsp_nf4_gemm_swiglu_fits(M, K, rows, 64, 256, int(nested)) == 1
+    w1 = to_linear(random_layer(M, K, nested, seed=M + rows), dtype)
+    w3 = to_linear(random_layer(M, K, nested, seed=M + rows + 1), dtype)
+    x = from_bits(randn_bits(rows * K, dtype, seed=rows + 5, scale=2.0), dtype).view(1, rows, K)
+    got = nf4.matmul_swiglu(w1, w3, x)
+    assert got is not None and got.shape == (1, rows, M)
+    g = nf4.matmul(w1, x)
+    ref = nf4.matmul(w3, x, epi=nf4.EPI_SILU_GATE, operand=g)
+    torch.cuda.synchronize()
+    gb, rb = bits(got), bits(ref)
+    assert np.array_equal(gb, rb), first_mismatch(gb, rb)
+    assert np.abs(o.to_f32(rb, dt_code(dtype))).max() > 0
+
+
 @pytest.mark.parametrize("shape,rows,bs2", [((2560, 9728), 512, 256), ((9728, 2560), 256, 256),
                                             ((9728, 2560), 512, 16), ((1536, 1024), 512, 256)])
 def test_swiglu_gemm_declines_what_one_launch_does_not_serve(nf4, shape, rows, bs2):

@@ -591,6 +591,20 @@ int gemm_dl_swiglu(const void* X, int dt, const uint8_t* W1, const uint8_t* A8_1
                    const float* CODE2_1, float offset_1, const uint8_t* W3, const uint8_t* A8_3,
                    const float* AMAX_3, const float* CODE2_3, float offset_3, const float* LUT, void* Y, int M, int K,
                    int N, int bs_shift, int bs2_shift, hipStream_t st);
+int gemm_skinny_pair(const void* X, int dt, const uint8_t* W1, const uint8_t* A8_1, const float* AMAX_1,
+                     const float* CODE2_1, float offset_1, const uint8_t* W3, const uint8_t* A8_3, const float* AMAX_3,
+                     const float* CODE2_3, float offset_3, const float* LUT, void* Y, int M, int K, int N, int bs_shift,
+                     int bs2_shift, hipStream_t st);
+bool skinny_pair_fits(int K, int N);
+
+// Whether the SwiGLU pair takes the skinny kernel's pair form: where each of
+// its two GEMMs would run the skinny kernel (3 to 32 rows, unsplit; two rows
+// take the GEMV, whose one-launch pair is ttsp_nf4_gemv_fused_rows).
+static bool swiglu_skinny(int M, int K, int N) {
+  if (M <= 0 || K <= 0 || K % 128 || N <= GEMV_ROWS_N || !skinny_pair_fits(K, N)) return false;
+  const GemmPlan p = gemm_plan(M, K, N);
+  return p.shape == 0 && p.splits == 1;
+}
 
 // Whether the SwiGLU pair fits one launch of the direct-to-LDS kernel: where
 // each of its two GEMMs would run that kernel unsplit (so the one launch
@@ -685,7 +699,7 @@ static int log2_of(int v) {
 extern "C" int ttsp_nf4_gemm_swiglu_fits(int M, int K, int N, int blocksize, int blocksize2, int nested) {
   const int bs = log2_of(blocksize), bs2 = nested ? log2_of(blocksize2) : 0;
   if (bs < 6 || bs2 < 0 || K % blocksize) return 0;
-  return swiglu_fits(M, K, N, bs, bs2, nested != 0) ? 1 : 0;
+  return swiglu_skinny(M, K, N) || swiglu_fits(M, K, N, bs, bs2, nested != 0) ? 1 : 0;
 }
 
 extern "C" int ttsp_nf4_gemm_swiglu(const void* X, int x_dtype, const uint8_t* W1, const uint8_t* A8_1,
@@ -700,6 +714,9 @@ extern "C" int ttsp_nf4_gemm_swiglu(const void* X, int x_dtype, const uint8_t* W
   if (!W3 || !AMAX_3 || (A8_3 != nullptr) != (A8_1 != nullptr) || (A8_3 && !CODE2_3))
     return (int)hipErrorInvalidValue;
   if ((uintptr_t)X % 16 || (uintptr_t)W1 % 16 || (uintptr_t)W3 % 16) return (int)hipErrorInvalidValue;
+  if (swiglu_skinny(M, K, N))
+    return gemm_skinny_pair(X, x_dtype, W1, A8_1, AMAX_1, CODE2_1, offset_1, W3, A8_3, AMAX_3, CODE2_3, offset_3, LUT,
+                            Y, M, K, N, bs_shift, bs2_shift, stream);
   if (!swiglu_fits(M, K, N, bs_shift, bs2_shift, A8_1 != nullptr)) return (int)hipErrorInvalidValue;
   return gemm_dl_swiglu(X, x_dtype, W1, A8_1, AMAX_1, CODE2_1, offset_1, W3, A8_3, AMAX_3, CODE2_3, offset_3, LUT, Y,
                         M, K, N, bs_shift, bs2_shift, stream);

@@ -37,6 +37,10 @@
 //     of the weight byte next to the lane's offset. The 64 KB are reused for
 //     the partial sums after the loop, so two workgroups fit a CU. A lane's 32 codes of a step lie in one scale block
 //     (64-code blocks start at multiples of 64).
+//   * The SwiGLU pair (PAIR): each of a workgroup's R row tiles is read from
+//     W1 and from W3 (2 R tile slots, two code2 tables), and the epilogue
+//     rounds as the two launches do: g = W1 x stored, then
+//     silu(g) rounded times (W3 x) rounded, rounded.
 #include "ttsp_common.h"
 
 namespace ttsp {
@@ -82,20 +86,30 @@ __device__ __forceinline__ uint32_t sk_pack2(float lo, float hi) {
 // b T / G .. (b + 1) T / G - 1, at most TG of them; a group past them repeats
 // the first tile's loads and stores nothing), so a matrix of 2-3 tiles a CU
 // runs in one round of workgroups instead of two and a tail.
-template <int DT, int R, int NT, int NW, int MS, bool NESTED, int TG = 1>
+// The second matrix of the SwiGLU pair (PAIR): its weights and scales.
+struct SkinnyW3 {
+  const uint8_t* W;
+  const uint8_t* A8;
+  const float* AMAX;
+  const float* CODE2;
+  float offset;
+};
+
+template <int DT, int R, int NT, int NW, int MS, bool NESTED, int TG = 1, bool PAIR = false>
 __global__ __launch_bounds__(64 * NW * TG) void nf4_skinny_kernel(
     const uint16_t* __restrict__ X, const uint8_t* __restrict__ W, const uint8_t* __restrict__ A8,
     const float* __restrict__ AMAX, const float* __restrict__ CODE2, float offset, const float* __restrict__ LUT,
     uint16_t* __restrict__ Y, const uint16_t* __restrict__ RES, int epi, int M, int K, int N, int bs_shift,
-    int bs2_shift) {
+    int bs2_shift, SkinnyW3 w3) {
   // byte e -> (code of its high nibble, code of its low nibble), copy j at
   // [e][j]; after the loop the same memory holds each wave's partial sums
   constexpr int NWT = NW * TG;  // waves a workgroup
-  static_assert(NWT * R * NT * 64 * sizeof(f32x4) <= SK_LDS, "partial sums exceed the table's LDS");
+  constexpr int S = PAIR ? 2 * R : R;  // tile slots: slot r < R of W, slot R + r of W3 (same rows)
+  static_assert(NWT * S * NT * 64 * sizeof(f32x4) <= SK_LDS, "partial sums exceed the table's LDS");
   __shared__ __align__(16) unsigned char lds[SK_LDS];
-  __shared__ __align__(16) float code2_s[NESTED ? 256 : 4];
+  __shared__ __align__(16) float code2_s[NESTED ? (PAIR ? 512 : 256) : 4];
   float2 (*lut2)[SK_REP] = reinterpret_cast<float2 (*)[SK_REP]>(lds);
-  f32x4 (*part)[R * NT][64] = reinterpret_cast<f32x4 (*)[R * NT][64]>(lds);
+  f32x4 (*part)[S * NT][64] = reinterpret_cast<f32x4 (*)[S * NT][64]>(lds);
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int grp = TG > 1 ? wave / NW : 0, wk = TG > 1 ? wave % NW : wave;  // row-tile group, K run
@@ -124,10 +138,13 @@ __global__ __launch_bounds__(64 * NW * TG) void nf4_skinny_kernel(
   // so no branch separates a load from its use and the compiler's wait counts
   // stay exact (a load under a branch makes it wait for everything).
   const float c16 = LUT[lane & 15];
-  f32x4 c2v = {0.0f, 0.0f, 0.0f, 0.0f};
+  f32x4 c2v = {0.0f, 0.0f, 0.0f, 0.0f}, c2v3 = {0.0f, 0.0f, 0.0f, 0.0f};
   if constexpr (NESTED)
 #pragma unroll
     for (int i = 0; i < 4; ++i) c2v[i] = CODE2[4 * lane + i];
+  if constexpr (NESTED && PAIR)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) c2v3[i] = w3.CODE2[4 * lane + i];
   u32x4 xq[SK_PF][NT][4];
   auto load_x = [&](u32x4 (&xs)[NT][4], int step) {
     const int st = min(step, max(s1 - 1, 0));
@@ -144,31 +161,32 @@ __global__ __launch_bounds__(64 * NW * TG) void nf4_skinny_kernel(
 #pragma unroll
   for (int i = 0; i < SK_PF; ++i) load_x(xq[i], s0 + i);
   __builtin_amdgcn_sched_barrier(0);  // keep the issue order: the scheduler would move later loads ahead
-  u32x4 wq[MS][R];
-  float sq[MS][R];
-  uint32_t aq[NESTED ? MS : 1][R];
+  u32x4 wq[MS][S];
+  float sq[MS][S];
+  uint32_t aq[NESTED ? MS : 1][S];
 #pragma unroll
   for (int j = 0; j < MS; ++j) {
     const int st = min(s0 + j, slast);
 #pragma unroll
-    for (int r = 0; r < R; ++r) {
-      const int row = min(row0 + 16 * r + m, M - 1);
+    for (int r = 0; r < S; ++r) {
+      const bool m3 = PAIR && r >= R;
+      const int row = min(row0 + 16 * (r % R) + m, M - 1);
       wq[j][r] = __builtin_nontemporal_load(
-          reinterpret_cast<const u32x4*>(W + (size_t)row * rowbytes + 64 * (size_t)st + 16 * q));
+          reinterpret_cast<const u32x4*>((m3 ? w3.W : W) + (size_t)row * rowbytes + 64 * (size_t)st + 16 * q));
       const int b = row * nblk + ((128 * st + 32 * q) >> bs_shift);
       if constexpr (NESTED) {
-        aq[j][r] = A8[b];
-        sq[j][r] = AMAX[b >> bs2_shift];
+        aq[j][r] = (m3 ? w3.A8 : A8)[b] + (m3 ? 256u : 0u);
+        sq[j][r] = (m3 ? w3.AMAX : AMAX)[b >> bs2_shift];
       } else {
-        sq[j][r] = AMAX[b];
+        sq[j][r] = (m3 ? w3.AMAX : AMAX)[b];
       }
     }
     __builtin_amdgcn_sched_barrier(0);
   }
 
-  f32x4 acc[R][NT];
+  f32x4 acc[S][NT];
 #pragma unroll
-  for (int r = 0; r < R; ++r)
+  for (int r = 0; r < S; ++r)
 #pragma unroll
     for (int c = 0; c < NT; ++c) acc[r][c] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 
@@ -187,6 +205,7 @@ __global__ __launch_bounds__(64 * NW * TG) void nf4_skinny_kernel(
   }
   // every wave writes the same code2 values (no branch on the wave)
   if constexpr (NESTED) reinterpret_cast<f32x4*>(code2_s)[lane] = c2v;
+  if constexpr (NESTED && PAIR) reinterpret_cast<f32x4*>(code2_s + 256)[lane] = c2v3;
   // (no arithmetic on the streamed operands may move above the barrier: each
   // such use waits for its load, and the in-order counter for every load
   // issued before it)
@@ -208,9 +227,9 @@ __global__ __launch_bounds__(64 * NW * TG) void nf4_skinny_kernel(
     u32x4 (&xs)[NT][4] = xq[j % SK_PF];
     const bool live = s0 + j < s1;
 #pragma unroll
-    for (int r = 0; r < R; ++r) {
+    for (int r = 0; r < S; ++r) {
       float sc = sq[j][r];
-      if constexpr (NESTED) sc = __fadd_rn(__fmul_rn(code2_s[aq[j][r]], sc), offset);
+      if constexpr (NESTED) sc = __fadd_rn(__fmul_rn(code2_s[aq[j][r]], sc), PAIR && r >= R ? w3.offset : offset);
       sc = live ? sc : 0.0f;
       const uint32_t wv[4] = {wq[j][r][0], wq[j][r][1], wq[j][r][2], wq[j][r][3]};
 #pragma unroll
@@ -238,7 +257,7 @@ __global__ __launch_bounds__(64 * NW * TG) void nf4_skinny_kernel(
   // tiles r with r % NW == w
   __syncthreads();  // every wave is past its last lookup: the table's memory takes the partial sums
 #pragma unroll
-  for (int r = 0; r < R; ++r)
+  for (int r = 0; r < S; ++r)
 #pragma unroll
     for (int c = 0; c < NT; ++c) part[wave][r * NT + c][lane] = acc[r][c];
   __syncthreads();
@@ -249,12 +268,18 @@ __global__ __launch_bounds__(64 * NW * TG) void nf4_skinny_kernel(
     const int row = row0 + 16 * r + m;
 #pragma unroll
     for (int c = 0; c < NT; ++c) {
-      f32x4 v = part[grp * NW][r * NT + c][lane];
+      f32x4 v = part[grp * NW][r * NT + c][lane], v3 = {0.0f, 0.0f, 0.0f, 0.0f};
+      if constexpr (PAIR) v3 = part[grp * NW][(R + r) * NT + c][lane];
 #pragma unroll
       for (int w = 1; w < NW; ++w) {
         const f32x4 o = part[grp * NW + w][r * NT + c][lane];
 #pragma unroll
         for (int i = 0; i < 4; ++i) v[i] = __fadd_rn(v[i], o[i]);
+        if constexpr (PAIR) {
+          const f32x4 o3 = part[grp * NW + w][(R + r) * NT + c][lane];
+#pragma unroll
+          for (int i = 0; i < 4; ++i) v3[i] = __fadd_rn(v3[i], o3[i]);
+        }
       }
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
@@ -263,7 +288,9 @@ __global__ __launch_bounds__(64 * NW * TG) void nf4_skinny_kernel(
         const size_t o = (size_t)n * M + row;
         const float y = Elem<DT>::load(Elem<DT>::store(v[i]));
         float out = y;
-        if (ep == 1) out = __fadd_rn(Elem<DT>::load(RES[o]), y);
+        if constexpr (PAIR)  // W1's output as its launch stores it, then W3's gate epilogue
+          out = __fmul_rn(Elem<DT>::load(Elem<DT>::store(silu_rn(y))), Elem<DT>::load(Elem<DT>::store(v3[i])));
+        else if (ep == 1) out = __fadd_rn(Elem<DT>::load(RES[o]), y);
         else if (ep == 2) out = __fmul_rn(Elem<DT>::load(Elem<DT>::store(silu_rn(Elem<DT>::load(RES[o])))), y);
         Y[o] = Elem<DT>::store(out);
       }
@@ -273,20 +300,27 @@ __global__ __launch_bounds__(64 * NW * TG) void nf4_skinny_kernel(
 
 int skinny_max_k(int N);
 
-template <int DT, int R, int NT, int NW, int MS, int TG = 1>
+bool skinny_pair_fits(int K, int N);
+
+// PAIR: the SwiGLU pair (w3 set), with half the row tiles a workgroup of the
+// single form where that has several (each tile slot is a tile of one
+// matrix; a pair tile is two slots, which keeps the loads in flight and the
+// registers as they were).
+template <int DT, int RV, int NT, int NW, int MS, int TG = 1, bool PAIR = false>
 static void launch_skinny(const void* X, const uint8_t* W, const uint8_t* A8, const float* AMAX, const float* CODE2,
                           float offset, const float* LUT, void* Y, const void* RES, int epi, int M, int K, int N,
-                          int bs_shift, int bs2_shift, hipStream_t st) {
+                          int bs_shift, int bs2_shift, hipStream_t st, const SkinnyW3& w3) {
+  constexpr int R = PAIR && RV > 1 ? RV / 2 : RV;
   const int tiles = (M + 16 * R - 1) / (16 * R);
   const dim3 grid((tiles + TG - 1) / TG);  // TG tiles a workgroup (the last may hold fewer)
   if (A8)
-    hipLaunchKernelGGL((nf4_skinny_kernel<DT, R, NT, NW, MS, true, TG>), grid, dim3(64 * NW * TG), 0, st,
+    hipLaunchKernelGGL((nf4_skinny_kernel<DT, R, NT, NW, MS, true, TG, PAIR>), grid, dim3(64 * NW * TG), 0, st,
                        (const uint16_t*)X, W, A8, AMAX, CODE2, offset, LUT, (uint16_t*)Y, (const uint16_t*)RES, epi,
-                       M, K, N, bs_shift, bs2_shift);
+                       M, K, N, bs_shift, bs2_shift, w3);
   else
-    hipLaunchKernelGGL((nf4_skinny_kernel<DT, R, NT, NW, MS, false, TG>), grid, dim3(64 * NW * TG), 0, st,
+    hipLaunchKernelGGL((nf4_skinny_kernel<DT, R, NT, NW, MS, false, TG, PAIR>), grid, dim3(64 * NW * TG), 0, st,
                        (const uint16_t*)X, W, A8, AMAX, CODE2, offset, LUT, (uint16_t*)Y, (const uint16_t*)RES, epi,
-                       M, K, N, bs_shift, bs2_shift);
+                       M, K, N, bs_shift, bs2_shift, w3);
 }
 
 // Launch shape. NW: the fewest waves (4, 8, 16) whose K runs fit SK_MAXS
@@ -305,10 +339,10 @@ static void launch_skinny(const void* X, const uint8_t* W, const uint8_t* A8, co
 // 5.7 / 6.4 / 9.3 us for 4 / 16 / 32 rows against 6.9 / 9.1 / 14.2 with
 // eight, at 2560 x 4096 and 1024 x 3072 eight are faster.) Returns false when
 // no shape fits (see skinny_max_k).
-template <int DT, int NT>
+template <int DT, int NT, bool PAIR = false>
 static bool skinny_shape(const void* X, const uint8_t* W, const uint8_t* A8, const float* AMAX, const float* CODE2,
                          float offset, const float* LUT, void* Y, const void* RES, int epi, int M, int K, int N,
-                         int bs_shift, int bs2_shift, hipStream_t st) {
+                         int bs_shift, int bs2_shift, hipStream_t st, const SkinnyW3& w3 = SkinnyW3{}) {
   const int tiles = (M + 15) / 16, steps = K >> 7;
   int nw = (steps + SK_MAXS - 1) / SK_MAXS;
   if (nw > 16) return false;
@@ -317,8 +351,9 @@ static bool skinny_shape(const void* X, const uint8_t* W, const uint8_t* A8, con
   const int run = (steps + nw - 1) / nw;
   const bool ms5 = run <= 5;
   const bool r2 = NT <= 2 && nw <= 8 && tiles >= 2 * 256 && N > 8;
-#define TTSP_L(RV, NWV, MSV) \
-  launch_skinny<DT, RV, NT, NWV, MSV>(X, W, A8, AMAX, CODE2, offset, LUT, Y, RES, epi, M, K, N, bs_shift, bs2_shift, st)
+#define TTSP_L(RV, NWV, MSV)                                                                                 \
+  launch_skinny<DT, RV, NT, NWV, MSV, 1, PAIR>(X, W, A8, AMAX, CODE2, offset, LUT, Y, RES, epi, M, K, N, bs_shift, \
+                                               bs2_shift, st, w3)
 #define TTSP_MS(RV, NWV) \
   do {                   \
     if (ms5) TTSP_L(RV, NWV, 5); \
@@ -340,15 +375,15 @@ static bool skinny_shape(const void* X, const uint8_t* W, const uint8_t* A8, con
   // against 10.4 us at 4 rows, 10.5 against 10.7 at 8; 16 rows tie)
   if constexpr (NT == 1) {
     if (many && tiles < 3 * 256 && N <= 8 && nw == 4 && ms5) {
-      launch_skinny<DT, 1, 1, 4, 5, 3>(X, W, A8, AMAX, CODE2, offset, LUT, Y, RES, epi, M, K, N, bs_shift, bs2_shift,
-                                        st);
+      launch_skinny<DT, 1, 1, 4, 5, 3, PAIR>(X, W, A8, AMAX, CODE2, offset, LUT, Y, RES, epi, M, K, N, bs_shift,
+                                              bs2_shift, st, w3);
       return true;
     }
   }
   if constexpr (NT == 2) {
     if (many && nw == 4 && ms5) { TTSP_L(4, 4, 5); return true; }
   }
-  if constexpr (NT == 4) {
+  if constexpr (NT == 4 && !PAIR) {
     if (many && nw == 4 && ms5) { TTSP_L(2, 4, 5); return true; }
   }
   if constexpr (NT <= 2) {
@@ -357,7 +392,7 @@ static bool skinny_shape(const void* X, const uint8_t* W, const uint8_t* A8, con
   }
   if (nw == 4) TTSP_MS1(4);
   else if (nw == 8) TTSP_MS1(8);
-  else if constexpr (NT == 1) TTSP_MS1(16);  // 1024 threads: 128 registers a lane, enough for one X tile only
+  else if constexpr (NT == 1 && !PAIR) TTSP_MS1(16);  // 1024 threads: 128 registers a lane, enough for one X tile only
   else return false;
 #undef TTSP_MS1
 #undef TTSP_MS
@@ -388,6 +423,34 @@ int gemm_skinny(const void* X, int dt, const uint8_t* W, const uint8_t* A8, cons
   if (!ok) return (int)hipErrorInvalidValue;
   TTSP_RETURN_LAUNCH();
 }
+
+// The SwiGLU pair in one launch: Y = silu(X W1^T) * (X W3^T), rounded and
+// with the bits of gemm_skinny(W1) then gemm_skinny(W3, epi 2) on its output.
+// Up to 32 rows (one or two X tiles) and K runs of at most 8 waves.
+int gemm_skinny_pair(const void* X, int dt, const uint8_t* W1, const uint8_t* A8_1, const float* AMAX_1,
+                     const float* CODE2_1, float offset_1, const uint8_t* W3, const uint8_t* A8_3, const float* AMAX_3,
+                     const float* CODE2_3, float offset_3, const float* LUT, void* Y, int M, int K, int N, int bs_shift,
+                     int bs2_shift, hipStream_t st) {
+  if (!skinny_pair_fits(K, N) || bs_shift < 6 || (uintptr_t)X % 16 || (uintptr_t)W1 % 16 || (uintptr_t)W3 % 16)
+    return (int)hipErrorInvalidValue;
+  const SkinnyW3 w3{W3, A8_3, AMAX_3, CODE2_3, offset_3};
+  bool ok;
+#define TTSP_SK(DTV)                                                                                                \
+  do {                                                                                                              \
+    if (N <= 16) ok = skinny_shape<DTV, 1, true>(X, W1, A8_1, AMAX_1, CODE2_1, offset_1, LUT, Y, nullptr, 0, M, K, N, \
+                                                 bs_shift, bs2_shift, st, w3);                                      \
+    else ok = skinny_shape<DTV, 2, true>(X, W1, A8_1, AMAX_1, CODE2_1, offset_1, LUT, Y, nullptr, 0, M, K, N,        \
+                                         bs_shift, bs2_shift, st, w3);                                              \
+  } while (0)
+  if (dt == DT_BF16) TTSP_SK(DT_BF16);
+  else if (dt == DT_F16) TTSP_SK(DT_F16);
+  else return (int)hipErrorInvalidValue;
+#undef TTSP_SK
+  if (!ok) return (int)hipErrorInvalidValue;
+  TTSP_RETURN_LAUNCH();
+}
+
+bool skinny_pair_fits(int K, int N) { return N >= 2 && N <= 32 && K % 128 == 0 && K <= 8 * SK_MAXS * 128; }
 
 // The longest row the skinny kernel takes for N activation rows: 16 waves of
 // SK_MAXS steps for one X tile (N <= 16), 8 waves otherwise.

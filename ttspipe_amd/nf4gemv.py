@@ -399,7 +399,9 @@ def matmul_swiglu(module1, module3, x, *, out=None):
     two-launch form `matmul(w3, x, epi=EPI_SILU_GATE, operand=matmul(w1, x))`
     and with its bits; None where one launch does not serve the shape (it
     serves where both GEMMs would run the direct-to-LDS kernel unsplit, e.g.
-    385 to 512 rows of 9728 x 2560)."""
+    385 to 512 rows of 9728 x 2560, and where both would run the few-row
+    kernel, 3 to 32 rows, whose pair form reads each row tile of w1 and w3
+    in one workgroup)."""
     import torch
 
     if not (prepare(module1) and prepare(module3)):
