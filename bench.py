@@ -469,18 +469,55 @@ def bench_small_n(ns=(1, 2, 4, 8, 16, 32), min_bytes: int = 2 * MALL_BYTES, repl
                     if rc:
                         raise RuntimeError(f"ttsp_nf4_gemm failed: {rc}")
 
-        body()
-        torch.cuda.synchronize()
-        graph = capture(body)
+        def body_pair():  # gate and up as the prefill block runs them: one launch (silu(gate) * up)
+            st = torch.cuda.current_stream().cuda_stream
+            for layer in copies:
+                for (name, M, K), lin in zip(LAYER, layer):
+                    if name == "gate":
+                        continue
+                    if name != "up":
+                        rc = lib.ttsp_nf4_gemm(xs[K].data_ptr(), _lib.DT_BF16, lin.w.data_ptr(), _lib.ptr(lin.a8),
+                                               lin.amax.data_ptr(), _lib.ptr(lin.code2), lin.offset, lut.data_ptr(),
+                                               ys[name].data_ptr(), 0, 0, M, K, n, 64, 256, st)
+                        if rc:
+                            raise RuntimeError(f"ttsp_nf4_gemm failed: {rc}")
+                        continue
+                    g = layer[[nm for nm, _, _ in LAYER].index("gate")]
+                    pair = (g.w.data_ptr(), _lib.ptr(g.a8), g.amax.data_ptr(), _lib.ptr(g.code2), g.offset,
+                            lin.w.data_ptr(), _lib.ptr(lin.a8), lin.amax.data_ptr(), _lib.ptr(lin.code2), lin.offset,
+                            lut.data_ptr(), ys[name].data_ptr())
+                    if n <= 2:
+                        rc = lib.ttsp_nf4_gemv_fused_rows(xs[K].data_ptr(), _lib.DT_BF16, None, 0.0, *pair, 0, 0, M,
+                                                          K, n, 64, 256, st)
+                    else:
+                        rc = lib.ttsp_nf4_gemm_swiglu(xs[K].data_ptr(), _lib.DT_BF16, *pair, M, K, n, 64, 256, st)
+                    if rc:
+                        raise RuntimeError(f"gate and up in one launch failed: {rc}")
+
         stream = torch.cuda.current_stream()
-        time_graph(graph, 2, stream)
-        sec = time_graph(graph, replays, stream) / ncopy
-        nbytes = sum(nf4_bytes(M, K, True, 2) + 2 * (n - 1) * (M + K) for _, M, K in LAYER)
-        out.append({"rows": n, "layer_us": round(sec * 1e6, 2), "effective_gbs": round(nbytes / sec / 1e9, 1),
-                    "rel_to_n1": None})
+        point = {"rows": n}
+        for key, fn in (("", body), ("_gate_up_one_launch", body_pair)):
+            if key and n > 2 and not lib.ttsp_nf4_gemm_swiglu_fits(9728, 2560, n, 64, 256, 1):
+                continue
+            fn()
+            torch.cuda.synchronize()
+            graph = capture(fn)
+            time_graph(graph, 2, stream)
+            sec = time_graph(graph, replays, stream) / ncopy
+            point["layer_us" + key] = round(sec * 1e6, 2)
+            if not key:
+                nbytes = sum(nf4_bytes(M, K, True, 2) + 2 * (n - 1) * (M + K) for _, M, K in LAYER)
+                point["effective_gbs"] = round(nbytes / sec / 1e9, 1)
+            del graph
+        out.append(point)
     for r in out:
         r["rel_to_n1"] = round(r["layer_us"] / out[0]["layer_us"], 2)
-    return {"layer": "q, k, v, o, gate, up, down (7 launches), NF4 nested, bf16", "copies": ncopy, "points": out}
+        if "layer_us_gate_up_one_launch" in r:
+            r["rel_to_n1_gate_up_one_launch"] = round(
+                r["layer_us_gate_up_one_launch"] / out[0]["layer_us_gate_up_one_launch"], 2)
+    return {"layer": "q, k, v, o, gate, up, down (7 launches), NF4 nested, bf16; "
+            "_gate_up_one_launch: gate and up as one launch, as the prefill block runs them (6 launches)",
+            "copies": ncopy, "points": out}
 
 
 def bench_norm_rope(min_bytes: int = 2 * MALL_BYTES, replays: int = 20):
