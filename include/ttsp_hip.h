@@ -123,8 +123,9 @@ int ttsp_nf4_gemm_split_norm(const void* X, int x_dtype, const uint8_t* W, const
  * of one shape [M, K] with the same blocksize and nesting, every value the
  * bits of ttsp_nf4_gemm(W1) then ttsp_nf4_gemm(W3, epi 2, R = the first's
  * output). Served where both of those would run the direct-to-LDS kernel
- * unsplit (ttsp_nf4_gemm_swiglu_fits; e.g. 385-512 rows of 9728 x 2560); other
- * shapes return hipErrorInvalidValue and the caller runs the two launches.
+ * unsplit (ttsp_nf4_gemm_swiglu_fits; e.g. 385-512 rows of 9728 x 2560) or
+ * the few-row kernel unsplit (3-32 rows, K up to 10240); other shapes return
+ * hipErrorInvalidValue and the caller runs the two launches.
  * 16-byte aligned X, W1, W3. Replaces: w1 then w3 with the SwiGLU gate in
  * the fork's FeedForward for S > 1 (the unfused block the reference runs
  * there, fastpath.py:207-271, through nf4gemv.matmul twice). */
